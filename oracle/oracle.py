@@ -1,0 +1,372 @@
+"""ctypes view of the CPU oracle (needle_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, as the checker or the CPU baseline -- never by
+the shipped library.  Each wrapper calls the C restatement of the
+reference function it names; the citations live in needle_oracle.c.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libneedle_oracle.so")
+
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_f64p = np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
+_i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
+_sz = C.c_size_t
+
+TERNARY = 5
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+class _AttnDims(C.Structure):
+    _fields_ = [("seq", _sz), ("num_heads", _sz), ("num_kv_heads", _sz),
+                ("qk_head_dim", _sz), ("v_head_dim", _sz)]
+
+
+class _Ring(C.Structure):
+    _fields_ = [("int8", C.c_int), ("num_kv_heads", _sz), ("qk_head_dim", _sz),
+                ("v_head_dim", _sz), ("slots", _sz), ("cap", _sz), ("window", _sz),
+                ("k", C.POINTER(C.c_float)), ("v", C.POINTER(C.c_float)),
+                ("kq", C.POINTER(C.c_int8)), ("vq", C.POINTER(C.c_int8)),
+                ("k_scale", C.POINTER(C.c_float)), ("v_scale", C.POINTER(C.c_float))]
+
+
+class _Cq(C.Structure):
+    _fields_ = [("packed", C.POINTER(C.c_uint8)), ("norms", C.POINTER(C.c_float)),
+                ("lut", C.POINTER(C.c_float)), ("per_byte", _sz), ("row_bytes", _sz),
+                ("num_groups", _sz), ("out_feat", _sz), ("in_feat", _sz),
+                ("in_padded", _sz), ("group", _sz), ("bits", C.c_uint8),
+                ("levels", C.c_float * 16), ("n_levels", _sz)]
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = C.CDLL(LIB_PATH)
+        L.or_f16_to_f32.argtypes = [C.c_uint16]
+        L.or_f16_to_f32.restype = C.c_float
+        L.or_fwht.argtypes = [_f32p, _sz]
+        L.or_fwht_normalized.argtypes = [_f32p, _sz]
+        L.or_packed_row_bytes.argtypes = [_sz, C.c_uint8]
+        L.or_packed_row_bytes.restype = _sz
+        L.or_read_bits.argtypes = [_u8p, _sz, _sz, C.c_uint32]
+        L.or_read_bits.restype = C.c_uint32
+        L.or_build_lut.argtypes = [C.c_uint8, _f32p, C.c_void_p]
+        L.or_build_lut.restype = _sz
+        L.or_cq_from_blob.argtypes = [_u8p, _sz, _sz, _sz, _sz, C.c_uint8, C.c_void_p, _sz,
+                                      C.POINTER(C.POINTER(_Cq))]
+        L.or_cq_free.argtypes = [C.POINTER(_Cq)]
+        L.or_cq_prepare_input.argtypes = [C.POINTER(_Cq), _f32p, _f32p]
+        L.or_cq_matvec_rows_prepared.argtypes = [C.POINTER(_Cq), _f32p, _sz, _sz, _f32p]
+        L.or_cq_matvec.argtypes = [C.POINTER(_Cq), _f32p, _f32p]
+        L.or_cq_matvec_prepared_reference.argtypes = [C.POINTER(_Cq), _f32p, _f32p]
+        L.or_cq_matmul_rows_prepared.argtypes = [C.POINTER(_Cq), _f32p, _sz, _sz, _sz, _f32p]
+        L.or_cq_dequantize_row.argtypes = [C.POINTER(_Cq), _sz, _f32p]
+        L.or_cb8_gemv.argtypes = [_u8p, _f32p, _f32p, _f32p, _sz, _sz]
+        L.or_cb8_gemv_omp.argtypes = [_u8p, _f32p, _f32p, _f32p, _sz, _sz]
+        L.or_cb8_gemv_f64.argtypes = [_u8p, _f32p, _f32p, _f64p, _sz, _sz]
+        L.or_cb8_gemm.argtypes = [_f32p, _u8p, _f32p, _f32p, _sz, _sz, _sz]
+        L.or_fake_quant_vec.argtypes = [_f32p, _sz, C.c_uint32]
+        L.or_quant_into.argtypes = [_f32p, _sz, _i8p]
+        L.or_quant_into.restype = C.c_float
+        L.or_quantize_rows.argtypes = [_f32p, _sz, _sz, _i8p, _f32p]
+        L.or_quant_rows.argtypes = [_f32p, _sz, _sz, _sz]
+        L.or_ring_new.argtypes = [C.c_int, _sz, _sz, _sz, _sz, _sz, _sz]
+        L.or_ring_new.restype = C.POINTER(_Ring)
+        L.or_ring_free.argtypes = [C.POINTER(_Ring)]
+        L.or_ring_write_kv.argtypes = [C.POINTER(_Ring), _sz, _f32p, _f32p]
+        L.or_ring_span.argtypes = [C.POINTER(_Ring), _sz, C.POINTER(_sz), C.POINTER(_sz)]
+        L.or_ring_attend_step.argtypes = [C.POINTER(_Ring), _f32p, _sz, _sz, _sz, _f32p]
+        L.or_attend_step_f32.argtypes = [_f32p, _f32p, _f32p, _sz, _sz, _sz,
+                                         C.POINTER(_AttnDims), _f32p]
+        L.or_attend_step_i8.argtypes = [_f32p, _i8p, _f32p, _i8p, _f32p, _sz, _sz, _sz,
+                                        C.POINTER(_AttnDims), _f32p]
+        L.or_attend_f32.argtypes = [_f32p, _f32p, _f32p, C.POINTER(_AttnDims), _sz, _f32p]
+        L.or_attend_i8.argtypes = [_f32p, _i8p, _f32p, _i8p, _f32p, C.POINTER(_AttnDims),
+                                   _sz, _f32p]
+        _lib = L
+    return _lib
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+# ---- math.rs / hadamard.rs --------------------------------------------------
+
+def f16_to_f32(bits: int) -> float:
+    return lib().or_f16_to_f32(bits)
+
+
+def fwht(x):
+    y = _f32(x).copy()
+    lib().or_fwht(y, y.size)
+    return y
+
+
+def fwht_normalized(x):
+    y = _f32(x).copy()
+    lib().or_fwht_normalized(y, y.size)
+    return y
+
+
+# ---- cq.rs ------------------------------------------------------------------
+
+def packed_row_bytes(in_padded: int, bits: int) -> int:
+    return lib().or_packed_row_bytes(in_padded, bits)
+
+
+def read_bits(row, bit: int, bits: int) -> int:
+    return lib().or_read_bits(np.ascontiguousarray(row, np.uint8), bit, bits, (1 << bits) - 1)
+
+
+def build_lut(bits: int, levels):
+    lv = _f32(levels)
+    per = lib().or_build_lut(bits, lv, None)
+    if per == 0:
+        return 0, np.zeros(0, np.float32)
+    out = np.zeros(256 * per, np.float32)
+    lib().or_build_lut(bits, lv, out.ctypes.data)
+    return per, out
+
+
+class CqError(Exception):
+    NAMES = {1: "UnsupportedBits", 2: "BadGroup", 3: "BadCodebookLen",
+             4: "ShortBlob", 5: "EmptyShape"}
+
+    def __init__(self, code):
+        super().__init__(self.NAMES.get(code, str(code)))
+        self.code = code
+
+
+class CqWeight:
+    """The oracle's CqWeight (cq.rs:117-810)."""
+
+    def __init__(self, blob, out_feat, in_feat, group, bits, codebook):
+        blob = np.ascontiguousarray(blob, np.uint8)
+        cb = _f32(codebook)
+        p = C.POINTER(_Cq)()
+        rc = lib().or_cq_from_blob(blob, blob.size, out_feat, in_feat, group, bits,
+                                   cb.ctypes.data, cb.size, C.byref(p))
+        if rc:
+            raise CqError(rc)
+        self._p = p
+        c = p.contents
+        self.out_feat, self.in_feat, self.in_padded = c.out_feat, c.in_feat, c.in_padded
+        self.group, self.bits, self.num_groups = c.group, c.bits, c.num_groups
+        self.row_bytes, self.per_byte = c.row_bytes, c.per_byte
+        self.levels = np.array(c.levels[:c.n_levels], np.float32)
+
+    def __del__(self):
+        if getattr(self, "_p", None) is not None and _lib is not None:
+            _lib.or_cq_free(self._p)
+            self._p = None
+
+    def norms(self):
+        c = self._p.contents
+        return np.ctypeslib.as_array(c.norms, (self.out_feat * self.num_groups,)).copy()
+
+    def prepare_input(self, x):
+        x = _f32(x)
+        xh = np.zeros(self.in_padded, np.float32)
+        lib().or_cq_prepare_input(self._p, x, xh)
+        return xh
+
+    def prepare_batch(self, xs):
+        xs = _f32(xs).reshape(-1, self.in_feat)
+        return np.stack([self.prepare_input(r) for r in xs]).astype(np.float32)
+
+    def matvec(self, x):
+        y = np.zeros(self.out_feat, np.float32)
+        lib().or_cq_matvec(self._p, _f32(x), y)
+        return y
+
+    def matvec_rows_prepared(self, xh, row_start, rows):
+        y = np.zeros(rows, np.float32)
+        lib().or_cq_matvec_rows_prepared(self._p, _f32(xh), row_start, rows, y)
+        return y
+
+    def matvec_prepared(self, xh):
+        return self.matvec_rows_prepared(xh, 0, self.out_feat)
+
+    def matvec_prepared_reference(self, xh):
+        y = np.zeros(self.out_feat, np.float32)
+        lib().or_cq_matvec_prepared_reference(self._p, _f32(xh), y)
+        return y
+
+    def matmul_rows_prepared(self, xh, batch, row_start, rows):
+        y = np.zeros(batch * rows, np.float32)
+        lib().or_cq_matmul_rows_prepared(self._p, _f32(xh).reshape(-1), batch, row_start,
+                                         rows, y)
+        return y
+
+    def dequantize_row(self, o):
+        out = np.zeros(self.in_feat, np.float32)
+        lib().or_cq_dequantize_row(self._p, o, out)
+        return out
+
+    def dequantize(self):
+        return np.stack([self.dequantize_row(o) for o in range(self.out_feat)])
+
+
+# ---- Format B ---------------------------------------------------------------
+
+def cb8_gemv(w, cb, x):
+    w = np.ascontiguousarray(w, np.uint8)
+    out, inn = w.shape
+    y = np.zeros(out, np.float32)
+    lib().or_cb8_gemv(w, _f32(cb), _f32(x), y, out, inn)
+    return y
+
+
+def cb8_gemv_omp(w, cb, x, y):
+    out, inn = w.shape
+    lib().or_cb8_gemv_omp(w, cb, x, y, out, inn)
+
+
+def cb8_gemv_f64(w, cb, x):
+    w = np.ascontiguousarray(w, np.uint8)
+    out, inn = w.shape
+    y = np.zeros(out, np.float64)
+    lib().or_cb8_gemv_f64(w, _f32(cb), _f32(x), y, out, inn)
+    return y
+
+
+def cb8_gemm(x, w, cb):
+    x = _f32(x)
+    w = np.ascontiguousarray(w, np.uint8)
+    m = x.shape[0]
+    out, inn = w.shape
+    y = np.zeros((m, out), np.float32)
+    lib().or_cb8_gemm(x, w, _f32(cb), y, m, out, inn)
+    return y
+
+
+# ---- v3/cache.rs ------------------------------------------------------------
+
+def fake_quant_vec(x, bits=8):
+    y = _f32(x).copy()
+    lib().or_fake_quant_vec(y, y.size, bits)
+    return y
+
+
+def quant_into(x):
+    x = _f32(x)
+    d = np.zeros(x.size, np.int8)
+    s = lib().or_quant_into(x, x.size, d)
+    return d, np.float32(s)
+
+
+def quantize_rows(x, head_dim):
+    x = _f32(x).reshape(-1)
+    rows = x.size // head_dim
+    ints = np.zeros(x.size, np.int8)
+    scales = np.ones(rows, np.float32)
+    lib().or_quantize_rows(x, rows, head_dim, ints, scales)
+    return ints, scales
+
+
+def quant_rows(x, seq, heads, head_dim):
+    y = _f32(x).copy()
+    lib().or_quant_rows(y, seq, heads, head_dim)
+    return y
+
+
+class Ring:
+    """One layer of the oracle's V3Cache (cache.rs:125-393)."""
+
+    def __init__(self, int8, num_kv_heads, qk, vd, hint, window, max_seq_len):
+        self._p = lib().or_ring_new(int(int8), num_kv_heads, qk, vd, hint, window, max_seq_len)
+        self.num_kv_heads, self.qk, self.vd = num_kv_heads, qk, vd
+
+    def __del__(self):
+        if getattr(self, "_p", None) is not None and _lib is not None:
+            _lib.or_ring_free(self._p)
+            self._p = None
+
+    @property
+    def slots(self):
+        return self._p.contents.slots
+
+    @property
+    def cap(self):
+        return self._p.contents.cap
+
+    def write_kv(self, pos, k, v):
+        lib().or_ring_write_kv(self._p, pos, _f32(k), _f32(v))
+
+    def span(self, pos):
+        lo, hi = _sz(), _sz()
+        lib().or_ring_span(self._p, pos, C.byref(lo), C.byref(hi))
+        return lo.value, hi.value
+
+    def store(self):
+        c = self._p.contents
+        s, H = c.slots, c.num_kv_heads
+        if c.int8:
+            return dict(
+                k=np.ctypeslib.as_array(c.kq, (s * H * c.qk_head_dim,)).copy(),
+                v=np.ctypeslib.as_array(c.vq, (s * H * c.v_head_dim,)).copy(),
+                k_scale=np.ctypeslib.as_array(c.k_scale, (s * H,)).copy(),
+                v_scale=np.ctypeslib.as_array(c.v_scale, (s * H,)).copy())
+        return dict(k=np.ctypeslib.as_array(c.k, (s * H * c.qk_head_dim,)).copy(),
+                    v=np.ctypeslib.as_array(c.v, (s * H * c.v_head_dim,)).copy())
+
+    def attend_step(self, q, lo, hi, num_heads):
+        out = np.zeros(num_heads * self.vd, np.float32)
+        lib().or_ring_attend_step(self._p, _f32(q), lo, hi, num_heads, out)
+        return out
+
+
+# ---- v3/attention.rs --------------------------------------------------------
+
+def _dims(seq, nh, nkv, qk, vd):
+    return _AttnDims(seq, nh, nkv, qk, vd)
+
+
+def attend_step_f32(q, k, v, slots, lo, hi, nh, nkv, qk, vd):
+    out = np.zeros(nh * vd, np.float32)
+    d = _dims(1, nh, nkv, qk, vd)
+    lib().or_attend_step_f32(_f32(q), _f32(k), _f32(v), slots, lo, hi, C.byref(d), out)
+    return out
+
+
+def attend_step_i8(q, k, ks, v, vs, slots, lo, hi, nh, nkv, qk, vd):
+    out = np.zeros(nh * vd, np.float32)
+    d = _dims(1, nh, nkv, qk, vd)
+    lib().or_attend_step_i8(_f32(q), np.ascontiguousarray(k, np.int8), _f32(ks),
+                            np.ascontiguousarray(v, np.int8), _f32(vs), slots, lo, hi,
+                            C.byref(d), out)
+    return out
+
+
+def attend_f32(q, k, v, seq, nh, nkv, qk, vd, window=0):
+    out = np.zeros(seq * nh * vd, np.float32)
+    d = _dims(seq, nh, nkv, qk, vd)
+    lib().or_attend_f32(_f32(q), _f32(k), _f32(v), C.byref(d), window or 0, out)
+    return out
+
+
+def attend_i8(q, k, ks, v, vs, seq, nh, nkv, qk, vd, window=0):
+    out = np.zeros(seq * nh * vd, np.float32)
+    d = _dims(seq, nh, nkv, qk, vd)
+    lib().or_attend_i8(_f32(q), np.ascontiguousarray(k, np.int8), _f32(ks),
+                       np.ascontiguousarray(v, np.int8), _f32(vs), C.byref(d),
+                       window or 0, out)
+    return out
