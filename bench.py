@@ -1,0 +1,236 @@
+"""Benchmark of the Needle-3 hot path on one MI355X.
+
+Headline (BASELINE metric "codebook GEMV GB/s (% HBM peak)"): the codebook
+dequant-GEMV at config 1's shape -- W [3072 x 768] uint8 codes, one 256-entry
+fp32 codebook per 64 rows, x [768], batch 1 -- over R = 448 distinct weight
+copies per step (1.09 GB, beyond the 256 MB MALL), as one strided launch.
+A step is one such launch; value = algorithmic bytes / time.
+
+Also reported ("secondary"): int8-KV decode attention at ctx 2048 (config 3,
+12 heads x 64) over 320 independent session caches per step (append one
+token + attend), and the batch-1 latencies of both kernels.
+
+cpu_baseline: the oracle's Format-B GEMV (the closed form, fp32, row-parallel
+with OpenMP like the reference's rayon row bands) on the host cores, on a
+bounded sample of the same workload.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "needle-rs_amd"))
+
+HBM_PEAK_GBS = 8000.0
+GEMV_OUT, GEMV_IN = 3072, 768
+GEMV_BYTES = GEMV_OUT * GEMV_IN + (GEMV_OUT // 64) * 256 * 4 + GEMV_IN * 4 + GEMV_OUT * 4
+GEMV_COPIES = 448
+ATT_H, ATT_D, ATT_CTX, ATT_SESSIONS = 12, 64, 2048, 320
+# int8 K and V plus their f32 scales over the span, plus q (fp32) in and out.
+ATT_BYTES = ATT_CTX * (2 * ATT_H * ATT_D + 2 * ATT_H * 4) + 2 * ATT_H * ATT_D * 4
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--no-secondary", action="store_true")
+    p.add_argument("--only", choices=["gemv", "attn"], default=None,
+                   help="run one workload only, without the batch-1 latency probes "
+                        "(for per-kernel profiles)")
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="also run a plain 1 GiB device copy (PMC byte-counter scale)")
+    return p.parse_args()
+
+
+def timed_loop(torch, fn, steps, warmup, min_warm_s=0.5):
+    """W untimed warm-up steps (continued until `min_warm_s` has passed, so the
+    clocks have left their idle state), then exactly `steps` timed steps
+    between two events on the stream the kernels run on."""
+    t0 = time.perf_counter()
+    n = 0
+    while n < warmup or time.perf_counter() - t0 < min_warm_s:
+        fn()
+        n += 1
+        if n % 16 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps  # ms
+
+
+def cpu_baseline(seconds=12.0):
+    """Oracle Format-B GEMV on the host: 64 distinct copies (151 MB), looped
+    until `seconds` have elapsed, OpenMP over the rows."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    rng = np.random.default_rng(1)
+    copies = 64
+    W = rng.integers(0, 256, size=(copies, GEMV_OUT, GEMV_IN), dtype=np.uint8)
+    CB = rng.normal(0, 0.02, size=(copies, GEMV_OUT // 64, 256)).astype(np.float32)
+    X = rng.normal(size=(copies, GEMV_IN)).astype(np.float32)
+    y = np.zeros(GEMV_OUT, np.float32)
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    O.cb8_gemv_omp(W[0], CB[0], X[0], y)  # warm
+    calls, t0 = 0, time.perf_counter()
+    while True:
+        i = calls % copies
+        O.cb8_gemv_omp(W[i], CB[i], X[i], y)
+        calls += 1
+        el = time.perf_counter() - t0
+        if el >= seconds and calls >= copies:
+            break
+    return {"value": round(calls * GEMV_BYTES / el / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{calls} GEMVs of 3072x768 u8 over 64 distinct weight copies in "
+                      f"{el:.1f} s (oracle or_cb8_gemv_omp, {threads} OpenMP threads)"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+    import needle_amd as nd
+
+    assert torch.cuda.is_available(), "bench needs a GPU"
+    torch.cuda.set_device(0)
+    ctx = nd.Ctx(0)
+    gen = torch.Generator(device="cuda").manual_seed(1234)
+
+    # ---- headline: batched codebook GEMV ------------------------------------
+    R = GEMV_COPIES if args.only in (None, "gemv") else 1
+    W = torch.randint(0, 256, (R, GEMV_OUT, GEMV_IN), dtype=torch.uint8, device="cuda", generator=gen)
+    CB = torch.randn(R, GEMV_OUT // 64, 256, device="cuda", generator=gen) * 0.02
+    X = torch.randn(R, GEMV_IN, device="cuda", generator=gen)
+    Y = torch.empty(R, GEMV_OUT, device="cuda")
+
+    def gemv_step():
+        nd.cb8_gemv_batched(ctx, W, CB, X, Y)
+
+    ms = ms1 = float("nan")
+    if args.only in (None, "gemv"):
+        ms = timed_loop(torch, gemv_step, args.steps, args.warmup)
+    step_bytes = R * GEMV_BYTES
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+
+    if args.only is None:
+        # batch-1 latency of one GEMV (a single 2.4 MB weight; L2/MALL-warm)
+        w1, cb1, x1, y1 = W[0], CB[0], X[0], Y[0]
+        ms1 = timed_loop(torch, lambda: nd.cb8_gemv(ctx, w1, cb1, x1, y1), 200, 20)
+
+    result = {
+        "metric": "codebook GEMV GB/s (% HBM peak); decode tok/s @ ctx2048 int8 KV",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "codebook dequant-GEMV, batch 1: W [3072 x 768] uint8 codes uniform "
+                        "0..255, one 256-entry fp32 codebook per 64 rows ~N(0,0.02), x fp32 "
+                        "[768] ~N(0,1); 448 distinct (W, codebook, x) problems per step in one "
+                        "launch (1.086 GB per step)",
+            "bytes_per_gemv": GEMV_BYTES,
+            "gemvs_per_step": R,
+            "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
+            "single_gemv_us": round(ms1 * 1e3, 2),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gbs, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "cb8_gemv_kernel<3>",
+        },
+    }
+
+    # ---- secondary: int8 KV append + decode attention at ctx 2048 -----------
+    if not args.no_secondary and args.only in (None, "attn"):
+        S = ATT_SESSIONS
+        g = nd.kv_geom(ATT_H, ATT_H, ATT_D, ATT_D, ATT_CTX)
+        nb = nd.kv_block_bytes(g)
+        off = nd.kv_offsets(g)
+        blk = torch.empty(S * nb, dtype=torch.uint8, device="cuda")
+        view = blk.view(S, nb)
+        codes = torch.randint(-127, 128, (S, off["ks"]), dtype=torch.int8, device="cuda",
+                              generator=gen)
+        view[:, :off["ks"]].copy_(codes.view(torch.uint8))
+        del codes
+        scales = torch.rand(S, 2 * ATT_H * ATT_CTX, device="cuda", generator=gen) * 0.03 + 1e-3
+        view[:, off["ks"]:off["ks"] + 8 * ATT_H * ATT_CTX].copy_(scales.view(torch.uint8).view(S, -1))
+        del scales
+        q = torch.randn(S, ATT_H * ATT_D, device="cuda", generator=gen)
+        knew = torch.randn(S, ATT_H * ATT_D, device="cuda", generator=gen)
+        vnew = torch.randn(S, ATT_H * ATT_D, device="cuda", generator=gen)
+        pos = torch.full((S,), ATT_CTX - 1, dtype=torch.int32, device="cuda")
+        lo = torch.zeros(S, dtype=torch.int32, device="cuda")
+        out = torch.empty(S, ATT_H * ATT_D, device="cuda")
+
+        def attn_only():
+            nd.attend_step_i8(ctx, g, blk, nb, lo, pos, q, quant_query=True, out=out)
+
+        def decode_step():
+            nd.kv_write(ctx, g, blk, nb, pos, knew, vnew)
+            attn_only()
+
+        ms_dec = ms_att1 = float("nan")
+        if args.only is None:
+            ms_dec = timed_loop(torch, decode_step, max(10, args.steps // 2), 5)
+        ms_att = timed_loop(torch, attn_only, max(10, args.steps // 2), 5)
+        att_gbs = S * ATT_BYTES / (ms_att * 1e-3) / 1e9
+        if args.only is None:
+            one = lambda: nd.attend_step_i8(ctx, g, blk, nb, lo[:1], pos[:1], q[:1],
+                                            quant_query=True, out=out[:1])
+            ms_att1 = timed_loop(torch, one, 200, 20)
+        result["secondary"] = {
+            "decode_attention_int8_ctx2048": {
+                "workload": f"{S} sessions x 12 heads x 64, ctx 2048, int8 K/V + f32 scales; "
+                            "step = append one token per session + split-K attention",
+                "session_tokens_per_s": round(S / (ms_dec * 1e-3), 1),
+                "ms_per_step": round(ms_dec, 4),
+                "attention_GBps": round(att_gbs, 2),
+                "attention_frac_hbm": round(att_gbs / HBM_PEAK_GBS, 4),
+                "bytes_per_session_decode": ATT_BYTES,
+                "single_session_attention_us": round(ms_att1 * 1e3, 2),
+            }
+        }
+
+    if args.calibrate_copy:
+        a = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+
+    ctx.close()
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

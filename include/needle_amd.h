@@ -1,0 +1,192 @@
+/*
+ * needle_amd.h -- C ABI of the MI355X (gfx950) Needle-3 hot path.
+ *
+ * Plain pointers and sizes only.  Unless a parameter says "host", every
+ * buffer pointer is a device pointer (hipMalloc'd, or nd_malloc'd) and
+ * every call is asynchronous on the context's stream; nd_ctx_synchronize()
+ * waits for it.  Each call returns ND_OK (0) or an error code, and keeps a
+ * per-thread message for nd_last_error(), mirroring needle_last_error
+ * (crates/needle-c/include/needle.h:487, crates/needle-c/src/lib.rs:27-39).
+ *
+ * Citations name the reference interface each entry point replaces, as
+ * path:line in the needle-rs checkout.
+ */
+#ifndef NEEDLE_AMD_H
+#define NEEDLE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status ------------------------------------------------------------ */
+enum nd_status {
+    ND_OK = 0,
+    ND_ERR_ARG = 1,      /* invalid argument (shape, NULL, range) */
+    ND_ERR_HIP = 2,      /* a HIP runtime call failed */
+    ND_ERR_NOMEM = 3,    /* device or host allocation failed */
+    /* CqWeight::from_blob errors, cq.rs:76-89 (CqError), same order */
+    ND_ERR_CQ_UNSUPPORTED_BITS = 11,
+    ND_ERR_CQ_BAD_GROUP = 12,
+    ND_ERR_CQ_BAD_CODEBOOK_LEN = 13,
+    ND_ERR_CQ_SHORT_BLOB = 14,
+    ND_ERR_CQ_EMPTY_SHAPE = 15
+};
+
+/* Last error message on this thread, or NULL.  Borrowed; valid until the
+ * next nd_* call on this thread.  Replaces needle_last_error
+ * (needle.h:487; lib.rs:27-39). */
+const char *nd_last_error(void);
+
+/* ---- context: one device, one stream ------------------------------------ */
+typedef struct nd_ctx nd_ctx;
+
+/* A context with a non-blocking stream it creates and owns.  No reference
+ * counterpart: the reference is CPU-only. */
+int nd_ctx_create(int device, nd_ctx **out);
+/* A context that launches on the caller's hipStream_t `stream` (NULL: the
+ * device's default stream), e.g. the stream a framework's tensors live on. */
+int nd_ctx_create_on_stream(int device, void *stream, nd_ctx **out);
+void nd_ctx_destroy(nd_ctx *ctx);
+int nd_ctx_synchronize(nd_ctx *ctx);
+
+/* Device memory helpers, so a C caller needs no HIP headers. */
+int nd_malloc(nd_ctx *ctx, size_t bytes, void **out);
+int nd_free(nd_ctx *ctx, void *ptr);
+int nd_memcpy_htod(nd_ctx *ctx, void *dst, const void *host_src, size_t bytes);
+int nd_memcpy_dtoh(nd_ctx *ctx, void *host_dst, const void *src, size_t bytes);
+
+/* ---- Format B: uint8 codes, one 256-entry fp32 codebook per 64 rows ----- */
+/*
+ * y[o] = sum_k cb[o/64][w[o*in + k]] * x[k].
+ * w: [out][in] uint8; cb: [ceil(out/64)][256] f32; x: [in]; y: [out].
+ * in must be a multiple of 16.  The format has no reference function; its
+ * nearest analogues are the byte-LUT matvec (cq.rs:838-873) and the simple
+ * reference matvec (cq.rs:393-426).
+ */
+int nd_cb8_gemv(nd_ctx *ctx, const uint8_t *w, const float *cb,
+                const float *x, float *y, size_t out, size_t in);
+
+/* `count` independent GEMVs in one launch: problem i reads
+ * w + i*w_stride, cb + i*cb_stride, x + i*x_stride and writes
+ * y + i*y_stride (strides in elements). */
+int nd_cb8_gemv_batched(nd_ctx *ctx, size_t count,
+                        const uint8_t *w, size_t w_stride,
+                        const float *cb, size_t cb_stride,
+                        const float *x, size_t x_stride,
+                        float *y, size_t y_stride, size_t out, size_t in);
+
+/* Y[m][o] = sum_k X[m][k] * cb[o/64][w[o][k]], with X and the decoded
+ * weights rounded to bf16 and products accumulated in fp32 on MFMA.
+ * out must be a multiple of 64 and in a multiple of 32.  Batched analogue:
+ * CqWeight::matmul_rows_prepared (cq.rs:446-472). */
+int nd_cb8_gemm(nd_ctx *ctx, const float *x, const uint8_t *w,
+                const float *cb, float *y, size_t m, size_t out, size_t in);
+
+/* ---- Format A: Cactus-Quants weights (cq.rs) ----------------------------- */
+typedef struct nd_cq nd_cq;
+
+/* Parse a CQ blob (host memory: packed LSB-first codes then FP16 norms)
+ * and upload it.  Replaces CqWeight::from_blob (cq.rs:181-238); the same
+ * errors in the same order (ND_ERR_CQ_*).  `codebook` (host) is the
+ * 28-float cb2|cb3|cb4 header block, ignored for ternary (bits == 5). */
+int nd_cq_from_blob(nd_ctx *ctx, const uint8_t *blob, size_t blob_len,
+                    size_t out_feat, size_t in_feat, size_t group,
+                    uint8_t bits, const float *codebook, size_t codebook_len,
+                    nd_cq **out);
+void nd_cq_free(nd_cq *w);
+/* Geometry: CqWeight::{out_feat, in_feat, in_padded, group, bits}. */
+int nd_cq_shape(const nd_cq *w, size_t *out_feat, size_t *in_feat,
+                size_t *in_padded, size_t *group, uint8_t *bits);
+
+/* xh[b] = per-group normalised FWHT of zero-padded x[b], for `batch` rows.
+ * x: [batch][in_feat], xh: [batch][in_padded].  Replaces
+ * CqWeight::prepare_input (cq.rs:264-274) -> fwht_normalized
+ * (hadamard.rs:48-55). */
+int nd_cq_prepare_input(nd_ctx *ctx, const nd_cq *w, const float *x,
+                        size_t batch, float *xh);
+
+/* y[r] = W[row_start + r] . xh, r < rows.  Replaces
+ * CqWeight::matvec_rows_prepared (cq.rs:301-307 -> 721-757, 838-873). */
+int nd_cq_matvec_rows_prepared(nd_ctx *ctx, const nd_cq *w, const float *xh,
+                               size_t row_start, size_t rows, float *y);
+
+/* y[b*rows + r] = W[row_start + r] . xh[b], batch-major.  Replaces
+ * CqWeight::matmul_rows_prepared (cq.rs:446-472 -> 632-679). */
+int nd_cq_matmul_rows_prepared(nd_ctx *ctx, const nd_cq *w, const float *xh,
+                               size_t batch, size_t row_start, size_t rows,
+                               float *y);
+
+/* out[i] = dequantized row rows[i] (in_feat floats each); rows is a device
+ * int32 array of n row indices.  Replaces CqWeight::dequantize_row
+ * (cq.rs:763-779), gathered. */
+int nd_cq_dequantize_rows(nd_ctx *ctx, const nd_cq *w, const int32_t *rows,
+                          size_t n, float *out);
+
+/* ---- int8 KV cache (v3/cache.rs, v3/attention.rs) -------------------------- */
+
+/* fake_quant_vec(x[r], 8) for every row r of `dim` floats, in place.
+ * Replaces fake_quant_vec (cache.rs:68-73) and quant_rows
+ * (v3/model.rs:99-106). */
+int nd_fake_quant(nd_ctx *ctx, float *x, size_t rows, size_t dim);
+
+/* ints[r] = quant_into(x[r]); scales[r] its scale.  Replaces quantize_rows
+ * (cache.rs:113-122).  Bit-exact. */
+int nd_quantize_rows(nd_ctx *ctx, const float *x, size_t rows,
+                     size_t head_dim, int8_t *ints, float *scales);
+
+/*
+ * Geometry of one int8 KV block: one layer of one session.  Device layout
+ * (head-major, so one kv head's span is one contiguous byte run):
+ *   k  int8 [num_kv_heads][cap][qk_head_dim]    at offset 0
+ *   v  int8 [num_kv_heads][cap][v_head_dim]     at nd_kv_v_offset()
+ *   ks f32  [num_kv_heads][cap]                 at nd_kv_ks_offset()
+ *   vs f32  [num_kv_heads][cap]                 at nd_kv_vs_offset()
+ * Logical position p lives at slot p % cap.  qk_head_dim and v_head_dim
+ * must be multiples of 16 and at most 256; num_heads a multiple of
+ * num_kv_heads with num_heads / num_kv_heads <= 8.
+ */
+typedef struct nd_kv_geom {
+    int32_t num_heads;
+    int32_t num_kv_heads;
+    int32_t qk_head_dim;
+    int32_t v_head_dim;
+    int32_t cap;
+} nd_kv_geom;
+
+size_t nd_kv_block_bytes(const nd_kv_geom *g);
+size_t nd_kv_v_offset(const nd_kv_geom *g);
+size_t nd_kv_ks_offset(const nd_kv_geom *g);
+size_t nd_kv_vs_offset(const nd_kv_geom *g);
+
+/* For i < count: quantise k[i] ([num_kv_heads][qk] f32) and v[i] per kv
+ * head and store them, with their scales, at slot pos[i] % cap of the block
+ * at kv + i*kv_stride bytes (kv_stride 0: every row into one block, e.g. a
+ * prompt).  pos: device int32[count].  Replaces V3Cache::write_kv
+ * (cache.rs:346-379) -> quant_into (cache.rs:98-104); bit-exact. */
+int nd_kv_write(nd_ctx *ctx, const nd_kv_geom *g, void *kv, size_t kv_stride,
+                size_t count, const int32_t *pos, const float *k,
+                const float *v);
+
+/*
+ * For i < count: out[i] ([num_heads][v_head_dim]) = softmax attention of
+ * q[i] ([num_heads][qk_head_dim]) over logical positions lo[i]..=hi[i] of
+ * the block at kv + i*kv_stride bytes, GQA head h reading kv head
+ * h / (num_heads / num_kv_heads), scores scaled by `scale`.  With
+ * quant_query != 0, each query head is first fake-quantised to 8 bits
+ * (quant_rows, v3/model.rs:289-293).  Requires hi[i] - lo[i] < cap.
+ * Split-K over the span; partials live in a context workspace.
+ * Replaces attend_step with KvStore::Int8 (attention.rs:300-377) -- and,
+ * with kv_stride 0 and lo/hi per prompt row, attend (attention.rs:218-287).
+ */
+int nd_attend_step_i8(nd_ctx *ctx, const nd_kv_geom *g, const void *kv,
+                      size_t kv_stride, size_t count, const int32_t *lo,
+                      const int32_t *hi, const float *q, float scale,
+                      int quant_query, float *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* NEEDLE_AMD_H */

@@ -1,0 +1,413 @@
+// Format B: one uint8 code per weight, one 256-entry fp32 codebook per 64
+// consecutive output rows.  y[o] = sum_k cb[o/64][W[o,k]] * x[k].
+//
+// The format has no reference function (its nearest analogue is the byte-LUT
+// decode of crates/needle-core/src/cq.rs:838-873); the semantics are the
+// closed form above.
+//
+// GEMV (decode, batch 1) is HBM-bound: 1 byte of code per multiply-add, so
+// the kernel is shaped around keeping HBM streaming while each code costs a
+// byte extract, an LDS gather and one FMA:
+//   * one 64-row codebook tile per 4-wave workgroup, 32 lanes per row, the
+//     lane's activations in registers (fast path: in = 256*M);
+//   * the codebook in LDS as 32 lane-private replicas, so random gathers do
+//     not conflict on banks;
+//   * code loads split in two halves so the second half is in flight while
+//     the first computes; nontemporal loads, since codes are read once.
+// Other widths fall back to a kernel with the activations in LDS.
+// GEMM (prefill) dequantises a 64x32 weight tile to bf16 in LDS and feeds
+// v_mfma_f32_16x16x32_bf16 with fp32 accumulation.
+#include "nd_internal.h"
+
+#include <hip/hip_bf16.h>
+
+namespace {
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kTileRows = 64;      // rows sharing one codebook
+constexpr int kThreads = 256;      // 4 waves
+constexpr int kLanesPerRow = 16;
+constexpr int kRowsPerPass = kThreads / kLanesPerRow;  // 16
+
+// Fast path, in = 256*M (M = 1..4; config 1's 768 is M = 3).  One 256-thread
+// block owns one 64-row tile.  32 lanes share a row: lane j reads M/2
+// 16-byte vectors (bytes 512k + 16j) and, for odd M, one 8-byte vector
+// (bytes 512*(M/2) + 8j) -- every load instruction covers two rows x 256 or
+// 512 contiguous bytes -- and keeps the matching 8*M activations in
+// registers.  The 16 row passes of a wave are loaded in two halves: the
+// second half is issued as the first pass starts computing, so HBM traffic
+// overlaps the gathers.  Rows past `out` are clamped (a valid row is read
+// and its sum discarded) rather than predicated.
+//
+// The codebook sits in LDS as 32 lane-private replicas, entry-major (entry
+// e, replica r at dword 32e + r): lane l's gathers all hit bank l % 32, so a
+// random gather does not conflict.
+template <int M>
+struct RowCodes {
+    u32x4_t a[M / 2 > 0 ? M / 2 : 1];
+    u32x2_t b;
+};
+
+template <int M>
+__device__ inline void load_row(RowCodes<M> &c, const uint8_t *__restrict__ rp, int j)
+{
+#pragma unroll
+    for (int k = 0; k < M / 2; ++k)
+        c.a[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(rp + 512 * k) + j);
+    if (M % 2)
+        c.b = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t *>(rp + 512 * (M / 2)) + j);
+}
+
+template <int M>
+__global__ __launch_bounds__(kThreads, 4) void cb8_gemv_kernel(
+    const uint8_t *__restrict__ w, size_t w_stride, const float *__restrict__ cb,
+    size_t cb_stride, const float *__restrict__ x, size_t x_stride, float *__restrict__ y,
+    size_t y_stride, int out)
+{
+    constexpr int K = 256 * M;
+    constexpr int kPasses = 8;  // 16 rows per wave, 2 per pass
+    constexpr int kFirst = kPasses / 2;
+    __shared__ float4 rep4[256 * 32 / 4];  // 32 KB
+
+    const size_t prob = blockIdx.y;
+    w += prob * w_stride;
+    cb += prob * cb_stride + size_t(blockIdx.x) * 256;
+    x += prob * x_stride;
+    y += prob * y_stride;
+    const int t = threadIdx.x;
+    const int wave = t >> 6;
+    const int lane = t & 63;
+    const int j = lane & 31;
+    const int row0 = blockIdx.x * kTileRows + wave * 16 + (lane >> 5);
+
+    RowCodes<M> c[kPasses];
+#pragma unroll
+    for (int p = 0; p < kFirst; ++p) {
+        const int r = min(row0 + 2 * p, out - 1);
+        load_row(c[p], w + size_t(r) * K, j);
+    }
+    // float4 slot f4 = i*256 + t of the replica array holds entry f4 / 8.
+    float cbv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) cbv[i] = cb[(i * kThreads + t) >> 3];
+    float xa[M / 2 > 0 ? M / 2 : 1][16], xb[8];
+#pragma unroll
+    for (int k = 0; k < M / 2; ++k) {
+        const float4 *xp = reinterpret_cast<const float4 *>(x + 512 * k + 16 * j);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 v = xp[q];
+            xa[k][4 * q + 0] = v.x;
+            xa[k][4 * q + 1] = v.y;
+            xa[k][4 * q + 2] = v.z;
+            xa[k][4 * q + 3] = v.w;
+        }
+    }
+    if (M % 2) {
+        const float4 *xp = reinterpret_cast<const float4 *>(x + 512 * (M / 2) + 8 * j);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const float4 v = xp[q];
+            xb[4 * q + 0] = v.x;
+            xb[4 * q + 1] = v.y;
+            xb[4 * q + 2] = v.z;
+            xb[4 * q + 3] = v.w;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) rep4[i * kThreads + t] = make_float4(cbv[i], cbv[i], cbv[i], cbv[i]);
+    __syncthreads();
+
+    const float *cbl = reinterpret_cast<const float *>(rep4) + (lane & 31);
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+        if (p == 0) {
+#pragma unroll
+            for (int q = kFirst; q < kPasses; ++q) {
+                const int r = min(row0 + 2 * q, out - 1);
+                load_row(c[q], w + size_t(r) * K, j);
+            }
+        }
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int k = 0; k < M / 2; ++k) {
+            const uint32_t dw[4] = {c[p].a[k].x, c[p].a[k].y, c[p].a[k].z, c[p].a[k].w};
+#pragma unroll
+            for (int d = 0; d < 4; ++d)
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    const uint32_t e = (dw[d] >> (8 * b)) & 0xffu;
+                    acc[b] += cbl[e * 32] * xa[k][4 * d + b];
+                }
+        }
+        if (M % 2) {
+            const uint32_t dw[2] = {c[p].b.x, c[p].b.y};
+#pragma unroll
+            for (int d = 0; d < 2; ++d)
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    const uint32_t e = (dw[d] >> (8 * b)) & 0xffu;
+                    acc[b] += cbl[e * 32] * xb[4 * d + b];
+                }
+        }
+        float s = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+        s += __shfl_xor(s, 16, 32);
+        s += __shfl_xor(s, 8, 32);
+        s += __shfl_xor(s, 4, 32);
+        s += __shfl_xor(s, 2, 32);
+        s += __shfl_xor(s, 1, 32);
+        const int r = row0 + 2 * p;
+        if (j == 0 && r < out) y[r] = s;
+    }
+}
+
+// Any `in` (multiple of 16): activations staged in LDS instead of registers.
+template <int REP>
+__global__ __launch_bounds__(kThreads) void cb8_gemv_generic_kernel(
+    const uint8_t *__restrict__ w, size_t w_stride, const float *__restrict__ cb,
+    size_t cb_stride, const float *__restrict__ x, size_t x_stride, float *__restrict__ y,
+    size_t y_stride, int out, int in)
+{
+    __shared__ float4 rep4[256 * REP / 4];
+    __shared__ float stage[256];
+    extern __shared__ float xs[];
+    float *rep = reinterpret_cast<float *>(rep4);
+    const int tile = blockIdx.x;
+    const size_t prob = blockIdx.y;
+    w += prob * w_stride;
+    cb += prob * cb_stride + size_t(tile) * 256;
+    x += prob * x_stride;
+    y += prob * y_stride;
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int j = t & (kLanesPerRow - 1);
+    const int rg = t / kLanesPerRow;
+    const int nvec = in >> 4;
+    stage[t] = cb[t];
+    for (int k = t; k < in; k += kThreads) xs[k] = x[k];
+    __syncthreads();
+    for (int i = 0; i < REP / 4; ++i) {
+        const int f4 = i * kThreads + t;
+        const float v = stage[(f4 * 4) / REP];
+        rep4[f4] = make_float4(v, v, v, v);
+    }
+    __syncthreads();
+    const float *cbl = rep + (lane & (REP - 1));
+    const int row0 = tile * kTileRows;
+    for (int p = 0; p < kTileRows / kRowsPerPass; ++p) {
+        const int r = row0 + rg + kRowsPerPass * p;
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (r < out) {
+            const uint4 *wr = reinterpret_cast<const uint4 *>(w + size_t(r) * in);
+            for (int c = j; c < nvec; c += kLanesPerRow) {
+                const uint4 cv = wr[c];
+                const uint32_t dw[4] = {cv.x, cv.y, cv.z, cv.w};
+#pragma unroll
+                for (int d = 0; d < 4; ++d)
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) {
+                        const uint32_t e = (dw[d] >> (8 * b)) & 0xffu;
+                        acc[b] += cbl[e * REP] * xs[c * 16 + 4 * d + b];
+                    }
+            }
+        }
+        float s = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+        s += __shfl_xor(s, 8, kLanesPerRow);
+        s += __shfl_xor(s, 4, kLanesPerRow);
+        s += __shfl_xor(s, 2, kLanesPerRow);
+        s += __shfl_xor(s, 1, kLanesPerRow);
+        if (j == 0 && r < out) y[r] = s;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// GEMM: Y[m][o] = sum_k bf16(X[m][k]) * bf16(cb[o/64][W[o][k]]), fp32 accumulate.
+// Block tile 64 (M) x 64 (N, one codebook) with K steps of 32; 4 waves in a
+// 2x2 grid, each wave a 32x32 output = 2x2 MFMA 16x16x32 tiles.
+// ---------------------------------------------------------------------------
+typedef __attribute__((__vector_size__(8 * sizeof(short)))) short bf16x8_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float floatx4_t;
+
+__device__ inline unsigned short f32_to_bf16_rne(float f)
+{
+    uint32_t u = __float_as_uint(f);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<unsigned short>(u >> 16);
+}
+
+constexpr int kGM = 64, kGN = 64, kGK = 32;
+constexpr int kLdsPad = 8;  // bf16 elements of padding per LDS row
+
+__global__ __launch_bounds__(256) void cb8_gemm_kernel(const float *__restrict__ X,
+                                                       const uint8_t *__restrict__ W,
+                                                       const float *__restrict__ cb,
+                                                       float *__restrict__ Y, int M, int N,
+                                                       int K)
+{
+    __shared__ float cbs[256];
+    __shared__ unsigned short As[kGM][kGK + kLdsPad];
+    __shared__ unsigned short Bs[kGN][kGK + kLdsPad];
+
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int n0 = blockIdx.x * kGN;
+    const int m0 = blockIdx.y * kGM;
+    const int wm = (wave >> 1) * 32;  // wave's row offset within the tile
+    const int wn = (wave & 1) * 32;   // wave's column offset
+
+    cbs[t] = cb[size_t(n0 / 64) * 256 + t];
+
+    floatx4_t acc[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) acc[a][b] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // Staging assignment: A tile 64x32 f32 = 2048 floats -> 8 per thread;
+    // B tile 64x32 bytes = 2048 codes -> 8 per thread.
+    const int ar = t >> 2;          // row 0..63
+    const int ac = (t & 3) * 8;     // col 0,8,16,24
+    __syncthreads();
+
+    for (int k0 = 0; k0 < K; k0 += kGK) {
+        {
+            const int m = m0 + ar;
+            float v[8];
+            if (m < M) {
+                const float4 *xp = reinterpret_cast<const float4 *>(X + size_t(m) * K + k0 + ac);
+                float4 a = xp[0], b = xp[1];
+                v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+                v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+            } else {
+#pragma unroll
+                for (int q = 0; q < 8; ++q) v[q] = 0.0f;
+            }
+#pragma unroll
+            for (int q = 0; q < 8; ++q) As[ar][ac + q] = f32_to_bf16_rne(v[q]);
+        }
+        {
+            const int n = n0 + ar;
+            uint2 c = make_uint2(0, 0);
+            if (n < N) c = *reinterpret_cast<const uint2 *>(W + size_t(n) * K + k0 + ac);
+            const uint32_t d[2] = {c.x, c.y};
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const uint32_t e = (d[q >> 2] >> (8 * (q & 3))) & 0xffu;
+                Bs[ar][ac + q] = f32_to_bf16_rne(n < N ? cbs[e] : 0.0f);
+            }
+        }
+        __syncthreads();
+        // MFMA 16x16x32 bf16: lane l supplies A[row l%16][k 8*(l/16) .. +8]
+        // and B[k 8*(l/16) .. +8][col l%16].
+        const int r16 = lane & 15;
+        const int kq = (lane >> 4) * 8;
+        bf16x8_t afrag[2], bfrag[2];
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+            afrag[a] = *reinterpret_cast<const bf16x8_t *>(&As[wm + a * 16 + r16][kq]);
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+            bfrag[b] = *reinterpret_cast<const bf16x8_t *>(&Bs[wn + b * 16 + r16][kq]);
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afrag[a], bfrag[b], acc[a][b],
+                                                                    0, 0, 0);
+        __syncthreads();
+    }
+    // C layout: lane l holds C[4*(l/16) + i][l%16], i < 4.
+    const int col = lane & 15;
+    const int rb = (lane >> 4) * 4;
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = m0 + wm + a * 16 + rb + i;
+                const int n = n0 + wn + b * 16 + col;
+                if (m < M && n < N) Y[size_t(m) * N + n] = acc[a][b][i];
+            }
+}
+
+constexpr int kRep = 32;
+
+int launch_gemv(nd_ctx *ctx, size_t count, const uint8_t *w, size_t w_stride, const float *cb,
+                size_t cb_stride, const float *x, size_t x_stride, float *y, size_t y_stride,
+                size_t out, size_t in)
+{
+    ND_REQUIRE(w && cb && x && y, "null buffer");
+    ND_REQUIRE(out > 0 && in > 0, "empty shape %zux%zu", out, in);
+    ND_REQUIRE(in % 16 == 0, "in (%zu) must be a multiple of 16", in);
+    ND_REQUIRE(out <= (size_t(1) << 30) && in <= (size_t(1) << 24), "shape too large");
+    ND_REQUIRE(count >= 1 && count <= 65535, "count %zu out of range 1..65535", count);
+    ND_REQUIRE((reinterpret_cast<uintptr_t>(w) & 15) == 0 && w_stride % 16 == 0,
+               "codes must be 16-byte aligned");
+    ND_REQUIRE((reinterpret_cast<uintptr_t>(x) & 15) == 0 && x_stride % 4 == 0,
+               "activations must be 16-byte aligned");
+    const int tiles = static_cast<int>((out + kTileRows - 1) / kTileRows);
+    dim3 grid(tiles, static_cast<unsigned>(count));
+    const bool fast = in % 256 == 0 && in <= 1024 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+                      x_stride % 4 == 0;
+#define ND_GEMV(MM)                                                                          \
+    hipLaunchKernelGGL((cb8_gemv_kernel<MM>), grid, dim3(kThreads), 0, ctx->stream, w, w_stride, \
+                       cb, cb_stride, x, x_stride, y, y_stride, int(out))
+    if (fast) {
+        switch (in / 256) {
+        case 1: ND_GEMV(1); break;
+        case 2: ND_GEMV(2); break;
+        case 3: ND_GEMV(3); break;
+        default: ND_GEMV(4); break;
+        }
+    } else {
+        ND_REQUIRE(in * sizeof(float) <= 64 * 1024, "in (%zu) too large", in);
+        hipLaunchKernelGGL((cb8_gemv_generic_kernel<kRep>), grid, dim3(kThreads),
+                           in * sizeof(float), ctx->stream, w, w_stride, cb, cb_stride, x,
+                           x_stride, y, y_stride, int(out), int(in));
+    }
+#undef ND_GEMV
+    return nd::check_launch("cb8_gemv");
+}
+
+}  // namespace
+
+extern "C" {
+
+int nd_cb8_gemv(nd_ctx *ctx, const uint8_t *w, const float *cb, const float *x, float *y,
+                size_t out, size_t in)
+{
+    if (int rc = nd::enter(ctx)) return rc;
+    return launch_gemv(ctx, 1, w, 0, cb, 0, x, 0, y, 0, out, in);
+}
+
+int nd_cb8_gemv_batched(nd_ctx *ctx, size_t count, const uint8_t *w, size_t w_stride,
+                        const float *cb, size_t cb_stride, const float *x, size_t x_stride,
+                        float *y, size_t y_stride, size_t out, size_t in)
+{
+    if (int rc = nd::enter(ctx)) return rc;
+    return launch_gemv(ctx, count, w, w_stride, cb, cb_stride, x, x_stride, y, y_stride, out, in);
+}
+
+int nd_cb8_gemm(nd_ctx *ctx, const float *x, const uint8_t *w, const float *cb, float *y,
+                size_t m, size_t out, size_t in)
+{
+    if (int rc = nd::enter(ctx)) return rc;
+    ND_REQUIRE(x && w && cb && y, "null buffer");
+    ND_REQUIRE(m > 0 && out > 0 && in > 0, "empty shape");
+    ND_REQUIRE(out % kGN == 0, "out (%zu) must be a multiple of %d", out, kGN);
+    ND_REQUIRE(in % kGK == 0, "in (%zu) must be a multiple of %d", in, kGK);
+    ND_REQUIRE(m <= (size_t(1) << 24) && out <= (size_t(1) << 24) && in <= (size_t(1) << 24),
+               "shape too large");
+    ND_REQUIRE((reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(w) & 7) == 0,
+               "x must be 16-byte and w 8-byte aligned");
+    dim3 grid(static_cast<unsigned>(out / kGN), static_cast<unsigned>((m + kGM - 1) / kGM));
+    hipLaunchKernelGGL(cb8_gemm_kernel, grid, dim3(256), 0, ctx->stream, x, w, cb, y, int(m),
+                       int(out), int(in));
+    return nd::check_launch("cb8_gemm");
+}
+
+}  // extern "C"

@@ -1,0 +1,626 @@
+// Format A: Cactus-Quants weights (crates/needle-core/src/cq.rs).
+//
+// A logical [out, in] matrix stored as packed LSB-first 2/3/4-bit codes (or
+// ternary crumbs) per row, one FP16 norm per (row, 128-wide group), levels
+// from a shared codebook; reconstruction w_g = (levels[idx] * norm) @ H with
+// H the normalised Walsh-Hadamard matrix, applied to the activation instead
+// (cq.rs:1-48).
+//
+// Kernels:
+//   cq_prepare   per-group normalised FWHT of the activation (cq.rs:264-274).
+//                Same butterfly, same pairing, same final multiply as
+//                hadamard.rs:24-55, so the result is bit-identical.
+//   cq_gemv      decode GEMV for the byte-aligned widths.  16 lanes per row,
+//                each lane keeps its 48 activations in registers and reads
+//                one code dword per step; the byte LUT (256 x P levels) sits
+//                in LDS in lane-private replicas so the gathers do not
+//                conflict on banks; a group's norm multiplies the group dot
+//                as in cq.rs:731.
+//   cq_gemv_generic   any width/group (3-bit, tiny groups): bit reader.
+//   cq_matmul    batched prefill: a 64x64 output tile, the weight tile
+//                decoded to fp32 (level * norm) in LDS, fp32 MFMA 16x16x4.
+//   cq_dequant   dequantize_row (cq.rs:763-779), bit-identical.
+#include "nd_internal.h"
+
+#include <cmath>
+#include <cstring>
+#include <new>
+#include <vector>
+
+struct nd_cq {
+    int device = 0;
+    size_t out_feat = 0, in_feat = 0, in_padded = 0, group = 0, num_groups = 0;
+    size_t row_bytes = 0, per_byte = 0;
+    uint8_t bits = 0;
+    int n_levels = 0;
+    float levels[16] = {};
+    float inv_sqrt_group = 1.0f;  // 1 / sqrtf(group), as hadamard.rs:51-52
+    uint8_t *packed = nullptr;    // device [out][row_bytes] (+16 bytes slack)
+    float *norms = nullptr;       // device [out][num_groups]
+    float *lut = nullptr;         // device [256][per_byte] (empty for 3-bit)
+    float *lv = nullptr;          // device levels[16]
+};
+
+namespace {
+
+constexpr uint8_t kTernary = 5;
+constexpr size_t kCodebookLen = 28;
+constexpr size_t kMaxGroup = 1024;
+
+// cq.rs:948-958
+__host__ __device__ inline int ternary_index(uint32_t code)
+{
+    return code == 3 ? 0 : (code == 1 ? 2 : 1);
+}
+
+// f16 -> f32, exact (math.rs:53-68).
+float f16_to_f32(uint16_t bits)
+{
+    uint32_t sign = uint32_t(bits >> 15) << 31;
+    uint32_t exp = (bits >> 10) & 0x1F;
+    uint32_t mant = bits & 0x3FF;
+    uint32_t out;
+    if (exp == 0) {
+        float val = float(mant) / float(1u << 24);
+        return sign ? -val : val;
+    }
+    if (exp == 31)
+        out = sign | 0x7F800000u | (mant << 13);
+    else
+        out = sign | ((exp + 127 - 15) << 23) | (mant << 13);
+    float f;
+    std::memcpy(&f, &out, 4);
+    return f;
+}
+
+// ---------------------------------------------------------------------------
+// prepare_input: one block per (group, batch row).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(512) void cq_prepare_kernel(const float *__restrict__ x,
+                                                         float *__restrict__ xh, int in_feat,
+                                                         int in_padded, int group, float inv)
+{
+    extern __shared__ float buf[];
+    const int g = blockIdx.x;
+    const size_t b = blockIdx.y;
+    const int t = threadIdx.x;
+    const float *xr = x + b * size_t(in_feat);
+    for (int k = t; k < group; k += blockDim.x) {
+        const int col = g * group + k;
+        buf[k] = col < in_feat ? xr[col] : 0.0f;
+    }
+    __syncthreads();
+    for (int h = 1; h < group; h <<= 1) {
+        for (int i = t; i < group / 2; i += blockDim.x) {
+            const int jj = (i / h) * (2 * h) + (i % h);
+            const float a = buf[jj];
+            const float c = buf[jj + h];
+            buf[jj] = a + c;
+            buf[jj + h] = a - c;
+        }
+        __syncthreads();
+    }
+    float *out = xh + b * size_t(in_padded) + size_t(g) * group;
+    for (int k = t; k < group; k += blockDim.x) out[k] = buf[k] * inv;
+}
+
+// ---------------------------------------------------------------------------
+// GEMV, byte-aligned widths.  P levels per byte (4: 2-bit/ternary, 2: 4-bit).
+// ND code dwords per lane; each dword holds 4*P elements of one group.
+// ---------------------------------------------------------------------------
+constexpr int kThreads = 256;
+constexpr int kLanesPerRow = 16;
+constexpr int kRowsPerPass = kThreads / kLanesPerRow;  // 16
+constexpr int kPasses = 4;                              // 64 rows per block
+
+template <int P>
+struct LutVec;
+template <>
+struct LutVec<4> {
+    using T = float4;
+};
+template <>
+struct LutVec<2> {
+    using T = float2;
+};
+
+// REPL replicas of the P-float entry, entry-major: entry e replica r at
+// (e * REPL + r) * P floats.  Lane l reads replica l % REPL.
+template <int P, int ND, int REPL>
+__global__ __launch_bounds__(kThreads) void cq_gemv_kernel(
+    const uint8_t *__restrict__ packed, const float *__restrict__ norms,
+    const float *__restrict__ lut, const float *__restrict__ xh, float *__restrict__ y,
+    int row_start, int rows, int row_bytes, int num_groups, int group)
+{
+    using V = typename LutVec<P>::T;
+    constexpr int E = 4 * P;  // elements per code dword
+    __shared__ V rep[256 * REPL];
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int j = t & (kLanesPerRow - 1);
+    const int rg = t / kLanesPerRow;
+    const int row_dwords = row_bytes >> 2;
+
+    for (int f = t; f < 256 * REPL; f += kThreads) {
+        const int e = f / REPL;
+        rep[f] = *reinterpret_cast<const V *>(lut + e * P);
+    }
+    // Lane j owns dwords j + 16*i: elements [E*d, E*d + E).
+    float xr[ND][E];
+    int gi[ND];
+#pragma unroll
+    for (int i = 0; i < ND; ++i) {
+        const int d = j + kLanesPerRow * i;
+        gi[i] = (d * E) / group;
+        if (d < row_dwords) {
+            const float4 *xp = reinterpret_cast<const float4 *>(xh + d * E);
+#pragma unroll
+            for (int q = 0; q < E / 4; ++q) {
+                float4 v = xp[q];
+                xr[i][4 * q + 0] = v.x;
+                xr[i][4 * q + 1] = v.y;
+                xr[i][4 * q + 2] = v.z;
+                xr[i][4 * q + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < E; ++q) xr[i][q] = 0.0f;
+        }
+    }
+    __syncthreads();
+
+    const V *lutl = rep + (lane & (REPL - 1));
+    const int r0 = blockIdx.x * (kRowsPerPass * kPasses);
+    uint32_t codes[kPasses][ND];
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+        const int r = r0 + rg + kRowsPerPass * p;
+        const uint32_t *wr =
+            reinterpret_cast<const uint32_t *>(packed + size_t(row_start + r) * row_bytes);
+#pragma unroll
+        for (int i = 0; i < ND; ++i) {
+            const int d = j + kLanesPerRow * i;
+            codes[p][i] = (r < rows && d < row_dwords) ? __builtin_nontemporal_load(wr + d) : 0u;
+        }
+    }
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+        const int r = r0 + rg + kRowsPerPass * p;
+        const float *nr = norms + size_t(row_start + (r < rows ? r : 0)) * num_groups;
+        float total = 0.0f;
+#pragma unroll
+        for (int i = 0; i < ND; ++i) {
+            const int d = j + kLanesPerRow * i;
+            float acc[P];
+#pragma unroll
+            for (int q = 0; q < P; ++q) acc[q] = 0.0f;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const uint32_t e = (codes[p][i] >> (8 * b)) & 0xffu;
+                const V v = lutl[e * REPL];
+                const float *vf = reinterpret_cast<const float *>(&v);
+#pragma unroll
+                for (int q = 0; q < P; ++q) acc[q] += vf[q] * xr[i][b * P + q];
+            }
+            float dot = acc[0];
+#pragma unroll
+            for (int q = 1; q < P; ++q) dot += acc[q];
+            if (r < rows && d < row_dwords) total += nr[gi[i]] * dot;
+        }
+        total += __shfl_xor(total, 8, kLanesPerRow);
+        total += __shfl_xor(total, 4, kLanesPerRow);
+        total += __shfl_xor(total, 2, kLanesPerRow);
+        total += __shfl_xor(total, 1, kLanesPerRow);
+        if (j == 0 && r < rows) y[r] = total;
+    }
+}
+
+// Reads code k of a row with the bit reader of cq.rs:914-925 (any width).
+__device__ inline uint32_t read_code(const uint8_t *row, int k, int w, int row_bytes)
+{
+    const int bit = k * w;
+    const int byte = bit >> 3;
+    const int shift = bit & 7;
+    uint32_t lo = row[byte];
+    uint32_t hi = (shift + w > 8 && byte + 1 < row_bytes) ? row[byte + 1] : 0u;
+    return ((lo | (hi << 8)) >> shift) & ((1u << w) - 1u);
+}
+
+__device__ inline float level_of(const float *lv, uint32_t code, int ternary)
+{
+    return lv[ternary ? ternary_index(code) : int(code)];
+}
+
+// One wave per row, any width: lanes stride the reduction axis and fold
+// each group's norm into its terms.
+__global__ __launch_bounds__(256) void cq_gemv_generic_kernel(
+    const uint8_t *__restrict__ packed, const float *__restrict__ norms,
+    const float *__restrict__ lv, const float *__restrict__ xh, float *__restrict__ y,
+    int row_start, int rows, int row_bytes, int num_groups, int group, int in_padded, int w,
+    int ternary)
+{
+    __shared__ float lvs[16];
+    if (threadIdx.x < 16) lvs[threadIdx.x] = lv[threadIdx.x];
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const uint8_t *row = packed + size_t(row_start + r) * row_bytes;
+    const float *nr = norms + size_t(row_start + r) * num_groups;
+    float total = 0.0f;
+    for (int g = 0; g < num_groups; ++g) {
+        float acc = 0.0f;
+        for (int k = lane; k < group; k += 64) {
+            const int kk = g * group + k;
+            acc += level_of(lvs, read_code(row, kk, w, row_bytes), ternary) * xh[kk];
+        }
+        total += nr[g] * acc;
+    }
+    for (int off = 32; off > 0; off >>= 1) total += __shfl_xor(total, off, 64);
+    if (lane == 0) y[r] = total;
+    (void)in_padded;
+}
+
+// ---------------------------------------------------------------------------
+// Batched matmul on fp32 MFMA: Y[b][r] = sum_k xh[b][k] * level(W[r][k]) *
+// norm[r][k/group].  Tile 64 (batch) x 64 (rows), K steps of 32 (zero-filled
+// past in_padded).
+// ---------------------------------------------------------------------------
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float floatx4_t;
+constexpr int kMM = 64, kMN = 64, kMK = 32;
+
+__global__ __launch_bounds__(256) void cq_matmul_kernel(
+    const uint8_t *__restrict__ packed, const float *__restrict__ norms,
+    const float *__restrict__ lv, const float *__restrict__ xh, float *__restrict__ y,
+    int batch, int row_start, int rows, int row_bytes, int num_groups, int group, int in_padded,
+    int w, int ternary)
+{
+    __shared__ float lvs[16];
+    __shared__ float As[kMM][kMK + 1];
+    __shared__ float Bs[kMN][kMK + 1];
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int n0 = blockIdx.x * kMN;  // row tile
+    const int m0 = blockIdx.y * kMM;  // batch tile
+    const int wm = (wave >> 1) * 32;
+    const int wn = (wave & 1) * 32;
+    if (t < 16) lvs[t] = lv[t];
+
+    floatx4_t acc[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) acc[a][b] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int sr = t >> 2;        // staging row 0..63
+    const int sc = (t & 3) * 8;   // staging col 0..24
+    __syncthreads();
+    for (int k0 = 0; k0 < in_padded; k0 += kMK) {
+        {
+            const int m = m0 + sr;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const int k = k0 + sc + q;
+                As[sr][sc + q] = (m < batch && k < in_padded) ? xh[size_t(m) * in_padded + k] : 0.0f;
+            }
+        }
+        {
+            const int n = n0 + sr;
+            if (n < rows) {
+                const uint8_t *row = packed + size_t(row_start + n) * row_bytes;
+                const float *nr = norms + size_t(row_start + n) * num_groups;
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    const int k = k0 + sc + q;
+                    Bs[sr][sc + q] = k < in_padded ? level_of(lvs, read_code(row, k, w, row_bytes), ternary) *
+                                                         nr[k / group]
+                                                   : 0.0f;
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < 8; ++q) Bs[sr][sc + q] = 0.0f;
+            }
+        }
+        __syncthreads();
+        // MFMA 16x16x4 f32: lane l supplies A[l%16][k0+l/16], B[k0+l/16][l%16].
+        const int r16 = lane & 15;
+        const int kq = lane >> 4;
+#pragma unroll
+        for (int kk = 0; kk < kMK; kk += 4) {
+            float af[2], bf[2];
+#pragma unroll
+            for (int a = 0; a < 2; ++a) af[a] = As[wm + a * 16 + r16][kk + kq];
+#pragma unroll
+            for (int b = 0; b < 2; ++b) bf[b] = Bs[wn + b * 16 + r16][kk + kq];
+#pragma unroll
+            for (int a = 0; a < 2; ++a)
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[a], bf[b], acc[a][b], 0, 0, 0);
+        }
+        __syncthreads();
+    }
+    const int col = lane & 15;
+    const int rb = (lane >> 4) * 4;
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = m0 + wm + a * 16 + rb + i;
+                const int n = n0 + wn + b * 16 + col;
+                if (m < batch && n < rows) y[size_t(m) * rows + n] = acc[a][b][i];
+            }
+}
+
+// ---------------------------------------------------------------------------
+// dequantize rows: one block per (group, requested row).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(512) void cq_dequant_kernel(
+    const uint8_t *__restrict__ packed, const float *__restrict__ norms,
+    const float *__restrict__ lv, const int32_t *__restrict__ rows_idx, float *__restrict__ out,
+    int out_feat, int in_feat, int row_bytes, int num_groups, int group, int w, int ternary,
+    float inv)
+{
+    extern __shared__ float buf[];
+    __shared__ float lvs[16];
+    const int g = blockIdx.x;
+    const size_t i = blockIdx.y;
+    const int t = threadIdx.x;
+    if (t < 16) lvs[t] = lv[t];
+    int o = rows_idx[i];
+    o = o < 0 ? 0 : (o >= out_feat ? out_feat - 1 : o);
+    const uint8_t *row = packed + size_t(o) * row_bytes;
+    const float norm = norms[size_t(o) * num_groups + g];
+    __syncthreads();
+    for (int k = t; k < group; k += blockDim.x)
+        buf[k] = level_of(lvs, read_code(row, g * group + k, w, row_bytes), ternary) * norm;
+    __syncthreads();
+    for (int h = 1; h < group; h <<= 1) {
+        for (int q = t; q < group / 2; q += blockDim.x) {
+            const int jj = (q / h) * (2 * h) + (q % h);
+            const float a = buf[jj];
+            const float c = buf[jj + h];
+            buf[jj] = a + c;
+            buf[jj + h] = a - c;
+        }
+        __syncthreads();
+    }
+    float *dst = out + i * size_t(in_feat);
+    for (int k = t; k < group; k += blockDim.x) {
+        const int col = g * group + k;
+        if (col < in_feat) dst[col] = buf[k] * inv;
+    }
+}
+
+int code_width(const nd_cq *w) { return w->bits == kTernary ? 2 : w->bits; }
+
+int check_cq(const nd_cq *w)
+{
+    ND_REQUIRE(w && w->packed, "null weight");
+    return ND_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int nd_cq_from_blob(nd_ctx *ctx, const uint8_t *blob, size_t blob_len, size_t out_feat,
+                    size_t in_feat, size_t group, uint8_t bits, const float *codebook,
+                    size_t codebook_len, nd_cq **out)
+{
+    if (int rc = nd::enter(ctx)) return rc;
+    ND_REQUIRE(out, "null output pointer");
+    *out = nullptr;
+    // Validation order follows CqWeight::from_blob (cq.rs:189-225).
+    if (out_feat == 0 || in_feat == 0) return nd::fail(ND_ERR_CQ_EMPTY_SHAPE, "EmptyShape");
+    if (group == 0 || group % 8 != 0 || (group & (group - 1)) != 0 || group > kMaxGroup)
+        return nd::fail(ND_ERR_CQ_BAD_GROUP, "BadGroup(%zu)", group);
+    float levels[16] = {};
+    int n_levels = 0;
+    if (bits == kTernary) {
+        const float s = 1.2240064f / std::sqrt(float(group));
+        levels[0] = -s;
+        levels[1] = 0.0f;
+        levels[2] = s;
+        n_levels = 3;
+    } else {
+        if (codebook_len != kCodebookLen)
+            return nd::fail(ND_ERR_CQ_BAD_CODEBOOK_LEN, "BadCodebookLen(%zu)", codebook_len);
+        size_t off;
+        switch (bits) {
+        case 2: off = 0; n_levels = 4; break;
+        case 3: off = 4; n_levels = 8; break;
+        case 4: off = 12; n_levels = 16; break;
+        default: return nd::fail(ND_ERR_CQ_UNSUPPORTED_BITS, "UnsupportedBits(%u)", unsigned(bits));
+        }
+        ND_REQUIRE(codebook, "null codebook");
+        std::memcpy(levels, codebook + off, n_levels * sizeof(float));
+    }
+    const size_t in_padded = (in_feat + group - 1) / group * group;
+    const size_t num_groups = in_padded / group;
+    const size_t eff = bits == kTernary ? 2 : bits;
+    const size_t row_bytes = in_padded * eff / 8;
+    const size_t n_packed = out_feat * row_bytes;
+    const size_t n_norm = out_feat * num_groups * 2;
+    if (!blob || blob_len < n_packed + n_norm)
+        return nd::fail(ND_ERR_CQ_SHORT_BLOB, "ShortBlob { need: %zu, got: %zu }", n_packed + n_norm,
+                        blob_len);
+    ND_REQUIRE(out_feat < (size_t(1) << 31) && in_padded < (size_t(1) << 24), "shape too large");
+
+    nd_cq *w = new (std::nothrow) nd_cq;
+    if (!w) return nd::fail(ND_ERR_NOMEM, "host allocation failed");
+    w->device = ctx->device;
+    w->out_feat = out_feat;
+    w->in_feat = in_feat;
+    w->in_padded = in_padded;
+    w->group = group;
+    w->num_groups = num_groups;
+    w->row_bytes = row_bytes;
+    w->bits = bits;
+    w->n_levels = n_levels;
+    std::memcpy(w->levels, levels, sizeof levels);
+    w->inv_sqrt_group = 1.0f / std::sqrt(float(group));
+    w->per_byte = eff == 2 ? 4 : (eff == 4 ? 2 : 0);
+
+    std::vector<float> norms(out_feat * num_groups);
+    for (size_t i = 0; i < norms.size(); ++i) {
+        const uint8_t *c = blob + n_packed + 2 * i;
+        norms[i] = f16_to_f32(uint16_t(c[0] | (c[1] << 8)));
+    }
+    std::vector<float> lut;
+    if (w->per_byte) {
+        // cq.rs:932-964
+        const uint32_t mask = (1u << eff) - 1;
+        lut.resize(256 * w->per_byte);
+        for (uint32_t byte = 0; byte < 256; ++byte)
+            for (size_t k = 0; k < w->per_byte; ++k) {
+                const uint32_t code = (byte >> (k * eff)) & mask;
+                const int idx = bits == kTernary ? ternary_index(code) : int(code);
+                lut[byte * w->per_byte + k] = levels[idx];
+            }
+    }
+    auto cleanup = [&](int rc) {
+        nd_cq_free(w);
+        return rc;
+    };
+    hipError_t e;
+    if ((e = hipMalloc(&w->packed, n_packed + 16)) != hipSuccess) return cleanup(nd::hip_fail(e, "hipMalloc"));
+    if ((e = hipMalloc(&w->norms, norms.size() * 4)) != hipSuccess) return cleanup(nd::hip_fail(e, "hipMalloc"));
+    if ((e = hipMalloc(&w->lv, 16 * 4)) != hipSuccess) return cleanup(nd::hip_fail(e, "hipMalloc"));
+    if (!lut.empty() && (e = hipMalloc(&w->lut, lut.size() * 4)) != hipSuccess)
+        return cleanup(nd::hip_fail(e, "hipMalloc"));
+    if ((e = hipMemsetAsync(w->packed + n_packed, 0, 16, ctx->stream)) != hipSuccess ||
+        (e = hipMemcpyAsync(w->packed, blob, n_packed, hipMemcpyHostToDevice, ctx->stream)) != hipSuccess ||
+        (e = hipMemcpyAsync(w->norms, norms.data(), norms.size() * 4, hipMemcpyHostToDevice, ctx->stream)) != hipSuccess ||
+        (e = hipMemcpyAsync(w->lv, levels, 16 * 4, hipMemcpyHostToDevice, ctx->stream)) != hipSuccess ||
+        (!lut.empty() && (e = hipMemcpyAsync(w->lut, lut.data(), lut.size() * 4, hipMemcpyHostToDevice, ctx->stream)) != hipSuccess) ||
+        (e = hipStreamSynchronize(ctx->stream)) != hipSuccess)
+        return cleanup(nd::hip_fail(e, "upload"));
+    *out = w;
+    return ND_OK;
+}
+
+void nd_cq_free(nd_cq *w)
+{
+    if (!w) return;
+    (void)hipSetDevice(w->device);
+    if (w->packed) (void)hipFree(w->packed);
+    if (w->norms) (void)hipFree(w->norms);
+    if (w->lut) (void)hipFree(w->lut);
+    if (w->lv) (void)hipFree(w->lv);
+    delete w;
+}
+
+int nd_cq_shape(const nd_cq *w, size_t *out_feat, size_t *in_feat, size_t *in_padded,
+                size_t *group, uint8_t *bits)
+{
+    nd::clear_error();
+    if (int rc = check_cq(w)) return rc;
+    if (out_feat) *out_feat = w->out_feat;
+    if (in_feat) *in_feat = w->in_feat;
+    if (in_padded) *in_padded = w->in_padded;
+    if (group) *group = w->group;
+    if (bits) *bits = w->bits;
+    return ND_OK;
+}
+
+int nd_cq_prepare_input(nd_ctx *ctx, const nd_cq *w, const float *x, size_t batch, float *xh)
+{
+    if (int rc = nd::enter(ctx)) return rc;
+    if (int rc = check_cq(w)) return rc;
+    if (batch == 0) return ND_OK;
+    ND_REQUIRE(x && xh, "null buffer");
+    ND_REQUIRE(batch <= 65535, "batch %zu above 65535", batch);
+    const int threads = int(w->group / 2 < 64 ? 64 : (w->group / 2 > 512 ? 512 : w->group / 2));
+    dim3 grid(unsigned(w->num_groups), unsigned(batch));
+    hipLaunchKernelGGL(cq_prepare_kernel, grid, dim3(threads), w->group * sizeof(float), ctx->stream,
+                       x, xh, int(w->in_feat), int(w->in_padded), int(w->group), w->inv_sqrt_group);
+    return nd::check_launch("cq_prepare");
+}
+
+int nd_cq_matvec_rows_prepared(nd_ctx *ctx, const nd_cq *w, const float *xh, size_t row_start,
+                               size_t rows, float *y)
+{
+    if (int rc = nd::enter(ctx)) return rc;
+    if (int rc = check_cq(w)) return rc;
+    ND_REQUIRE(row_start + rows <= w->out_feat, "rows %zu+%zu beyond %zu", row_start, rows, w->out_feat);
+    if (rows == 0) return ND_OK;
+    ND_REQUIRE(xh && y, "null buffer");
+    ND_REQUIRE((reinterpret_cast<uintptr_t>(xh) & 15) == 0, "xh must be 16-byte aligned");
+    const int row_dwords = int(w->row_bytes / 4);
+    const int E = int(4 * w->per_byte);
+    const bool fast = w->per_byte != 0 && w->row_bytes % 4 == 0 && size_t(E) <= w->group &&
+                      row_dwords <= 16 * 6;
+    if (fast) {
+        const int nd = (row_dwords + 15) / 16;
+        dim3 grid(unsigned((rows + 63) / 64));
+        const int args_rb = int(w->row_bytes), ng = int(w->num_groups), gr = int(w->group);
+#define ND_CQ(P, NDV, REPL)                                                                 \
+    hipLaunchKernelGGL((cq_gemv_kernel<P, NDV, REPL>), grid, dim3(kThreads), 0, ctx->stream, \
+                       w->packed, w->norms, w->lut, xh, y, int(row_start), int(rows), args_rb, ng, gr)
+        if (w->per_byte == 4) {
+            switch (nd) {
+            case 1: ND_CQ(4, 1, 8); break;
+            case 2: ND_CQ(4, 2, 8); break;
+            case 3: ND_CQ(4, 3, 8); break;
+            case 4: ND_CQ(4, 4, 8); break;
+            case 5: ND_CQ(4, 5, 8); break;
+            default: ND_CQ(4, 6, 8); break;
+            }
+        } else {
+            switch (nd) {
+            case 1: ND_CQ(2, 1, 16); break;
+            case 2: ND_CQ(2, 2, 16); break;
+            case 3: ND_CQ(2, 3, 16); break;
+            case 4: ND_CQ(2, 4, 16); break;
+            case 5: ND_CQ(2, 5, 16); break;
+            default: ND_CQ(2, 6, 16); break;
+            }
+        }
+#undef ND_CQ
+        return nd::check_launch("cq_gemv");
+    }
+    dim3 grid(unsigned((rows + 3) / 4));
+    hipLaunchKernelGGL(cq_gemv_generic_kernel, grid, dim3(256), 0, ctx->stream, w->packed, w->norms,
+                       w->lv, xh, y, int(row_start), int(rows), int(w->row_bytes), int(w->num_groups),
+                       int(w->group), int(w->in_padded), code_width(w), int(w->bits == kTernary));
+    return nd::check_launch("cq_gemv_generic");
+}
+
+int nd_cq_matmul_rows_prepared(nd_ctx *ctx, const nd_cq *w, const float *xh, size_t batch,
+                               size_t row_start, size_t rows, float *y)
+{
+    if (int rc = nd::enter(ctx)) return rc;
+    if (int rc = check_cq(w)) return rc;
+    ND_REQUIRE(row_start + rows <= w->out_feat, "rows %zu+%zu beyond %zu", row_start, rows, w->out_feat);
+    if (rows == 0 || batch == 0) return ND_OK;
+    ND_REQUIRE(xh && y, "null buffer");
+    ND_REQUIRE(batch <= (size_t(1) << 22), "batch too large");
+    dim3 grid(unsigned((rows + kMN - 1) / kMN), unsigned((batch + kMM - 1) / kMM));
+    hipLaunchKernelGGL(cq_matmul_kernel, grid, dim3(256), 0, ctx->stream, w->packed, w->norms, w->lv,
+                       xh, y, int(batch), int(row_start), int(rows), int(w->row_bytes),
+                       int(w->num_groups), int(w->group), int(w->in_padded), code_width(w),
+                       int(w->bits == kTernary));
+    return nd::check_launch("cq_matmul");
+}
+
+int nd_cq_dequantize_rows(nd_ctx *ctx, const nd_cq *w, const int32_t *rows, size_t n, float *out)
+{
+    if (int rc = nd::enter(ctx)) return rc;
+    if (int rc = check_cq(w)) return rc;
+    if (n == 0) return ND_OK;
+    ND_REQUIRE(rows && out, "null buffer");
+    ND_REQUIRE(n <= 65535, "n %zu above 65535", n);
+    const int threads = int(w->group / 2 < 64 ? 64 : (w->group / 2 > 512 ? 512 : w->group / 2));
+    dim3 grid(unsigned(w->num_groups), unsigned(n));
+    hipLaunchKernelGGL(cq_dequant_kernel, grid, dim3(threads), w->group * sizeof(float), ctx->stream,
+                       w->packed, w->norms, w->lv, rows, out, int(w->out_feat), int(w->in_feat),
+                       int(w->row_bytes), int(w->num_groups), int(w->group), code_width(w),
+                       int(w->bits == kTernary), w->inv_sqrt_group);
+    return nd::check_launch("cq_dequant");
+}
+
+}  // extern "C"

@@ -1,0 +1,56 @@
+// Internal plumbing shared by the HIP translation units: the context, the
+// per-thread error message and launch-checking helpers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "needle_amd.h"
+
+struct nd_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    bool owns_stream = false;
+    int num_cus = 0;
+    // Growable device workspace for split-K partials.  Owned by the context,
+    // reused by every call on it; calls on one context are stream-ordered.
+    void *work = nullptr;
+    size_t work_bytes = 0;
+};
+
+namespace nd {
+
+// Records a printf-style message for nd_last_error() and returns `code`.
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+
+// Maps a failed HIP call to ND_ERR_HIP with the call's text.
+int hip_fail(hipError_t e, const char *what);
+
+// Makes the context's device current; returns ND_OK or an error.
+int enter(nd_ctx *ctx);
+
+// Ensures the context workspace holds at least `bytes`.
+int workspace(nd_ctx *ctx, size_t bytes, void **out);
+
+// Checks the launch that was just enqueued.
+int check_launch(const char *kernel);
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+}  // namespace nd
+
+#define ND_HIP(call)                                        \
+    do {                                                    \
+        hipError_t e_ = (call);                             \
+        if (e_ != hipSuccess) return nd::hip_fail(e_, #call); \
+    } while (0)
+
+#define ND_REQUIRE(cond, ...)                                  \
+    do {                                                       \
+        if (!(cond)) return nd::fail(ND_ERR_ARG, __VA_ARGS__); \
+    } while (0)

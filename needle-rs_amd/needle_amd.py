@@ -1,0 +1,364 @@
+"""Python mirror of needle-rs's hot-path operator interface over the C ABI
+(include/needle_amd.h), for callers that hold torch device tensors.
+
+Names follow the reference: CqWeight.{prepare_input, matvec_rows_prepared,
+matmul_rows_prepared, dequantize_row} (crates/needle-core/src/cq.rs),
+fake_quant_vec / quantize_rows / V3Cache.write_kv / span
+(v3/cache.rs), attend_step / attend (v3/attention.rs).  Every call goes
+through libneedle_amd.so; there is no CPU fallback -- a missing library or
+GPU raises.  torch supplies device memory and the stream only.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+import os
+import re
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libneedle_amd.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "needle_amd.h")
+
+ND_OK = 0
+ERRORS = {1: "ND_ERR_ARG", 2: "ND_ERR_HIP", 3: "ND_ERR_NOMEM", 11: "UnsupportedBits",
+          12: "BadGroup", 13: "BadCodebookLen", 14: "ShortBlob", 15: "EmptyShape"}
+
+
+class NeedleError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"{ERRORS.get(code, code)}: {msg}")
+        self.code = code
+
+
+class KvGeom(C.Structure):
+    _fields_ = [("num_heads", C.c_int32), ("num_kv_heads", C.c_int32),
+                ("qk_head_dim", C.c_int32), ("v_head_dim", C.c_int32), ("cap", C.c_int32)]
+
+
+_lib = None
+_vp, _sz = C.c_void_p, C.c_size_t
+
+# (name, restype, argtypes) for every entry point of include/needle_amd.h.
+_SIGS = [
+    ("nd_last_error", C.c_char_p, []),
+    ("nd_ctx_create", C.c_int, [C.c_int, C.POINTER(_vp)]),
+    ("nd_ctx_create_on_stream", C.c_int, [C.c_int, _vp, C.POINTER(_vp)]),
+    ("nd_ctx_destroy", None, [_vp]),
+    ("nd_ctx_synchronize", C.c_int, [_vp]),
+    ("nd_malloc", C.c_int, [_vp, _sz, C.POINTER(_vp)]),
+    ("nd_free", C.c_int, [_vp, _vp]),
+    ("nd_memcpy_htod", C.c_int, [_vp, _vp, _vp, _sz]),
+    ("nd_memcpy_dtoh", C.c_int, [_vp, _vp, _vp, _sz]),
+    ("nd_cb8_gemv", C.c_int, [_vp, _vp, _vp, _vp, _vp, _sz, _sz]),
+    ("nd_cb8_gemv_batched", C.c_int, [_vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _sz]),
+    ("nd_cb8_gemm", C.c_int, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz]),
+    ("nd_cq_from_blob", C.c_int, [_vp, _vp, _sz, _sz, _sz, _sz, C.c_uint8, _vp, _sz, C.POINTER(_vp)]),
+    ("nd_cq_free", None, [_vp]),
+    ("nd_cq_shape", C.c_int, [_vp, C.POINTER(_sz), C.POINTER(_sz), C.POINTER(_sz), C.POINTER(_sz),
+                              C.POINTER(C.c_uint8)]),
+    ("nd_cq_prepare_input", C.c_int, [_vp, _vp, _vp, _sz, _vp]),
+    ("nd_cq_matvec_rows_prepared", C.c_int, [_vp, _vp, _vp, _sz, _sz, _vp]),
+    ("nd_cq_matmul_rows_prepared", C.c_int, [_vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    ("nd_cq_dequantize_rows", C.c_int, [_vp, _vp, _vp, _sz, _vp]),
+    ("nd_fake_quant", C.c_int, [_vp, _vp, _sz, _sz]),
+    ("nd_quantize_rows", C.c_int, [_vp, _vp, _sz, _sz, _vp, _vp]),
+    ("nd_kv_block_bytes", _sz, [C.POINTER(KvGeom)]),
+    ("nd_kv_v_offset", _sz, [C.POINTER(KvGeom)]),
+    ("nd_kv_ks_offset", _sz, [C.POINTER(KvGeom)]),
+    ("nd_kv_vs_offset", _sz, [C.POINTER(KvGeom)]),
+    ("nd_kv_write", C.c_int, [_vp, C.POINTER(KvGeom), _vp, _sz, _sz, _vp, _vp, _vp]),
+    ("nd_attend_step_i8", C.c_int, [_vp, C.POINTER(KvGeom), _vp, _sz, _sz, _vp, _vp, _vp,
+                                    C.c_float, C.c_int, _vp]),
+]
+
+
+def header_symbols():
+    """Function names declared in include/needle_amd.h."""
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(nd_[a-z0-9_]+)\s*\(", text)))
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built: run `make -C needle-rs_amd` "
+                               "(or __graft_entry__.build()); there is no CPU fallback")
+        L = C.CDLL(LIB_PATH)
+        for name, res, args in _SIGS:
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def last_error():
+    m = lib().nd_last_error()
+    return m.decode() if m else None
+
+
+def _check(rc):
+    if rc != ND_OK:
+        raise NeedleError(rc, last_error())
+
+
+def _ptr(t):
+    return C.c_void_p(t.data_ptr()) if t is not None else C.c_void_p(0)
+
+
+def _torch():
+    import torch
+    if not torch.cuda.is_available():
+        raise RuntimeError("no GPU visible: the HIP path has no CPU fallback")
+    return torch
+
+
+class Ctx:
+    """nd_ctx bound to a device and to torch's current stream on it."""
+
+    def __init__(self, device=0, stream=None):
+        torch = _torch()
+        self.device = device
+        if stream is None:
+            stream = torch.cuda.current_stream(device)
+        self.stream = stream
+        h = C.c_void_p()
+        _check(lib().nd_ctx_create_on_stream(device, C.c_void_p(stream.cuda_stream), C.byref(h)))
+        self.h = h
+
+    def synchronize(self):
+        _check(lib().nd_ctx_synchronize(self.h))
+
+    def close(self):
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.nd_ctx_destroy(self.h)
+            self.h = None
+
+    __del__ = close
+
+
+# ---- Format B ---------------------------------------------------------------
+
+def cb8_gemv(ctx, w, cb, x, y=None):
+    torch = _torch()
+    out, inn = w.shape
+    if y is None:
+        y = torch.empty(out, dtype=torch.float32, device=w.device)
+    _check(lib().nd_cb8_gemv(ctx.h, _ptr(w), _ptr(cb), _ptr(x), _ptr(y), out, inn))
+    return y
+
+
+def cb8_gemv_batched(ctx, w, cb, x, y):
+    """w [count, out, in] u8, cb [count, out/64, 256], x [count, in], y [count, out]."""
+    count, out, inn = w.shape
+    _check(lib().nd_cb8_gemv_batched(ctx.h, count, _ptr(w), w.stride(0), _ptr(cb), cb.stride(0),
+                                     _ptr(x), x.stride(0), _ptr(y), y.stride(0), out, inn))
+    return y
+
+
+def cb8_gemm(ctx, x, w, cb, y=None):
+    torch = _torch()
+    m, inn = x.shape
+    out = w.shape[0]
+    if y is None:
+        y = torch.empty(m, out, dtype=torch.float32, device=x.device)
+    _check(lib().nd_cb8_gemm(ctx.h, _ptr(x), _ptr(w), _ptr(cb), _ptr(y), m, out, inn))
+    return y
+
+
+# ---- Format A ---------------------------------------------------------------
+
+class CqWeight:
+    """Device CqWeight (cq.rs:117-810) built from a host blob."""
+
+    def __init__(self, ctx, blob, out_feat, in_feat, group, bits, codebook):
+        self.ctx = ctx
+        blob = np.ascontiguousarray(blob, np.uint8)
+        cb = np.ascontiguousarray(codebook, np.float32)
+        h = C.c_void_p()
+        _check(lib().nd_cq_from_blob(ctx.h, blob.ctypes.data_as(C.c_void_p), blob.size, out_feat,
+                                     in_feat, group, bits, cb.ctypes.data_as(C.c_void_p), cb.size,
+                                     C.byref(h)))
+        self.h = h
+        o, i, p, g, b = _sz(), _sz(), _sz(), _sz(), C.c_uint8()
+        _check(lib().nd_cq_shape(h, C.byref(o), C.byref(i), C.byref(p), C.byref(g), C.byref(b)))
+        self.out_feat, self.in_feat, self.in_padded = o.value, i.value, p.value
+        self.group, self.bits = g.value, b.value
+
+    def close(self):
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.nd_cq_free(self.h)
+            self.h = None
+
+    __del__ = close
+
+    def prepare_input(self, x, xh=None):
+        torch = _torch()
+        x2 = x.reshape(-1, self.in_feat)
+        if xh is None:
+            xh = torch.empty(x2.shape[0], self.in_padded, dtype=torch.float32, device=x.device)
+        _check(lib().nd_cq_prepare_input(self.ctx.h, self.h, _ptr(x2), x2.shape[0], _ptr(xh)))
+        return xh
+
+    def matvec_rows_prepared(self, xh, row_start, rows, y=None):
+        torch = _torch()
+        if y is None:
+            y = torch.empty(rows, dtype=torch.float32, device=xh.device)
+        _check(lib().nd_cq_matvec_rows_prepared(self.ctx.h, self.h, _ptr(xh), row_start, rows,
+                                                _ptr(y)))
+        return y
+
+    def matvec_prepared(self, xh, y=None):
+        return self.matvec_rows_prepared(xh, 0, self.out_feat, y)
+
+    def matvec(self, x):
+        return self.matvec_prepared(self.prepare_input(x))
+
+    def matmul_rows_prepared(self, xh, batch, row_start, rows, y=None):
+        torch = _torch()
+        if y is None:
+            y = torch.empty(batch * rows, dtype=torch.float32, device=xh.device)
+        _check(lib().nd_cq_matmul_rows_prepared(self.ctx.h, self.h, _ptr(xh), batch, row_start,
+                                                rows, _ptr(y)))
+        return y
+
+    def dequantize_rows(self, rows_i32, out=None):
+        torch = _torch()
+        n = rows_i32.numel()
+        if out is None:
+            out = torch.empty(n, self.in_feat, dtype=torch.float32, device=rows_i32.device)
+        _check(lib().nd_cq_dequantize_rows(self.ctx.h, self.h, _ptr(rows_i32), n, _ptr(out)))
+        return out
+
+
+# ---- int8 KV ----------------------------------------------------------------
+
+def fake_quant(ctx, x, dim):
+    """fake_quant_vec(x[r], 8) for every row of `dim`, in place."""
+    _check(lib().nd_fake_quant(ctx.h, _ptr(x), x.numel() // dim, dim))
+    return x
+
+
+def quantize_rows(ctx, x, head_dim):
+    torch = _torch()
+    rows = x.numel() // head_dim
+    ints = torch.empty(rows * head_dim, dtype=torch.int8, device=x.device)
+    scales = torch.empty(rows, dtype=torch.float32, device=x.device)
+    _check(lib().nd_quantize_rows(ctx.h, _ptr(x), rows, head_dim, _ptr(ints), _ptr(scales)))
+    return ints, scales
+
+
+def kv_geom(num_heads, num_kv_heads, qk, vd, cap):
+    return KvGeom(num_heads, num_kv_heads, qk, vd, cap)
+
+
+def kv_block_bytes(g):
+    return lib().nd_kv_block_bytes(C.byref(g))
+
+
+def kv_offsets(g):
+    L = lib()
+    return dict(v=L.nd_kv_v_offset(C.byref(g)), ks=L.nd_kv_ks_offset(C.byref(g)),
+                vs=L.nd_kv_vs_offset(C.byref(g)), total=L.nd_kv_block_bytes(C.byref(g)))
+
+
+def kv_alloc(g, count=1, device=0):
+    """`count` zeroed KV blocks, one after another (stride = block bytes)."""
+    torch = _torch()
+    nb = kv_block_bytes(g)
+    return torch.zeros(count * nb, dtype=torch.uint8, device=device), nb
+
+
+def kv_write(ctx, g, kv, kv_stride, pos_i32, k, v):
+    _check(lib().nd_kv_write(ctx.h, C.byref(g), _ptr(kv), kv_stride, pos_i32.numel(), _ptr(pos_i32),
+                             _ptr(k), _ptr(v)))
+
+
+def attend_step_i8(ctx, g, kv, kv_stride, lo_i32, hi_i32, q, scale=None, quant_query=False,
+                   out=None):
+    torch = _torch()
+    count = lo_i32.numel()
+    if scale is None:
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(g.qk_head_dim)))
+    if out is None:
+        out = torch.empty(count, g.num_heads * g.v_head_dim, dtype=torch.float32, device=q.device)
+    _check(lib().nd_attend_step_i8(ctx.h, C.byref(g), _ptr(kv), kv_stride, count, _ptr(lo_i32),
+                                   _ptr(hi_i32), _ptr(q), scale, int(bool(quant_query)), _ptr(out)))
+    return out
+
+
+def kv_unpack(g, block_u8):
+    """Split one device block (as a CPU uint8 numpy array) into the
+    reference's slot-major views: k [cap][kvh][qk] i8, v, ks [cap][kvh], vs."""
+    off = kv_offsets(g)
+    H, cap, qk, vd = g.num_kv_heads, g.cap, g.qk_head_dim, g.v_head_dim
+    b = np.asarray(block_u8)
+    k = b[:H * cap * qk].view(np.int8).reshape(H, cap, qk).transpose(1, 0, 2)
+    v = b[off["v"]:off["v"] + H * cap * vd].view(np.int8).reshape(H, cap, vd).transpose(1, 0, 2)
+    ks = b[off["ks"]:off["ks"] + 4 * H * cap].view(np.float32).reshape(H, cap).T
+    vs = b[off["vs"]:off["vs"] + 4 * H * cap].view(np.float32).reshape(H, cap).T
+    return (np.ascontiguousarray(k), np.ascontiguousarray(ks), np.ascontiguousarray(v),
+            np.ascontiguousarray(vs))
+
+
+class V3LayerCache:
+    """One layer of V3Cache (cache.rs:125-393) with an int8 device block.
+
+    The device block holds `cap` slots from the start; the reference's
+    logical ring size (`slots`, grown by doubling, cache.rs:291-309) is kept
+    here because span() clamps with it (cache.rs:322-331).  Physical slot
+    pos % cap equals the reference's pos % slots at every write and read:
+    while slots < cap every live position is below slots.
+    """
+
+    def __init__(self, ctx, num_heads, num_kv_heads, qk, vd, hint, window, max_seq_len):
+        self.ctx = ctx
+        hint = min(max(hint, 1), max_seq_len)
+        self.window = window
+        self.cap = min(window, max_seq_len) if window else max_seq_len
+        self.slots = min(hint, self.cap)
+        self.geom = kv_geom(num_heads, num_kv_heads, qk, vd, self.cap)
+        self.block, self.block_bytes = kv_alloc(self.geom, 1, ctx.device)
+
+    def _ensure(self, pos):
+        if pos < self.slots or self.slots >= self.cap:
+            return
+        self.slots = min(max(self.slots * 2, pos + 1), self.cap)
+
+    def write_kv(self, pos, k, v):
+        torch = _torch()
+        self._ensure(pos)
+        p = torch.tensor([pos], dtype=torch.int32, device=k.device)
+        kv_write(self.ctx, self.geom, self.block, 0, p, k, v)
+
+    def span(self, pos):
+        lo = pos + 1 - self.window if (self.window and pos + 1 > self.window) else 0
+        lo = max(lo, max(pos + 1 - self.slots, 0))
+        return lo, pos
+
+    def attend_step(self, q, lo, hi, quant_query=False):
+        torch = _torch()
+        lo_t = torch.tensor([lo], dtype=torch.int32, device=q.device)
+        hi_t = torch.tensor([hi], dtype=torch.int32, device=q.device)
+        return attend_step_i8(self.ctx, self.geom, self.block, 0, lo_t, hi_t, q,
+                              quant_query=quant_query)[0]
+
+
+def attend_i8_prefill(ctx, num_heads, num_kv_heads, qk, vd, q, k, v, window=0, quant_query=False):
+    """attend (attention.rs:218-287) with an int8 store: every prompt row t
+    attends to max(0, t+1-window)..=t of the prompt's own quantised K/V."""
+    torch = _torch()
+    seq = q.shape[0]
+    g = kv_geom(num_heads, num_kv_heads, qk, vd, max(seq, 1))
+    blk, _ = kv_alloc(g, 1, q.device.index or 0)
+    pos = torch.arange(seq, dtype=torch.int32, device=q.device)
+    kv_write(ctx, g, blk, 0, pos, k.contiguous(), v.contiguous())
+    hi = pos
+    lo = torch.clamp(pos + 1 - window, min=0) if window else torch.zeros_like(pos)
+    scale = float(np.float32(1.0) / np.float32(math.sqrt(qk)))
+    return attend_step_i8(ctx, g, blk, 0, lo.to(torch.int32), hi, q.contiguous(), scale,
+                          quant_query)

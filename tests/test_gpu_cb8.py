@@ -1,0 +1,89 @@
+"""Format B (uint8 codes, per-64-row fp32 codebooks) on the GPU vs the oracle.
+
+GEMV: max-abs <= 1e-4 against the oracle's fp32 closed form (BASELINE's fp32
+bar).  GEMM: bf16 MFMA, max|Y - Y_ref| / max|Y_ref| <= 2e-2.
+"""
+import numpy as np
+import pytest
+import torch
+
+import needle_amd as nd
+import oracle as O
+from conftest import dev, host
+
+pytestmark = pytest.mark.gpu
+
+
+def _problem(rng, out, inn):
+    w = rng.integers(0, 256, size=(out, inn), dtype=np.uint8)
+    cb = rng.normal(0.0, 0.02, size=(-(-out // 64), 256)).astype(np.float32)
+    x = rng.normal(size=inn).astype(np.float32)
+    return w, cb, x
+
+
+def test_gemv_config1_shape(ctx):
+    """3072 x 768, 48 codebooks, x ~ N(0,1), seed 1."""
+    rng = np.random.default_rng(1)
+    w, cb, x = _problem(rng, 3072, 768)
+    y = host(nd.cb8_gemv(ctx, dev(w), dev(cb), dev(x)))
+    want = O.cb8_gemv(w, cb, x)
+    assert np.max(np.abs(y - want)) <= 1e-4
+    assert np.max(np.abs(y - O.cb8_gemv_f64(w, cb, x))) <= 1e-4
+
+
+@pytest.mark.parametrize("out,inn", [(1, 16), (64, 256), (128, 512), (100, 768), (1, 768),
+                                     (130, 784), (65, 1024), (200, 1040), (64, 4096)])
+def test_gemv_ragged(ctx, out, inn):
+    rng = np.random.default_rng(out * 7 + inn)
+    w, cb, x = _problem(rng, out, inn)
+    y = host(nd.cb8_gemv(ctx, dev(w), dev(cb), dev(x)))
+    assert np.max(np.abs(y - O.cb8_gemv(w, cb, x))) <= 1e-4
+
+
+def test_gemv_extreme_codes(ctx):
+    """All-0 and all-255 codes pick the first and last codebook entries."""
+    out, inn = 128, 768
+    cb = np.arange(2 * 256, dtype=np.float32).reshape(2, 256) * np.float32(1e-3)
+    x = np.ones(inn, np.float32)
+    for code in (0, 255):
+        w = np.full((out, inn), code, np.uint8)
+        y = host(nd.cb8_gemv(ctx, dev(w), dev(cb), dev(x)))
+        want = np.repeat(cb[:, code] * inn, 64)
+        assert np.max(np.abs(y - want)) <= 1e-4 * max(1.0, np.abs(want).max())
+
+
+def test_gemv_batched_distinct_problems(ctx):
+    rng = np.random.default_rng(5)
+    count, out, inn = 6, 3072, 768
+    W = rng.integers(0, 256, size=(count, out, inn), dtype=np.uint8)
+    CB = rng.normal(0, 0.02, size=(count, out // 64, 256)).astype(np.float32)
+    X = rng.normal(size=(count, inn)).astype(np.float32)
+    Y = torch.zeros(count, out, device="cuda")
+    nd.cb8_gemv_batched(ctx, dev(W), dev(CB), dev(X), Y)
+    Y = host(Y)
+    for i in range(count):
+        assert np.max(np.abs(Y[i] - O.cb8_gemv(W[i], CB[i], X[i]))) <= 1e-4
+
+
+def test_gemv_rejects_misaligned_width(ctx):
+    w = torch.zeros(64, 24, dtype=torch.uint8, device="cuda")
+    cb = torch.zeros(1, 256, device="cuda")
+    x = torch.zeros(24, device="cuda")
+    with pytest.raises(nd.NeedleError) as e:
+        nd.cb8_gemv(ctx, w, cb, x)
+    assert e.value.code == 1 and "multiple of 16" in str(e.value)
+
+
+@pytest.mark.parametrize("m,out", [(512, 3072), (512, 768), (1, 64), (100, 192)])
+def test_gemm_bf16_mfma(ctx, m, out):
+    rng = np.random.default_rng(m + out)
+    inn = 768
+    w = rng.integers(0, 256, size=(out, inn), dtype=np.uint8)
+    cb = rng.normal(0, 0.02, size=(out // 64, 256)).astype(np.float32)
+    X = rng.normal(size=(m, inn)).astype(np.float32)
+    Y = host(nd.cb8_gemm(ctx, dev(X), dev(w), dev(cb)))
+    ref = O.cb8_gemm(X, w, cb)
+    rel = np.max(np.abs(Y - ref)) / np.max(np.abs(ref))
+    assert rel <= 2e-2, rel
+    # bf16 inputs, fp32 accumulation: far tighter than the gate in practice
+    assert np.linalg.norm(Y - ref) / np.linalg.norm(ref) <= 5e-3

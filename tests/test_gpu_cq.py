@@ -1,0 +1,112 @@
+"""Format A (Cactus-Quants) on the GPU vs the oracle.
+
+Bit-exact: prepare_input (same butterfly) and dequantize_row (same decode,
+same butterfly).  Floating point: matvec/matmul within the reference's own
+tolerance form, 1e-4 * max(|want|, 1) (cq.rs:1184-1186), which at these
+magnitudes is BASELINE's fp32 max-abs 1e-4.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import needle_amd as nd
+import oracle as O
+from conftest import dev, host
+from cq_cases import TERNARY, WIDTHS, build_case, random_case
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+REAL_CB = np.array(json.load(open(os.path.join(GOLDEN, "cq_codebook.json")))["codebook"], np.float32)
+
+
+def _pair(ctx, c):
+    g = nd.CqWeight(ctx, c.blob, c.out, c.in_feat, c.group, c.bits, c.codebook)
+    o = O.CqWeight(c.blob, c.out, c.in_feat, c.group, c.bits, c.codebook)
+    return g, o
+
+
+def _close(got, want):
+    return np.all(np.abs(got - want) <= 1e-4 * np.maximum(np.abs(want), 1.0))
+
+
+@pytest.mark.parametrize("bits", WIDTHS)
+@pytest.mark.parametrize("shape", [(5, 16, 16), (3, 40, 8), (9, 128, 128), (4, 200, 64),
+                                   (24, 128, 128), (70, 768, 128)])
+def test_prepare_dequant_matvec(ctx, bits, shape):
+    c = build_case(*shape, bits)
+    g, o = _pair(ctx, c)
+    rng = np.random.default_rng(shape[0] * 10 + bits)
+    x = rng.normal(size=c.in_feat).astype(np.float32)
+    xh = g.prepare_input(dev(x))
+    assert np.array_equal(host(xh)[0], o.prepare_input(x)), "FWHT must be bit-exact"
+    rows = np.arange(c.out, dtype=np.int32)[::-1].copy()
+    deq = host(g.dequantize_rows(dev(rows)))
+    assert np.array_equal(deq, o.dequantize()[rows]), "dequantize_row must be bit-exact"
+    y = host(g.matvec_prepared(xh[0]))
+    assert _close(y, o.matvec(x))
+    assert np.all(np.abs(y - c.dense @ x.astype(np.float64)) <= 1e-4 * np.maximum(
+        np.abs(c.dense @ x.astype(np.float64)), 1.0))
+
+
+@pytest.mark.parametrize("bits", WIDTHS)
+def test_row_bands(ctx, bits):
+    """A band equals the same rows of the full matvec (cq.rs:1209-1229)."""
+    c = build_case(24, 128, 128, bits)
+    g, o = _pair(ctx, c)
+    x = np.sin(np.arange(128, dtype=np.float32) * np.float32(0.19)).astype(np.float32)
+    xh = g.prepare_input(dev(x))[0]
+    full = host(g.matvec_prepared(xh))
+    for start, n in [(0, 4), (4, 4), (8, 16), (20, 4), (23, 1)]:
+        band = host(g.matvec_rows_prepared(xh, start, n))
+        assert _close(band, full[start:start + n])
+        assert _close(band, o.matvec_rows_prepared(o.prepare_input(x), start, n))
+
+
+@pytest.mark.parametrize("bits", WIDTHS)
+@pytest.mark.parametrize("shape", [(24, 128, 128), (9, 40, 8), (5, 200, 64), (16, 512, 128)])
+def test_matmul(ctx, bits, shape):
+    c = build_case(*shape, bits)
+    g, o = _pair(ctx, c)
+    for batch in (1, 2, 7, 16, 70):
+        rng = np.random.default_rng(batch)
+        xs = rng.normal(size=(batch, c.in_feat)).astype(np.float32)
+        xh_d = g.prepare_input(dev(xs))
+        xh = o.prepare_batch(xs)
+        for rs, rows in [(0, c.out), (0, 1), (1, min(3, c.out - 1))]:
+            got = host(g.matmul_rows_prepared(xh_d, batch, rs, rows))
+            want = o.matmul_rows_prepared(xh, batch, rs, rows)
+            assert _close(got, want), (batch, rs, rows)
+
+
+V3_SHAPES = [(576, 768, 2), (96, 768, 2), (128, 768, 2), (768, 768, 2), (8192, 768, 4),
+             (80, 3072, 4), (84, 768, 4)]
+
+
+@pytest.mark.parametrize("out,inn,bits", V3_SHAPES)
+def test_v3_shapes_real_codebook(ctx, out, inn, bits):
+    """The shipped v3 projection shapes with the shipped codebook."""
+    rng = np.random.default_rng(out + bits)
+    c = random_case(rng, out, inn, 128, bits, REAL_CB)
+    g, o = _pair(ctx, c)
+    x = rng.normal(size=inn).astype(np.float32)
+    xh = g.prepare_input(dev(x))[0]
+    y = host(g.matvec_prepared(xh))
+    assert _close(y, o.matvec(x))
+    xs = rng.normal(size=(64, inn)).astype(np.float32)
+    got = host(g.matmul_rows_prepared(g.prepare_input(dev(xs)), 64, 0, out))
+    assert _close(got, o.matmul_rows_prepared(o.prepare_batch(xs), 64, 0, out))
+
+
+def test_errors_match_cqerror(ctx):
+    cb = np.zeros(28, np.float32)
+    blob = np.zeros(1 << 16, np.uint8)
+    for args, code in [((blob, 4, 128, 128, 7, cb), 11), ((blob, 4, 128, 96, 2, cb), 12),
+                       ((blob, 0, 128, 128, 2, cb), 15), ((np.zeros(4, np.uint8), 512, 512, 128, 2, cb), 14),
+                       ((blob, 4, 128, 128, 2, cb[:10]), 13)]:
+        with pytest.raises(nd.NeedleError) as e:
+            nd.CqWeight(ctx, *args)
+        assert e.value.code == code

@@ -1,0 +1,195 @@
+"""int8 KV cache on the GPU vs the oracle.
+
+Bit-exact: quantize_rows / fake_quant / write_kv (codes and scales).
+Attention: fp32 max-abs <= 1e-4 against the oracle's attend_step over the
+same stored ints (the GPU sums in a different order; expf may differ by an
+ulp).
+"""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import needle_amd as nd
+import oracle as O
+from conftest import dev, host
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def _golden_cases():
+    return json.load(open(os.path.join(GOLDEN, "kv_quant_vectors.json")))["cases"]
+
+
+def test_quantize_rows_golden_bit_exact(ctx):
+    for case in _golden_cases():
+        dim = case["dim"]
+        x = np.array(case["in"], np.float32)
+        qi, qs = nd.quantize_rows(ctx, dev(x), dim)
+        oi, os_ = O.quantize_rows(x, dim)
+        assert np.array_equal(host(qi), oi), case["name"]
+        assert np.array_equal(host(qs).view(np.uint32), os_.view(np.uint32)), case["name"]
+        fq = dev(x.copy())
+        nd.fake_quant(ctx, fq, dim)
+        want = np.concatenate([O.fake_quant_vec(r) for r in x.reshape(-1, dim)])
+        assert np.array_equal(host(fq), want), case["name"]
+        tol = np.maximum(np.abs(np.array(case["out"], np.float32)), 1.0) * 1e-5
+        assert np.all(np.abs(host(fq) - np.array(case["out"], np.float32)) <= tol)
+
+
+@pytest.mark.parametrize("dim", [48, 64, 16, 256, 100])
+def test_quantize_rows_random_bit_exact(ctx, dim):
+    rng = np.random.default_rng(dim)
+    rows = 4096
+    mags = 10.0 ** rng.uniform(-9, 7, size=(rows, 1))
+    x = (rng.normal(size=(rows, dim)) * mags).astype(np.float32)
+    x[0] = 0.0                       # all-zero row keeps scale 1
+    x[1] = 0.0
+    x[1, 3] = 7.0                    # one spike
+    x[2] = np.float32(0.5) * np.arange(dim, dtype=np.float32) / np.float32(dim)
+    qi, qs = nd.quantize_rows(ctx, dev(x), dim)
+    oi, os_ = O.quantize_rows(x, dim)
+    assert np.array_equal(host(qi), oi)
+    assert np.array_equal(host(qs).view(np.uint32), os_.view(np.uint32))
+    assert host(qs)[0] == 1.0
+
+
+def test_write_kv_ring_matches_oracle(ctx):
+    """A local ring (window 16) written past its window, int8 codes and
+    scales equal the oracle V3Cache ring's, slot for slot."""
+    H, KVH, QK, VD, W = 12, 2, 48, 64, 16
+    ring = O.Ring(True, KVH, QK, VD, hint=4, window=W, max_seq_len=64)
+    cache = nd.V3LayerCache(ctx, H, KVH, QK, VD, hint=4, window=W, max_seq_len=64)
+    rng = np.random.default_rng(2)
+    for pos in range(41):
+        k = (rng.normal(size=KVH * QK) * (pos + 1)).astype(np.float32)
+        v = rng.normal(size=KVH * VD).astype(np.float32)
+        ring.write_kv(pos, k, v)
+        cache.write_kv(pos, dev(k), dev(v))
+        assert cache.span(pos) == ring.span(pos)
+        assert cache.slots == ring.slots
+    k, ks, v, vs = nd.kv_unpack(cache.geom, host(cache.block))
+    st = ring.store()
+    assert np.array_equal(k.reshape(-1), st["k"]) and np.array_equal(v.reshape(-1), st["v"])
+    assert np.array_equal(ks.reshape(-1), st["k_scale"]) and np.array_equal(vs.reshape(-1), st["v_scale"])
+
+
+def _fill(ctx, rng, H, KVH, QK, VD, cap, npos, count=1):
+    """`count` blocks, positions 0..npos-1 written (ring-wrapped at cap)."""
+    g = nd.kv_geom(H, KVH, QK, VD, cap)
+    blk, nb = nd.kv_alloc(g, count)
+    ks_raw = rng.normal(size=(count, npos, KVH * QK)).astype(np.float32)
+    vs_raw = rng.normal(size=(count, npos, KVH * VD)).astype(np.float32)
+    for i in range(count):
+        pos = torch.arange(npos, dtype=torch.int32, device="cuda")
+        nd.kv_write(ctx, g, blk[i * nb:(i + 1) * nb], 0, pos, dev(ks_raw[i]), dev(vs_raw[i]))
+    return g, blk, nb
+
+
+def _oracle_step(g, block_np, q, lo, hi):
+    k, ks, v, vs = nd.kv_unpack(g, block_np)
+    return O.attend_step_i8(q, k.reshape(-1), ks.reshape(-1), v.reshape(-1), vs.reshape(-1),
+                            g.cap, lo, hi, g.num_heads, g.num_kv_heads, g.qk_head_dim,
+                            g.v_head_dim)
+
+
+@pytest.mark.parametrize("H,KVH,QK,VD", [(12, 2, 48, 64), (12, 12, 64, 64)])
+@pytest.mark.parametrize("ctxlen", [1, 7, 512, 2048, 8192])
+def test_attend_step_causal(ctx, H, KVH, QK, VD, ctxlen):
+    """Config 3 (MHA 12 x 64) and the v3 GQA geometry, causal span 0..ctx-1."""
+    rng = np.random.default_rng(ctxlen + H * KVH)
+    g, blk, nb = _fill(ctx, rng, H, KVH, QK, VD, ctxlen, ctxlen)
+    q = rng.normal(size=H * QK).astype(np.float32)
+    lo = torch.tensor([0], dtype=torch.int32, device="cuda")
+    hi = torch.tensor([ctxlen - 1], dtype=torch.int32, device="cuda")
+    out = host(nd.attend_step_i8(ctx, g, blk, nb, lo, hi, dev(q)[None]))[0]
+    want = _oracle_step(g, host(blk), q, 0, ctxlen - 1)
+    assert np.max(np.abs(out - want)) <= 1e-4
+
+
+@pytest.mark.parametrize("lo,hi", [(0, 0), (5, 5), (3, 16), (1000, 1023), (1000, 2023),
+                                   (4000, 5023), (17, 1040)])
+def test_attend_step_ring_window(ctx, lo, hi):
+    """A 1024-slot local ring read across its wrap point."""
+    H, KVH, QK, VD, cap = 12, 2, 48, 64, 1024
+    rng = np.random.default_rng(lo * 31 + hi)
+    g = nd.kv_geom(H, KVH, QK, VD, cap)
+    blk, nb = nd.kv_alloc(g)
+    n = hi + 1
+    k = rng.normal(size=(n, KVH * QK)).astype(np.float32)
+    v = rng.normal(size=(n, KVH * VD)).astype(np.float32)
+    nd.kv_write(ctx, g, blk, 0, torch.arange(n, dtype=torch.int32, device="cuda"), dev(k), dev(v))
+    q = rng.normal(size=H * QK).astype(np.float32)
+    out = host(nd.attend_step_i8(ctx, g, blk, nb, dev(np.array([lo], np.int32)),
+                                 dev(np.array([hi], np.int32)), dev(q)[None]))[0]
+    want = _oracle_step(g, host(blk), q, lo, hi)
+    assert np.max(np.abs(out - want)) <= 1e-4
+
+
+def test_hoisted_scale_geometry(ctx):
+    """v3_kv_quant_parity.rs:102-218 geometry (4/2 heads, 17 slots)."""
+    H, KVH, QK, VD, SLOTS = 4, 2, 48, 64, 17
+    rng = np.random.default_rng(17)
+    g, blk, nb = _fill(ctx, rng, H, KVH, QK, VD, SLOTS, SLOTS)
+    q = rng.normal(size=H * QK).astype(np.float32)
+    for lo, hi in [(0, 0), (0, 9), (3, 16), (5, 5)]:
+        out = host(nd.attend_step_i8(ctx, g, blk, nb, dev(np.array([lo], np.int32)),
+                                     dev(np.array([hi], np.int32)), dev(q)[None]))[0]
+        assert np.max(np.abs(out - _oracle_step(g, host(blk), q, lo, hi))) <= 1e-4
+
+
+def test_quant_query_fused(ctx):
+    """quant_rows(q) then attend_step (v3/model.rs:289-307), fused."""
+    H, KVH, QK, VD, n = 12, 2, 48, 64, 300
+    rng = np.random.default_rng(3)
+    g, blk, nb = _fill(ctx, rng, H, KVH, QK, VD, 512, n)
+    q = (rng.normal(size=H * QK) * 3).astype(np.float32)
+    out = host(nd.attend_step_i8(ctx, g, blk, nb, dev(np.array([0], np.int32)),
+                                 dev(np.array([n - 1], np.int32)), dev(q)[None], quant_query=True))[0]
+    qq = O.quant_rows(q, 1, H, QK)
+    assert np.max(np.abs(out - _oracle_step(g, host(blk), qq, 0, n - 1))) <= 1e-4
+
+
+def test_batched_sessions(ctx):
+    """Several sessions, one launch, each with its own block and span."""
+    H, KVH, QK, VD, cap, count = 12, 12, 64, 64, 2048, 5
+    rng = np.random.default_rng(11)
+    g, blk, nb = _fill(ctx, rng, H, KVH, QK, VD, cap, cap, count)
+    q = rng.normal(size=(count, H * QK)).astype(np.float32)
+    lo = np.array([0, 100, 2047, 5, 0], np.int32)
+    hi = np.array([2047, 1900, 2047, 5, 511], np.int32)
+    out = host(nd.attend_step_i8(ctx, g, blk, nb, dev(lo), dev(hi), dev(q)))
+    blocks = host(blk)
+    for i in range(count):
+        want = _oracle_step(g, blocks[i * nb:(i + 1) * nb], q[i], int(lo[i]), int(hi[i]))
+        assert np.max(np.abs(out[i] - want)) <= 1e-4, i
+
+
+def test_bad_span_is_nan(ctx):
+    H, KVH, QK, VD, cap = 12, 2, 48, 64, 64
+    g = nd.kv_geom(H, KVH, QK, VD, cap)
+    blk, nb = nd.kv_alloc(g)
+    q = torch.zeros(1, H * QK, device="cuda")
+    for lo, hi in [(5, 4), (0, 64)]:
+        out = host(nd.attend_step_i8(ctx, g, blk, nb, dev(np.array([lo], np.int32)),
+                                     dev(np.array([hi], np.int32)), q))
+        assert np.isnan(out).all()
+
+
+@pytest.mark.parametrize("seq,window", [(1, 0), (40, 16), (128, 0), (300, 64)])
+def test_prefill_attend(ctx, seq, window):
+    """attend over the prompt's own int8 K/V with a window (attention.rs:218-287)."""
+    H, KVH, QK, VD = 12, 2, 48, 64
+    rng = np.random.default_rng(seq + window)
+    q = rng.normal(size=(seq, H * QK)).astype(np.float32)
+    k = rng.normal(size=(seq, KVH * QK)).astype(np.float32)
+    v = rng.normal(size=(seq, KVH * VD)).astype(np.float32)
+    out = host(nd.attend_i8_prefill(ctx, H, KVH, QK, VD, dev(q), dev(k), dev(v), window))
+    kq, ks = O.quantize_rows(k, QK)
+    vq, vs = O.quantize_rows(v, VD)
+    want = O.attend_i8(q, kq, ks, vq, vs, seq, H, KVH, QK, VD, window=window).reshape(seq, -1)
+    assert np.max(np.abs(out - want)) <= 1e-4
