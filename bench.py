@@ -35,6 +35,20 @@ ATT_H, ATT_D, ATT_CTX, ATT_SESSIONS = 12, 64, 2048, 320
 ATT_BYTES = ATT_CTX * (2 * ATT_H * ATT_D + 2 * ATT_H * 4) + 2 * ATT_H * ATT_D * 4
 
 
+def pmc_traffic(kernel):
+    """HBM bytes per launch of `kernel` as measured by the FETCH_SIZE /
+    WRITE_SIZE counter runs summarised in profiles/hbm_traffic_pmc.md."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic_pmc.md")
+    try:
+        for line in open(path):
+            parts = line.split()
+            if len(parts) == 3 and parts[0] == "traffic_bytes_per_launch" and parts[1] == kernel:
+                return int(parts[2])
+    except OSError:
+        pass
+    return None
+
+
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
@@ -45,15 +59,22 @@ def parse():
     p.add_argument("--only", choices=["gemv", "attn"], default=None,
                    help="run one workload only, without the batch-1 latency probes "
                         "(for per-kernel profiles)")
+    p.add_argument("--min-warm", type=float, default=0.5,
+                   help="seconds of untimed warm-up before each timed loop (0 for counter runs)")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="also run a plain 1 GiB device copy (PMC byte-counter scale)")
     return p.parse_args()
 
 
-def timed_loop(torch, fn, steps, warmup, min_warm_s=0.5):
+MIN_WARM_S = 0.5
+
+
+def timed_loop(torch, fn, steps, warmup, min_warm_s=None):
     """W untimed warm-up steps (continued until `min_warm_s` has passed, so the
     clocks have left their idle state), then exactly `steps` timed steps
     between two events on the stream the kernels run on."""
+    if min_warm_s is None:
+        min_warm_s = MIN_WARM_S
     t0 = time.perf_counter()
     n = 0
     while n < warmup or time.perf_counter() - t0 < min_warm_s:
@@ -100,7 +121,9 @@ def cpu_baseline(seconds=12.0):
 
 
 def main():
+    global MIN_WARM_S
     args = parse()
+    MIN_WARM_S = args.min_warm
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1",
                           "n_gpus": args.gpus}))
@@ -163,7 +186,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": pmc_traffic("cb8_gemv_kernel<3>"),
             "kernel": "cb8_gemv_kernel<3>",
         },
     }
@@ -209,22 +232,26 @@ def main():
         result["secondary"] = {
             "decode_attention_int8_ctx2048": {
                 "workload": f"{S} sessions x 12 heads x 64, ctx 2048, int8 K/V + f32 scales; "
-                            "step = append one token per session + split-K attention",
+                            "step = append one token per session + decode attention",
                 "session_tokens_per_s": round(S / (ms_dec * 1e-3), 1),
                 "ms_per_step": round(ms_dec, 4),
                 "attention_GBps": round(att_gbs, 2),
                 "attention_frac_hbm": round(att_gbs / HBM_PEAK_GBS, 4),
+                "attention_traffic_bytes": pmc_traffic("attn_i8_kernel<1,64,64,16>"),
+                "attention_algorithmic_bytes": S * ATT_BYTES,
                 "bytes_per_session_decode": ATT_BYTES,
                 "single_session_attention_us": round(ms_att1 * 1e3, 2),
             }
         }
 
     if args.calibrate_copy:
+        # A plain device copy of exactly 1 GiB: the byte counters' reference.
         a = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
         b = torch.empty_like(a)
         for _ in range(3):
             b.copy_(a)
         torch.cuda.synchronize()
+        del a, b
 
     ctx.close()
     if not args.no_cpu:

@@ -6,16 +6,12 @@
 // inv = 1 / scale, q = clamp(roundf(x * inv), -128, 127), roundf being
 // round-half-away-from-zero as libm::roundf.  One wave per head vector.
 //
-// Attention (attend_step over Int8View, attention.rs:300-377) is split-K:
-// a workgroup owns (query, kv head, span chunk) and every query head of its
-// GQA group, so a kv head's int8 rows are read once for all of them.
-//   scores  16-byte K vectors, NQ = qk/16 lanes per position, the lane's
-//           16-wide slice of each query head in registers; lane partials are
-//           summed per position through LDS, then * k_scale * scale.
-//   softmax chunk max, e = exp(s - m), l = sum e.
-//   values  4 columns per lane (one int8 dword per position), all query
-//           heads accumulated in registers, reduced over position groups.
-// Chunks merge in a second kernel with the usual (m, l, o) rescaling.
+// Attention (attend_step over Int8View, attention.rs:300-377) reads the int8
+// cache directly: a workgroup owns (query, kv head) -- every query head of
+// the GQA group, so a kv head's int8 rows are read once for all of them --
+// and walks its span in chunks with an online softmax (flash decoding).  The
+// span is split across workgroups, with a merge pass, only when there are
+// too few (query, kv head) pairs to fill the GPU (batch-1 decode).
 #include "nd_internal.h"
 
 #include <cmath>
@@ -120,38 +116,71 @@ __global__ __launch_bounds__(128) void kv_write_kernel(Geom g, uint8_t *__restri
 }
 
 // ---------------------------------------------------------------------------
-// Split-K decode attention.
-// ---------------------------------------------------------------------------
-template <int REP, int NQ, int NV4>
+// Decode attention over the int8 ring, flash-decoding style.
+//
+// Block = (query i, kv head g, split s).  It walks its share of the span in
+// chunks of CH positions with an online softmax (running max m, running sum
+// l, accumulator rescaled by exp(m_old - m_new)), so one block can cover a
+// whole span and no merge is needed when sessions x kv heads fill the GPU.
+// Register pipeline: a chunk's K and V are already in registers when it
+// starts; the next chunk's K loads are issued as soon as the scores are
+// done, and its V loads as soon as the value pass is done.
+//   K: KL = qk/16 lanes per position, one 16-byte int8 vector each, the
+//      lane's 16-wide slice of every query head of the group in registers.
+//   V: VL = vd/VW lanes per position, VW bytes each (16 for up to two query
+//      heads per kv head, else 8), REP x VW accumulators per lane.
+// Scores, weights and block reductions go through LDS.
+template <int REP, int QK, int VD, int VW>
+struct AttnShape {
+    static constexpr int KL = QK / 16;
+    static constexpr int KPP = kThreads / KL;                 // positions per K pass
+    static constexpr int VL = VD / VW;
+    static constexpr int VPP = kThreads / VL;                 // positions per V pass
+    static constexpr int CH = REP <= 2 ? 512 : 256;           // positions per chunk
+    static constexpr int KP = (CH + KPP - 1) / KPP;           // K passes per chunk
+    static constexpr int VP = CH / VPP;                       // V passes per chunk
+};
+
+template <int VW>
+struct VVec;
+template <>
+struct VVec<16> {
+    typedef uint32_t T __attribute__((ext_vector_type(4)));
+};
+template <>
+struct VVec<8> {
+    typedef uint32_t T __attribute__((ext_vector_type(2)));
+};
+
+__device__ inline float i8_at(uint32_t dw, int b) { return float(int32_t(dw << (24 - 8 * b)) >> 24); }
+
+template <int REP, int QK, int VD, int VW>
 __global__ __launch_bounds__(kThreads) void attn_i8_kernel(
     Geom g, const uint8_t *__restrict__ kv, size_t kv_stride, const int32_t *__restrict__ lo_a,
     const int32_t *__restrict__ hi_a, const float *__restrict__ q, float scale, int quant_query,
-    int chunk, int nchunks, float *__restrict__ out, float *__restrict__ part_o,
-    float *__restrict__ part_ml)
+    int splits, float *__restrict__ out, float *__restrict__ part_o, float *__restrict__ part_ml)
 {
-    // NQ = qk/16 lanes per position for K; NV4 = vd/4 lanes per position for V.
-    constexpr int kTPK = kThreads / NQ;   // positions per K pass
-    constexpr int kTPV = kThreads / NV4;  // positions per V pass (position groups)
-    extern __shared__ float smem[];
-    float *qs = smem;                          // [REP][QK]
-    float *sp = qs + REP * kMaxDim;            // [REP][chunk][NQ] partial dots
-    float *ss = sp + REP * chunk * NQ;         // [chunk][REP] scores, then weights
-    float *red = ss + chunk * REP;             // reductions: [REP][kThreads/64] + stats
-    float *vred = red + 2 * REP * (kThreads / 64) + 2 * REP;  // [4 waves][16 lanes][REP*4]
+    using S = AttnShape<REP, QK, VD, VW>;
+    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+    using VT = typename VVec<VW>::T;
+    constexpr int CH = S::CH, NW = kThreads / 64;
+    __shared__ float qs[REP][QK];
+    __shared__ float sp[REP][CH * S::KL];  // lane partial dots
+    __shared__ float wsh[REP][CH];         // scores, then weights
+    __shared__ float red[REP][NW];
+    __shared__ float vred[NW][REP][VD];
 
     const size_t qi = blockIdx.z;
     const int kvh = blockIdx.y;
-    const int c = blockIdx.x;
-    const int t = threadIdx.x;
-    const int lane = t & 63;
-    const int wave = t >> 6;
-    const int QK = NQ * 16, VD = NV4 * 4;
+    const int split = blockIdx.x;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
 
     const int lo = lo_a[qi], hi = hi_a[qi];
     const int span = hi - lo + 1;
-    const bool bad = lo < 0 || span < 1 || span > g.cap || span > chunk * nchunks;
-    const int p0 = c * chunk;
-    const int n = bad ? 0 : max(0, min(chunk, span - p0));
+    const bool bad = lo < 0 || span < 1 || span > g.cap;
+    const int nch = bad ? 0 : (span + CH - 1) / CH;
+    const int c_begin = int((long long)nch * split / splits);
+    const int c_end = int((long long)nch * (split + 1) / splits);
 
     const uint8_t *blk = kv + qi * kv_stride;
     const int8_t *kb = reinterpret_cast<const int8_t *>(blk) + size_t(kvh) * g.cap * QK;
@@ -159,153 +188,195 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(
     const float *ksb = reinterpret_cast<const float *>(blk + g.ks_off) + size_t(kvh) * g.cap;
     const float *vsb = reinterpret_cast<const float *>(blk + g.vs_off) + size_t(kvh) * g.cap;
 
-    // Query heads kvh*REP .. +REP, optionally fake-quantised per head.
+    // Query heads kvh*REP .. +REP (fake-quantised per head on request).
     const float *qg = q + qi * size_t(g.H) * QK + size_t(kvh) * REP * QK;
-    for (int e = t; e < REP * QK; e += kThreads) qs[(e / QK) * kMaxDim + e % QK] = qg[e];
+    for (int e = t; e < REP * QK; e += kThreads) qs[e / QK][e % QK] = qg[e];
     __syncthreads();
     if (quant_query) {
-        for (int r = wave; r < REP; r += kThreads / 64) {
+        for (int r = wave; r < REP; r += NW) {
             float sc, inv;
-            quant_scale_wave(qs + r * kMaxDim, QK, sc, inv);
-            for (int e = lane; e < QK; e += 64) qs[r * kMaxDim + e] = quant_code(qs[r * kMaxDim + e], inv) * sc;
+            quant_scale_wave(qs[r], QK, sc, inv);
+            for (int e = lane; e < QK; e += 64) qs[r][e] = quant_code(qs[r][e], inv) * sc;
         }
         __syncthreads();
     }
-
-    // ---- scores ----
-    const int sub = t % NQ;
-    const bool kact = t < kTPK * NQ;
+    const int ksub = t % S::KL;
+    const int kpos = t / S::KL;  // position within a K pass
+    const bool kact = t < S::KPP * S::KL;
     float qr[REP][16];
 #pragma unroll
     for (int r = 0; r < REP; ++r)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) qr[r][e] = qs[r * kMaxDim + sub * 16 + e];
-    for (int pl = t / NQ; kact && pl < n; pl += kTPK) {
-        const int slot = (lo + p0 + pl) % g.cap;
-        const uint4 kvv = *reinterpret_cast<const uint4 *>(kb + size_t(slot) * QK + sub * 16);
-        const uint32_t dw[4] = {kvv.x, kvv.y, kvv.z, kvv.w};
-        float kf[16];
-#pragma unroll
-        for (int d = 0; d < 4; ++d)
-#pragma unroll
-            for (int b = 0; b < 4; ++b)
-                kf[4 * d + b] = float(int32_t(dw[d] << (24 - 8 * b)) >> 24);
-#pragma unroll
-        for (int r = 0; r < REP; ++r) {
-            float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 16; e += 2) {
-                a0 += qr[r][e] * kf[e];
-                a1 += qr[r][e + 1] * kf[e + 1];
-            }
-            sp[(r * chunk + pl) * NQ + sub] = a0 + a1;
-        }
-    }
-    __syncthreads();
-    float mloc[REP];
-#pragma unroll
-    for (int r = 0; r < REP; ++r) mloc[r] = -INFINITY;
-    for (int pl = t; pl < n; pl += kThreads) {
-        const int slot = (lo + p0 + pl) % g.cap;
-        const float ks = ksb[slot];
-#pragma unroll
-        for (int r = 0; r < REP; ++r) {
-            float a = 0.0f;
-#pragma unroll
-            for (int s2 = 0; s2 < NQ; ++s2) a += sp[(r * chunk + pl) * NQ + s2];
-            const float s = (a * ks) * scale;
-            ss[pl * REP + r] = s;
-            mloc[r] = fmaxf(mloc[r], s);
-        }
-    }
-    // block max per head
-#pragma unroll
-    for (int r = 0; r < REP; ++r) {
-        const float m = wave_max(mloc[r]);
-        if (lane == 0) red[r * (kThreads / 64) + wave] = m;
-    }
-    __syncthreads();
-    float mx[REP];
-#pragma unroll
-    for (int r = 0; r < REP; ++r) {
-        float m = -INFINITY;
-#pragma unroll
-        for (int w2 = 0; w2 < kThreads / 64; ++w2) m = fmaxf(m, red[r * (kThreads / 64) + w2]);
-        mx[r] = m;
-    }
-    __syncthreads();
-    // e = exp(s - m); weights w = e * v_scale for the value pass; l = sum e.
-    float lloc[REP];
-#pragma unroll
-    for (int r = 0; r < REP; ++r) lloc[r] = 0.0f;
-    for (int pl = t; pl < n; pl += kThreads) {
-        const int slot = (lo + p0 + pl) % g.cap;
-        const float vs = vsb[slot];
-#pragma unroll
-        for (int r = 0; r < REP; ++r) {
-            const float e = expf(ss[pl * REP + r] - mx[r]);
-            lloc[r] += e;
-            ss[pl * REP + r] = e * vs;
-        }
-    }
-#pragma unroll
-    for (int r = 0; r < REP; ++r) {
-        const float l = wave_sum(lloc[r]);
-        if (lane == 0) red[r * (kThreads / 64) + wave] = l;
-    }
-    __syncthreads();
+        for (int e = 0; e < 16; ++e) qr[r][e] = qs[r][ksub * 16 + e];
+    const int vsub = t % S::VL;
+    const int vpos = t / S::VL;
 
-    // ---- values: lane owns columns 4*(t % NV4) .. +4 ----
-    const int vsub = t % NV4;
-    float acc[REP][4];
+    u4 kr[S::KP];
+    VT vr[S::VP];
+    auto load_k = [&](int c) {
 #pragma unroll
-    for (int r = 0; r < REP; ++r)
+        for (int p = 0; p < S::KP; ++p) {
+            const int pl = p * S::KPP + kpos;
+            const int pc = min(c * CH + pl, span - 1);  // clamp: read a valid slot
+            const int slot = (lo + pc) % g.cap;
+            kr[p] = __builtin_nontemporal_load(reinterpret_cast<const u4 *>(kb + size_t(slot) * QK) + ksub);
+        }
+    };
+    auto load_v = [&](int c) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[r][e] = 0.0f;
-    for (int pl = t / NV4; pl < n; pl += kTPV) {
-        const int slot = (lo + p0 + pl) % g.cap;
-        const uint32_t dw = *reinterpret_cast<const uint32_t *>(vb + size_t(slot) * VD + vsub * 4);
-        float vf[4];
+        for (int p = 0; p < S::VP; ++p) {
+            const int pc = min(c * CH + p * S::VPP + vpos, span - 1);
+            const int slot = (lo + pc) % g.cap;
+            vr[p] = __builtin_nontemporal_load(reinterpret_cast<const VT *>(vb + size_t(slot) * VD) + vsub);
+        }
+    };
+    if (c_begin < c_end) {
+        load_k(c_begin);
+        load_v(c_begin);
+    }
+
+    float m_run[REP], l_loc[REP], acc[REP][VW];
 #pragma unroll
-        for (int b = 0; b < 4; ++b) vf[b] = float(int32_t(dw << (24 - 8 * b)) >> 24);
+    for (int r = 0; r < REP; ++r) {
+        m_run[r] = -INFINITY;
+        l_loc[r] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < VW; ++e) acc[r][e] = 0.0f;
+    }
+
+    for (int c = c_begin; c < c_end; ++c) {
+        const int n = min(CH, span - c * CH);
+        // ---- scores: lane partial dots ----
+#pragma unroll
+        for (int p = 0; p < S::KP; ++p) {
+            const int pl = p * S::KPP + kpos;
+            if (kact && pl < CH) {
+                const uint32_t dw[4] = {kr[p].x, kr[p].y, kr[p].z, kr[p].w};
+                float kf[16];
+#pragma unroll
+                for (int d = 0; d < 4; ++d)
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) kf[4 * d + b] = i8_at(dw[d], b);
+#pragma unroll
+                for (int r = 0; r < REP; ++r) {
+                    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 16; e += 2) {
+                        a0 += qr[r][e] * kf[e];
+                        a1 += qr[r][e + 1] * kf[e + 1];
+                    }
+                    sp[r][pl * S::KL + ksub] = a0 + a1;
+                }
+            }
+        }
+        if (c + 1 < c_end) load_k(c + 1);  // lands during softmax and values
+        __syncthreads();
+        // ---- per-position score, chunk max ----
+        float cmax[REP];
+#pragma unroll
+        for (int r = 0; r < REP; ++r) cmax[r] = -INFINITY;
+        for (int pl = t; pl < n; pl += kThreads) {
+            const int slot = (lo + c * CH + pl) % g.cap;
+            const float ks = ksb[slot];
+#pragma unroll
+            for (int r = 0; r < REP; ++r) {
+                float a = 0.0f;
+#pragma unroll
+                for (int s2 = 0; s2 < S::KL; ++s2) a += sp[r][pl * S::KL + s2];
+                const float sc = (a * ks) * scale;
+                wsh[r][pl] = sc;
+                cmax[r] = fmaxf(cmax[r], sc);
+            }
+        }
 #pragma unroll
         for (int r = 0; r < REP; ++r) {
-            const float wgt = ss[pl * REP + r];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc[r][e] += wgt * vf[e];
+            const float m = wave_max(cmax[r]);
+            if (lane == 0) red[r][wave] = m;
         }
-    }
-    // Reduce over position groups: lanes sharing vsub within a wave, then
-    // across waves through LDS.
+        __syncthreads();
+        float alpha[REP], mnew[REP];
 #pragma unroll
-    for (int r = 0; r < REP; ++r)
+        for (int r = 0; r < REP; ++r) {
+            float m = m_run[r];
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-            for (int off = NV4; off < 64; off <<= 1) acc[r][e] += __shfl_xor(acc[r][e], off, 64);
-    if (lane < NV4) {
+            for (int w2 = 0; w2 < NW; ++w2) m = fmaxf(m, red[r][w2]);
+            mnew[r] = m;
+            alpha[r] = expf(m_run[r] - m);  // exp(-inf) = 0 on the first chunk
+            m_run[r] = m;
+            l_loc[r] *= alpha[r];
+        }
+        // ---- weights e * v_scale; running sum ----
+        for (int pl = t; pl < n; pl += kThreads) {
+            const int slot = (lo + c * CH + pl) % g.cap;
+            const float vs = vsb[slot];
+#pragma unroll
+            for (int r = 0; r < REP; ++r) {
+                const float e = expf(wsh[r][pl] - mnew[r]);
+                l_loc[r] = l_loc[r] + e;
+                wsh[r][pl] = e * vs;
+            }
+        }
+        __syncthreads();
+        // ---- values ----
 #pragma unroll
         for (int r = 0; r < REP; ++r)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) vred[(wave * NV4 + lane) * REP * 4 + r * 4 + e] = acc[r][e];
+            for (int e = 0; e < VW; ++e) acc[r][e] *= alpha[r];
+#pragma unroll
+        for (int p = 0; p < S::VP; ++p) {
+            const int pl = p * S::VPP + vpos;
+            if (pl < n) {
+                float vf[VW];
+#pragma unroll
+                for (int d = 0; d < VW / 4; ++d)
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) vf[4 * d + b] = i8_at(vr[p][d], b);
+#pragma unroll
+                for (int r = 0; r < REP; ++r) {
+                    const float wgt = wsh[r][pl];
+#pragma unroll
+                    for (int e = 0; e < VW; ++e) acc[r][e] += wgt * vf[e];
+                }
+            }
+        }
+        if (c + 1 < c_end) load_v(c + 1);  // lands during the next scores
+        __syncthreads();
+    }
+
+    // ---- reduce over the lanes sharing a V column slice ----
+#pragma unroll
+    for (int r = 0; r < REP; ++r)
+#pragma unroll
+        for (int e = 0; e < VW; ++e)
+            for (int off = S::VL; off < 64; off <<= 1) acc[r][e] += __shfl_xor(acc[r][e], off, 64);
+    if (lane < S::VL) {
+#pragma unroll
+        for (int r = 0; r < REP; ++r)
+#pragma unroll
+            for (int e = 0; e < VW; ++e) vred[wave][r][lane * VW + e] = acc[r][e];
+    }
+#pragma unroll
+    for (int r = 0; r < REP; ++r) {
+        const float l = wave_sum(l_loc[r]);
+        if (lane == 0) red[r][wave] = l;
     }
     __syncthreads();
-
-    // ---- write this chunk ----
     for (int o = t; o < REP * VD; o += kThreads) {
         const int r = o / VD, col = o % VD;
-        const int ls = col / 4, e = col % 4;
-        float s = 0.0f;
-        for (int w2 = 0; w2 < kThreads / 64; ++w2) s += vred[(w2 * NV4 + ls) * REP * 4 + r * 4 + e];
-        float l = 0.0f;
-        for (int w2 = 0; w2 < kThreads / 64; ++w2) l += red[r * (kThreads / 64) + w2];
+        float s = 0.0f, l = 0.0f;
+#pragma unroll
+        for (int w2 = 0; w2 < NW; ++w2) {
+            s += vred[w2][r][col];
+            l += red[r][w2];
+        }
         const int head = kvh * REP + r;
-        if (nchunks == 1) {
+        if (splits == 1) {
             out[qi * size_t(g.H) * VD + size_t(head) * VD + col] = bad ? NAN : s / l;
         } else {
-            part_o[((qi * g.H + head) * size_t(nchunks) + c) * VD + col] = s;
+            part_o[((qi * g.H + head) * size_t(splits) + split) * VD + col] = s;
             if (col == 0) {
-                float *ml = part_ml + ((qi * g.H + head) * size_t(nchunks) + c) * 2;
-                ml[0] = bad ? NAN : (n > 0 ? mx[r] : -INFINITY);
+                float *ml = part_ml + ((qi * g.H + head) * size_t(splits) + split) * 2;
+                ml[0] = bad ? NAN : (c_begin < c_end ? m_run[r] : -INFINITY);
                 ml[1] = l;
             }
         }
@@ -366,47 +437,41 @@ int check_geom(const nd_kv_geom *g)
     return ND_OK;
 }
 
-size_t attn_smem_bytes(int rep, int nq, int chunk)
-{
-    return sizeof(float) * (size_t(rep) * kMaxDim + size_t(rep) * chunk * nq + size_t(chunk) * rep +
-                            2 * rep * (kThreads / 64) + 2 * rep + 4 * 16 * rep * 4);
-}
-
-template <int REP, int NQ, int NV4>
-void launch_attn(dim3 grid, size_t smem, hipStream_t s, Geom g, const uint8_t *kv, size_t stride,
+template <int REP, int QK>
+void launch_attn(dim3 grid, hipStream_t s, Geom g, const uint8_t *kv, size_t stride,
                  const int32_t *lo, const int32_t *hi, const float *q, float scale, int qq,
-                 int chunk, int nchunks, float *out, float *po, float *pml)
+                 int splits, float *out, float *po, float *pml)
 {
-    hipLaunchKernelGGL((attn_i8_kernel<REP, NQ, NV4>), grid, dim3(kThreads), smem, s, g, kv, stride,
-                       lo, hi, q, scale, qq, chunk, nchunks, out, po, pml);
+    constexpr int VW = REP <= 2 ? 16 : 8;
+    hipLaunchKernelGGL((attn_i8_kernel<REP, QK, 64, VW>), grid, dim3(kThreads), 0, s, g, kv, stride,
+                       lo, hi, q, scale, qq, splits, out, po, pml);
 }
 
-using AttnFn = void (*)(dim3, size_t, hipStream_t, Geom, const uint8_t *, size_t, const int32_t *,
-                        const int32_t *, const float *, float, int, int, int, float *, float *,
-                        float *);
+using AttnFn = void (*)(dim3, hipStream_t, Geom, const uint8_t *, size_t, const int32_t *,
+                        const int32_t *, const float *, float, int, int, float *, float *, float *);
 
-// Instantiated shapes: the v3 geometry (12/2 heads, qk 48, v 64) and the
-// MHA cache (qk = v = 64), plus every repeat 1..8 at qk 48/64, v 64.
+// Instantiated: qk 48 (the shipped v3 geometry) and 64 (the MHA cache), v 64,
+// query heads per kv head 1, 2, 3, 4, 6, 8.
 template <int REP>
-AttnFn pick_nq(int nq, int nv4)
+AttnFn pick_qk(int qk, int vd)
 {
-    if (nv4 != 16) return nullptr;
-    switch (nq) {
-    case 3: return launch_attn<REP, 3, 16>;
-    case 4: return launch_attn<REP, 4, 16>;
+    if (vd != 64) return nullptr;
+    switch (qk) {
+    case 48: return launch_attn<REP, 48>;
+    case 64: return launch_attn<REP, 64>;
     default: return nullptr;
     }
 }
 
-AttnFn pick_attn(int rep, int nq, int nv4)
+AttnFn pick_attn(int rep, int qk, int vd)
 {
     switch (rep) {
-    case 1: return pick_nq<1>(nq, nv4);
-    case 2: return pick_nq<2>(nq, nv4);
-    case 3: return pick_nq<3>(nq, nv4);
-    case 4: return pick_nq<4>(nq, nv4);
-    case 6: return pick_nq<6>(nq, nv4);
-    case 8: return pick_nq<8>(nq, nv4);
+    case 1: return pick_qk<1>(qk, vd);
+    case 2: return pick_qk<2>(qk, vd);
+    case 3: return pick_qk<3>(qk, vd);
+    case 4: return pick_qk<4>(qk, vd);
+    case 6: return pick_qk<6>(qk, vd);
+    case 8: return pick_qk<8>(qk, vd);
     default: return nullptr;
     }
 }
@@ -486,36 +551,34 @@ int nd_attend_step_i8(nd_ctx *ctx, const nd_kv_geom *g, const void *kv, size_t k
     ND_REQUIRE((reinterpret_cast<uintptr_t>(kv) & 255) == 0 && kv_stride % 256 == 0,
                "kv blocks must be 256-byte aligned");
     const int rep = g->num_heads / g->num_kv_heads;
-    const int nq = g->qk_head_dim / 16, nv4 = g->v_head_dim / 4;
-    AttnFn fn = pick_attn(rep, nq, nv4);
+    AttnFn fn = pick_attn(rep, g->qk_head_dim, g->v_head_dim);
     ND_REQUIRE(fn, "no attention kernel for repeat %d, qk %d, v %d", rep, g->qk_head_dim,
                g->v_head_dim);
-    // Chunk: the largest that keeps the partial buffer within 32 KB and still
-    // gives the launch a few thousand workgroups.
-    const int span = g->cap;
-    int chunk = 512;
-    while (chunk > 64 && size_t(rep) * chunk * nq > 8192) chunk /= 2;
-    while (chunk > 64 && count * size_t(g->num_kv_heads) * ((span + chunk - 1) / chunk) < 2048)
-        chunk /= 2;
-    const int nchunks = (span + chunk - 1) / chunk;
-    ND_REQUIRE(nchunks <= 65535, "span too long");
+    // Split each span across blocks only when (query, kv head) pairs cannot
+    // give every CU a few blocks; the split partials merge in a second pass.
+    const size_t pairs = count * size_t(g->num_kv_heads);
+    const size_t want = size_t(ctx->num_cus > 0 ? ctx->num_cus : 256) * 4;
+    const int chunk = rep <= 2 ? 512 : 256;
+    const size_t max_chunks = (size_t(g->cap) + chunk - 1) / chunk;
+    size_t splits = pairs >= want ? 1 : (want + pairs - 1) / pairs;
+    if (splits > max_chunks) splits = max_chunks;
+    if (splits > 65535) splits = 65535;
     float *po = nullptr, *pml = nullptr;
-    if (nchunks > 1) {
+    if (splits > 1) {
         void *wsp = nullptr;
-        const size_t n_o = count * size_t(g->num_heads) * nchunks * g->v_head_dim;
-        const size_t n_ml = count * size_t(g->num_heads) * nchunks * 2;
+        const size_t n_o = count * size_t(g->num_heads) * splits * g->v_head_dim;
+        const size_t n_ml = count * size_t(g->num_heads) * splits * 2;
         if (int rc = nd::workspace(ctx, (n_o + n_ml) * sizeof(float), &wsp)) return rc;
         po = static_cast<float *>(wsp);
         pml = po + n_o;
     }
-    const size_t smem = attn_smem_bytes(rep, nq, chunk);
-    dim3 grid(unsigned(nchunks), unsigned(g->num_kv_heads), unsigned(count));
-    fn(grid, smem, ctx->stream, make_geom(g), static_cast<const uint8_t *>(kv), kv_stride, lo, hi, q,
-       scale, quant_query, chunk, nchunks, out, po, pml);
+    dim3 grid(unsigned(splits), unsigned(g->num_kv_heads), unsigned(count));
+    fn(grid, ctx->stream, make_geom(g), static_cast<const uint8_t *>(kv), kv_stride, lo, hi, q,
+       scale, quant_query, int(splits), out, po, pml);
     if (int rc = nd::check_launch("attn_i8")) return rc;
-    if (nchunks > 1) {
+    if (splits > 1) {
         hipLaunchKernelGGL(attn_combine_kernel, dim3(unsigned(g->num_heads), unsigned(count)),
-                           dim3(64), 0, ctx->stream, make_geom(g), nchunks, po, pml, out);
+                           dim3(64), 0, ctx->stream, make_geom(g), int(splits), po, pml, out);
         return nd::check_launch("attn_combine");
     }
     return ND_OK;
