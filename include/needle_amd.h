@@ -119,9 +119,22 @@ int nd_cq_matmul_rows_prepared(nd_ctx *ctx, const nd_cq *w, const float *xh,
                                size_t batch, size_t row_start, size_t rows,
                                float *y);
 
+/* As nd_cq_matvec_rows_prepared / nd_cq_matmul_rows_prepared, summing in
+ * the reference's order (eight lane accumulators per 128-group, element e
+ * into lane e % 8, lanes added 0..7, group totals added in group order), so
+ * the outputs are bit-identical to CqWeight::matvec_rows_prepared
+ * (cq.rs:721-757, 838-873) and matmul_rows_prepared (cq.rs:632-679,
+ * 879-906).  The Needle-3 forward uses these. */
+int nd_cq_matvec_rows_exact(nd_ctx *ctx, const nd_cq *w, const float *xh,
+                            size_t row_start, size_t rows, float *y);
+int nd_cq_matmul_rows_exact(nd_ctx *ctx, const nd_cq *w, const float *xh,
+                            size_t batch, size_t row_start, size_t rows,
+                            float *y);
+
 /* out[i] = dequantized row rows[i] (in_feat floats each); rows is a device
- * int32 array of n row indices.  Replaces CqWeight::dequantize_row
- * (cq.rs:763-779), gathered. */
+ * int32 array of n row indices, a negative index giving a row of zeros (a
+ * masked Engram fetch, v3/model.rs:172-183).  Replaces
+ * CqWeight::dequantize_row (cq.rs:763-779), gathered. */
 int nd_cq_dequantize_rows(nd_ctx *ctx, const nd_cq *w, const int32_t *rows,
                           size_t n, float *out);
 
@@ -185,6 +198,75 @@ int nd_attend_step_i8(nd_ctx *ctx, const nd_kv_geom *g, const void *kv,
                       size_t kv_stride, size_t count, const int32_t *lo,
                       const int32_t *hi, const float *q, float scale,
                       int quant_query, float *out);
+
+/* As nd_attend_step_i8, bit-identical to attend_step over the int8 view
+ * (attention.rs:327-377): each score is one dot chain over the head dim,
+ * scaled by the key scale and then `scale`; the softmax sum and every
+ * output column are single chains over the span in position order; exp is
+ * libm's expf algorithm.  Also requires cap <= 16384 (one span's scores sit
+ * in LDS).  The Needle-3 forward uses this. */
+int nd_attend_step_i8_exact(nd_ctx *ctx, const nd_kv_geom *g, const void *kv,
+                            size_t kv_stride, size_t count, const int32_t *lo,
+                            const int32_t *hi, const float *q, float scale,
+                            int quant_query, float *out);
+
+/* ---- Needle-3 forward on the device (v3/model.rs, v3/cache.rs) ----------- */
+
+/* V3Config (crates/needle-core/src/v3/config.rs:45-77), Engram flattened. */
+typedef struct nd_v3_cfg {
+    int32_t vocab_size, out_vocab, d_model, num_heads, num_kv_heads, num_layers;
+    int32_t qk_head_dim, v_head_dim, max_seq_len, hada_n, mhc_lanes;
+    float rope_theta;
+    int32_t sliding_window, n_global, global_layers[64], qkv_conv_taps;
+    int32_t n_orders, orders[8], e_heads, e_slots, e_sub_dim, n_sites, sites[64];
+    int32_t e_conv_taps, e_conv_dilation, e_seed_heads;
+} nd_v3_cfg;
+
+enum { ND_REC_F32 = 1, ND_REC_CQ = 3 };
+
+/* One container record (host memory): a Cactus-Quants blob (kind 3, shape
+ * out x in, group, bits) or f32 data (kind 1; `in` is the second dimension
+ * of a 2-D tensor, else 1). */
+typedef struct nd_v3_record {
+    int32_t kind;
+    const void *data;
+    size_t len, out, in, group, bits;
+} nd_v3_record;
+
+typedef struct nd_v3_model nd_v3_model;
+typedef struct nd_v3_batch nd_v3_batch;
+
+/* Upload a model from records in the canonical container order walked by
+ * V3Layout::derive (crates/needle-infer/src/v3.rs:236-330) and bound as in
+ * model_from_cact (v3.rs:395-482).  `codebook` (host) is the 28-float
+ * cb2|cb3|cb4 header block.  ND_ERR_ARG names the first record that does not
+ * fit the geometry. */
+int nd_v3_model_create(nd_ctx *ctx, const nd_v3_cfg *cfg, const float *codebook,
+                       size_t codebook_len, const nd_v3_record *recs, size_t n,
+                       nd_v3_model **out);
+void nd_v3_model_free(nd_v3_model *m);
+/* Rows of the tied head scored per position (V3Config::logit_rows). */
+size_t nd_v3_logit_rows(const nd_v3_model *m);
+
+/* `sessions` decode sessions with int8 KV caches (V3Cache::with_precision
+ * (.., KvPrecision::Int8), cache.rs:177-238) able to hold `max_len`
+ * positions each; `hint` sizes the reference's logical ring growth. */
+int nd_v3_batch_create(nd_ctx *ctx, const nd_v3_model *m, size_t sessions, size_t max_len,
+                       size_t hint, nd_v3_batch **out);
+void nd_v3_batch_free(nd_v3_batch *b);
+/* Each session's next write position (V3Cache::pos). */
+int nd_v3_positions(const nd_v3_batch *b, int32_t *pos);
+
+/* One decode position for every session: tokens[i] (host) is fed to
+ * session i, exactly as V3Model::decode_step (v3/model.rs:150-375) with an
+ * int8 cache.  When `next` (host, per session) is given it receives the
+ * greedy argmax of the logits, first maximum winning
+ * (needle-infer/src/v3_engine.rs:410-420); when `logits` (device,
+ * [sessions][logit_rows]) is given the logits are copied there.  A prompt is
+ * prefilled by stepping it: the reference's batched prefill is
+ * bit-identical to stepping (needle-infer/tests/v3_kv_int8.rs:190-302). */
+int nd_v3_step(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *tokens,
+               int32_t *next, float *logits);
 
 #ifdef __cplusplus
 }

@@ -21,25 +21,12 @@
 //                decoded to fp32 (level * norm) in LDS, fp32 MFMA 16x16x4.
 //   cq_dequant   dequantize_row (cq.rs:763-779), bit-identical.
 #include "nd_internal.h"
+#include "nd_cq_internal.h"
 
 #include <cmath>
 #include <cstring>
 #include <new>
 #include <vector>
-
-struct nd_cq {
-    int device = 0;
-    size_t out_feat = 0, in_feat = 0, in_padded = 0, group = 0, num_groups = 0;
-    size_t row_bytes = 0, per_byte = 0;
-    uint8_t bits = 0;
-    int n_levels = 0;
-    float levels[16] = {};
-    float inv_sqrt_group = 1.0f;  // 1 / sqrtf(group), as hadamard.rs:51-52
-    uint8_t *packed = nullptr;    // device [out][row_bytes] (+16 bytes slack)
-    float *norms = nullptr;       // device [out][num_groups]
-    float *lut = nullptr;         // device [256][per_byte] (empty for 3-bit)
-    float *lv = nullptr;          // device levels[16]
-};
 
 namespace {
 
@@ -371,7 +358,15 @@ __global__ __launch_bounds__(512) void cq_dequant_kernel(
     const int t = threadIdx.x;
     if (t < 16) lvs[t] = lv[t];
     int o = rows_idx[i];
-    o = o < 0 ? 0 : (o >= out_feat ? out_feat - 1 : o);
+    float *dst = out + i * size_t(in_feat);
+    if (o < 0) {  // a masked row (e.g. an n-gram without enough history) reads as zeros
+        for (int k = t; k < group; k += blockDim.x) {
+            const int col = g * group + k;
+            if (col < in_feat) dst[col] = 0.0f;
+        }
+        return;
+    }
+    o = o >= out_feat ? out_feat - 1 : o;
     const uint8_t *row = packed + size_t(o) * row_bytes;
     const float norm = norms[size_t(o) * num_groups + g];
     __syncthreads();
@@ -388,7 +383,6 @@ __global__ __launch_bounds__(512) void cq_dequant_kernel(
         }
         __syncthreads();
     }
-    float *dst = out + i * size_t(in_feat);
     for (int k = t; k < group; k += blockDim.x) {
         const int col = g * group + k;
         if (col < in_feat) dst[col] = buf[k] * inv;

@@ -13,48 +13,15 @@
 // span is split across workgroups, with a merge pass, only when there are
 // too few (query, kv head) pairs to fill the GPU (batch-1 decode).
 #include "nd_internal.h"
+#include "nd_kv_internal.h"
 
 #include <cmath>
 
 namespace {
 
+using namespace ndkv;
+
 constexpr int kThreads = 256;
-constexpr int kMaxRep = 8;
-constexpr int kMaxDim = 256;
-
-__device__ inline float wave_max(float v)
-{
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
-}
-
-__device__ inline float wave_sum(float v)
-{
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-
-// absmax of a head vector read by one wave; returns (scale, inv) exactly as
-// quant_scale (cache.rs:80-91).
-__device__ inline void quant_scale_wave(const float *x, int n, float &scale, float &inv)
-{
-    const int lane = threadIdx.x & 63;
-    float a = 0.0f;
-    for (int i = lane; i < n; i += 64) {
-        const float v = x[i];
-        const float av = v < 0.0f ? -v : v;
-        if (av > a) a = av;
-    }
-    const float absmax = wave_max(a);
-    scale = absmax > 0.0f ? absmax / 127.0f : 1.0f;
-    inv = 1.0f / scale;
-}
-
-__device__ inline float quant_code(float x, float inv)
-{
-    const float r = roundf(x * inv);
-    return r < -128.0f ? -128.0f : (r > 127.0f ? 127.0f : r);
-}
 
 // fake_quant_vec over rows (cache.rs:68-73); one wave per row.
 __global__ __launch_bounds__(kThreads) void fake_quant_kernel(float *__restrict__ x, size_t rows,
@@ -83,10 +50,6 @@ __global__ __launch_bounds__(kThreads) void quantize_rows_kernel(const float *__
     if ((threadIdx.x & 63) == 0) scales[r] = scale;
 }
 
-struct Geom {
-    int H, KVH, QK, VD, cap;
-    size_t v_off, ks_off, vs_off;
-};
 
 // write_kv (cache.rs:346-379): wave w of block (i, h) quantises K (w=0) or
 // V (w=1) of kv head h for row i into slot pos[i] % cap.
@@ -407,35 +370,7 @@ __global__ __launch_bounds__(kThreads) void attn_combine_kernel(Geom g, int nchu
     }
 }
 
-Geom make_geom(const nd_kv_geom *k)
-{
-    Geom g;
-    g.H = k->num_heads;
-    g.KVH = k->num_kv_heads;
-    g.QK = k->qk_head_dim;
-    g.VD = k->v_head_dim;
-    g.cap = k->cap;
-    g.v_off = nd_kv_v_offset(k);
-    g.ks_off = nd_kv_ks_offset(k);
-    g.vs_off = nd_kv_vs_offset(k);
-    return g;
-}
 
-int check_geom(const nd_kv_geom *g)
-{
-    ND_REQUIRE(g, "null geometry");
-    ND_REQUIRE(g->num_kv_heads > 0 && g->num_heads > 0 && g->num_heads % g->num_kv_heads == 0,
-               "num_heads %d must be a positive multiple of num_kv_heads %d", g->num_heads,
-               g->num_kv_heads);
-    ND_REQUIRE(g->num_heads / g->num_kv_heads <= kMaxRep, "kv repeat %d above %d",
-               g->num_heads / g->num_kv_heads, kMaxRep);
-    ND_REQUIRE(g->qk_head_dim > 0 && g->qk_head_dim % 16 == 0 && g->qk_head_dim <= kMaxDim,
-               "qk_head_dim %d must be a multiple of 16 in 16..%d", g->qk_head_dim, kMaxDim);
-    ND_REQUIRE(g->v_head_dim > 0 && g->v_head_dim % 16 == 0 && g->v_head_dim <= kMaxDim,
-               "v_head_dim %d must be a multiple of 16 in 16..%d", g->v_head_dim, kMaxDim);
-    ND_REQUIRE(g->cap > 0 && g->cap <= (1 << 24), "cap %d out of range", g->cap);
-    return ND_OK;
-}
 
 template <int REP, int QK>
 void launch_attn(dim3 grid, hipStream_t s, Geom g, const uint8_t *kv, size_t stride,

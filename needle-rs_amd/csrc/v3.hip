@@ -1,0 +1,1163 @@
+// Needle-3 forward on the device: the caller of the codebook projections and
+// the int8 KV cache (crates/needle-core/src/v3/model.rs:150-375,
+// decode_step), batched over sessions.
+//
+// The forward reproduces the reference's result bits.  Every projection is
+// the reference-order Cactus-Quants matvec/matmul and the attention the
+// reference-order attend_step (ref_order.hip); the int8 KV append is
+// kv.hip's bit-exact quantiser.  The per-position glue is a handful of fused
+// kernels, one workgroup per session:
+//   mhc_in     mHC gate + mix down, Engram gate, ZCRMSNorm   (mhc.rs:80-103,
+//              engram.rs:111-132, norm.rs:23-30)
+//   qkv_post   causal conv step over q/k/v with the retained tails, then
+//              ZCRMSNorm + RoPE on q and k                    (cache.rs:401-438,
+//              attention.rs:108-150)
+//   gate       attn *= sigmoid(gate)                          (model.rs:309-312)
+//   post_attn  post-norm, gated residual, pre-MLP norm        (model.rs:313-321)
+//   hada_mlp   HadamardMLP: low-rank conditioning, three Kronecker stages of
+//              32x32 factors, permutations, silu; residual and block delta
+//              (v3/kernels.rs:119-180)
+//   mhc_out    post/res gates, 4x4 Sinkhorn, lane scatter    (mhc.rs:111-152)
+//   engram     dilated value conv step with its tail         (cache.rs:445-482)
+//   final      lane mean + final norm; argmax (first maximum wins)
+// This file is built without FP contraction, so elementwise arithmetic
+// rounds as rustc's (which never fuses a*b+c); every reduction the reference
+// folds sequentially (norms, the Engram gate, the conditioning projection,
+// lane sums) is one sequential chain on one thread, in the reference's
+// index order; exp and log are libm's algorithms (nd_libm.h).
+#include "nd_internal.h"
+#include "nd_libm.h"
+
+#include <cmath>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+namespace {
+
+constexpr int kT = 256;
+
+__device__ inline float sigmoidf_(float x) { return nd_sigmoidf(x); }
+
+// sum_i a[i] * b[i] for i = 0..n-1 as one left-to-right chain (a sequential
+// fold, as the reference's loops and iterator sums); run by one thread.
+__device__ inline float dot_chain(const float *a, const float *b, int n)
+{
+    float s = 0.0f;
+    int i = 0;
+    if (((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15) == 0) {
+        for (; i + 8 <= n; i += 8) {
+            const float4 a0 = *reinterpret_cast<const float4 *>(a + i);
+            const float4 a1 = *reinterpret_cast<const float4 *>(a + i + 4);
+            const float4 b0 = *reinterpret_cast<const float4 *>(b + i);
+            const float4 b1 = *reinterpret_cast<const float4 *>(b + i + 4);
+            s += a0.x * b0.x;
+            s += a0.y * b0.y;
+            s += a0.z * b0.z;
+            s += a0.w * b0.w;
+            s += a1.x * b1.x;
+            s += a1.y * b1.y;
+            s += a1.z * b1.z;
+            s += a1.w * b1.w;
+        }
+    }
+    for (; i < n; ++i) s += a[i] * b[i];
+    return s;
+}
+
+__device__ inline float sumsq_chain(const float *x, int n) { return dot_chain(x, x, n); }
+
+// ---- embedding broadcast: lanes[b][l][c] = emb[b][c] * scale ---------------
+__global__ void k_embed(const float *__restrict__ emb, float *__restrict__ lanes, float scale,
+                        int n, int d)
+{
+    const size_t b = blockIdx.y;
+    for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < d; c += gridDim.x * blockDim.x) {
+        const float e = emb[b * d + c] * scale;
+        for (int l = 0; l < n; ++l) lanes[(b * n + l) * d + c] = e;
+    }
+}
+
+// ---- rms_unit over a row (kernels.rs:33-41) ----------------------------------
+__global__ __launch_bounds__(kT) void k_rms_unit(const float *__restrict__ x, float *__restrict__ out,
+                                                int n)
+{
+    __shared__ float tot;
+    const size_t b = blockIdx.x;
+    if (threadIdx.x == 0) tot = sumsq_chain(x + b * n, n);
+    __syncthreads();
+    const float inv = 1.0f / sqrtf(tot / float(n) + 1e-6f);
+    for (int i = threadIdx.x; i < n; i += kT) out[b * n + i] = x[b * n + i] * inv;
+}
+
+// ---- Engram value conv step (cache.rs:445-482) -------------------------------
+__global__ void k_engram_conv(float *__restrict__ ev, const float *__restrict__ taps,
+                              float *__restrict__ tail, const int32_t *__restrict__ pos, int taps_n,
+                              int dil, int max_order, int reach, int d)
+{
+    const size_t b = blockIdx.y;
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= d) return;
+    const int p = pos[b];
+    float *tb = tail + b * size_t(reach) * d;
+    const float raw = ev[b * d + c];
+    float acc = 0.0f;
+    for (int j = 0; j < taps_n; ++j) {
+        const int back = j * dil;
+        if (back > p || p < j * max_order) continue;
+        const float val = j == 0 ? raw : tb[size_t(reach - back) * d + c];
+        acc += taps[j * d + c] * val;
+    }
+    for (int r = 0; r + 1 < reach; ++r) tb[size_t(r) * d + c] = tb[size_t(r + 1) * d + c];
+    if (reach > 0) tb[size_t(reach - 1) * d + c] = raw;
+    ev[b * d + c] = acc;
+}
+
+// ---- mHC mix down + Engram gate + ZCRMSNorm ----------------------------------
+struct MhcIn {
+    const float *hraw;   // [B][n]  nx . phi_pre rows of this layer
+    const float *lanes;  // [B][n][d]
+    const float *b_pre;  // [n] this layer's slice
+    float a_pre;
+    int layer, n, d;
+    const float *ek, *ev;  // [B][d] this layer's Engram site, or null
+    const float *norm_in;  // [d]
+    float *u, *bx, *h;     // [B][d]
+};
+
+__global__ __launch_bounds__(kT) void k_mhc_in(MhcIn a)
+{
+    __shared__ float hp[16], tot[4];
+    __shared__ __align__(16) float us[1024], bxs[1024];
+    const size_t b = blockIdx.x;
+    const int d = a.d, n = a.n;
+    if (threadIdx.x < n) {
+        const int lane = threadIdx.x;
+        const float off = lane == a.layer % n ? 4.0f : -4.0f;
+        hp[lane] = sigmoidf_(a.a_pre * a.hraw[b * n + lane] + a.b_pre[lane] + off);
+    }
+    __syncthreads();
+    const float *lb = a.lanes + b * size_t(n) * d;
+    for (int c = threadIdx.x; c < d; c += kT) {
+        float acc = 0.0f;
+        for (int l = 0; l < n; ++l) acc += hp[l] * lb[size_t(l) * d + c];
+        us[c] = acc;
+        a.u[b * d + c] = acc;
+    }
+    __syncthreads();
+    if (a.ek) {
+        // engram.rs:111-132: three sequential sums, one per wave
+        const float *ek = a.ek + b * d;
+        if (threadIdx.x == 0) tot[0] = sumsq_chain(us, d);
+        if (threadIdx.x == 64) tot[1] = sumsq_chain(ek, d);
+        if (threadIdx.x == 128) tot[2] = dot_chain(us, ek, d);
+        __syncthreads();
+        const float ux = 1.0f / sqrtf(tot[0] / float(d) + 1e-6f);
+        const float uk = 1.0f / sqrtf(tot[1] / float(d) + 1e-6f);
+        const float alpha = sigmoidf_(tot[2] * ux * uk / sqrtf(float(d)));
+        for (int c = threadIdx.x; c < d; c += kT) bxs[c] = us[c] + alpha * a.ev[b * d + c];
+    } else {
+        for (int c = threadIdx.x; c < d; c += kT) bxs[c] = us[c];
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) tot[3] = sumsq_chain(bxs, d);
+    __syncthreads();
+    const float inv = 1.0f / sqrtf(tot[3] / float(d) + 1e-6f);
+    for (int c = threadIdx.x; c < d; c += kT) {
+        a.bx[b * d + c] = bxs[c];
+        a.h[b * d + c] = (1.0f + a.norm_in[c]) * bxs[c] * inv;
+    }
+}
+
+// ---- conv step over q/k/v, then ZCRMSNorm + RoPE on q and k -------------------
+struct QkvPost {
+    float *q, *k, *v;                     // [B][dim]
+    float *qt, *kt, *vt;                  // tails [B][taps-1][dim]
+    const float *q_taps, *k_taps, *v_taps;  // [taps][dim]
+    const float *q_norm, *k_norm;          // [hd]
+    const float *rope;                     // [B][2][hd/2]: cos then sin
+    const int32_t *pos;
+    int qd, kd, vd, taps, H, KVH, hd;
+};
+
+__device__ inline void conv_one(float *x, float *tail, const float *taps, int dim, int c, int T,
+                                int p)
+{
+    const float raw = x[c];
+    float acc = taps[c] * raw;
+    for (int j = 1; j < T; ++j) {
+        if (j > p) break;
+        acc += taps[j * dim + c] * tail[size_t(T - 1 - j) * dim + c];
+    }
+    for (int r = 0; r + 2 < T; ++r) tail[size_t(r) * dim + c] = tail[size_t(r + 1) * dim + c];
+    if (T > 1) tail[size_t(T - 2) * dim + c] = raw;
+    x[c] = acc;
+}
+
+__global__ __launch_bounds__(kT) void k_qkv_post(QkvPost a)
+{
+    const size_t b = blockIdx.x;
+    const int p = a.pos[b], T = a.taps;
+    if (T > 0) {
+        for (int c = threadIdx.x; c < a.qd + a.kd + a.vd; c += kT) {
+            if (c < a.qd)
+                conv_one(a.q + b * a.qd, a.qt + b * size_t(T - 1) * a.qd, a.q_taps, a.qd, c, T, p);
+            else if (c < a.qd + a.kd)
+                conv_one(a.k + b * a.kd, a.kt + b * size_t(T - 1) * a.kd, a.k_taps, a.kd, c - a.qd,
+                         T, p);
+            else
+                conv_one(a.v + b * a.vd, a.vt + b * size_t(T - 1) * a.vd, a.v_taps, a.vd,
+                         c - a.qd - a.kd, T, p);
+        }
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = a.hd / 2;
+    const float *cs = a.rope + b * 2 * half, *sn = cs + half;
+    for (int hh = wave; hh < a.H + a.KVH; hh += kT / 64) {
+        float *x = hh < a.H ? a.q + b * a.qd + hh * a.hd : a.k + b * a.kd + (hh - a.H) * a.hd;
+        const float *sc = hh < a.H ? a.q_norm : a.k_norm;
+        float sq = lane == 0 ? sumsq_chain(x, a.hd) : 0.0f;
+        sq = __shfl(sq, 0, 64);
+        const float rms = sqrtf(sq / float(a.hd) + 1e-6f);
+        for (int i = lane; i < half; i += 64) {
+            const float x1 = (1.0f + sc[i]) * x[i] / rms;
+            const float x2 = (1.0f + sc[half + i]) * x[half + i] / rms;
+            const float c = cs[i], s = sn[i];
+            x[i] = x1 * c - x2 * s;
+            x[half + i] = x2 * c + x1 * s;
+        }
+    }
+}
+
+__global__ void k_gate_mul(float *__restrict__ attn, const float *__restrict__ gate, size_t n)
+{
+    const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) attn[i] *= sigmoidf_(gate[i]);
+}
+
+// ---- post-norm, gated residual, pre-MLP norm ---------------------------------
+__global__ __launch_bounds__(kT) void k_post_attn(const float *__restrict__ proj, float *__restrict__ bx,
+                                                 const float *__restrict__ post_norm,
+                                                 const float *__restrict__ pre_hada, float agate,
+                                                 float *__restrict__ p2, int d)
+{
+    __shared__ float tot[2];
+    __shared__ __align__(16) float nbs[1024];
+    const size_t b = blockIdx.x;
+    if (threadIdx.x == 0) tot[0] = sumsq_chain(proj + b * d, d);
+    __syncthreads();
+    float inv = 1.0f / sqrtf(tot[0] / float(d) + 1e-6f);
+    for (int c = threadIdx.x; c < d; c += kT) {
+        const float pn = (1.0f + post_norm[c]) * proj[b * d + c] * inv;
+        const float nb = bx[b * d + c] + agate * pn;
+        bx[b * d + c] = nb;
+        nbs[c] = nb;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) tot[1] = sumsq_chain(nbs, d);
+    __syncthreads();
+    inv = 1.0f / sqrtf(tot[1] / float(d) + 1e-6f);
+    for (int c = threadIdx.x; c < d; c += kT) p2[b * d + c] = (1.0f + pre_hada[c]) * nbs[c] * inv;
+}
+
+// ---- HadamardMLP (v3/kernels.rs:119-180), hada_n = 1024 = 32 x 32 -----------
+struct HadaArgs {
+    const float *p2;  // [B][d] the normed block state
+    const float *u;   // [B][d]
+    float *bx, *y;    // [B][d]
+    const float *d1, *d2, *b2, *d3, *d4;  // [1024]
+    const float *w1a, *w1b, *w2a, *w2b, *w3a, *w3b;  // [32*32]
+    const float *cond_v;  // [d][rank]
+    const float *cond_u;  // [rank][1024]
+    const int32_t *p1, *p2perm;  // [1024]
+    int d, rank;
+};
+
+// out[k][l] = sum_j (sum_i z[i][j] a[i][k]) b[j][l], i and j ascending, zero
+// factors skipped as kron_apply (v3/kernels.rs:41-81) skips them.
+__device__ inline void kron32(const float *z, const float *a, const float *bm, float *t, float *out)
+{
+    const int tid = threadIdx.x;  // 1024 threads: (row, col) = (tid / 32, tid % 32)
+    const int r = tid >> 5, c = tid & 31;
+    {
+        float acc = 0.0f;
+        for (int i = 0; i < 32; ++i) {
+            const float aik = a[i * 32 + r];
+            if (aik == 0.0f) continue;
+            acc += z[i * 32 + c] * aik;
+        }
+        t[r * 32 + c] = acc;
+    }
+    __syncthreads();
+    {
+        float acc = 0.0f;
+        for (int j = 0; j < 32; ++j) {
+            const float tkj = t[r * 32 + j];
+            if (tkj == 0.0f) continue;
+            acc += tkj * bm[j * 32 + c];
+        }
+        out[r * 32 + c] = acc;
+    }
+    __syncthreads();
+}
+
+__global__ __launch_bounds__(1024) void k_hada_mlp(HadaArgs a)
+{
+    __shared__ __align__(16) float z[1024], buf[1024], t[1024], fa[1024], fb[1024], cond[1024];
+    __shared__ float proj[64];
+    const size_t b = blockIdx.x;
+    const int tid = threadIdx.x, d = a.d, r = a.rank;
+    const float xv = tid < d ? a.p2[b * d + tid] : 0.0f;
+    // cond = 1 + softmax(x . cond_v) . cond_u; projection j is one chain
+    // over the model dim, run by lane 0 of wave j % 16
+    buf[tid] = xv;
+    __syncthreads();
+    if ((tid & 63) == 0)
+        for (int j = tid >> 6; j < r; j += 16) {
+            float acc = 0.0f;
+            for (int i = 0; i < d; ++i) acc += buf[i] * a.cond_v[i * r + j];
+            proj[j] = acc;
+        }
+    __syncthreads();
+    if (tid == 0) {
+        float mx = -INFINITY;
+        for (int j = 0; j < r; ++j) mx = fmaxf(mx, proj[j]);
+        float sum = 0.0f;
+        for (int j = 0; j < r; ++j) {
+            proj[j] = nd_expf(proj[j] - mx);
+            sum += proj[j];
+        }
+        for (int j = 0; j < r; ++j) proj[j] /= sum;
+    }
+    __syncthreads();
+    {
+        float c = 1.0f;
+        for (int j = 0; j < r; ++j) {
+            if (proj[j] == 0.0f) continue;
+            c += proj[j] * a.cond_u[j * 1024 + tid];
+        }
+        cond[tid] = c;
+    }
+    z[tid] = xv * a.d1[tid];
+    fa[tid] = a.w1a[tid];
+    fb[tid] = a.w1b[tid];
+    __syncthreads();
+    kron32(z, fa, fb, t, buf);
+    z[tid] = buf[a.p1[tid]];
+    fa[tid] = a.w2a[tid];
+    fb[tid] = a.w2b[tid];
+    __syncthreads();
+    {
+        const float zz = a.d2[tid] * cond[tid] * z[tid] + a.b2[tid];
+        z[tid] = zz * sigmoidf_(zz);
+    }
+    __syncthreads();
+    kron32(z, fa, fb, t, buf);
+    z[tid] = buf[a.p2perm[tid]] * a.d3[tid];
+    fa[tid] = a.w3a[tid];
+    fb[tid] = a.w3b[tid];
+    __syncthreads();
+    kron32(z, fa, fb, t, buf);
+    if (tid < d) {
+        const float o = buf[tid] * a.d4[tid];
+        const float nb = a.bx[b * d + tid] + o;
+        a.bx[b * d + tid] = nb;
+        a.y[b * d + tid] = nb - a.u[b * d + tid];
+    }
+}
+
+// ---- mHC scatter up (mhc.rs:111-152) ------------------------------------------
+struct MhcOut {
+    float *lanes;              // [B][n][d]
+    const float *hpost_raw;    // [B][n]
+    const float *hres_raw;     // [B][n*n]
+    const float *y;            // [B][d]
+    const float *b_post;       // [n]
+    const float *b_res;        // [n*n]
+    float a_post, a_res;
+    int layer, n, d;
+};
+
+__device__ inline float lse_row(const float *x, int n)
+{
+    float mx = -INFINITY;
+    for (int i = 0; i < n; ++i) mx = fmaxf(mx, x[i]);
+    if (!(mx == mx) || mx == INFINITY || mx == -INFINITY) return mx;
+    float s = 0.0f;
+    for (int i = 0; i < n; ++i) s += nd_expf(x[i] - mx);
+    return mx + nd_logf(s);
+}
+
+__global__ __launch_bounds__(kT) void k_mhc_out(MhcOut a)
+{
+    __shared__ float hp[16], hr[256];
+    const size_t b = blockIdx.x;
+    const int n = a.n, d = a.d;
+    if (threadIdx.x == 0) {
+        for (int l = 0; l < n; ++l) {
+            const float off = l == a.layer % n ? 0.0f : -4.0f;
+            hp[l] = 2.0f * sigmoidf_(a.a_post * a.hpost_raw[b * n + l] + a.b_post[l] + off);
+        }
+        for (int x = 0; x < n * n; ++x) hr[x] = a.a_res * a.hres_raw[b * n * n + x] + a.b_res[x];
+        // sinkhorn (kernels.rs:48-74)
+        for (int it = 0; it < 20; ++it) {
+            for (int i = 0; i < n; ++i) {
+                const float lse = lse_row(hr + i * n, n);
+                for (int j = 0; j < n; ++j) hr[i * n + j] -= lse;
+            }
+            for (int j = 0; j < n; ++j) {
+                float mx = -INFINITY;
+                for (int i = 0; i < n; ++i) mx = fmaxf(mx, hr[i * n + j]);
+                float s = 0.0f;
+                for (int i = 0; i < n; ++i) s += nd_expf(hr[i * n + j] - mx);
+                const float lse = mx + nd_logf(s);
+                for (int i = 0; i < n; ++i) hr[i * n + j] -= lse;
+            }
+        }
+        for (int x = 0; x < n * n; ++x) hr[x] = nd_expf(hr[x]);
+    }
+    __syncthreads();
+    float *lb = a.lanes + b * size_t(n) * d;
+    for (int c = threadIdx.x; c < d; c += kT) {
+        float old[16];
+        for (int j = 0; j < n; ++j) old[j] = lb[size_t(j) * d + c];
+        const float yc = a.y[b * d + c];
+        for (int i = 0; i < n; ++i) {
+            float acc = 0.0f;
+            for (int j = 0; j < n; ++j) acc += hr[i * n + j] * old[j];
+            lb[size_t(i) * d + c] = acc + hp[i] * yc;
+        }
+    }
+}
+
+// ---- lane mean + final norm (model.rs:360-368) ---------------------------------
+__global__ __launch_bounds__(kT) void k_final(const float *__restrict__ lanes,
+                                             const float *__restrict__ final_norm,
+                                             float *__restrict__ x, int n, int d)
+{
+    __shared__ float tot;
+    __shared__ __align__(16) float ms[1024];
+    const size_t b = blockIdx.x;
+    const float *lb = lanes + b * size_t(n) * d;
+    for (int c = threadIdx.x; c < d; c += kT) {
+        float acc = 0.0f;
+        for (int l = 0; l < n; ++l) acc += lb[size_t(l) * d + c];
+        ms[c] = acc / float(n);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) tot = sumsq_chain(ms, d);
+    __syncthreads();
+    const float inv = 1.0f / sqrtf(tot / float(d) + 1e-6f);
+    for (int c = threadIdx.x; c < d; c += kT) x[b * d + c] = (1.0f + final_norm[c]) * ms[c] * inv;
+}
+
+// ---- greedy argmax, first maximum wins (v3_engine.rs:410-420) -----------------
+__global__ __launch_bounds__(kT) void k_argmax(const float *__restrict__ logits, int rows,
+                                              int32_t *__restrict__ next)
+{
+    __shared__ float sv[kT];
+    __shared__ int si[kT];
+    const size_t b = blockIdx.x;
+    float best = -INFINITY;
+    int bi = 0;
+    for (int i = threadIdx.x; i < rows; i += kT) {
+        const float v = logits[b * rows + i];
+        if (v > best) {
+            best = v;
+            bi = i;
+        }
+    }
+    sv[threadIdx.x] = best;
+    si[threadIdx.x] = bi;
+    __syncthreads();
+    for (int s = kT / 2; s > 0; s >>= 1) {
+        if (threadIdx.x < s) {
+            const float ov = sv[threadIdx.x + s];
+            const int oi = si[threadIdx.x + s];
+            if (ov > sv[threadIdx.x] || (ov == sv[threadIdx.x] && oi < si[threadIdx.x])) {
+                sv[threadIdx.x] = ov;
+                si[threadIdx.x] = oi;
+            }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) next[b] = si[0];
+}
+
+// ---------------------------------------------------------------------------
+// Host side.
+// ---------------------------------------------------------------------------
+
+struct Layer {
+    float *norm_in = nullptr;
+    nd_cq *q = nullptr, *k = nullptr, *v = nullptr, *gate = nullptr, *out = nullptr;
+    float *q_taps = nullptr, *k_taps = nullptr, *v_taps = nullptr, *q_norm = nullptr,
+          *k_norm = nullptr;
+    float *post_norm = nullptr, attn_gate = 0.0f, *pre_hada = nullptr;
+    float *d1 = nullptr, *d2 = nullptr, *b2 = nullptr, *d3 = nullptr, *d4 = nullptr;
+    float *w1a = nullptr, *w1b = nullptr, *w2a = nullptr, *w2b = nullptr, *w3a = nullptr,
+          *w3b = nullptr, *cond_v = nullptr, *cond_u = nullptr;
+    int cond_rank = 0;
+};
+
+struct Site {
+    nd_cq *tables = nullptr, *key = nullptr, *value = nullptr;
+    float *taps = nullptr;
+};
+
+bool is_global(const nd_v3_cfg &c, int li)
+{
+    for (int i = 0; i < c.n_global; ++i)
+        if (c.global_layers[i] == li) return true;
+    return false;
+}
+
+int site_of(const nd_v3_cfg &c, int li)
+{
+    for (int s = 0; s < c.n_sites; ++s)
+        if (c.sites[s] == li) return s;
+    return -1;
+}
+
+int max_order(const nd_v3_cfg &c)
+{
+    int m = 1;
+    for (int i = 0; i < c.n_orders; ++i) m = c.orders[i] > m ? c.orders[i] : m;
+    return m;
+}
+
+}  // namespace
+
+struct nd_v3_model {
+    nd_v3_cfg cfg{};
+    int device = 0;
+    nd_cq *embedding = nullptr;
+    std::vector<Layer> layers;
+    std::vector<float> a_pre, a_post, a_res;  // host copies, per layer
+    float *b_pre = nullptr, *b_post = nullptr, *b_res = nullptr;
+    nd_cq *phi_pre = nullptr, *phi_post = nullptr, *phi_res = nullptr;
+    int32_t *p1 = nullptr, *p2 = nullptr;
+    std::vector<Site> sites;
+    float *final_norm = nullptr;
+    float embed_scale = 1.0f;
+    std::vector<void *> mem;  // every device float/int buffer
+    std::vector<nd_cq *> cqs;
+
+    ~nd_v3_model()
+    {
+        (void)hipSetDevice(device);
+        for (void *p : mem) (void)hipFree(p);
+        for (nd_cq *w : cqs) nd_cq_free(w);
+    }
+};
+
+struct SessionHost {
+    int pos = 0;
+    std::vector<uint32_t> hist;
+    std::vector<int> slots;  // the reference's logical ring size per layer
+};
+
+struct nd_v3_batch {
+    int device = 0;
+    int B = 0, max_len = 0;
+    std::vector<SessionHost> s;
+    std::vector<uint8_t *> kv;        // per layer: B blocks
+    std::vector<size_t> kv_stride;    // per layer
+    std::vector<nd_kv_geom> geom;     // per layer
+    std::vector<int> cap;             // per layer
+    std::vector<float *> qt, kt, vt;  // per layer conv tails [B][taps-1][dim]
+    std::vector<float *> et;          // per site Engram tails [B][reach][d]
+    // activations
+    float *lanes = nullptr, *nx = nullptr, *nxh = nullptr, *u = nullptr, *bx = nullptr,
+          *h = nullptr, *hh = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *gate = nullptr,
+          *attn = nullptr, *ah = nullptr, *proj = nullptr, *p2 = nullptr, *y = nullptr,
+          *hpre = nullptr, *hpost = nullptr, *hres = nullptr, *emb = nullptr, *fetched = nullptr,
+          *fh = nullptr, *ek = nullptr, *ev = nullptr, *x = nullptr, *xh = nullptr,
+          *logits = nullptr;
+    int32_t *next = nullptr;
+    // Per-step inputs, uploaded from pinned host memory in one copy.  The
+    // copy is asynchronous, so a host buffer is reused only once the copy
+    // that read it has completed: a ring of kStages buffers, each with the
+    // event recorded after its copy, lets the host run that many steps ahead.
+    static constexpr int kStages = 4;
+    void *step_dev = nullptr;
+    void *stage_host[kStages] = {};
+    hipEvent_t stage_done[kStages] = {};
+    bool stage_pending[kStages] = {};
+    int stage_next = 0;
+    size_t step_bytes = 0;
+    int32_t *tok_dev = nullptr, *pos_dev = nullptr, *lo_dev = nullptr, *hi_dev = nullptr,
+            *rows_dev = nullptr;
+    float *rope_dev = nullptr;
+    int32_t *next_host = nullptr;
+    std::vector<void *> mem;
+
+    ~nd_v3_batch()
+    {
+        (void)hipSetDevice(device);
+        for (int i = 0; i < kStages; ++i)
+            if (stage_pending[i]) (void)hipEventSynchronize(stage_done[i]);
+        for (void *p : mem) (void)hipFree(p);  // hipFree waits for the device's work
+        for (int i = 0; i < kStages; ++i) {
+            if (stage_host[i]) (void)hipHostFree(stage_host[i]);
+            if (stage_done[i]) (void)hipEventDestroy(stage_done[i]);
+        }
+        if (next_host) (void)hipHostFree(next_host);
+    }
+};
+
+namespace {
+
+template <typename T>
+int dalloc(std::vector<void *> &mem, T **p, size_t count)
+{
+    void *q = nullptr;
+    hipError_t e = hipMalloc(&q, count * sizeof(T) + 16);
+    if (e != hipSuccess) return nd::hip_fail(e, "hipMalloc");
+    mem.push_back(q);
+    *p = static_cast<T *>(q);
+    return ND_OK;
+}
+
+int upload_floats(nd_ctx *ctx, nd_v3_model *m, const nd_v3_record &r, size_t want, float **out,
+                  const char *what, size_t idx)
+{
+    if (r.kind != ND_REC_F32 || r.len != want * 4)
+        return nd::fail(ND_ERR_ARG, "record %zu (%s): want %zu f32, got kind %d with %zu bytes", idx,
+                        what, want, int(r.kind), r.len);
+    if (int rc = dalloc(m->mem, out, want)) return rc;
+    ND_HIP(hipMemcpyAsync(*out, r.data, want * 4, hipMemcpyHostToDevice, ctx->stream));
+    return ND_OK;
+}
+
+int take_cq(nd_ctx *ctx, nd_v3_model *m, const nd_v3_record &r, const float *cb, size_t out,
+            size_t in, nd_cq **w, const char *what, size_t idx)
+{
+    if (r.kind != ND_REC_CQ || r.out != out || r.in != in)
+        return nd::fail(ND_ERR_ARG, "record %zu (%s): want a %zux%zu CQ tensor, got kind %d %zux%zu",
+                        idx, what, out, in, int(r.kind), r.out, r.in);
+    if (int rc = nd_cq_from_blob(ctx, static_cast<const uint8_t *>(r.data), r.len, r.out, r.in,
+                                 r.group, uint8_t(r.bits), cb, 28, w))
+        return rc;
+    m->cqs.push_back(*w);
+    return ND_OK;
+}
+
+// Projection over `B` prepared rows in the reference's summation order
+// (matvec for one session, matmul over sessions; bit-identical results),
+// batch-major output.
+int project(nd_ctx *ctx, const nd_cq *w, const float *xh, int B, size_t row_start, size_t rows,
+            float *y)
+{
+    if (B == 1) return nd_cq_matvec_rows_exact(ctx, w, xh, row_start, rows, y);
+    return nd_cq_matmul_rows_exact(ctx, w, xh, size_t(B), row_start, rows, y);
+}
+
+}  // namespace
+
+extern "C" {
+
+int nd_v3_model_create(nd_ctx *ctx, const nd_v3_cfg *cfg, const float *codebook,
+                       size_t codebook_len, const nd_v3_record *recs, size_t n, nd_v3_model **out)
+{
+    if (int rc = nd::enter(ctx)) return rc;
+    ND_REQUIRE(cfg && recs && out && codebook, "null argument");
+    ND_REQUIRE(codebook_len == 28, "codebook must be 28 floats (got %zu)", codebook_len);
+    *out = nullptr;
+    const nd_v3_cfg &c = *cfg;
+    ND_REQUIRE(c.hada_n == 1024, "hada_n %d: the device HadamardMLP is built for 1024 (32x32)",
+               c.hada_n);
+    ND_REQUIRE(c.mhc_lanes >= 1 && c.mhc_lanes <= 16, "mhc_lanes %d out of range", c.mhc_lanes);
+    ND_REQUIRE(c.d_model > 0 && c.d_model <= 1024, "d_model %d out of range", c.d_model);
+    ND_REQUIRE(c.num_layers > 0 && c.n_sites >= 0 && c.n_sites <= 64 && c.n_global <= 64 &&
+                   c.n_orders >= 1 && c.n_orders <= 8,
+               "bad layer/site counts");
+    ND_REQUIRE(c.qk_head_dim % 2 == 0 && c.qk_head_dim <= 128, "qk_head_dim %d", c.qk_head_dim);
+    nd_v3_model *m = new (std::nothrow) nd_v3_model;
+    if (!m) return nd::fail(ND_ERR_NOMEM, "host allocation failed");
+    m->cfg = c;
+    m->device = ctx->device;
+    const size_t d = c.d_model, L = c.num_layers, nl = c.mhc_lanes;
+    const size_t qd = size_t(c.num_heads) * c.qk_head_dim, kd = size_t(c.num_kv_heads) * c.qk_head_dim;
+    const size_t vd = size_t(c.num_kv_heads) * c.v_head_dim, od = size_t(c.num_heads) * c.v_head_dim;
+    const size_t T = c.qkv_conv_taps, hn = c.hada_n;
+    size_t i = 0;
+    int rc = ND_OK;
+    auto next = [&](const char *what) -> const nd_v3_record * {
+        if (i >= n) {
+            rc = nd::fail(ND_ERR_ARG, "records end before %s (record %zu)", what, i);
+            return nullptr;
+        }
+        return &recs[i++];
+    };
+#define REC(name) \
+    const nd_v3_record *r_##name = next(#name); \
+    if (!r_##name) goto fail;
+#define F32(dst, name, count)                                                          \
+    {                                                                                  \
+        REC(name);                                                                     \
+        if ((rc = upload_floats(ctx, m, *r_##name, (count), &(dst), #name, i - 1))) goto fail; \
+    }
+#define CQ(dst, name, o, in_)                                                              \
+    {                                                                                      \
+        REC(name);                                                                         \
+        if ((rc = take_cq(ctx, m, *r_##name, codebook, (o), (in_), &(dst), #name, i - 1))) goto fail; \
+    }
+    {
+        CQ(m->embedding, embedding, size_t(c.vocab_size), d);
+        m->layers.resize(L);
+        for (size_t li = 0; li < L; ++li) {
+            Layer &l = m->layers[li];
+            F32(l.norm_in, norm_in, d);
+            CQ(l.q, q_proj, qd, d);
+            CQ(l.k, k_proj, kd, d);
+            CQ(l.v, v_proj, vd, d);
+            if (T > 0) {
+                F32(l.q_taps, q_taps, T * qd);
+                F32(l.k_taps, k_taps, T * kd);
+                F32(l.v_taps, v_taps, T * vd);
+            }
+            F32(l.q_norm, q_norm, size_t(c.qk_head_dim));
+            F32(l.k_norm, k_norm, size_t(c.qk_head_dim));
+            CQ(l.gate, gate_proj, od, d);
+            CQ(l.out, out_proj, d, od);
+            F32(l.post_norm, post_norm, d);
+            {
+                REC(attn_gate);
+                if (r_attn_gate->kind != ND_REC_F32 || r_attn_gate->len != 4) {
+                    rc = nd::fail(ND_ERR_ARG, "record %zu (attn_gate): want 1 f32", i - 1);
+                    goto fail;
+                }
+                std::memcpy(&l.attn_gate, r_attn_gate->data, 4);
+            }
+            F32(l.pre_hada, pre_hada, d);
+            F32(l.d1, d1, hn);
+            F32(l.d2, d2, hn);
+            F32(l.b2, b2, hn);
+            F32(l.d3, d3, hn);
+            F32(l.d4, d4, hn);
+            F32(l.w1a, w1a, 1024);
+            F32(l.w1b, w1b, 1024);
+            F32(l.w2a, w2a, 1024);
+            F32(l.w2b, w2b, 1024);
+            F32(l.w3a, w3a, 1024);
+            F32(l.w3b, w3b, 1024);
+            {
+                if (i >= n) {
+                    rc = nd::fail(ND_ERR_ARG, "records end before cond_v");
+                    goto fail;
+                }
+                l.cond_rank = int(recs[i].in);
+                if (l.cond_rank < 1 || l.cond_rank > 64) {
+                    rc = nd::fail(ND_ERR_ARG, "record %zu (cond_v): rank %d out of 1..64", i, l.cond_rank);
+                    goto fail;
+                }
+            }
+            F32(l.cond_v, cond_v, d * l.cond_rank);
+            F32(l.cond_u, cond_u, size_t(l.cond_rank) * hn);
+        }
+        for (const char *nm : {"a_pre", "a_post", "a_res"}) {
+            REC(scalar);
+            if (r_scalar->kind != ND_REC_F32 || r_scalar->len != L * 4) {
+                rc = nd::fail(ND_ERR_ARG, "record %zu (%s): want %zu f32", i - 1, nm, L);
+                goto fail;
+            }
+            std::vector<float> &dst = nm[2] == 'p' && nm[3] == 'r' ? m->a_pre
+                                      : nm[2] == 'p'                ? m->a_post
+                                                                    : m->a_res;
+            dst.resize(L);
+            std::memcpy(dst.data(), r_scalar->data, L * 4);
+        }
+        F32(m->b_pre, b_pre, L * nl);
+        F32(m->b_post, b_post, L * nl);
+        F32(m->b_res, b_res, L * nl * nl);
+        CQ(m->phi_pre, phi_pre, L * nl, nl * d);
+        CQ(m->phi_post, phi_post, L * nl, nl * d);
+        CQ(m->phi_res, phi_res, L * nl * nl, nl * d);
+        for (int pi = 0; pi < 2; ++pi) {
+            REC(perm);
+            if (r_perm->kind != ND_REC_F32 || r_perm->len != hn * 4) {
+                rc = nd::fail(ND_ERR_ARG, "record %zu (hada perm): want %zu f32", i - 1, hn);
+                goto fail;
+            }
+            std::vector<int32_t> pv(hn);
+            const float *pf = static_cast<const float *>(r_perm->data);
+            for (size_t k2 = 0; k2 < hn; ++k2) {
+                const float f = pf[k2];
+                if (!(f >= 0.0f && f < float(hn))) {
+                    rc = nd::fail(ND_ERR_ARG, "record %zu: permutation entry %zu out of range", i - 1, k2);
+                    goto fail;
+                }
+                pv[k2] = int32_t(f);
+            }
+            int32_t **dst = pi == 0 ? &m->p1 : &m->p2;
+            if ((rc = dalloc(m->mem, dst, hn))) goto fail;
+            hipError_t e = hipMemcpy(*dst, pv.data(), hn * 4, hipMemcpyHostToDevice);
+            if (e != hipSuccess) {
+                rc = nd::hip_fail(e, "hipMemcpy");
+                goto fail;
+            }
+        }
+        const size_t nt = size_t(c.n_orders) * c.e_heads;
+        m->sites.resize(c.n_sites);
+        for (int s = 0; s < c.n_sites; ++s) {
+            Site &st = m->sites[s];
+            CQ(st.tables, tables, nt * c.e_slots, size_t(c.e_sub_dim));
+            CQ(st.key, key_proj, d, nt * c.e_sub_dim);
+            CQ(st.value, value_proj, d, nt * c.e_sub_dim);
+            F32(st.taps, engram_taps, size_t(c.e_conv_taps) * d);
+        }
+        F32(m->final_norm, final_norm, d);
+    }
+#undef REC
+#undef F32
+#undef CQ
+    m->embed_scale = std::sqrt(float(d));
+    {
+        hipError_t e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) {
+            rc = nd::hip_fail(e, "upload");
+            goto fail;
+        }
+    }
+    *out = m;
+    return ND_OK;
+fail:
+    (void)hipStreamSynchronize(ctx->stream);
+    delete m;
+    return rc ? rc : ND_ERR_ARG;
+}
+
+void nd_v3_model_free(nd_v3_model *m) { delete m; }
+
+size_t nd_v3_logit_rows(const nd_v3_model *m)
+{
+    if (!m) return 0;
+    return size_t(m->cfg.out_vocab ? m->cfg.out_vocab : m->cfg.vocab_size);
+}
+
+int nd_v3_batch_create(nd_ctx *ctx, const nd_v3_model *m, size_t sessions, size_t max_len,
+                       size_t hint, nd_v3_batch **out)
+{
+    if (int rc = nd::enter(ctx)) return rc;
+    ND_REQUIRE(m && out, "null argument");
+    *out = nullptr;
+    const nd_v3_cfg &c = m->cfg;
+    ND_REQUIRE(sessions >= 1 && sessions <= 4096, "sessions %zu out of 1..4096", sessions);
+    ND_REQUIRE(max_len >= 1 && max_len <= size_t(c.max_seq_len), "max_len %zu out of 1..%d",
+               max_len, c.max_seq_len);
+    nd_v3_batch *b = new (std::nothrow) nd_v3_batch;
+    if (!b) return nd::fail(ND_ERR_NOMEM, "host allocation failed");
+    b->device = ctx->device;
+    b->B = int(sessions);
+    b->max_len = int(max_len);
+    const int B = b->B, L = c.num_layers, nl = c.mhc_lanes, d = c.d_model;
+    const int qd = c.num_heads * c.qk_head_dim, kd = c.num_kv_heads * c.qk_head_dim;
+    const int vd = c.num_kv_heads * c.v_head_dim, od = c.num_heads * c.v_head_dim;
+    const int T = c.qkv_conv_taps, nt = c.n_orders * c.e_heads;
+    const int reach = (c.e_conv_taps > 0 ? c.e_conv_taps - 1 : 0) * c.e_conv_dilation;
+    const size_t rows = nd_v3_logit_rows(m);
+    const size_t hnt = hint < 1 ? 1 : (hint > size_t(c.max_seq_len) ? size_t(c.max_seq_len) : hint);
+    int rc = ND_OK;
+    b->s.resize(B);
+    for (auto &sh : b->s) sh.slots.resize(L);
+    b->kv.resize(L);
+    b->kv_stride.resize(L);
+    b->geom.resize(L);
+    b->cap.resize(L);
+    b->qt.resize(L);
+    b->kt.resize(L);
+    b->vt.resize(L);
+    for (int li = 0; li < L; ++li) {
+        // cache.rs:190-199: cap = window (local) or max_seq_len (global);
+        // the device block needs only the positions this batch can reach.
+        const int ref_cap = is_global(c, li) || c.sliding_window == 0
+                                ? c.max_seq_len
+                                : (c.sliding_window < c.max_seq_len ? c.sliding_window : c.max_seq_len);
+        b->cap[li] = ref_cap;
+        const int dev_cap = ref_cap < b->max_len ? ref_cap : b->max_len;
+        for (auto &sh : b->s) sh.slots[li] = int(hnt < size_t(ref_cap) ? hnt : size_t(ref_cap));
+        nd_kv_geom g{c.num_heads, c.num_kv_heads, c.qk_head_dim, c.v_head_dim, dev_cap};
+        b->geom[li] = g;
+        b->kv_stride[li] = nd_kv_block_bytes(&g);
+        if ((rc = dalloc(b->mem, &b->kv[li], b->kv_stride[li] * B))) goto fail;
+        {
+            hipError_t e = hipMemsetAsync(b->kv[li], 0, b->kv_stride[li] * B, ctx->stream);
+            if (e != hipSuccess) {
+                rc = nd::hip_fail(e, "hipMemsetAsync");
+                goto fail;
+            }
+        }
+        const int tt = T > 0 ? T - 1 : 0;
+        if ((rc = dalloc(b->mem, &b->qt[li], size_t(B) * tt * qd + 1))) goto fail;
+        if ((rc = dalloc(b->mem, &b->kt[li], size_t(B) * tt * kd + 1))) goto fail;
+        if ((rc = dalloc(b->mem, &b->vt[li], size_t(B) * tt * vd + 1))) goto fail;
+        (void)hipMemsetAsync(b->qt[li], 0, (size_t(B) * tt * qd + 1) * 4, ctx->stream);
+        (void)hipMemsetAsync(b->kt[li], 0, (size_t(B) * tt * kd + 1) * 4, ctx->stream);
+        (void)hipMemsetAsync(b->vt[li], 0, (size_t(B) * tt * vd + 1) * 4, ctx->stream);
+    }
+    b->et.resize(c.n_sites);
+    for (int s = 0; s < c.n_sites; ++s) {
+        if ((rc = dalloc(b->mem, &b->et[s], size_t(B) * reach * d + 1))) goto fail;
+        (void)hipMemsetAsync(b->et[s], 0, (size_t(B) * reach * d + 1) * 4, ctx->stream);
+    }
+#define A(p, cnt) \
+    if ((rc = dalloc(b->mem, &b->p, size_t(cnt)))) goto fail;
+    A(lanes, size_t(B) * nl * d);
+    A(nx, size_t(B) * nl * d);
+    {
+        size_t phi_pad = 0;
+        if ((rc = nd_cq_shape(m->phi_pre, nullptr, nullptr, &phi_pad, nullptr, nullptr))) goto fail;
+        if ((rc = dalloc(b->mem, &b->nxh, size_t(B) * phi_pad))) goto fail;
+    }
+    A(u, size_t(B) * d);
+    A(bx, size_t(B) * d);
+    A(h, size_t(B) * d);
+    A(hh, size_t(B) * d);
+    A(q, size_t(B) * qd);
+    A(k, size_t(B) * kd);
+    A(v, size_t(B) * vd);
+    A(gate, size_t(B) * od);
+    A(attn, size_t(B) * od);
+    A(ah, size_t(B) * od);
+    A(proj, size_t(B) * d);
+    A(p2, size_t(B) * d);
+    A(y, size_t(B) * d);
+    A(hpre, size_t(B) * nl);
+    A(hpost, size_t(B) * nl);
+    A(hres, size_t(B) * nl * nl);
+    A(emb, size_t(B) * d);
+    A(fetched, size_t(B) * nt * c.e_sub_dim);
+    A(fh, size_t(B) * nt * c.e_sub_dim);
+    A(ek, size_t(c.n_sites > 0 ? c.n_sites : 1) * B * d);
+    A(ev, size_t(c.n_sites > 0 ? c.n_sites : 1) * B * d);
+    A(x, size_t(B) * d);
+    A(xh, size_t(B) * d);
+    A(logits, size_t(B) * rows);
+    A(next, size_t(B));
+#undef A
+    {
+        // step inputs: tokens, pos, lo[L][B], hi[B], engram rows [B][nt], rope [B][qk]
+        const size_t ints = size_t(B) * (3 + L + nt);
+        const size_t floats = size_t(B) * c.qk_head_dim;
+        b->step_bytes = ints * 4 + floats * 4;
+        if ((rc = dalloc(b->mem, reinterpret_cast<uint8_t **>(&b->step_dev), b->step_bytes))) goto fail;
+        hipError_t e = hipSuccess;
+        for (int i = 0; i < nd_v3_batch::kStages && e == hipSuccess; ++i) {
+            e = hipHostMalloc(&b->stage_host[i], b->step_bytes, hipHostMallocDefault);
+            if (e == hipSuccess) e = hipEventCreateWithFlags(&b->stage_done[i], hipEventDisableTiming);
+        }
+        if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void **>(&b->next_host), size_t(B) * 4, hipHostMallocDefault);
+        if (e != hipSuccess) {
+            rc = nd::hip_fail(e, "hipHostMalloc");
+            goto fail;
+        }
+        int32_t *base = static_cast<int32_t *>(b->step_dev);
+        b->tok_dev = base;
+        b->pos_dev = base + B;
+        b->hi_dev = base + 2 * B;
+        b->lo_dev = base + 3 * B;
+        b->rows_dev = base + 3 * B + size_t(L) * B;
+        b->rope_dev = reinterpret_cast<float *>(base + ints);
+    }
+    {
+        hipError_t e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) {
+            rc = nd::hip_fail(e, "batch set-up");
+            goto fail;
+        }
+    }
+    *out = b;
+    return ND_OK;
+fail:
+    (void)hipStreamSynchronize(ctx->stream);
+    delete b;
+    return rc ? rc : ND_ERR_ARG;
+}
+
+void nd_v3_batch_free(nd_v3_batch *b) { delete b; }
+
+int nd_v3_positions(const nd_v3_batch *b, int32_t *pos)
+{
+    nd::clear_error();
+    ND_REQUIRE(b && pos, "null argument");
+    for (int i = 0; i < b->B; ++i) pos[i] = b->s[i].pos;
+    return ND_OK;
+}
+
+int nd_v3_step(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *tokens,
+               int32_t *next, float *logits)
+{
+    if (int rc = nd::enter(ctx)) return rc;
+    ND_REQUIRE(m && b && tokens, "null argument");
+    const nd_v3_cfg &c = m->cfg;
+    const int B = b->B, L = c.num_layers, nl = c.mhc_lanes, d = c.d_model;
+    const int qd = c.num_heads * c.qk_head_dim, kd = c.num_kv_heads * c.qk_head_dim;
+    const int vd = c.num_kv_heads * c.v_head_dim, od = c.num_heads * c.v_head_dim;
+    const int nt = c.n_orders * c.e_heads, half = c.qk_head_dim / 2;
+    const int mo = max_order(c);
+    const size_t rows = nd_v3_logit_rows(m);
+    for (int i = 0; i < B; ++i)
+        ND_REQUIRE(b->s[i].pos < b->max_len, "session %d is full (%d positions)", i, b->max_len);
+
+    // ---- host bookkeeping (V3Cache state that only steers addressing) -------
+    const int stage = b->stage_next;
+    if (b->stage_pending[stage]) ND_HIP(hipEventSynchronize(b->stage_done[stage]));
+    b->stage_pending[stage] = false;
+    int32_t *si = static_cast<int32_t *>(b->stage_host[stage]);
+    int32_t *h_tok = si, *h_pos = si + B, *h_hi = si + 2 * B, *h_lo = si + 3 * B;
+    int32_t *h_rows = si + 3 * B + size_t(L) * B;
+    float *h_rope = reinterpret_cast<float *>(si + size_t(B) * (3 + L + nt));
+    for (int i = 0; i < B; ++i) {
+        SessionHost &sh = b->s[i];
+        const int pos = sh.pos;
+        const uint32_t tok = uint32_t(tokens[i]);
+        // cache.rs:283-289 push_token, keeping max(order) ids
+        sh.hist.push_back(tok);
+        if (int(sh.hist.size()) > mo) sh.hist.erase(sh.hist.begin());
+        // model.rs:196-200 embedding row of the clamped token
+        h_tok[i] = int32_t(tok < uint32_t(c.vocab_size) ? tok : uint32_t(c.vocab_size - 1));
+        h_pos[i] = pos;
+        h_hi[i] = pos;
+        // engram.rs:30-67 hash of the retained history at its last position
+        const int here = int(sh.hist.size()) - 1;
+        const int stride = c.e_seed_heads == 0 ? c.e_heads : c.e_seed_heads;
+        for (int oi = 0; oi < c.n_orders; ++oi)
+            for (int hh = 0; hh < c.e_heads; ++hh) {
+                const int table = oi * c.e_heads + hh;
+                uint32_t acc = 0x9E3779B9u * uint32_t(oi * stride + hh + 1);
+                for (int j = 0; j < c.orders[oi]; ++j) {
+                    const uint32_t t2 = j > here ? 0u : sh.hist[here - j];
+                    acc = (acc ^ t2) * 0x01000193u;
+                }
+                acc ^= acc >> 15;
+                const uint32_t slot = acc % uint32_t(c.e_slots);
+                const bool valid = pos + 1 >= c.orders[oi];
+                h_rows[size_t(i) * nt + table] = valid ? int32_t(uint32_t(table) * uint32_t(c.e_slots) + slot) : -1;
+            }
+        // model.rs:378-394 RoPE angles for this position
+        for (int j = 0; j < half; ++j) {
+            const float freq = 1.0f / std::pow(c.rope_theta, float(2 * j) / float(c.qk_head_dim));
+            const float angle = float(pos) * freq;
+            h_rope[size_t(i) * 2 * half + j] = std::cos(angle);
+            h_rope[size_t(i) * 2 * half + half + j] = std::sin(angle);
+        }
+        // cache.rs:291-331 ensure + span per layer
+        for (int li = 0; li < L; ++li) {
+            const int cap = b->cap[li];
+            int &slots = sh.slots[li];
+            if (!(pos < slots || slots >= cap)) {
+                int want = slots * 2 > pos + 1 ? slots * 2 : pos + 1;
+                slots = want < cap ? want : cap;
+            }
+            const int window = is_global(c, li) ? 0 : c.sliding_window;
+            int lo = (window && pos + 1 > window) ? pos + 1 - window : 0;
+            const int clamp = pos + 1 > slots ? pos + 1 - slots : 0;
+            h_lo[size_t(li) * B + i] = lo > clamp ? lo : clamp;
+        }
+    }
+    ND_HIP(hipMemcpyAsync(b->step_dev, b->stage_host[stage], b->step_bytes, hipMemcpyHostToDevice,
+                          ctx->stream));
+    ND_HIP(hipEventRecord(b->stage_done[stage], ctx->stream));
+    b->stage_pending[stage] = true;
+    b->stage_next = (stage + 1) % nd_v3_batch::kStages;
+    hipStream_t st = ctx->stream;
+    int rc = ND_OK;
+#define CK(call) \
+    if ((rc = (call))) return rc;
+#define LCHK(name) \
+    if ((rc = nd::check_launch(name))) return rc;
+
+    // ---- Engram for this position (model.rs:162-191) -------------------------
+    for (int s = 0; s < c.n_sites; ++s) {
+        const Site &site = m->sites[s];
+        CK(nd_cq_dequantize_rows(ctx, site.tables, b->rows_dev, size_t(B) * nt, b->fetched));
+        CK(nd_cq_prepare_input(ctx, site.key, b->fetched, B, b->fh));
+        CK(project(ctx, site.key, b->fh, B, 0, d, b->ek + size_t(s) * B * d));
+        CK(project(ctx, site.value, b->fh, B, 0, d, b->ev + size_t(s) * B * d));
+        const int reach = (c.e_conv_taps - 1) * c.e_conv_dilation;
+        hipLaunchKernelGGL(k_engram_conv, dim3((d + 255) / 256, B), dim3(256), 0, st,
+                           b->ev + size_t(s) * B * d, site.taps, b->et[s], b->pos_dev,
+                           c.e_conv_taps, c.e_conv_dilation, mo, reach, d);
+        LCHK("k_engram_conv");
+    }
+    // ---- lane stream (model.rs:194-203) --------------------------------------
+    CK(nd_cq_dequantize_rows(ctx, m->embedding, b->tok_dev, size_t(B), b->emb));
+    hipLaunchKernelGGL(k_embed, dim3((d + 255) / 256, B), dim3(256), 0, st, b->emb, b->lanes,
+                       m->embed_scale, nl, d);
+    LCHK("k_embed");
+
+    const float qk_scale = 1.0f / std::sqrt(float(c.qk_head_dim));
+    for (int li = 0; li < L; ++li) {
+        const Layer &l = m->layers[li];
+        // mix down
+        hipLaunchKernelGGL(k_rms_unit, dim3(B), dim3(kT), 0, st, b->lanes, b->nx, nl * d);
+        LCHK("k_rms_unit");
+        CK(nd_cq_prepare_input(ctx, m->phi_pre, b->nx, B, b->nxh));
+        CK(project(ctx, m->phi_pre, b->nxh, B, size_t(li) * nl, nl, b->hpre));
+        const int site = site_of(c, li);
+        MhcIn mi{b->hpre, b->lanes, m->b_pre + size_t(li) * nl, m->a_pre[li], li, nl, d,
+                 site >= 0 ? b->ek + size_t(site) * B * d : nullptr,
+                 site >= 0 ? b->ev + size_t(site) * B * d : nullptr, l.norm_in, b->u, b->bx, b->h};
+        hipLaunchKernelGGL(k_mhc_in, dim3(B), dim3(kT), 0, st, mi);
+        LCHK("k_mhc_in");
+        // projections
+        CK(nd_cq_prepare_input(ctx, l.q, b->h, B, b->hh));
+        CK(project(ctx, l.q, b->hh, B, 0, qd, b->q));
+        CK(project(ctx, l.k, b->hh, B, 0, kd, b->k));
+        CK(project(ctx, l.v, b->hh, B, 0, vd, b->v));
+        CK(project(ctx, l.gate, b->hh, B, 0, od, b->gate));
+        QkvPost qp{b->q, b->k, b->v, b->qt[li], b->kt[li], b->vt[li], l.q_taps, l.k_taps, l.v_taps,
+                   l.q_norm, l.k_norm, b->rope_dev, b->pos_dev, qd, kd, vd, c.qkv_conv_taps,
+                   c.num_heads, c.num_kv_heads, c.qk_head_dim};
+        hipLaunchKernelGGL(k_qkv_post, dim3(B), dim3(kT), 0, st, qp);
+        LCHK("k_qkv_post");
+        // int8 KV append and attention (query fake-quant fused)
+        CK(nd_kv_write(ctx, &b->geom[li], b->kv[li], b->kv_stride[li], size_t(B), b->pos_dev, b->k, b->v));
+        CK(nd_attend_step_i8_exact(ctx, &b->geom[li], b->kv[li], b->kv_stride[li], size_t(B),
+                                   b->lo_dev + size_t(li) * B, b->hi_dev, b->q, qk_scale, 1,
+                                   b->attn));
+        hipLaunchKernelGGL(k_gate_mul, dim3(unsigned((size_t(B) * od + 255) / 256)), dim3(256), 0, st,
+                           b->attn, b->gate, size_t(B) * od);
+        LCHK("k_gate_mul");
+        CK(nd_cq_prepare_input(ctx, l.out, b->attn, B, b->ah));
+        CK(project(ctx, l.out, b->ah, B, 0, d, b->proj));
+        const float agate = nd_sigmoidf(l.attn_gate);
+        hipLaunchKernelGGL(k_post_attn, dim3(B), dim3(kT), 0, st, b->proj, b->bx, l.post_norm,
+                           l.pre_hada, agate, b->p2, d);
+        LCHK("k_post_attn");
+        HadaArgs ha{b->p2, b->u, b->bx, b->y, l.d1, l.d2, l.b2, l.d3, l.d4, l.w1a, l.w1b,
+                    l.w2a, l.w2b, l.w3a, l.w3b, l.cond_v, l.cond_u, m->p1, m->p2, d, l.cond_rank};
+        hipLaunchKernelGGL(k_hada_mlp, dim3(B), dim3(1024), 0, st, ha);
+        LCHK("k_hada_mlp");
+        // scatter up: lanes are unchanged since the mix down, so the prepared
+        // rms_unit(lanes) serves phi_post and phi_res too.
+        CK(project(ctx, m->phi_post, b->nxh, B, size_t(li) * nl, nl, b->hpost));
+        CK(project(ctx, m->phi_res, b->nxh, B, size_t(li) * nl * nl, size_t(nl) * nl, b->hres));
+        MhcOut mo2{b->lanes, b->hpost, b->hres, b->y, m->b_post + size_t(li) * nl,
+                   m->b_res + size_t(li) * nl * nl, m->a_post[li], m->a_res[li], li, nl, d};
+        hipLaunchKernelGGL(k_mhc_out, dim3(B), dim3(kT), 0, st, mo2);
+        LCHK("k_mhc_out");
+    }
+    // ---- head ---------------------------------------------------------------
+    hipLaunchKernelGGL(k_final, dim3(B), dim3(kT), 0, st, b->lanes, m->final_norm, b->x, nl, d);
+    LCHK("k_final");
+    CK(nd_cq_prepare_input(ctx, m->embedding, b->x, B, b->xh));
+    CK(project(ctx, m->embedding, b->xh, B, 0, rows, b->logits));
+    if (logits)
+        ND_HIP(hipMemcpyAsync(logits, b->logits, size_t(B) * rows * 4, hipMemcpyDeviceToDevice, st));
+    if (next) {
+        hipLaunchKernelGGL(k_argmax, dim3(B), dim3(kT), 0, st, b->logits, int(rows), b->next);
+        LCHK("k_argmax");
+        ND_HIP(hipMemcpyAsync(b->next_host, b->next, size_t(B) * 4, hipMemcpyDeviceToHost, st));
+        ND_HIP(hipStreamSynchronize(st));
+        std::memcpy(next, b->next_host, size_t(B) * 4);
+    }
+    for (int i = 0; i < B; ++i) b->s[i].pos++;
+#undef CK
+#undef LCHK
+    return ND_OK;
+}
+
+}  // extern "C"

@@ -61,6 +61,8 @@ _SIGS = [
     ("nd_cq_prepare_input", C.c_int, [_vp, _vp, _vp, _sz, _vp]),
     ("nd_cq_matvec_rows_prepared", C.c_int, [_vp, _vp, _vp, _sz, _sz, _vp]),
     ("nd_cq_matmul_rows_prepared", C.c_int, [_vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    ("nd_cq_matvec_rows_exact", C.c_int, [_vp, _vp, _vp, _sz, _sz, _vp]),
+    ("nd_cq_matmul_rows_exact", C.c_int, [_vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     ("nd_cq_dequantize_rows", C.c_int, [_vp, _vp, _vp, _sz, _vp]),
     ("nd_fake_quant", C.c_int, [_vp, _vp, _sz, _sz]),
     ("nd_quantize_rows", C.c_int, [_vp, _vp, _sz, _sz, _vp, _vp]),
@@ -71,6 +73,15 @@ _SIGS = [
     ("nd_kv_write", C.c_int, [_vp, C.POINTER(KvGeom), _vp, _sz, _sz, _vp, _vp, _vp]),
     ("nd_attend_step_i8", C.c_int, [_vp, C.POINTER(KvGeom), _vp, _sz, _sz, _vp, _vp, _vp,
                                     C.c_float, C.c_int, _vp]),
+    ("nd_attend_step_i8_exact", C.c_int, [_vp, C.POINTER(KvGeom), _vp, _sz, _sz, _vp, _vp, _vp,
+                                          C.c_float, C.c_int, _vp]),
+    ("nd_v3_model_create", C.c_int, [_vp, _vp, _vp, _sz, _vp, _sz, C.POINTER(_vp)]),
+    ("nd_v3_model_free", None, [_vp]),
+    ("nd_v3_logit_rows", _sz, [_vp]),
+    ("nd_v3_batch_create", C.c_int, [_vp, _vp, _sz, _sz, _sz, C.POINTER(_vp)]),
+    ("nd_v3_batch_free", None, [_vp]),
+    ("nd_v3_positions", C.c_int, [_vp, _vp]),
+    ("nd_v3_step", C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp]),
 ]
 
 
@@ -204,12 +215,13 @@ class CqWeight:
         _check(lib().nd_cq_prepare_input(self.ctx.h, self.h, _ptr(x2), x2.shape[0], _ptr(xh)))
         return xh
 
-    def matvec_rows_prepared(self, xh, row_start, rows, y=None):
+    def matvec_rows_prepared(self, xh, row_start, rows, y=None, exact=False):
+        """exact=True: the reference's summation order, bit-identical."""
         torch = _torch()
         if y is None:
             y = torch.empty(rows, dtype=torch.float32, device=xh.device)
-        _check(lib().nd_cq_matvec_rows_prepared(self.ctx.h, self.h, _ptr(xh), row_start, rows,
-                                                _ptr(y)))
+        fn = lib().nd_cq_matvec_rows_exact if exact else lib().nd_cq_matvec_rows_prepared
+        _check(fn(self.ctx.h, self.h, _ptr(xh), row_start, rows, _ptr(y)))
         return y
 
     def matvec_prepared(self, xh, y=None):
@@ -218,12 +230,13 @@ class CqWeight:
     def matvec(self, x):
         return self.matvec_prepared(self.prepare_input(x))
 
-    def matmul_rows_prepared(self, xh, batch, row_start, rows, y=None):
+    def matmul_rows_prepared(self, xh, batch, row_start, rows, y=None, exact=False):
+        """exact=True: the reference's summation order, bit-identical."""
         torch = _torch()
         if y is None:
             y = torch.empty(batch * rows, dtype=torch.float32, device=xh.device)
-        _check(lib().nd_cq_matmul_rows_prepared(self.ctx.h, self.h, _ptr(xh), batch, row_start,
-                                                rows, _ptr(y)))
+        fn = lib().nd_cq_matmul_rows_exact if exact else lib().nd_cq_matmul_rows_prepared
+        _check(fn(self.ctx.h, self.h, _ptr(xh), batch, row_start, rows, _ptr(y)))
         return y
 
     def dequantize_rows(self, rows_i32, out=None):
@@ -279,15 +292,17 @@ def kv_write(ctx, g, kv, kv_stride, pos_i32, k, v):
 
 
 def attend_step_i8(ctx, g, kv, kv_stride, lo_i32, hi_i32, q, scale=None, quant_query=False,
-                   out=None):
+                   out=None, exact=False):
+    """exact=True: nd_attend_step_i8_exact, bit-identical to attend_step."""
     torch = _torch()
     count = lo_i32.numel()
     if scale is None:
         scale = float(np.float32(1.0) / np.sqrt(np.float32(g.qk_head_dim)))
     if out is None:
         out = torch.empty(count, g.num_heads * g.v_head_dim, dtype=torch.float32, device=q.device)
-    _check(lib().nd_attend_step_i8(ctx.h, C.byref(g), _ptr(kv), kv_stride, count, _ptr(lo_i32),
-                                   _ptr(hi_i32), _ptr(q), scale, int(bool(quant_query)), _ptr(out)))
+    fn = lib().nd_attend_step_i8_exact if exact else lib().nd_attend_step_i8
+    _check(fn(ctx.h, C.byref(g), _ptr(kv), kv_stride, count, _ptr(lo_i32), _ptr(hi_i32), _ptr(q),
+              scale, int(bool(quant_query)), _ptr(out)))
     return out
 
 
@@ -362,3 +377,118 @@ def attend_i8_prefill(ctx, num_heads, num_kv_heads, qk, vd, q, k, v, window=0, q
     scale = float(np.float32(1.0) / np.float32(math.sqrt(qk)))
     return attend_step_i8(ctx, g, blk, 0, lo.to(torch.int32), hi, q.contiguous(), scale,
                           quant_query)
+
+
+# ---- Needle-3 forward on the device ----------------------------------------
+
+class V3Cfg(C.Structure):
+    _fields_ = [("vocab_size", C.c_int32), ("out_vocab", C.c_int32), ("d_model", C.c_int32),
+                ("num_heads", C.c_int32), ("num_kv_heads", C.c_int32), ("num_layers", C.c_int32),
+                ("qk_head_dim", C.c_int32), ("v_head_dim", C.c_int32), ("max_seq_len", C.c_int32),
+                ("hada_n", C.c_int32), ("mhc_lanes", C.c_int32), ("rope_theta", C.c_float),
+                ("sliding_window", C.c_int32), ("n_global", C.c_int32),
+                ("global_layers", C.c_int32 * 64), ("qkv_conv_taps", C.c_int32),
+                ("n_orders", C.c_int32), ("orders", C.c_int32 * 8), ("e_heads", C.c_int32),
+                ("e_slots", C.c_int32), ("e_sub_dim", C.c_int32), ("n_sites", C.c_int32),
+                ("sites", C.c_int32 * 64), ("e_conv_taps", C.c_int32),
+                ("e_conv_dilation", C.c_int32), ("e_seed_heads", C.c_int32)]
+
+
+class V3Record(C.Structure):
+    _fields_ = [("kind", C.c_int32), ("data", C.c_void_p), ("len", _sz), ("out", _sz),
+                ("inn", _sz), ("group", _sz), ("bits", _sz)]
+
+
+def v3_cfg(g):
+    c = V3Cfg()
+    for k in ("vocab_size", "out_vocab", "d_model", "num_heads", "num_kv_heads", "num_layers",
+              "qk_head_dim", "v_head_dim", "max_seq_len", "hada_n", "mhc_lanes",
+              "sliding_window", "qkv_conv_taps", "e_heads", "e_slots", "e_sub_dim",
+              "e_conv_taps", "e_conv_dilation", "e_seed_heads"):
+        setattr(c, k, g[k])
+    c.rope_theta = g["rope_theta"]
+    c.n_global = len(g["global_layers"])
+    for i, v in enumerate(g["global_layers"]):
+        c.global_layers[i] = v
+    c.n_orders = len(g["orders"])
+    for i, v in enumerate(g["orders"]):
+        c.orders[i] = v
+    c.n_sites = len(g["sites"])
+    for i, v in enumerate(g["sites"]):
+        c.sites[i] = v
+    return c
+
+
+class V3Model:
+    """A Needle-3 model on the device, from canonical container records
+    (V3Layout::derive order, crates/needle-infer/src/v3.rs:236-330)."""
+
+    def __init__(self, ctx, geom, records, codebook):
+        self.ctx, self.geom = ctx, geom
+        cfg = v3_cfg(geom)
+        keep = [np.ascontiguousarray(r["data"]) for r in records]
+        arr = (V3Record * len(records))()
+        for i, (r, buf) in enumerate(zip(records, keep)):
+            arr[i] = V3Record(r["kind"], buf.ctypes.data, buf.nbytes, r["out"], r["inn"],
+                              r["group"], r["bits"])
+        cb = np.ascontiguousarray(codebook, np.float32)
+        h = C.c_void_p()
+        _check(lib().nd_v3_model_create(ctx.h, C.byref(cfg), cb.ctypes.data_as(C.c_void_p), cb.size,
+                                        arr, len(records), C.byref(h)))
+        self.h = h
+        self.rows = lib().nd_v3_logit_rows(h)
+
+    def close(self):
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.nd_v3_model_free(self.h)
+            self.h = None
+
+    __del__ = close
+
+
+class V3Batch:
+    """`sessions` int8-KV decode sessions stepped in lockstep on the device."""
+
+    def __init__(self, model, sessions, max_len, hint=None):
+        self.model, self.sessions = model, sessions
+        h = C.c_void_p()
+        _check(lib().nd_v3_batch_create(model.ctx.h, model.h, sessions, max_len,
+                                        hint or max_len, C.byref(h)))
+        self.h = h
+
+    def close(self):
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.nd_v3_batch_free(self.h)
+            self.h = None
+
+    __del__ = close
+
+    def positions(self):
+        out = np.zeros(self.sessions, np.int32)
+        _check(lib().nd_v3_positions(self.h, out.ctypes.data_as(C.c_void_p)))
+        return out
+
+    def step(self, tokens, logits=None, want_next=True):
+        """Feed tokens[i] to session i (V3Model::decode_step); returns the greedy
+        next tokens, and fills `logits` ([sessions][rows] device tensor) if given."""
+        tok = np.ascontiguousarray(tokens, np.int32).reshape(self.sessions)
+        nxt = np.zeros(self.sessions, np.int32) if want_next else None
+        _check(lib().nd_v3_step(self.model.ctx.h, self.model.h, self.h,
+                                tok.ctypes.data_as(C.c_void_p),
+                                nxt.ctypes.data_as(C.c_void_p) if want_next else None,
+                                _ptr(logits) if logits is not None else None))
+        return nxt
+
+    def generate(self, prompts, steps):
+        """Prefill by stepping each session's prompt (the reference's batched
+        prefill is bit-identical to stepping), then `steps` greedy tokens."""
+        prompts = np.asarray(prompts, np.int32).reshape(self.sessions, -1)
+        nxt = None
+        for t in range(prompts.shape[1]):
+            nxt = self.step(prompts[:, t], want_next=(t == prompts.shape[1] - 1))
+        out = np.zeros((self.sessions, steps), np.int32)
+        for s in range(steps):
+            out[:, s] = nxt
+            if s + 1 < steps:
+                nxt = self.step(nxt)
+        return out

@@ -39,6 +39,142 @@ float or_f16_to_f32(uint16_t bits)
     return f;
 }
 
+/*
+ * math.rs:3-11 route exp and ln through libm 0.2.16 (Cargo.lock:267-269),
+ * whose expf/logf are the FreeBSD msun algorithms (e_expf.c, e_logf.c, as
+ * carried by musl).  Restated here from those published sources; glibc's
+ * expf/logf are a different (table-driven) algorithm and can differ in the
+ * last bit, which an int8 KV cache can amplify into a flipped code.
+ */
+static uint32_t bits_of(float f)
+{
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    return u;
+}
+
+static float float_of(uint32_t u)
+{
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+/* scalbnf: y * 2^n, with the two-step scaling near the exponent limits. */
+static float scale_pow2(float y, int n)
+{
+    if (n > 127) {
+        y *= float_of(0x7f000000u);
+        n -= 127;
+        if (n > 127) {
+            y *= float_of(0x7f000000u);
+            n -= 127;
+            if (n > 127)
+                n = 127;
+        }
+    } else if (n < -126) {
+        y *= float_of(0x00800000u) * float_of(0x4b800000u);
+        n += 102;
+        if (n < -126) {
+            y *= float_of(0x00800000u) * float_of(0x4b800000u);
+            n += 102;
+            if (n < -126)
+                n = -126;
+        }
+    }
+    return y * float_of((uint32_t)(127 + n) << 23);
+}
+
+float or_expf(float x)
+{
+    /* ln2 split so that k*LN2_HI is exact; |r| <= ln2/2 after reduction. */
+    const float LN2_HI = float_of(0x3f317200u), LN2_LO = float_of(0x35bfbe8eu);
+    const float INV_LN2 = float_of(0x3fb8aa3bu);
+    /* remez coefficients of r*(e^r+1)/(e^r-1) on [-ln2/2, ln2/2] */
+    const float P1 = float_of(0x3e2aaa8fu), P2 = float_of(0xbb355215u);
+    uint32_t ax = bits_of(x);
+    int neg = (int)(ax >> 31);
+    ax &= 0x7fffffffu;
+    if (ax >= 0x42aeac50u) {          /* |x| >= 87.33655 */
+        if (ax > 0x7f800000u)
+            return x;                 /* NaN */
+        if (!neg && ax >= 0x42b17218u)
+            return x * float_of(0x7f000000u); /* overflow to +inf */
+        if (neg && ax >= 0x42cff1b5u)
+            return 0.0f;              /* below -103.972084: underflow */
+    }
+    int k;
+    float hi, lo;
+    if (ax > 0x3eb17218u) {           /* |x| > ln2/2 */
+        if (ax > 0x3f851592u)         /* |x| > 1.5 ln2 */
+            k = (int)(INV_LN2 * x + (neg ? -0.5f : 0.5f));
+        else
+            k = neg ? -1 : 1;
+        hi = x - (float)k * LN2_HI;
+        lo = (float)k * LN2_LO;
+        x = hi - lo;
+    } else if (ax > 0x39000000u) {    /* |x| > 2^-14 */
+        k = 0;
+        hi = x;
+        lo = 0.0f;
+    } else {
+        return 1.0f + x;
+    }
+    float xx = x * x;
+    float c = x - xx * (P1 + xx * P2);
+    float y = 1.0f + (x * c / (2.0f - c) - lo + hi);
+    return k ? scale_pow2(y, k) : y;
+}
+
+float or_logf(float x)
+{
+    const float LN2_HI = float_of(0x3f317180u), LN2_LO = float_of(0x3717f7d1u);
+    /* |(log(1+s)-log(1-s))/s - Lg(s)| < 2^-34.24 */
+    const float LG1 = float_of(0x3f2aaaaau), LG2 = float_of(0x3eccce13u);
+    const float LG3 = float_of(0x3e91e9eeu), LG4 = float_of(0x3e789e26u);
+    uint32_t ix = bits_of(x);
+    int k = 0;
+    if (ix < 0x00800000u || (ix >> 31)) {
+        if ((ix << 1) == 0)
+            return -1.0f / (x * x);   /* log(+-0) = -inf */
+        if (ix >> 31)
+            return (x - x) / 0.0f;    /* log(x < 0) = NaN */
+        k = -25;                      /* subnormal: scale by 2^25 */
+        x *= float_of(0x4c000000u);
+        ix = bits_of(x);
+    } else if (ix >= 0x7f800000u) {
+        return x;
+    } else if (ix == 0x3f800000u) {
+        return 0.0f;
+    }
+    /* x = 2^k (1 + f) with 1 + f in [sqrt(2)/2, sqrt(2)) */
+    ix += 0x3f800000u - 0x3f3504f3u;
+    k += (int)(ix >> 23) - 0x7f;
+    ix = (ix & 0x007fffffu) + 0x3f3504f3u;
+    float f = float_of(ix) - 1.0f;
+    float s = f / (2.0f + f);
+    float z = s * s;
+    float w = z * z;
+    float t1 = w * (LG2 + w * LG4);
+    float t2 = z * (LG1 + w * LG3);
+    float r = t2 + t1;
+    float hfsq = 0.5f * f * f;
+    float dk = (float)k;
+    return s * (hfsq + r) + dk * LN2_LO - hfsq + f + dk * LN2_HI;
+}
+
+void or_expf_n(const float *x, size_t n, float *y)
+{
+    for (size_t i = 0; i < n; i++)
+        y[i] = or_expf(x[i]);
+}
+
+void or_logf_n(const float *x, size_t n, float *y)
+{
+    for (size_t i = 0; i < n; i++)
+        y[i] = or_logf(x[i]);
+}
+
 /* ======================================================================== */
 /* hadamard.rs                                                              */
 /* ======================================================================== */
@@ -669,7 +805,7 @@ static void attend_step_impl(const float *q, const float *kf, const float *vf,
         }
         float sum = 0.0f;
         for (size_t i = 0; i < span; i++) {
-            scores[i] = expf(scores[i] - max);
+            scores[i] = or_expf(scores[i] - max);
             sum += scores[i];
         }
         float inv = 1.0f / sum;
@@ -733,7 +869,7 @@ static void attend_impl(const float *q, const float *kf, const float *vf,
             }
             float sum = 0.0f;
             for (size_t n = lo; n <= t; n++) {
-                scores[n] = expf(scores[n] - max);
+                scores[n] = or_expf(scores[n] - max);
                 sum += scores[n];
             }
             float inv = 1.0f / sum;

@@ -53,6 +53,11 @@ extern "C" {
 
 /* ---- math.rs ---------------------------------------------------------- */
 float or_f16_to_f32(uint16_t bits);
+/* libm 0.2.16 expf / logf (FreeBSD e_expf.c / e_logf.c), math.rs:3-11. */
+float or_expf(float x);
+float or_logf(float x);
+void or_expf_n(const float *x, size_t n, float *y);
+void or_logf_n(const float *x, size_t n, float *y);
 
 /* ---- hadamard.rs ------------------------------------------------------ */
 void or_fwht(float *x, size_t n);

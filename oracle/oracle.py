@@ -61,6 +61,8 @@ def lib():
         L = C.CDLL(LIB_PATH)
         L.or_f16_to_f32.argtypes = [C.c_uint16]
         L.or_f16_to_f32.restype = C.c_float
+        L.or_expf_n.argtypes = [_f32p, _sz, _f32p]
+        L.or_logf_n.argtypes = [_f32p, _sz, _f32p]
         L.or_fwht.argtypes = [_f32p, _sz]
         L.or_fwht_normalized.argtypes = [_f32p, _sz]
         L.or_packed_row_bytes.argtypes = [_sz, C.c_uint8]
@@ -112,6 +114,22 @@ def _f32(a):
 
 def f16_to_f32(bits: int) -> float:
     return lib().or_f16_to_f32(bits)
+
+
+def expf(x):
+    """libm's expf (math.rs:3-6), elementwise."""
+    x = _f32(x).ravel()
+    y = np.empty_like(x)
+    lib().or_expf_n(x, x.size, y)
+    return y
+
+
+def logf(x):
+    """libm's logf (math.rs:8-11), elementwise."""
+    x = _f32(x).ravel()
+    y = np.empty_like(x)
+    lib().or_logf_n(x, x.size, y)
+    return y
 
 
 def fwht(x):
@@ -370,3 +388,158 @@ def attend_i8(q, k, ks, v, vs, seq, nh, nkv, qk, vd, window=0):
                        np.ascontiguousarray(v, np.int8), _f32(vs), C.byref(d),
                        window or 0, out)
     return out
+
+
+# ---- v3 forward (needle_oracle_v3.c) ----------------------------------------
+
+class V3Cfg(C.Structure):
+    _fields_ = [("vocab_size", _sz), ("out_vocab", _sz), ("d_model", _sz), ("num_heads", _sz),
+                ("num_kv_heads", _sz), ("num_layers", _sz), ("qk_head_dim", _sz),
+                ("v_head_dim", _sz), ("max_seq_len", _sz), ("hada_n", _sz), ("mhc_lanes", _sz),
+                ("rope_theta", C.c_float), ("sliding_window", _sz), ("n_global", _sz),
+                ("global_layers", _sz * 64), ("qkv_conv_taps", _sz), ("n_orders", _sz),
+                ("orders", _sz * 8), ("e_heads", _sz), ("e_slots", _sz), ("e_sub_dim", _sz),
+                ("n_sites", _sz), ("sites", _sz * 64), ("e_conv_taps", _sz),
+                ("e_conv_dilation", _sz), ("e_seed_heads", _sz)]
+
+
+class V3Record(C.Structure):
+    _fields_ = [("kind", C.c_int), ("data", C.c_void_p), ("len", _sz), ("out", _sz),
+                ("inn", _sz), ("group", _sz), ("bits", _sz)]
+
+
+def v3_cfg(g):
+    c = V3Cfg()
+    for k in ("vocab_size", "out_vocab", "d_model", "num_heads", "num_kv_heads", "num_layers",
+              "qk_head_dim", "v_head_dim", "max_seq_len", "hada_n", "mhc_lanes",
+              "sliding_window", "qkv_conv_taps", "e_heads", "e_slots", "e_sub_dim",
+              "e_conv_taps", "e_conv_dilation", "e_seed_heads"):
+        setattr(c, k, g[k])
+    c.rope_theta = g["rope_theta"]
+    c.n_global = len(g["global_layers"])
+    for i, v in enumerate(g["global_layers"]):
+        c.global_layers[i] = v
+    c.n_orders = len(g["orders"])
+    for i, v in enumerate(g["orders"]):
+        c.orders[i] = v
+    c.n_sites = len(g["sites"])
+    for i, v in enumerate(g["sites"]):
+        c.sites[i] = v
+    return c
+
+
+_v3_bound = False
+
+
+def _v3_lib():
+    global _v3_bound
+    L = lib()
+    if not _v3_bound:
+        L.or_v3_model_new.argtypes = [C.POINTER(V3Cfg), _f32p, C.POINTER(V3Record), _sz]
+        L.or_v3_model_new.restype = C.c_void_p
+        L.or_v3_model_free.argtypes = [C.c_void_p]
+        L.or_v3_cache_new.argtypes = [C.POINTER(V3Cfg), _sz, C.c_int]
+        L.or_v3_cache_new.restype = C.c_void_p
+        L.or_v3_cache_free.argtypes = [C.c_void_p]
+        L.or_v3_decode_step.argtypes = [C.c_void_p, C.c_void_p, C.c_uint32, _f32p]
+        L.or_v3_generate.argtypes = [C.c_void_p, C.c_void_p, np.ctypeslib.ndpointer(np.uint32),
+                                     _sz, _sz, np.ctypeslib.ndpointer(np.uint32), _f32p]
+        L.or_argmax.argtypes = [_f32p, _sz]
+        L.or_argmax.restype = C.c_uint32
+        L.or_sinkhorn.argtypes = [_f32p, _sz]
+        L.or_kron_apply.argtypes = [_f32p, _f32p, _f32p, _sz, _sz, _f32p]
+        L.or_engram_indices.argtypes = [np.ctypeslib.ndpointer(np.uint32), _sz,
+                                        np.ctypeslib.ndpointer(np.uintp), _sz, _sz, C.c_uint32,
+                                        _sz, np.ctypeslib.ndpointer(np.uint32)]
+        L.or_ngram_valid.argtypes = [_sz, _sz, np.ctypeslib.ndpointer(np.uintp), _sz]
+        L.or_ngram_valid.restype = C.c_int
+        L.or_v3_rope_at.argtypes = [C.POINTER(V3Cfg), _sz, _f32p, _f32p]
+        _v3_bound = True
+    return L
+
+
+class V3Model:
+    """The oracle's V3Model built from canonical records (v3_synth.build_records)."""
+
+    def __init__(self, geom, records, codebook):
+        L = _v3_lib()
+        self.geom = geom
+        self.cfg = v3_cfg(geom)
+        self._keep = [np.ascontiguousarray(r["data"]) for r in records]
+        arr = (V3Record * len(records))()
+        for i, (r, buf) in enumerate(zip(records, self._keep)):
+            arr[i] = V3Record(r["kind"], buf.ctypes.data, buf.nbytes, r["out"], r["inn"],
+                              r["group"], r["bits"])
+        self.codebook = np.ascontiguousarray(codebook, np.float32)
+        self._p = L.or_v3_model_new(C.byref(self.cfg), self.codebook, arr, len(records))
+        if not self._p:
+            raise ValueError("records do not match the v3 layout")
+        self.rows = geom["out_vocab"] or geom["vocab_size"]
+
+    def __del__(self):
+        if getattr(self, "_p", None) and _lib is not None:
+            _lib.or_v3_model_free(self._p)
+            self._p = None
+
+    def new_cache(self, hint, int8=True):
+        return V3Cache(self, hint, int8)
+
+
+class V3Cache:
+    def __init__(self, model, hint, int8):
+        self.model = model
+        self._p = _v3_lib().or_v3_cache_new(C.byref(model.cfg), hint, int(int8))
+
+    def __del__(self):
+        if getattr(self, "_p", None) and _lib is not None:
+            _lib.or_v3_cache_free(self._p)
+            self._p = None
+
+    def decode_step(self, token):
+        out = np.zeros(self.model.rows, np.float32)
+        _v3_lib().or_v3_decode_step(self.model._p, self._p, int(token), out)
+        return out
+
+
+def v3_generate(model, prompt, steps, int8=True, hint=None):
+    """Greedy tokens after stepping the prompt, and each step's top-1/top-2 margin."""
+    prompt = np.ascontiguousarray(prompt, np.uint32)
+    cache = model.new_cache(hint or (len(prompt) + steps), int8)
+    toks = np.zeros(steps, np.uint32)
+    margins = np.zeros(steps, np.float32)
+    _v3_lib().or_v3_generate(model._p, cache._p, prompt, len(prompt), steps, toks, margins)
+    return toks, margins
+
+
+def sinkhorn(m):
+    m = _f32(m).copy()
+    n = int(round(m.size ** 0.5))
+    _v3_lib().or_sinkhorn(m, n)
+    return m.reshape(n, n)
+
+
+def kron_apply(z, a, b):
+    ba, bb = a.shape[0], b.shape[0]
+    out = np.zeros(ba * bb, np.float32)
+    _v3_lib().or_kron_apply(_f32(z).reshape(-1), _f32(a).reshape(-1), _f32(b).reshape(-1), ba, bb, out)
+    return out.reshape(ba, bb)
+
+
+def engram_indices(tokens, orders, heads, slots, seed_heads=0):
+    tokens = np.ascontiguousarray(tokens, np.uint32)
+    orders = np.ascontiguousarray(orders, np.uintp)
+    out = np.zeros(len(tokens) * len(orders) * heads, np.uint32)
+    _v3_lib().or_engram_indices(tokens, len(tokens), orders, len(orders), heads, slots,
+                                seed_heads, out)
+    return out
+
+
+def ngram_valid(p, table, orders, heads):
+    return bool(_v3_lib().or_ngram_valid(p, table, np.ascontiguousarray(orders, np.uintp), heads))
+
+
+def rope_at(geom, pos):
+    half = geom["qk_head_dim"] // 2
+    c, s = np.zeros(half, np.float32), np.zeros(half, np.float32)
+    _v3_lib().or_v3_rope_at(C.byref(v3_cfg(geom)), pos, c, s)
+    return c, s

@@ -1,0 +1,109 @@
+"""The device Needle-3 forward (decode_step, int8 KV) vs the oracle's.
+
+Same canonical records (random init, v3_synth) on both sides.  The device
+forward sums in the reference's order (reference-order projections and
+attention, sequential norm chains, libm's exp/log), so the logits match the
+oracle's bit for bit at every step -- the only bar under which an int8 KV
+cache cannot drift (a last-bit difference upstream of the quantiser can flip
+a cached code) -- and greedy tokens are identical (first maximum wins), with
+the top-1/top-2 margins reported.
+"""
+import numpy as np
+import pytest
+import torch
+
+import needle_amd as nd
+import oracle as O
+import v3_synth as S
+
+pytestmark = pytest.mark.gpu
+
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+@pytest.fixture(scope="module")
+def small(ctx):
+    g, recs = S.build_records(S.small_geometry(4), seed=11)
+    return g, recs, O.V3Model(g, recs, S.CODEBOOK), nd.V3Model(ctx, g, recs, S.CODEBOOK)
+
+
+def _oracle_logits(om, prompt, int8=True):
+    cache = om.new_cache(len(prompt), int8)
+    return np.stack([cache.decode_step(t) for t in prompt])
+
+
+def test_small_model_logits_track_the_oracle(small):
+    """4 layers, window 32 (the local rings wrap), Engram on layers 1 and 3."""
+    g, recs, om, dm = small
+    prompt = S.prompt_tokens(48, 3)
+    want = _oracle_logits(om, prompt)
+    batch = nd.V3Batch(dm, 1, max_len=64)
+    got = torch.empty(1, dm.rows, device="cuda")
+    errs, first_bad = [], -1
+    for t, tok in enumerate(prompt):
+        batch.step([tok], logits=got, want_next=False)
+        g = got.cpu().numpy()[0]
+        errs.append(float(np.max(np.abs(g - want[t]))))
+        if first_bad < 0 and not np.array_equal(_bits(g), _bits(want[t])):
+            first_bad = t
+    print(f"max-abs logit error per step: max {max(errs):.3e}, logit scale {np.abs(want).max():.3e}, "
+          f"first step with a differing bit {first_bad}")
+    assert first_bad == -1, errs
+    assert list(batch.positions()) == [48]
+
+
+def test_sessions_are_independent(small):
+    """Three sessions stepped in one batch (M = 3 projections) each equal
+    their own oracle run."""
+    g, recs, om, dm = small
+    prompts = np.stack([S.prompt_tokens(20, 100 + i) for i in range(3)])
+    batch = nd.V3Batch(dm, 3, max_len=32)
+    got = torch.empty(3, dm.rows, device="cuda")
+    outs = []
+    for t in range(prompts.shape[1]):
+        batch.step(prompts[:, t], logits=got, want_next=False)
+        outs.append(got.cpu().numpy().copy())
+    outs = np.stack(outs, axis=1)
+    for i in range(3):
+        want = _oracle_logits(om, prompts[i])
+        assert np.array_equal(_bits(outs[i]), _bits(want)), (i, np.max(np.abs(outs[i] - want)))
+
+
+def test_greedy_matches_oracle_small(small):
+    g, recs, om, dm = small
+    prompt = S.prompt_tokens(16, 5)
+    toks, margins = O.v3_generate(om, prompt, 48)
+    batch = nd.V3Batch(dm, 1, max_len=64)
+    got = batch.generate(prompt[None], 48)[0]
+    print(f"min top-1/top-2 margin {margins.min():.4e}; distinct tokens {len(set(toks.tolist()))}")
+    assert np.array_equal(got, toks.astype(np.int32))
+
+
+def test_model_rejects_a_wrong_record(ctx):
+    g, recs = S.build_records(S.small_geometry(2), seed=1)
+    bad = list(recs)
+    bad[2] = dict(bad[2], out=bad[2]["out"] + 1)  # q_proj with the wrong row count
+    with pytest.raises(nd.NeedleError) as e:
+        nd.V3Model(ctx, g, bad, S.CODEBOOK)
+    assert "q_proj" in str(e.value)
+    with pytest.raises(nd.NeedleError):
+        nd.V3Model(ctx, g, recs[:-1], S.CODEBOOK)
+
+
+def test_shipped_geometry_prompt128_greedy256(ctx):
+    """The shipped v3 geometry (20 layers, ~121M params), a 128-token
+    uniform prompt, 256 greedy steps, int8 KV: tokens identical."""
+    g, recs = S.build_records(None, seed=0)
+    om = O.V3Model(g, recs, S.CODEBOOK)
+    dm = nd.V3Model(ctx, g, recs, S.CODEBOOK)
+    prompt = S.prompt_tokens(128, 4)
+    toks, margins = O.v3_generate(om, prompt, 256)
+    batch = nd.V3Batch(dm, 1, max_len=128 + 256)
+    got = batch.generate(prompt[None], 256)[0]
+    first_diff = int(np.argmax(got != toks)) if not np.array_equal(got, toks) else -1
+    print(f"shipped geometry: min margin {margins.min():.4e}, median {np.median(margins):.4e}, "
+          f"distinct {len(set(toks.tolist()))}, first difference at {first_diff}")
+    assert np.array_equal(got, toks.astype(np.int32)), first_diff
