@@ -30,6 +30,7 @@
 #include "nd_internal.h"
 #include "nd_kv_internal.h"
 #include "nd_libm.h"
+#include "nd_ref_order.h"
 
 #include <cmath>
 
@@ -38,7 +39,8 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kMaxBt = 8;             // activation rows per workgroup
 constexpr size_t kLdsBudget = 64 * 1024;
-constexpr int kAttnMaxCap = 16384;    // scores of one span live in LDS
+constexpr int kVChunk = 16384;        // bytes of V rows staged per pass
+constexpr int kAttnMaxCap = 12288;    // one span's scores + a V chunk fit 64 KB of LDS
 constexpr uint8_t kTernary = 5;
 
 struct CqExact {
@@ -51,86 +53,119 @@ struct CqExact {
     int in_padded, group, G, row_start, rows, batch, rpb, ternary;
 };
 
+// Up to kMaxSet weights with the same input, width and group in one launch:
+// blocks [tile0[k], tile0[k + 1]) work on weight k.
+constexpr int kMaxSet = 4;
+struct CqExactSet {
+    CqExact w[kMaxSet];
+    int tile0[kMaxSet + 1];
+    int n;
+};
+
 // cq.rs:948-958
 __device__ inline int ternary_index(int code) { return code == 3 ? 0 : (code == 1 ? 2 : 1); }
 
-template <int P, int BT>
-__global__ __launch_bounds__(kThreads) void cq_exact_kernel(CqExact a)
+// GR: the group size when it is 128 (codes preloaded into registers), or 0
+// for any other multiple of 8 (codes read as the loop needs them).
+template <int P, int BT, int GR>
+__global__ __launch_bounds__(kThreads) void cq_exact_kernel(CqExactSet set)
 {
+    int wk = set.n - 1;
+    while (wk > 0 && int(blockIdx.x) < set.tile0[wk]) --wk;
+    const CqExact &a = set.w[wk];
+    const int tile = int(blockIdx.x) - set.tile0[wk];
     constexpr int W = 8 / P;                // bits per code
     constexpr uint32_t MASK = (1u << W) - 1;
     constexpr int PER_DW = 32 / W;          // codes per dword (8 or 16)
+    constexpr int NDW = GR ? GR / PER_DW : 1;
     extern __shared__ __align__(16) float sm[];
     float *lvl = sm;                        // [16] code -> level
-    float *xs = sm + 16;                    // [BT][in_padded]
+    float *ns = sm + 16;                    // [kThreads] this block's norms
+    float *xs = sm + 16 + kThreads;         // [BT][in_padded]
     float *gs = xs + BT * a.in_padded;      // [BT][rpb * G] group sums
     const int tid = threadIdx.x;
     const int b0 = blockIdx.y * BT;
     const int nb = a.batch - b0 < BT ? a.batch - b0 : BT;
+    const int pairs = a.rpb * a.G;
+    const int r0 = a.row_start + tile * a.rpb;
+    const int row_end = a.row_start + a.rows;
+    const int nrows = row_end - r0 < a.rpb ? row_end - r0 : a.rpb;
     if (tid < 16) lvl[tid] = a.lv[a.ternary ? ternary_index(tid) : tid];
+    if (tid < nrows * a.G) ns[tid] = a.norms[size_t(r0) * a.G + tid];
     for (int bb = 0; bb < nb; ++bb) {
-        const float *src = a.xh + size_t(b0 + bb) * a.in_padded;
-        for (int e = tid; e < a.in_padded; e += kThreads) xs[bb * a.in_padded + e] = src[e];
+        const float4 *src = reinterpret_cast<const float4 *>(a.xh + size_t(b0 + bb) * a.in_padded);
+        float4 *dst = reinterpret_cast<float4 *>(xs + bb * a.in_padded);
+        for (int e = tid; e < a.in_padded / 4; e += kThreads) dst[e] = src[e];
+    }
+    // this thread's (row, group) and its codes
+    const int rl = tid / a.G, g = tid - rl * a.G;
+    const int r = r0 + rl;
+    const bool active = tid < pairs && rl < nrows;
+    const uint32_t *cw = reinterpret_cast<const uint32_t *>(
+        a.packed + size_t(active ? r : a.row_start) * a.row_bytes + size_t(g) * (a.group / P));
+    uint32_t code[NDW];
+    if (GR && active) {
+#pragma unroll
+        for (int k = 0; k < NDW; k += 4) {
+            const uint4 c4 = *reinterpret_cast<const uint4 *>(cw + k);
+            code[k] = c4.x;
+            code[k + 1] = c4.y;
+            code[k + 2] = c4.z;
+            code[k + 3] = c4.w;
+        }
     }
     __syncthreads();
-    const int pairs = a.rpb * a.G;
-    const int r0 = a.row_start + int(blockIdx.x) * a.rpb;
-    const int row_end = a.row_start + a.rows;
-    if (tid < pairs) {
-        const int rl = tid / a.G, g = tid - rl * a.G;
-        const int r = r0 + rl;
-        if (r < row_end) {
-            const uint32_t *cw = reinterpret_cast<const uint32_t *>(
-                a.packed + size_t(r) * a.row_bytes + size_t(g) * (a.group / P));
-            float lanes[BT][8];
+    if (active) {
+        float lanes[BT][8];
 #pragma unroll
-            for (int bb = 0; bb < BT; ++bb)
+        for (int bb = 0; bb < BT; ++bb)
 #pragma unroll
-                for (int k = 0; k < 8; ++k) lanes[bb][k] = 0.0f;
-            const int iters = a.group / 8;
-            const float *xg = xs + g * a.group;
-            for (int i = 0; i < iters; ++i) {
-                const uint32_t dw = cw[(i * 8) / PER_DW];
-                const int sh = (i * 8 * W) & 31;
-                float v[8];
+            for (int k = 0; k < 8; ++k) lanes[bb][k] = 0.0f;
+        const float *xg = xs + g * a.group;
+        // iteration i: elements 8i..8i+7 of the group, element 8i+k into lane k
+        auto step = [&](int i, uint32_t dw) {
+            const int sh = (i * 8 * W) & 31;
+            float v[8];
 #pragma unroll
-                for (int k = 0; k < 8; ++k) v[k] = lvl[(dw >> (sh + k * W)) & MASK];
-#pragma unroll
-                for (int bb = 0; bb < BT; ++bb) {
-                    if (bb < nb) {
-                        const float4 xa = *reinterpret_cast<const float4 *>(xg + bb * a.in_padded + i * 8);
-                        const float4 xb = *reinterpret_cast<const float4 *>(xg + bb * a.in_padded + i * 8 + 4);
-                        lanes[bb][0] += v[0] * xa.x;
-                        lanes[bb][1] += v[1] * xa.y;
-                        lanes[bb][2] += v[2] * xa.z;
-                        lanes[bb][3] += v[3] * xa.w;
-                        lanes[bb][4] += v[4] * xb.x;
-                        lanes[bb][5] += v[5] * xb.y;
-                        lanes[bb][6] += v[6] * xb.z;
-                        lanes[bb][7] += v[7] * xb.w;
-                    }
-                }
-            }
+            for (int k = 0; k < 8; ++k) v[k] = lvl[(dw >> (sh + k * W)) & MASK];
 #pragma unroll
             for (int bb = 0; bb < BT; ++bb) {
-                float acc = 0.0f;
-#pragma unroll
-                for (int k = 0; k < 8; ++k) acc += lanes[bb][k];
-                if (bb < nb) gs[bb * pairs + tid] = acc;
+                if (bb < nb) {
+                    const float4 xa = *reinterpret_cast<const float4 *>(xg + bb * a.in_padded + i * 8);
+                    const float4 xb = *reinterpret_cast<const float4 *>(xg + bb * a.in_padded + i * 8 + 4);
+                    lanes[bb][0] += v[0] * xa.x;
+                    lanes[bb][1] += v[1] * xa.y;
+                    lanes[bb][2] += v[2] * xa.z;
+                    lanes[bb][3] += v[3] * xa.w;
+                    lanes[bb][4] += v[4] * xb.x;
+                    lanes[bb][5] += v[5] * xb.y;
+                    lanes[bb][6] += v[6] * xb.z;
+                    lanes[bb][7] += v[7] * xb.w;
+                }
             }
+        };
+        if constexpr (GR != 0) {
+#pragma unroll
+            for (int i = 0; i < GR / 8; ++i) step(i, code[(i * 8) / PER_DW]);
+        } else {
+            for (int i = 0; i < a.group / 8; ++i) step(i, cw[(i * 8) / PER_DW]);
+        }
+#pragma unroll
+        for (int bb = 0; bb < BT; ++bb) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) acc += lanes[bb][k];
+            if (bb < nb) gs[bb * pairs + tid] = acc;
         }
     }
     __syncthreads();
-    for (int o = tid; o < a.rpb * nb; o += kThreads) {
-        const int bb = o / a.rpb, rl = o - bb * a.rpb;
-        const int r = r0 + rl;
-        if (r < row_end) {
-            const float *rn = a.norms + size_t(r) * a.G;
-            const float *gp = gs + bb * pairs + rl * a.G;
-            float total = 0.0f;
-            for (int g = 0; g < a.G; ++g) total += rn[g] * gp[g];
-            a.y[size_t(b0 + bb) * a.rows + (r - a.row_start)] = total;
-        }
+    for (int o = tid; o < nrows * nb; o += kThreads) {
+        const int bb = o / nrows, rr = o - bb * nrows;
+        const float *rn = ns + rr * a.G;
+        const float *gp = gs + bb * pairs + rr * a.G;
+        float total = 0.0f;
+        for (int gg = 0; gg < a.G; ++gg) total += rn[gg] * gp[gg];
+        a.y[size_t(b0 + bb) * a.rows + (r0 + rr - a.row_start)] = total;
     }
 }
 
@@ -195,66 +230,114 @@ __global__ __launch_bounds__(kThreads) void cq_exact_serial_kernel(CqSerial a)
     a.y[size_t(b) * a.rows + rl] = total;
 }
 
-template <int P, int BT>
-void launch_exact(const CqExact &a, hipStream_t s)
+size_t exact_lds(int bt, size_t in_padded, size_t pairs)
 {
-    const unsigned gx = unsigned((a.rows + a.rpb - 1) / a.rpb);
+    return 4 * (16 + size_t(kThreads) + size_t(bt) * in_padded + size_t(bt) * pairs);
+}
+
+template <int P, int BT>
+void launch_exact(const CqExactSet &set, hipStream_t s)
+{
+    const CqExact &a = set.w[0];
     const unsigned gy = unsigned((a.batch + BT - 1) / BT);
-    const size_t lds = 4 * (16 + size_t(BT) * a.in_padded + size_t(BT) * a.rpb * a.G);
-    hipLaunchKernelGGL((cq_exact_kernel<P, BT>), dim3(gx, gy), dim3(kThreads), lds, s, a);
+    const size_t lds = exact_lds(BT, a.in_padded, size_t(a.rpb) * a.G);
+    const dim3 grid(unsigned(set.tile0[set.n]), gy);
+    if (a.group == 128)
+        hipLaunchKernelGGL((cq_exact_kernel<P, BT, 128>), grid, dim3(kThreads), lds, s, set);
+    else
+        hipLaunchKernelGGL((cq_exact_kernel<P, BT, 0>), grid, dim3(kThreads), lds, s, set);
 }
 
 template <int P>
-void launch_bt(const CqExact &a, int bt, hipStream_t s)
+void launch_bt(const CqExactSet &set, int bt, hipStream_t s)
 {
     switch (bt) {
-    case 8: launch_exact<P, 8>(a, s); break;
-    case 4: launch_exact<P, 4>(a, s); break;
-    case 2: launch_exact<P, 2>(a, s); break;
-    default: launch_exact<P, 1>(a, s); break;
+    case 8: launch_exact<P, 8>(set, s); break;
+    case 4: launch_exact<P, 4>(set, s); break;
+    case 2: launch_exact<P, 2>(set, s); break;
+    default: launch_exact<P, 1>(set, s); break;
     }
 }
 
-int cq_exact(nd_ctx *ctx, const nd_cq *w, const float *xh, size_t batch, size_t row_start,
-             size_t rows, float *y, const char *what)
+int cq_serial(hipStream_t stream, const nd_cq *w, const float *xh, size_t batch,
+              size_t row_start, size_t rows, float *y, const char *what)
 {
-    if (int rc = nd::enter(ctx)) return rc;
-    ND_REQUIRE(w && xh && y, "%s: null argument", what);
-    if (rows == 0 || batch == 0) return ND_OK;
-    ND_REQUIRE(row_start <= w->out_feat && rows <= w->out_feat - row_start,
-               "%s: rows %zu..%zu outside %zu", what, row_start, row_start + rows, w->out_feat);
-    ND_REQUIRE(w->out_feat < (1u << 30) && batch <= 65535u * kMaxBt && w->in_padded < (1u << 24),
-               "%s: shape too large", what);
-    const size_t G = w->num_groups;
-    const int P = int(w->per_byte);
-    const bool fast = (P == 2 || P == 4) && w->group % 8 == 0 && (w->group / P) % 4 == 0 && G <= kThreads &&
-                      w->row_bytes % 4 == 0;
-    if (fast) {
-        const int rpb = int(kThreads / G);
-        int bt = kMaxBt;
-        while (bt > 1 && (size_t(bt) / 2 >= batch ||
-                          4 * (16 + size_t(bt) * w->in_padded + size_t(bt) * rpb * G) > kLdsBudget))
-            bt /= 2;
-        if (4 * (16 + size_t(bt) * w->in_padded + size_t(bt) * rpb * G) <= kLdsBudget) {
-            CqExact a{w->packed, w->norms, w->lv, xh, y, w->row_bytes, int(w->in_padded),
-                      int(w->group), int(G), int(row_start), int(rows), int(batch), rpb,
-                      int(w->bits == kTernary)};
-            if (P == 4)
-                launch_bt<4>(a, bt, ctx->stream);
-            else
-                launch_bt<2>(a, bt, ctx->stream);
-            return nd::check_launch(what);
-        }
-    }
     const size_t total = batch * rows;
     ND_REQUIRE((total + kThreads - 1) / kThreads <= 0x7fffffffu, "%s: too many outputs", what);
     CqSerial a{w->packed, w->norms, w->lut, w->lv, xh, y, w->row_bytes, int(w->in_padded),
-               int(w->group), int(G), int(row_start), int(rows), int(batch), P,
-               int(w->bits == kTernary ? 2 : w->bits)};
+               int(w->group), int(w->num_groups), int(row_start), int(rows), int(batch),
+               int(w->per_byte), int(w->bits == kTernary ? 2 : w->bits)};
     hipLaunchKernelGGL(cq_exact_serial_kernel, dim3(unsigned((total + kThreads - 1) / kThreads)),
-                       dim3(kThreads), 0, ctx->stream, a);
+                       dim3(kThreads), 0, stream, a);
     return nd::check_launch(what);
 }
+
+}  // namespace
+
+// n weights sharing the input xh ([batch][in_padded]); y[k] gets
+// rows[k] rows of weight k from row_start[k], batch-major.
+int nd_cq_exact_set(nd_ctx *ctx, hipStream_t stream, int n, const nd_cq *const *w, const float *xh,
+                    size_t batch, const size_t *row_start, const size_t *rows, float *const *y,
+                    const char *what)
+{
+    if (int rc = nd::enter(ctx)) return rc;
+    ND_REQUIRE(n >= 1 && n <= kMaxSet && w && xh && row_start && rows && y, "%s: bad arguments",
+               what);
+    if (batch == 0) return ND_OK;
+    const nd_cq *w0 = w[0];
+    bool same = true;
+    for (int k = 0; k < n; ++k) {
+        ND_REQUIRE(w[k] && y[k], "%s: null weight or output", what);
+        ND_REQUIRE(row_start[k] <= w[k]->out_feat && rows[k] <= w[k]->out_feat - row_start[k],
+                   "%s: rows %zu..%zu outside %zu", what, row_start[k], row_start[k] + rows[k],
+                   w[k]->out_feat);
+        ND_REQUIRE(w[k]->out_feat < (1u << 30) && w[k]->in_padded < (1u << 24),
+                   "%s: shape too large", what);
+        same = same && w[k]->per_byte == w0->per_byte && w[k]->group == w0->group &&
+               w[k]->in_padded == w0->in_padded && w[k]->bits == w0->bits;
+    }
+    ND_REQUIRE(batch <= 65535u * kMaxBt, "%s: batch too large", what);
+    const size_t G = w0->num_groups;
+    const int P = int(w0->per_byte);
+    const bool fast = same && (P == 2 || P == 4) && w0->group % 8 == 0 && (w0->group / P) % 4 == 0 &&
+                      G <= kThreads && w0->row_bytes % 4 == 0 &&
+                      (reinterpret_cast<uintptr_t>(xh) & 15) == 0;
+    if (fast) {
+        const int rpb = int(kThreads / G);
+        const size_t pairs = size_t(rpb) * G;
+        int bt = kMaxBt;
+        while (bt > 1 && (size_t(bt) / 2 >= batch || exact_lds(bt, w0->in_padded, pairs) > kLdsBudget))
+            bt /= 2;
+        if (exact_lds(bt, w0->in_padded, pairs) <= kLdsBudget) {
+            CqExactSet set{};
+            set.n = 0;
+            int tiles = 0;
+            for (int k = 0; k < n; ++k) {
+                if (rows[k] == 0) continue;
+                set.w[set.n] = CqExact{w[k]->packed, w[k]->norms, w[k]->lv, xh, y[k], w[k]->row_bytes,
+                                       int(w[k]->in_padded), int(w[k]->group), int(G),
+                                       int(row_start[k]), int(rows[k]), int(batch), rpb,
+                                       int(w[k]->bits == kTernary)};
+                set.tile0[set.n++] = tiles;
+                tiles += int((rows[k] + rpb - 1) / rpb);
+            }
+            if (set.n == 0) return ND_OK;
+            set.tile0[set.n] = tiles;
+            if (P == 4)
+                launch_bt<4>(set, bt, stream);
+            else
+                launch_bt<2>(set, bt, stream);
+            return nd::check_launch(what);
+        }
+    }
+    for (int k = 0; k < n; ++k)
+        if (rows[k])
+            if (int rc = cq_serial(stream, w[k], xh, batch, row_start[k], rows[k], y[k], what))
+                return rc;
+    return ND_OK;
+}
+
+namespace {
 
 // ---------------------------------------------------------------------------
 // attend_step over the int8 view, in the reference's order.
@@ -325,14 +408,18 @@ __global__ __launch_bounds__(kThreads) void attn_exact_kernel(ndkv::Geom g,
     for (int t = tid; t < span; t += kThreads) sc[t] = nd_expf(sc[t] - mx);
     __syncthreads();
     if (tid == 0) {
+        // the softmax sum: one chain in position order
         float s = 0.0f;
         int t = 0;
-        for (; t + 4 <= span; t += 4) {
-            const float4 v = *reinterpret_cast<const float4 *>(sc + t);
-            s += v.x;
-            s += v.y;
-            s += v.z;
-            s += v.w;
+        for (; t + 16 <= span; t += 16) {
+            const float4 a = *reinterpret_cast<const float4 *>(sc + t);
+            const float4 b = *reinterpret_cast<const float4 *>(sc + t + 4);
+            const float4 c = *reinterpret_cast<const float4 *>(sc + t + 8);
+            const float4 d = *reinterpret_cast<const float4 *>(sc + t + 12);
+            s += a.x; s += a.y; s += a.z; s += a.w;
+            s += b.x; s += b.y; s += b.z; s += b.w;
+            s += c.x; s += c.y; s += c.z; s += c.w;
+            s += d.x; s += d.y; s += d.z; s += d.w;
         }
         for (; t < span; ++t) s += sc[t];
         total = s;
@@ -345,18 +432,39 @@ __global__ __launch_bounds__(kThreads) void attn_exact_kernel(ndkv::Geom g,
         if (slot >= g.cap) slot -= g.cap;
         sc[t] = sc[t] * inv * vs[slot];
     }
-    __syncthreads();
+    // Output column j: one chain over the span in position order.  V rows
+    // are staged through LDS a chunk at a time so the chain reads LDS.
+    int8_t *vl = reinterpret_cast<int8_t *>(sc + ((g.cap + 3) & ~3));
     const int8_t *vb = reinterpret_cast<const int8_t *>(blk + g.v_off) + size_t(kvh) * g.cap * g.VD;
-    float *o = out + (i * g.H + h) * size_t(g.VD);
-    for (int j = tid; j < g.VD; j += kThreads) {
-        float acc = 0.0f;
-        int slot = base;
-        for (int t = 0; t < span; ++t) {
-            acc += sc[t] * float(vb[size_t(slot) * g.VD + j]);
-            if (++slot == g.cap) slot = 0;
+    const int pieces = g.VD / 16;        // 16-byte pieces per V row
+    const int chunk = kVChunk / g.VD;    // positions per pass
+    float acc = 0.0f;
+    for (int c0 = 0; c0 < span; c0 += chunk) {
+        const int cn = span - c0 < chunk ? span - c0 : chunk;
+        __syncthreads();  // weights written / previous chunk consumed
+        for (int e = tid; e < cn * pieces; e += kThreads) {
+            const int t = e / pieces, pc = e - t * pieces;
+            int slot = base + c0 + t;
+            if (slot >= g.cap) slot -= g.cap;
+            reinterpret_cast<uint4 *>(vl)[e] =
+                *reinterpret_cast<const uint4 *>(vb + size_t(slot) * g.VD + pc * 16);
         }
-        o[j] = acc;
+        __syncthreads();
+        if (tid < g.VD) {
+            const float *w = sc + c0;
+            const int8_t *col = vl + tid;
+            int t = 0;
+            for (; t + 8 <= cn; t += 8) {
+                float p[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) p[u] = w[t + u] * float(col[(t + u) * g.VD]);
+#pragma unroll
+                for (int u = 0; u < 8; ++u) acc += p[u];
+            }
+            for (; t < cn; ++t) acc += w[t] * float(col[t * g.VD]);
+        }
     }
+    if (tid < g.VD) out[(i * g.H + h) * size_t(g.VD) + tid] = acc;
 }
 
 }  // namespace
@@ -366,13 +474,15 @@ extern "C" {
 int nd_cq_matvec_rows_exact(nd_ctx *ctx, const nd_cq *w, const float *xh, size_t row_start,
                             size_t rows, float *y)
 {
-    return cq_exact(ctx, w, xh, 1, row_start, rows, y, "cq_matvec_exact");
+    return nd_cq_exact_set(ctx, ctx ? ctx->stream : nullptr, 1, &w, xh, 1, &row_start, &rows, &y,
+                           "cq_matvec_exact");
 }
 
 int nd_cq_matmul_rows_exact(nd_ctx *ctx, const nd_cq *w, const float *xh, size_t batch,
                             size_t row_start, size_t rows, float *y)
 {
-    return cq_exact(ctx, w, xh, batch, row_start, rows, y, "cq_matmul_exact");
+    return nd_cq_exact_set(ctx, ctx ? ctx->stream : nullptr, 1, &w, xh, batch, &row_start, &rows, &y,
+                           "cq_matmul_exact");
 }
 
 int nd_attend_step_i8_exact(nd_ctx *ctx, const nd_kv_geom *g, const void *kv, size_t kv_stride,
@@ -389,7 +499,8 @@ int nd_attend_step_i8_exact(nd_ctx *ctx, const nd_kv_geom *g, const void *kv, si
     ND_REQUIRE((reinterpret_cast<uintptr_t>(kv) & 255) == 0 && kv_stride % 256 == 0,
                "kv blocks must be 256-byte aligned");
     dim3 grid(unsigned(g->num_heads), unsigned(count));
-    hipLaunchKernelGGL(attn_exact_kernel, grid, dim3(kThreads), size_t(g->cap) * 4, ctx->stream,
+    const size_t lds = size_t((g->cap + 3) & ~3) * 4 + kVChunk;
+    hipLaunchKernelGGL(attn_exact_kernel, grid, dim3(kThreads), lds, ctx->stream,
                        ndkv::make_geom(g), static_cast<const uint8_t *>(kv), kv_stride, lo, hi, q,
                        scale, quant_query, out);
     return nd::check_launch("attn_exact");

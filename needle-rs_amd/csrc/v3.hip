@@ -25,8 +25,11 @@
 // folds sequentially (norms, the Engram gate, the conditioning projection,
 // lane sums) is one sequential chain on one thread, in the reference's
 // index order; exp and log are libm's algorithms (nd_libm.h).
+#include "nd_cq_internal.h"
 #include "nd_internal.h"
+#include "nd_kv_internal.h"
 #include "nd_libm.h"
+#include "nd_ref_order.h"
 
 #include <cmath>
 #include <cstring>
@@ -40,33 +43,67 @@ constexpr int kT = 256;
 
 __device__ inline float sigmoidf_(float x) { return nd_sigmoidf(x); }
 
-// sum_i a[i] * b[i] for i = 0..n-1 as one left-to-right chain (a sequential
-// fold, as the reference's loops and iterator sums); run by one thread.
-__device__ inline float dot_chain(const float *a, const float *b, int n)
+// ((0 + p[0]) + p[1]) + ... + p[n-1]: a sequential fold, as the reference's
+// loops and iterator sums, run by one thread over values already in LDS
+// (16-byte aligned).  Products are formed in parallel beforehand; a product
+// rounds the same whether it is formed here or inside the fold.
+__device__ inline float chain_sum(const float *p, int n)
 {
     float s = 0.0f;
     int i = 0;
-    if (((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15) == 0) {
-        for (; i + 8 <= n; i += 8) {
-            const float4 a0 = *reinterpret_cast<const float4 *>(a + i);
-            const float4 a1 = *reinterpret_cast<const float4 *>(a + i + 4);
-            const float4 b0 = *reinterpret_cast<const float4 *>(b + i);
-            const float4 b1 = *reinterpret_cast<const float4 *>(b + i + 4);
-            s += a0.x * b0.x;
-            s += a0.y * b0.y;
-            s += a0.z * b0.z;
-            s += a0.w * b0.w;
-            s += a1.x * b1.x;
-            s += a1.y * b1.y;
-            s += a1.z * b1.z;
-            s += a1.w * b1.w;
+    if ((reinterpret_cast<uintptr_t>(p) & 15) == 0 && n >= 16) {
+        // the next 16 values load while the current 16 are added
+        const float4 *q = reinterpret_cast<const float4 *>(p);
+        float4 a = q[0], b = q[1], c = q[2], e = q[3];
+        for (; i + 32 <= n; i += 16) {
+            const float4 a2 = q[(i >> 2) + 4], b2 = q[(i >> 2) + 5], c2 = q[(i >> 2) + 6],
+                         e2 = q[(i >> 2) + 7];
+            s += a.x; s += a.y; s += a.z; s += a.w;
+            s += b.x; s += b.y; s += b.z; s += b.w;
+            s += c.x; s += c.y; s += c.z; s += c.w;
+            s += e.x; s += e.y; s += e.z; s += e.w;
+            a = a2;
+            b = b2;
+            c = c2;
+            e = e2;
         }
+        s += a.x; s += a.y; s += a.z; s += a.w;
+        s += b.x; s += b.y; s += b.z; s += b.w;
+        s += c.x; s += c.y; s += c.z; s += c.w;
+        s += e.x; s += e.y; s += e.z; s += e.w;
+        i += 16;
     }
-    for (; i < n; ++i) s += a[i] * b[i];
+    for (; i < n; ++i) s += p[i];
     return s;
 }
 
-__device__ inline float sumsq_chain(const float *x, int n) { return dot_chain(x, x, n); }
+// CqWeight::prepare_input's normalised FWHT (hadamard.rs:24-55) over the
+// n / group groups of buf (LDS), in place: the butterfly pairs of a stage
+// are disjoint, so evaluating them in parallel gives the sequential loop's
+// bits; then x * (1 / sqrtf(group)).  Every thread of the block calls it,
+// after buf is written and synchronised.
+__device__ inline void fwht_groups_lds(float *buf, int n, int group, float inv)
+{
+    const int half = group / 2, pairs = n / 2;
+    for (int h = 1; h < group; h <<= 1) {
+        for (int e = threadIdx.x; e < pairs; e += blockDim.x) {
+            const int g = e / half, i = e - g * half;
+            const int jj = g * group + (i / h) * (2 * h) + (i % h);
+            const float a = buf[jj], c = buf[jj + h];
+            buf[jj] = a + c;
+            buf[jj + h] = a - c;
+        }
+        __syncthreads();
+    }
+    for (int e = threadIdx.x; e < n; e += blockDim.x) buf[e] *= inv;
+    __syncthreads();
+}
+
+// Geometry of a prepared input: in_padded floats in groups of `group`.
+struct Prep {
+    int in_padded, group;
+    float inv;  // 1 / sqrtf(group)
+};
 
 // ---- embedding broadcast: lanes[b][l][c] = emb[b][c] * scale ---------------
 __global__ void k_embed(const float *__restrict__ emb, float *__restrict__ lanes, float scale,
@@ -79,16 +116,24 @@ __global__ void k_embed(const float *__restrict__ emb, float *__restrict__ lanes
     }
 }
 
-// ---- rms_unit over a row (kernels.rs:33-41) ----------------------------------
-__global__ __launch_bounds__(kT) void k_rms_unit(const float *__restrict__ x, float *__restrict__ out,
-                                                int n)
+// mhc.rs:111-152, scatter up: lanes[i] = sum_j H_res[i][j] lanes[j] +
+// H_post[i] y, for one channel c (j ascending), into `ln` (LDS) and the
+// global lanes.
+__device__ inline void scatter_up(float *lg, float *ln, const float *gp, const float *gr,
+                                  const float *y, int n, int d)
 {
-    __shared__ float tot;
-    const size_t b = blockIdx.x;
-    if (threadIdx.x == 0) tot = sumsq_chain(x + b * n, n);
-    __syncthreads();
-    const float inv = 1.0f / sqrtf(tot / float(n) + 1e-6f);
-    for (int i = threadIdx.x; i < n; i += kT) out[b * n + i] = x[b * n + i] * inv;
+    for (int c = threadIdx.x; c < d; c += blockDim.x) {
+        float old[16];
+        for (int j = 0; j < n; ++j) old[j] = lg[size_t(j) * d + c];
+        const float yc = y[c];
+        for (int i = 0; i < n; ++i) {
+            float acc = 0.0f;
+            for (int j = 0; j < n; ++j) acc += gr[i * n + j] * old[j];
+            const float v = acc + gp[i] * yc;
+            lg[size_t(i) * d + c] = v;
+            ln[i * d + c] = v;
+        }
+    }
 }
 
 // ---- Engram value conv step (cache.rs:445-482) -------------------------------
@@ -114,77 +159,185 @@ __global__ void k_engram_conv(float *__restrict__ ev, const float *__restrict__ 
     ev[b * d + c] = acc;
 }
 
-// ---- mHC mix down + Engram gate + ZCRMSNorm ----------------------------------
-struct MhcIn {
-    const float *hraw;   // [B][n]  nx . phi_pre rows of this layer
-    const float *lanes;  // [B][n][d]
-    const float *b_pre;  // [n] this layer's slice
+// ---- layer input: the previous layer's scatter up, then this layer's mix
+// down (mhc.rs:80-103): rms_unit of the lanes, prepare_input, the phi_pre
+// rows, the gated lane sum, the Engram gate and ZCRMSNorm, prepared for the
+// q/k/v/gate projections.  One workgroup per session.
+constexpr int kMaxLanesD = 4096;  // mhc_lanes * d_model
+constexpr int kMaxPhiPairs = 512; // mhc_lanes * (phi input groups)
+
+struct LayerIn {
+    float *lanes;             // [B][n][d]
+    const float *y;           // [B][d]     previous layer's block delta   (update)
+    const float *gp, *gr;     // [B][n], [B][n*n] previous layer's gates (update)
+    int update;
+    float *nxh;               // [B][pnx.in_padded] prepared rms_unit(lanes)
+    Prep pnx;
+    const uint8_t *phi_packed;  // phi_pre
+    const float *phi_norms, *phi_lv;
+    size_t phi_row_bytes;
+    int phi_G, phi_row0, phi_ternary;
+    const float *b_pre;       // [n] this layer's slice
     float a_pre;
     int layer, n, d;
-    const float *ek, *ev;  // [B][d] this layer's Engram site, or null
-    const float *norm_in;  // [d]
-    float *u, *bx, *h;     // [B][d]
+    const float *ek, *ev;     // [B][d] this layer's Engram site, or null
+    const float *norm_in;     // [d]
+    float *u, *bx;            // [B][d]
+    float *hh;                // [B][ph.in_padded]
+    Prep ph;
 };
 
-__global__ __launch_bounds__(kT) void k_mhc_in(MhcIn a)
+template <int PP>
+__global__ __launch_bounds__(kT) void k_layer_in(LayerIn a)
 {
-    __shared__ float hp[16], tot[4];
-    __shared__ __align__(16) float us[1024], bxs[1024];
+    constexpr int kCh = 1024 / kT;  // model-dim channels per thread
+    __shared__ __align__(16) float ln[kMaxLanesD], nb[kMaxLanesD];
+    __shared__ __align__(16) float us[1024], bxs[1024], pa[1024], pb[1024], pc[1024];
+    __shared__ float gs[kMaxPhiPairs], pn[kMaxPhiPairs], lvl[16], hp[16], gpp[16], grr[256], tot[4];
     const size_t b = blockIdx.x;
-    const int d = a.d, n = a.n;
-    if (threadIdx.x < n) {
-        const int lane = threadIdx.x;
-        const float off = lane == a.layer % n ? 4.0f : -4.0f;
-        hp[lane] = sigmoidf_(a.a_pre * a.hraw[b * n + lane] + a.b_pre[lane] + off);
+    const int tid = threadIdx.x, n = a.n, d = a.d, nd = n * d;
+    const int G = a.phi_G, pairs = n * G;
+    float *lg = a.lanes + b * size_t(nd);
+    // global operands issued up front: this thread's phi_pre group codes
+    // and norm, and its channels' norm_in / Engram key and value
+    CqGroupCodes<PP> codes;
+    const bool has_pair = tid < pairs;
+    {
+        const int r = has_pair ? tid / G : 0, g = has_pair ? tid - (tid / G) * G : 0;
+        cq_group_codes128<PP>(a.phi_packed + size_t(a.phi_row0 + r) * a.phi_row_bytes +
+                                  size_t(g) * (128 / PP),
+                              codes);
+        if (has_pair) pn[tid] = a.phi_norms[size_t(a.phi_row0 + r) * G + g];
+    }
+    const float *ek = a.ek ? a.ek + b * d : nullptr;
+    float nin[kCh], ekv[kCh], evv[kCh];
+#pragma unroll
+    for (int k = 0; k < kCh; ++k) {
+        const int c = tid + k * kT;
+        nin[k] = c < d ? a.norm_in[c] : 0.0f;
+        ekv[k] = ek && c < d ? ek[c] : 0.0f;
+        evv[k] = ek && c < d ? a.ev[b * d + c] : 0.0f;
+    }
+    const float bpre = tid < n ? a.b_pre[tid] : 0.0f;
+    if (tid < 16) lvl[tid] = a.phi_lv[a.phi_ternary ? (tid == 3 ? 0 : (tid == 1 ? 2 : 1)) : tid];
+    if (a.update) {
+        if (tid < n) gpp[tid] = a.gp[b * n + tid];
+        if (tid < n * n) grr[tid] = a.gr[b * n * n + tid];
+        __syncthreads();
+        scatter_up(lg, ln, gpp, grr, a.y + b * d, n, d);
+    } else {
+        for (int e = tid; e < nd; e += kT) ln[e] = lg[e];
     }
     __syncthreads();
-    const float *lb = a.lanes + b * size_t(n) * d;
-    for (int c = threadIdx.x; c < d; c += kT) {
+    // rms_unit (kernels.rs:33-41): products, then one chain
+    for (int e = tid; e < nd; e += kT) nb[e] = ln[e] * ln[e];
+    __syncthreads();
+    if (tid == 0) tot[0] = chain_sum(nb, nd);
+    __syncthreads();
+    {
+        const float inv = 1.0f / sqrtf(tot[0] / float(nd) + 1e-6f);
+        for (int e = tid; e < a.pnx.in_padded; e += kT) nb[e] = e < nd ? ln[e] * inv : 0.0f;
+    }
+    __syncthreads();
+    fwht_groups_lds(nb, a.pnx.in_padded, a.pnx.group, a.pnx.inv);
+    for (int e = tid; e < a.pnx.in_padded; e += kT) a.nxh[b * a.pnx.in_padded + e] = nb[e];
+    // phi_pre rows of this layer (matvec_rows_prepared, reference order)
+    if (has_pair) gs[tid] = cq_group_dot128<PP>(codes, lvl, nb + (tid % G) * 128);
+    for (int t = tid + kT; t < pairs; t += kT) {  // more pairs than threads
+        const int r = t / G, g = t - r * G;
+        CqGroupCodes<PP> more;
+        cq_group_codes128<PP>(a.phi_packed + size_t(a.phi_row0 + r) * a.phi_row_bytes +
+                                  size_t(g) * (128 / PP),
+                              more);
+        gs[t] = cq_group_dot128<PP>(more, lvl, nb + g * 128);
+        pn[t] = a.phi_norms[size_t(a.phi_row0 + r) * G + g];
+    }
+    __syncthreads();
+    if (tid < n) {
+        float total = 0.0f;
+        for (int g = 0; g < G; ++g) total += pn[tid * G + g] * gs[tid * G + g];
+        const float off = tid == a.layer % n ? 4.0f : -4.0f;
+        hp[tid] = sigmoidf_(a.a_pre * total + bpre + off);
+    }
+    __syncthreads();
+    // gated lane sum, Engram gate (engram.rs:111-132), ZCRMSNorm (norm.rs:23-30)
+#pragma unroll
+    for (int k = 0; k < kCh; ++k) {
+        const int c = tid + k * kT;
+        if (c >= d) continue;
         float acc = 0.0f;
-        for (int l = 0; l < n; ++l) acc += hp[l] * lb[size_t(l) * d + c];
+        for (int l = 0; l < n; ++l) acc += hp[l] * ln[l * d + c];
         us[c] = acc;
         a.u[b * d + c] = acc;
+        if (ek) {
+            pa[c] = acc * acc;
+            pb[c] = ekv[k] * ekv[k];
+            pc[c] = acc * ekv[k];
+        }
     }
     __syncthreads();
-    if (a.ek) {
-        // engram.rs:111-132: three sequential sums, one per wave
-        const float *ek = a.ek + b * d;
-        if (threadIdx.x == 0) tot[0] = sumsq_chain(us, d);
-        if (threadIdx.x == 64) tot[1] = sumsq_chain(ek, d);
-        if (threadIdx.x == 128) tot[2] = dot_chain(us, ek, d);
+    if (ek) {
+        // three sequential sums, side by side on lanes 0-2
+        if (tid < 3) tot[1 + tid] = chain_sum(tid == 0 ? pa : (tid == 1 ? pb : pc), d);
         __syncthreads();
-        const float ux = 1.0f / sqrtf(tot[0] / float(d) + 1e-6f);
-        const float uk = 1.0f / sqrtf(tot[1] / float(d) + 1e-6f);
-        const float alpha = sigmoidf_(tot[2] * ux * uk / sqrtf(float(d)));
-        for (int c = threadIdx.x; c < d; c += kT) bxs[c] = us[c] + alpha * a.ev[b * d + c];
+        const float ux = 1.0f / sqrtf(tot[1] / float(d) + 1e-6f);
+        const float uk = 1.0f / sqrtf(tot[2] / float(d) + 1e-6f);
+        const float alpha = sigmoidf_(tot[3] * ux * uk / sqrtf(float(d)));
+#pragma unroll
+        for (int k = 0; k < kCh; ++k) {
+            const int c = tid + k * kT;
+            if (c >= d) continue;
+            const float v = us[c] + alpha * evv[k];
+            bxs[c] = v;
+            pa[c] = v * v;
+        }
     } else {
-        for (int c = threadIdx.x; c < d; c += kT) bxs[c] = us[c];
+        for (int c = tid; c < d; c += kT) {
+            bxs[c] = us[c];
+            pa[c] = us[c] * us[c];
+        }
     }
     __syncthreads();
-    if (threadIdx.x == 0) tot[3] = sumsq_chain(bxs, d);
+    if (tid == 0) tot[0] = chain_sum(pa, d);
     __syncthreads();
-    const float inv = 1.0f / sqrtf(tot[3] / float(d) + 1e-6f);
-    for (int c = threadIdx.x; c < d; c += kT) {
-        a.bx[b * d + c] = bxs[c];
-        a.h[b * d + c] = (1.0f + a.norm_in[c]) * bxs[c] * inv;
+    const float inv = 1.0f / sqrtf(tot[0] / float(d) + 1e-6f);
+#pragma unroll
+    for (int k = 0; k < kCh; ++k) {
+        const int c = tid + k * kT;
+        if (c < d) {
+            a.bx[b * d + c] = bxs[c];
+            pa[c] = (1.0f + nin[k]) * bxs[c] * inv;
+        }
     }
+    for (int c = d + tid; c < a.ph.in_padded; c += kT) pa[c] = 0.0f;
+    __syncthreads();
+    fwht_groups_lds(pa, a.ph.in_padded, a.ph.group, a.ph.inv);
+    for (int c = tid; c < a.ph.in_padded; c += kT) a.hh[b * a.ph.in_padded + c] = pa[c];
 }
 
-// ---- conv step over q/k/v, then ZCRMSNorm + RoPE on q and k -------------------
-struct QkvPost {
-    float *q, *k, *v;                     // [B][dim]
-    float *qt, *kt, *vt;                  // tails [B][taps-1][dim]
+// ---- after the projections: causal conv step over q/k/v with the retained
+// tails (cache.rs:401-438), ZCRMSNorm + RoPE on q and k
+// (attention.rs:108-150), q to global, and k and v quantised straight into
+// the session's int8 KV block at slot pos % cap (write_kv, cache.rs:346-379).
+struct QkvKv {
+    float *q;                               // [B][qd] in: projection, out: normed + roped
+    const float *k, *v;                     // [B][kd], [B][vd] projections
+    float *qt, *kt, *vt;                    // tails [B][taps-1][dim]
     const float *q_taps, *k_taps, *v_taps;  // [taps][dim]
-    const float *q_norm, *k_norm;          // [hd]
-    const float *rope;                     // [B][2][hd/2]: cos then sin
+    const float *q_norm, *k_norm;           // [hd]
+    const float *rope;                      // [B][2][hd/2]: cos then sin
     const int32_t *pos;
-    int qd, kd, vd, taps, H, KVH, hd;
+    int qd, kd, vd, taps, H, KVH, hd, VD;
+    uint8_t *kv;                            // session b's block at kv + b * kv_stride
+    size_t kv_stride, v_off, ks_off, vs_off;
+    int cap;
 };
 
-__device__ inline void conv_one(float *x, float *tail, const float *taps, int dim, int c, int T,
-                                int p)
+// cache.rs:401-438 for one channel: the conv output, with the tail shifted
+// and the raw value retained.
+__device__ inline float conv_one(float raw, float *tail, const float *taps, int dim, int c, int T,
+                                 int p)
 {
-    const float raw = x[c];
     float acc = taps[c] * raw;
     for (int j = 1; j < T; ++j) {
         if (j > p) break;
@@ -192,78 +345,105 @@ __device__ inline void conv_one(float *x, float *tail, const float *taps, int di
     }
     for (int r = 0; r + 2 < T; ++r) tail[size_t(r) * dim + c] = tail[size_t(r + 1) * dim + c];
     if (T > 1) tail[size_t(T - 2) * dim + c] = raw;
-    x[c] = acc;
+    return acc;
 }
 
-__global__ __launch_bounds__(kT) void k_qkv_post(QkvPost a)
+constexpr int kMaxQkDims = 2048;  // (num_heads + num_kv_heads) * qk_head_dim
+constexpr int kMaxVDims = 1024;   // num_kv_heads * v_head_dim
+
+__global__ __launch_bounds__(kT) void k_qkv_kv(QkvKv a)
 {
+    __shared__ __align__(16) float qk[kMaxQkDims], sq[kMaxQkDims], vl[kMaxVDims];
+    __shared__ float rms[64];
     const size_t b = blockIdx.x;
-    const int p = a.pos[b], T = a.taps;
-    if (T > 0) {
-        for (int c = threadIdx.x; c < a.qd + a.kd + a.vd; c += kT) {
-            if (c < a.qd)
-                conv_one(a.q + b * a.qd, a.qt + b * size_t(T - 1) * a.qd, a.q_taps, a.qd, c, T, p);
-            else if (c < a.qd + a.kd)
-                conv_one(a.k + b * a.kd, a.kt + b * size_t(T - 1) * a.kd, a.k_taps, a.kd, c - a.qd,
-                         T, p);
-            else
-                conv_one(a.v + b * a.vd, a.vt + b * size_t(T - 1) * a.vd, a.v_taps, a.vd,
-                         c - a.qd - a.kd, T, p);
+    const int p = a.pos[b], T = a.taps, hd = a.hd, half = hd / 2;
+    const int nq = a.qd + a.kd, heads = a.H + a.KVH;
+    for (int c = threadIdx.x; c < nq + a.vd; c += kT) {
+        if (c < a.qd) {
+            float v = a.q[b * a.qd + c];
+            if (T > 0) v = conv_one(v, a.qt + b * size_t(T - 1) * a.qd, a.q_taps, a.qd, c, T, p);
+            qk[c] = v;
+            sq[c] = v * v;
+        } else if (c < nq) {
+            float v = a.k[b * a.kd + c - a.qd];
+            if (T > 0)
+                v = conv_one(v, a.kt + b * size_t(T - 1) * a.kd, a.k_taps, a.kd, c - a.qd, T, p);
+            qk[c] = v;
+            sq[c] = v * v;
+        } else {
+            float v = a.v[b * a.vd + c - nq];
+            if (T > 0)
+                v = conv_one(v, a.vt + b * size_t(T - 1) * a.vd, a.v_taps, a.vd, c - nq, T, p);
+            vl[c - nq] = v;
         }
     }
     __syncthreads();
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = a.hd / 2;
+    // one sequential sum of squares per head, the heads side by side
+    if (threadIdx.x < heads)
+        rms[threadIdx.x] = sqrtf(chain_sum(sq + threadIdx.x * hd, hd) / float(hd) + 1e-6f);
+    __syncthreads();
     const float *cs = a.rope + b * 2 * half, *sn = cs + half;
-    for (int hh = wave; hh < a.H + a.KVH; hh += kT / 64) {
-        float *x = hh < a.H ? a.q + b * a.qd + hh * a.hd : a.k + b * a.kd + (hh - a.H) * a.hd;
+    for (int e = threadIdx.x; e < heads * half; e += kT) {
+        const int hh = e / half, i = e - hh * half;
         const float *sc = hh < a.H ? a.q_norm : a.k_norm;
-        float sq = lane == 0 ? sumsq_chain(x, a.hd) : 0.0f;
-        sq = __shfl(sq, 0, 64);
-        const float rms = sqrtf(sq / float(a.hd) + 1e-6f);
-        for (int i = lane; i < half; i += 64) {
-            const float x1 = (1.0f + sc[i]) * x[i] / rms;
-            const float x2 = (1.0f + sc[half + i]) * x[half + i] / rms;
-            const float c = cs[i], s = sn[i];
-            x[i] = x1 * c - x2 * s;
-            x[half + i] = x2 * c + x1 * s;
+        const float *x = qk + hh * hd;
+        const float r = rms[hh];
+        const float x1 = (1.0f + sc[i]) * x[i] / r;
+        const float x2 = (1.0f + sc[half + i]) * x[half + i] / r;
+        const float c = cs[i], s = sn[i];
+        const float o1 = x1 * c - x2 * s, o2 = x2 * c + x1 * s;
+        if (hh < a.H) {
+            float *o = a.q + b * a.qd + hh * hd;
+            o[i] = o1;
+            o[half + i] = o2;
+        } else {
+            sq[hh * hd + i] = o1;  // the roped k, reusing the squares' space
+            sq[hh * hd + half + i] = o2;
         }
     }
-}
-
-__global__ void k_gate_mul(float *__restrict__ attn, const float *__restrict__ gate, size_t n)
-{
-    const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i < n) attn[i] *= sigmoidf_(gate[i]);
-}
-
-// ---- post-norm, gated residual, pre-MLP norm ---------------------------------
-__global__ __launch_bounds__(kT) void k_post_attn(const float *__restrict__ proj, float *__restrict__ bx,
-                                                 const float *__restrict__ post_norm,
-                                                 const float *__restrict__ pre_hada, float agate,
-                                                 float *__restrict__ p2, int d)
-{
-    __shared__ float tot[2];
-    __shared__ __align__(16) float nbs[1024];
-    const size_t b = blockIdx.x;
-    if (threadIdx.x == 0) tot[0] = sumsq_chain(proj + b * d, d);
     __syncthreads();
-    float inv = 1.0f / sqrtf(tot[0] / float(d) + 1e-6f);
-    for (int c = threadIdx.x; c < d; c += kT) {
-        const float pn = (1.0f + post_norm[c]) * proj[b * d + c] * inv;
-        const float nb = bx[b * d + c] + agate * pn;
-        bx[b * d + c] = nb;
-        nbs[c] = nb;
+    // quantise (cache.rs:80-104): one wave per kv head vector, K then V
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    uint8_t *blk = a.kv + b * a.kv_stride;
+    const int slot = p % a.cap;
+    for (int vec = wave; vec < 2 * a.KVH; vec += kT / 64) {
+        const bool isv = vec >= a.KVH;
+        const int h = isv ? vec - a.KVH : vec;
+        const int dim = isv ? a.VD : hd;
+        const float *src = isv ? vl + h * a.VD : sq + (a.H + h) * hd;
+        int8_t *dst = reinterpret_cast<int8_t *>(blk + (isv ? a.v_off : 0)) + (size_t(h) * a.cap + slot) * dim;
+        float *scl = reinterpret_cast<float *>(blk + (isv ? a.vs_off : a.ks_off)) + size_t(h) * a.cap + slot;
+        float scale, inv;
+        ndkv::quant_scale_wave(src, dim, scale, inv);
+        for (int e = lane; e < dim; e += 64) dst[e] = int8_t(ndkv::quant_code(src[e], inv));
+        if (lane == 0) *scl = scale;
     }
-    __syncthreads();
-    if (threadIdx.x == 0) tot[1] = sumsq_chain(nbs, d);
-    __syncthreads();
-    inv = 1.0f / sqrtf(tot[1] / float(d) + 1e-6f);
-    for (int c = threadIdx.x; c < d; c += kT) p2[b * d + c] = (1.0f + pre_hada[c]) * nbs[c] * inv;
 }
 
-// ---- HadamardMLP (v3/kernels.rs:119-180), hada_n = 1024 = 32 x 32 -----------
+// attn *= sigmoid(gate) (model.rs:309-312), then prepare_input for out_proj.
+constexpr int kMaxGatePad = 2048;
+
+__global__ __launch_bounds__(kT) void k_gate_prep(const float *__restrict__ attn,
+                                                 const float *__restrict__ gate,
+                                                 float *__restrict__ ah, int od, Prep pp)
+{
+    __shared__ __align__(16) float buf[kMaxGatePad];
+    const size_t b = blockIdx.x;
+    for (int c = threadIdx.x; c < pp.in_padded; c += kT)
+        buf[c] = c < od ? attn[b * od + c] * sigmoidf_(gate[b * od + c]) : 0.0f;
+    __syncthreads();
+    fwht_groups_lds(buf, pp.in_padded, pp.group, pp.inv);
+    for (int c = threadIdx.x; c < pp.in_padded; c += kT) ah[b * pp.in_padded + c] = buf[c];
+}
+
+// ---- post-norm, gated residual, pre-MLP norm (model.rs:313-321), then the
+// HadamardMLP (v3/kernels.rs:119-180, hada_n = 1024 = 32 x 32), the
+// residual and the block delta y = bx - u.  One 1024-thread workgroup per
+// session.
 struct HadaArgs {
-    const float *p2;  // [B][d] the normed block state
+    const float *proj;  // [B][d] out_proj output
+    const float *post_norm, *pre_hada;  // [d]
+    float agate;
     const float *u;   // [B][d]
     float *bx, *y;    // [B][d]
     const float *d1, *d2, *b2, *d3, *d4;  // [1024]
@@ -302,81 +482,141 @@ __device__ inline void kron32(const float *z, const float *a, const float *bm, f
     __syncthreads();
 }
 
-__global__ __launch_bounds__(1024) void k_hada_mlp(HadaArgs a)
+constexpr int kMaxCondRegs = 8;     // cond_v / cond_u values a thread preloads
+constexpr int kCondProd = 6144;     // conditioning products held in LDS at once
+
+__global__ __launch_bounds__(1024) void k_post_hada(HadaArgs a)
 {
     __shared__ __align__(16) float z[1024], buf[1024], t[1024], fa[1024], fb[1024], cond[1024];
-    __shared__ float proj[64];
+    __shared__ __align__(16) float nbs[1024], prod[kCondProd];
+    __shared__ float proj[64], tot[2];
     const size_t b = blockIdx.x;
     const int tid = threadIdx.x, d = a.d, r = a.rank;
-    const float xv = tid < d ? a.p2[b * d + tid] : 0.0f;
-    // cond = 1 + softmax(x . cond_v) . cond_u; projection j is one chain
-    // over the model dim, run by lane 0 of wave j % 16
-    buf[tid] = xv;
+    // every global operand this thread needs, issued up front
+    const bool ch = tid < d;
+    const float pv = ch ? a.proj[b * d + tid] : 0.0f;
+    const float bxv = ch ? a.bx[b * d + tid] : 0.0f;
+    const float uv = ch ? a.u[b * d + tid] : 0.0f;
+    const float post_n = ch ? a.post_norm[tid] : 0.0f;
+    const float pre_n = ch ? a.pre_hada[tid] : 0.0f;
+    const float d1 = a.d1[tid], d2 = a.d2[tid], b2 = a.b2[tid], d3 = a.d3[tid], d4 = a.d4[tid];
+    const float w1a = a.w1a[tid], w1b = a.w1b[tid], w2a = a.w2a[tid], w2b = a.w2b[tid];
+    const float w3a = a.w3a[tid], w3b = a.w3b[tid];
+    const int p1 = a.p1[tid], p2 = a.p2perm[tid];
+    const bool regs = r <= kMaxCondRegs && r * d <= kCondProd;
+    float cv[kMaxCondRegs], cu[kMaxCondRegs];
+#pragma unroll
+    for (int j = 0; j < kMaxCondRegs; ++j) {
+        cv[j] = regs && ch && j < r ? a.cond_v[tid * r + j] : 0.0f;
+        cu[j] = regs && j < r ? a.cond_u[j * 1024 + tid] : 0.0f;
+    }
+    // post-norm of the projection, gated residual, pre-MLP norm: two chains
+    buf[tid] = pv * pv;
     __syncthreads();
-    if ((tid & 63) == 0)
-        for (int j = tid >> 6; j < r; j += 16) {
-            float acc = 0.0f;
-            for (int i = 0; i < d; ++i) acc += buf[i] * a.cond_v[i * r + j];
-            proj[j] = acc;
+    if (tid == 0) tot[0] = chain_sum(buf, d);
+    __syncthreads();
+    if (ch) {
+        const float inv = 1.0f / sqrtf(tot[0] / float(d) + 1e-6f);
+        const float pn = (1.0f + post_n) * pv * inv;
+        const float nb = bxv + a.agate * pn;
+        nbs[tid] = nb;
+        z[tid] = nb * nb;
+    }
+    __syncthreads();
+    if (tid == 0) tot[1] = chain_sum(z, d);
+    __syncthreads();
+    const float xv = ch ? (1.0f + pre_n) * nbs[tid] * (1.0f / sqrtf(tot[1] / float(d) + 1e-6f)) : 0.0f;
+    // cond = 1 + softmax(x . cond_v) . cond_u.  Projection j is one chain
+    // over the model dim, the r chains side by side on lanes 0..r-1 of wave
+    // 0, over products formed in parallel (prod[j][i], contiguous per j).
+    if (regs) {
+        if (ch)
+#pragma unroll
+            for (int j = 0; j < kMaxCondRegs; ++j)
+                if (j < r) prod[j * d + tid] = xv * cv[j];
+        __syncthreads();
+        if (tid < r) proj[tid] = chain_sum(prod + tid * d, d);
+    } else {
+        // wide rank: products a chunk of rows at a time
+        buf[tid] = xv;
+        __syncthreads();
+        const int chn = kCondProd / r;
+        float acc = 0.0f;
+        for (int i0 = 0; i0 < d; i0 += chn) {
+            const int ni = d - i0 < chn ? d - i0 : chn;
+            for (int e = tid; e < ni * r; e += 1024) {
+                const int ii = e / r, j = e - ii * r;
+                prod[j * chn + ii] = buf[i0 + ii] * a.cond_v[(i0 + ii) * r + j];
+            }
+            __syncthreads();
+            if (tid < r)
+                for (int ii = 0; ii < ni; ++ii) acc += prod[tid * chn + ii];
+            __syncthreads();
         }
+        if (tid < r) proj[tid] = acc;
+    }
     __syncthreads();
     if (tid == 0) {
         float mx = -INFINITY;
         for (int j = 0; j < r; ++j) mx = fmaxf(mx, proj[j]);
+#pragma unroll 8
+        for (int j = 0; j < r; ++j) proj[j] = nd_expf(proj[j] - mx);  // independent of each other
         float sum = 0.0f;
-        for (int j = 0; j < r; ++j) {
-            proj[j] = nd_expf(proj[j] - mx);
-            sum += proj[j];
-        }
+        for (int j = 0; j < r; ++j) sum += proj[j];
         for (int j = 0; j < r; ++j) proj[j] /= sum;
     }
     __syncthreads();
     {
         float c = 1.0f;
-        for (int j = 0; j < r; ++j) {
-            if (proj[j] == 0.0f) continue;
-            c += proj[j] * a.cond_u[j * 1024 + tid];
+        if (regs) {
+#pragma unroll
+            for (int j = 0; j < kMaxCondRegs; ++j)
+                if (j < r && proj[j] != 0.0f) c += proj[j] * cu[j];
+        } else {
+            for (int j = 0; j < r; ++j)
+                if (proj[j] != 0.0f) c += proj[j] * a.cond_u[j * 1024 + tid];
         }
         cond[tid] = c;
     }
-    z[tid] = xv * a.d1[tid];
-    fa[tid] = a.w1a[tid];
-    fb[tid] = a.w1b[tid];
+    z[tid] = xv * d1;
+    fa[tid] = w1a;
+    fb[tid] = w1b;
     __syncthreads();
     kron32(z, fa, fb, t, buf);
-    z[tid] = buf[a.p1[tid]];
-    fa[tid] = a.w2a[tid];
-    fb[tid] = a.w2b[tid];
+    z[tid] = buf[p1];
+    fa[tid] = w2a;
+    fb[tid] = w2b;
     __syncthreads();
     {
-        const float zz = a.d2[tid] * cond[tid] * z[tid] + a.b2[tid];
+        const float zz = d2 * cond[tid] * z[tid] + b2;
         z[tid] = zz * sigmoidf_(zz);
     }
     __syncthreads();
     kron32(z, fa, fb, t, buf);
-    z[tid] = buf[a.p2perm[tid]] * a.d3[tid];
-    fa[tid] = a.w3a[tid];
-    fb[tid] = a.w3b[tid];
+    z[tid] = buf[p2] * d3;
+    fa[tid] = w3a;
+    fb[tid] = w3b;
     __syncthreads();
     kron32(z, fa, fb, t, buf);
-    if (tid < d) {
-        const float o = buf[tid] * a.d4[tid];
-        const float nb = a.bx[b * d + tid] + o;
+    if (ch) {
+        const float o = buf[tid] * d4;
+        const float nb = nbs[tid] + o;
         a.bx[b * d + tid] = nb;
-        a.y[b * d + tid] = nb - a.u[b * d + tid];
+        a.y[b * d + tid] = nb - uv;
     }
 }
 
-// ---- mHC scatter up (mhc.rs:111-152) ------------------------------------------
-struct MhcOut {
-    float *lanes;              // [B][n][d]
+// ---- the scatter-up gates of a layer (mhc.rs:111-152), on the side stream:
+// H_post = 2 sigmoid(a_post . raw + b_post + off), H_res = Sinkhorn(a_res .
+// raw + b_res).  They depend only on the layer's input lanes.
+struct MhcGates {
     const float *hpost_raw;    // [B][n]
     const float *hres_raw;     // [B][n*n]
-    const float *y;            // [B][d]
     const float *b_post;       // [n]
     const float *b_res;        // [n*n]
     float a_post, a_res;
-    int layer, n, d;
+    int layer, n;
+    float *gp, *gr;            // [B][n], [B][n*n]
 };
 
 __device__ inline float lse_row(const float *x, int n)
@@ -389,18 +629,56 @@ __device__ inline float lse_row(const float *x, int n)
     return mx + nd_logf(s);
 }
 
-__global__ __launch_bounds__(kT) void k_mhc_out(MhcOut a)
+// kernels.rs:48-74 on an n x n matrix (n * n <= 64) held one entry per lane
+// of one wave: every row (then column) logsumexp is the reference's loop --
+// max, sequential sum of exps, max + log.  Each lane exponentiates its own
+// entry; the lanes of a row (column) then fold the row's exps in index
+// order from shuffles, all rows at once.
+__device__ inline float sinkhorn_wave(float m, int n)
 {
-    __shared__ float hp[16], hr[256];
-    const size_t b = blockIdx.x;
-    const int n = a.n, d = a.d;
-    if (threadIdx.x == 0) {
-        for (int l = 0; l < n; ++l) {
-            const float off = l == a.layer % n ? 0.0f : -4.0f;
-            hp[l] = 2.0f * sigmoidf_(a.a_post * a.hpost_raw[b * n + l] + a.b_post[l] + off);
+    const int lane = threadIdx.x & 63;
+    const int i = lane / n, j = lane - (lane / n) * n;
+    const int rb = i * n;  // first lane of this row
+    for (int it = 0; it < 20; ++it) {
+        {
+            float mx = -INFINITY;
+            for (int k = 0; k < n; ++k) mx = fmaxf(mx, __shfl(m, rb + k, 64));
+            const float e = nd_expf(m - mx);
+            float s = 0.0f;
+            for (int k = 0; k < n; ++k) s += __shfl(e, rb + k, 64);
+            const bool finite = mx == mx && mx != INFINITY && mx != -INFINITY;
+            m -= finite ? mx + nd_logf(s) : mx;
         }
+        {
+            float mx = -INFINITY;
+            for (int k = 0; k < n; ++k) mx = fmaxf(mx, __shfl(m, k * n + j, 64));
+            const float e = nd_expf(m - mx);
+            float s = 0.0f;
+            for (int k = 0; k < n; ++k) s += __shfl(e, k * n + j, 64);
+            m -= mx + nd_logf(s);
+        }
+    }
+    return nd_expf(m);
+}
+
+__global__ __launch_bounds__(64) void k_mhc_gates(MhcGates a)
+{
+    __shared__ float hr[256];
+    const size_t b = blockIdx.x;
+    const int n = a.n, tid = threadIdx.x;
+    if (tid < n) {
+        const float off = tid == a.layer % n ? 0.0f : -4.0f;
+        a.gp[b * n + tid] = 2.0f * sigmoidf_(a.a_post * a.hpost_raw[b * n + tid] + a.b_post[tid] + off);
+    }
+    if (n * n <= 64) {
+        const bool on = tid < n * n;
+        float m = on ? a.a_res * a.hres_raw[b * n * n + tid] + a.b_res[tid] : 0.0f;
+        m = sinkhorn_wave(m, n);
+        if (on) a.gr[b * n * n + tid] = m;
+        return;
+    }
+    if (tid == 0) {
         for (int x = 0; x < n * n; ++x) hr[x] = a.a_res * a.hres_raw[b * n * n + x] + a.b_res[x];
-        // sinkhorn (kernels.rs:48-74)
         for (int it = 0; it < 20; ++it) {
             for (int i = 0; i < n; ++i) {
                 const float lse = lse_row(hr + i * n, n);
@@ -415,41 +693,41 @@ __global__ __launch_bounds__(kT) void k_mhc_out(MhcOut a)
                 for (int i = 0; i < n; ++i) hr[i * n + j] -= lse;
             }
         }
-        for (int x = 0; x < n * n; ++x) hr[x] = nd_expf(hr[x]);
-    }
-    __syncthreads();
-    float *lb = a.lanes + b * size_t(n) * d;
-    for (int c = threadIdx.x; c < d; c += kT) {
-        float old[16];
-        for (int j = 0; j < n; ++j) old[j] = lb[size_t(j) * d + c];
-        const float yc = a.y[b * d + c];
-        for (int i = 0; i < n; ++i) {
-            float acc = 0.0f;
-            for (int j = 0; j < n; ++j) acc += hr[i * n + j] * old[j];
-            lb[size_t(i) * d + c] = acc + hp[i] * yc;
-        }
+        for (int x = 0; x < n * n; ++x) a.gr[b * n * n + x] = nd_expf(hr[x]);
     }
 }
 
-// ---- lane mean + final norm (model.rs:360-368) ---------------------------------
-__global__ __launch_bounds__(kT) void k_final(const float *__restrict__ lanes,
+// ---- the last layer's scatter up, lane mean, final norm (model.rs:360-368),
+// prepared for the tied LM head.
+__global__ __launch_bounds__(kT) void k_final(float *__restrict__ lanes, const float *__restrict__ y,
+                                             const float *__restrict__ gp, const float *__restrict__ gr,
                                              const float *__restrict__ final_norm,
-                                             float *__restrict__ x, int n, int d)
+                                             float *__restrict__ xh, int n, int d, Prep pp)
 {
-    __shared__ float tot;
-    __shared__ __align__(16) float ms[1024];
+    __shared__ __align__(16) float ln[kMaxLanesD], ms[1024], sq[1024];
+    __shared__ float gpp[16], grr[256], tot;
     const size_t b = blockIdx.x;
-    const float *lb = lanes + b * size_t(n) * d;
+    if (threadIdx.x < n) gpp[threadIdx.x] = gp[b * n + threadIdx.x];
+    if (threadIdx.x < n * n) grr[threadIdx.x] = gr[b * n * n + threadIdx.x];
+    __syncthreads();
+    scatter_up(lanes + b * size_t(n) * d, ln, gpp, grr, y + b * d, n, d);
+    __syncthreads();
     for (int c = threadIdx.x; c < d; c += kT) {
         float acc = 0.0f;
-        for (int l = 0; l < n; ++l) acc += lb[size_t(l) * d + c];
-        ms[c] = acc / float(n);
+        for (int l = 0; l < n; ++l) acc += ln[l * d + c];
+        const float m = acc / float(n);
+        ms[c] = m;
+        sq[c] = m * m;
     }
     __syncthreads();
-    if (threadIdx.x == 0) tot = sumsq_chain(ms, d);
+    if (threadIdx.x == 0) tot = chain_sum(sq, d);
     __syncthreads();
     const float inv = 1.0f / sqrtf(tot / float(d) + 1e-6f);
-    for (int c = threadIdx.x; c < d; c += kT) x[b * d + c] = (1.0f + final_norm[c]) * ms[c] * inv;
+    for (int c = threadIdx.x; c < pp.in_padded; c += kT)
+        sq[c] = c < d ? (1.0f + final_norm[c]) * ms[c] * inv : 0.0f;
+    __syncthreads();
+    fwht_groups_lds(sq, pp.in_padded, pp.group, pp.inv);
+    for (int c = threadIdx.x; c < pp.in_padded; c += kT) xh[b * pp.in_padded + c] = sq[c];
 }
 
 // ---- greedy argmax, first maximum wins (v3_engine.rs:410-420) -----------------
@@ -541,6 +819,8 @@ struct nd_v3_model {
     std::vector<Site> sites;
     float *final_norm = nullptr;
     float embed_scale = 1.0f;
+    // prepared-input geometry of the projections each fused kernel feeds
+    Prep pre_nx{}, pre_h{}, pre_attn{}, pre_x{};
     std::vector<void *> mem;  // every device float/int buffer
     std::vector<nd_cq *> cqs;
 
@@ -569,13 +849,20 @@ struct nd_v3_batch {
     std::vector<float *> qt, kt, vt;  // per layer conv tails [B][taps-1][dim]
     std::vector<float *> et;          // per site Engram tails [B][reach][d]
     // activations
-    float *lanes = nullptr, *nx = nullptr, *nxh = nullptr, *u = nullptr, *bx = nullptr,
-          *h = nullptr, *hh = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *gate = nullptr,
-          *attn = nullptr, *ah = nullptr, *proj = nullptr, *p2 = nullptr, *y = nullptr,
-          *hpre = nullptr, *hpost = nullptr, *hres = nullptr, *emb = nullptr, *fetched = nullptr,
-          *fh = nullptr, *ek = nullptr, *ev = nullptr, *x = nullptr, *xh = nullptr,
-          *logits = nullptr;
+    // (nxh, hh, ah, xh: prepared inputs of the projections, in_padded wide)
+    float *lanes = nullptr, *nxh = nullptr, *u = nullptr, *bx = nullptr, *hh = nullptr,
+          *q = nullptr, *k = nullptr, *v = nullptr, *gate = nullptr, *attn = nullptr,
+          *ah = nullptr, *proj = nullptr, *p2 = nullptr, *y = nullptr, *hpre = nullptr,
+          *hpost = nullptr, *hres = nullptr, *emb = nullptr, *fetched = nullptr, *fh = nullptr,
+          *ek = nullptr, *ev = nullptr, *xh = nullptr, *logits = nullptr;
+    float *gp = nullptr, *gr = nullptr;  // scatter-up gates of the latest layer
     int32_t *next = nullptr;
+    // The scatter-up gates of a layer depend only on its input lanes: they
+    // run on `side` while the layer's attention and MLP run on the caller's
+    // stream; ev_in[l % 2] marks a layer's input ready, ev_gates[l % 2] its
+    // gates.
+    hipStream_t side = nullptr;
+    hipEvent_t ev_in[2] = {}, ev_gates[2] = {};
     // Per-step inputs, uploaded from pinned host memory in one copy.  The
     // copy is asynchronous, so a host buffer is reused only once the copy
     // that read it has completed: a ring of kStages buffers, each with the
@@ -596,6 +883,7 @@ struct nd_v3_batch {
     ~nd_v3_batch()
     {
         (void)hipSetDevice(device);
+        if (side) (void)hipStreamSynchronize(side);
         for (int i = 0; i < kStages; ++i)
             if (stage_pending[i]) (void)hipEventSynchronize(stage_done[i]);
         for (void *p : mem) (void)hipFree(p);  // hipFree waits for the device's work
@@ -604,6 +892,11 @@ struct nd_v3_batch {
             if (stage_done[i]) (void)hipEventDestroy(stage_done[i]);
         }
         if (next_host) (void)hipHostFree(next_host);
+        for (int i = 0; i < 2; ++i) {
+            if (ev_in[i]) (void)hipEventDestroy(ev_in[i]);
+            if (ev_gates[i]) (void)hipEventDestroy(ev_gates[i]);
+        }
+        if (side) (void)hipStreamDestroy(side);
     }
 };
 
@@ -644,14 +937,18 @@ int take_cq(nd_ctx *ctx, nd_v3_model *m, const nd_v3_record &r, const float *cb,
     return ND_OK;
 }
 
-// Projection over `B` prepared rows in the reference's summation order
-// (matvec for one session, matmul over sessions; bit-identical results),
-// batch-major output.
+// Projections over `B` prepared rows in the reference's summation order,
+// batch-major output; weights that share the input go in one launch.
 int project(nd_ctx *ctx, const nd_cq *w, const float *xh, int B, size_t row_start, size_t rows,
             float *y)
 {
-    if (B == 1) return nd_cq_matvec_rows_exact(ctx, w, xh, row_start, rows, y);
-    return nd_cq_matmul_rows_exact(ctx, w, xh, size_t(B), row_start, rows, y);
+    return nd_cq_exact_set(ctx, ctx->stream, 1, &w, xh, size_t(B), &row_start, &rows, &y,
+                           "v3 projection");
+}
+
+Prep prep_of(const nd_cq *w)
+{
+    return Prep{int(w->in_padded), int(w->group), w->inv_sqrt_group};
 }
 
 }  // namespace
@@ -674,6 +971,10 @@ int nd_v3_model_create(nd_ctx *ctx, const nd_v3_cfg *cfg, const float *codebook,
                    c.n_orders >= 1 && c.n_orders <= 8,
                "bad layer/site counts");
     ND_REQUIRE(c.qk_head_dim % 2 == 0 && c.qk_head_dim <= 128, "qk_head_dim %d", c.qk_head_dim);
+    ND_REQUIRE(c.num_heads >= 1 && c.num_kv_heads >= 1 && c.num_heads + c.num_kv_heads <= 64 &&
+                   (c.num_heads + c.num_kv_heads) * c.qk_head_dim <= kMaxQkDims,
+               "%d query + %d kv heads of %d: the q/k post-processing holds at most 64 heads "
+               "and %d values", c.num_heads, c.num_kv_heads, c.qk_head_dim, kMaxQkDims);
     nd_v3_model *m = new (std::nothrow) nd_v3_model;
     if (!m) return nd::fail(ND_ERR_NOMEM, "host allocation failed");
     m->cfg = c;
@@ -814,6 +1115,35 @@ int nd_v3_model_create(nd_ctx *ctx, const nd_v3_cfg *cfg, const float *codebook,
 #undef F32
 #undef CQ
     m->embed_scale = std::sqrt(float(d));
+    m->pre_nx = prep_of(m->phi_pre);
+    m->pre_h = prep_of(m->layers[0].q);
+    m->pre_attn = prep_of(m->layers[0].out);
+    m->pre_x = prep_of(m->embedding);
+    {
+        auto same = [](const nd_cq *a, const Prep &p) {
+            return int(a->in_padded) == p.in_padded && int(a->group) == p.group;
+        };
+        bool ok = same(m->phi_post, m->pre_nx) && same(m->phi_res, m->pre_nx);
+        for (const Layer &l : m->layers)
+            ok = ok && same(l.q, m->pre_h) && same(l.k, m->pre_h) && same(l.v, m->pre_h) &&
+                 same(l.gate, m->pre_h) && same(l.out, m->pre_attn);
+        if (!ok) {
+            rc = nd::fail(ND_ERR_ARG, "projections sharing an input must share group size");
+            goto fail;
+        }
+        if (m->pre_h.in_padded > 1024 || m->pre_x.in_padded > 1024 ||
+            m->pre_attn.in_padded > kMaxGatePad || m->pre_nx.in_padded > kMaxLanesD ||
+            nl * d > kMaxLanesD || size_t(c.num_kv_heads) * c.v_head_dim > size_t(kMaxVDims)) {
+            rc = nd::fail(ND_ERR_ARG, "padded projection inputs exceed the fused kernels' LDS");
+            goto fail;
+        }
+        const nd_cq *phi = m->phi_pre;
+        if (phi->group != 128 || !(phi->per_byte == 2 || phi->per_byte == 4) ||
+            nl * phi->num_groups > size_t(kMaxPhiPairs)) {
+            rc = nd::fail(ND_ERR_ARG, "phi_pre must be 2- or 4-bit with 128-wide groups");
+            goto fail;
+        }
+    }
     {
         hipError_t e = hipStreamSynchronize(ctx->stream);
         if (e != hipSuccess) {
@@ -905,7 +1235,6 @@ int nd_v3_batch_create(nd_ctx *ctx, const nd_v3_model *m, size_t sessions, size_
 #define A(p, cnt) \
     if ((rc = dalloc(b->mem, &b->p, size_t(cnt)))) goto fail;
     A(lanes, size_t(B) * nl * d);
-    A(nx, size_t(B) * nl * d);
     {
         size_t phi_pad = 0;
         if ((rc = nd_cq_shape(m->phi_pre, nullptr, nullptr, &phi_pad, nullptr, nullptr))) goto fail;
@@ -913,14 +1242,13 @@ int nd_v3_batch_create(nd_ctx *ctx, const nd_v3_model *m, size_t sessions, size_
     }
     A(u, size_t(B) * d);
     A(bx, size_t(B) * d);
-    A(h, size_t(B) * d);
-    A(hh, size_t(B) * d);
+    A(hh, size_t(B) * m->pre_h.in_padded);
     A(q, size_t(B) * qd);
     A(k, size_t(B) * kd);
     A(v, size_t(B) * vd);
     A(gate, size_t(B) * od);
     A(attn, size_t(B) * od);
-    A(ah, size_t(B) * od);
+    A(ah, size_t(B) * m->pre_attn.in_padded);
     A(proj, size_t(B) * d);
     A(p2, size_t(B) * d);
     A(y, size_t(B) * d);
@@ -932,11 +1260,23 @@ int nd_v3_batch_create(nd_ctx *ctx, const nd_v3_model *m, size_t sessions, size_
     A(fh, size_t(B) * nt * c.e_sub_dim);
     A(ek, size_t(c.n_sites > 0 ? c.n_sites : 1) * B * d);
     A(ev, size_t(c.n_sites > 0 ? c.n_sites : 1) * B * d);
-    A(x, size_t(B) * d);
-    A(xh, size_t(B) * d);
+    A(xh, size_t(B) * m->pre_x.in_padded);
     A(logits, size_t(B) * rows);
+    A(gp, size_t(B) * nl);
+    A(gr, size_t(B) * nl * nl);
     A(next, size_t(B));
 #undef A
+    {
+        hipError_t e = hipStreamCreateWithFlags(&b->side, hipStreamNonBlocking);
+        for (int i = 0; i < 2 && e == hipSuccess; ++i) {
+            e = hipEventCreateWithFlags(&b->ev_in[i], hipEventDisableTiming);
+            if (e == hipSuccess) e = hipEventCreateWithFlags(&b->ev_gates[i], hipEventDisableTiming);
+        }
+        if (e != hipSuccess) {
+            rc = nd::hip_fail(e, "stream/event creation");
+            goto fail;
+        }
+    }
     {
         // step inputs: tokens, pos, lo[L][B], hi[B], engram rows [B][nt], rope [B][qk]
         const size_t ints = size_t(B) * (3 + L + nt);
@@ -1074,8 +1414,13 @@ int nd_v3_step(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t 
         const Site &site = m->sites[s];
         CK(nd_cq_dequantize_rows(ctx, site.tables, b->rows_dev, size_t(B) * nt, b->fetched));
         CK(nd_cq_prepare_input(ctx, site.key, b->fetched, B, b->fh));
-        CK(project(ctx, site.key, b->fh, B, 0, d, b->ek + size_t(s) * B * d));
-        CK(project(ctx, site.value, b->fh, B, 0, d, b->ev + size_t(s) * B * d));
+        {
+            const nd_cq *ws[2] = {site.key, site.value};
+            const size_t r0[2] = {0, 0};
+            const size_t nr[2] = {size_t(d), size_t(d)};
+            float *ys[2] = {b->ek + size_t(s) * B * d, b->ev + size_t(s) * B * d};
+            CK(nd_cq_exact_set(ctx, st, 2, ws, b->fh, size_t(B), r0, nr, ys, "v3 engram key/value"));
+        }
         const int reach = (c.e_conv_taps - 1) * c.e_conv_dilation;
         hipLaunchKernelGGL(k_engram_conv, dim3((d + 255) / 256, B), dim3(256), 0, st,
                            b->ev + size_t(s) * B * d, site.taps, b->et[s], b->pos_dev,
@@ -1089,61 +1434,77 @@ int nd_v3_step(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t 
     LCHK("k_embed");
 
     const float qk_scale = 1.0f / std::sqrt(float(c.qk_head_dim));
+    hipStream_t side = b->side;
+    const nd_cq *phi = m->phi_pre;
     for (int li = 0; li < L; ++li) {
         const Layer &l = m->layers[li];
-        // mix down
-        hipLaunchKernelGGL(k_rms_unit, dim3(B), dim3(kT), 0, st, b->lanes, b->nx, nl * d);
-        LCHK("k_rms_unit");
-        CK(nd_cq_prepare_input(ctx, m->phi_pre, b->nx, B, b->nxh));
-        CK(project(ctx, m->phi_pre, b->nxh, B, size_t(li) * nl, nl, b->hpre));
         const int site = site_of(c, li);
-        MhcIn mi{b->hpre, b->lanes, m->b_pre + size_t(li) * nl, m->a_pre[li], li, nl, d,
-                 site >= 0 ? b->ek + size_t(site) * B * d : nullptr,
-                 site >= 0 ? b->ev + size_t(site) * B * d : nullptr, l.norm_in, b->u, b->bx, b->h};
-        hipLaunchKernelGGL(k_mhc_in, dim3(B), dim3(kT), 0, st, mi);
-        LCHK("k_mhc_in");
-        // projections
-        CK(nd_cq_prepare_input(ctx, l.q, b->h, B, b->hh));
-        CK(project(ctx, l.q, b->hh, B, 0, qd, b->q));
-        CK(project(ctx, l.k, b->hh, B, 0, kd, b->k));
-        CK(project(ctx, l.v, b->hh, B, 0, vd, b->v));
-        CK(project(ctx, l.gate, b->hh, B, 0, od, b->gate));
-        QkvPost qp{b->q, b->k, b->v, b->qt[li], b->kt[li], b->vt[li], l.q_taps, l.k_taps, l.v_taps,
-                   l.q_norm, l.k_norm, b->rope_dev, b->pos_dev, qd, kd, vd, c.qkv_conv_taps,
-                   c.num_heads, c.num_kv_heads, c.qk_head_dim};
-        hipLaunchKernelGGL(k_qkv_post, dim3(B), dim3(kT), 0, st, qp);
-        LCHK("k_qkv_post");
-        // int8 KV append and attention (query fake-quant fused)
-        CK(nd_kv_write(ctx, &b->geom[li], b->kv[li], b->kv_stride[li], size_t(B), b->pos_dev, b->k, b->v));
+        // previous layer's scatter up + this layer's mix down
+        if (li > 0) ND_HIP(hipStreamWaitEvent(st, b->ev_gates[(li - 1) & 1], 0));
+        LayerIn in{b->lanes, b->y, b->gp, b->gr, li > 0, b->nxh, m->pre_nx, phi->packed,
+                   phi->norms, phi->lv, phi->row_bytes, int(phi->num_groups), li * nl,
+                   int(phi->bits == 5), m->b_pre + size_t(li) * nl, m->a_pre[li], li, nl, d,
+                   site >= 0 ? b->ek + size_t(site) * B * d : nullptr,
+                   site >= 0 ? b->ev + size_t(site) * B * d : nullptr, l.norm_in, b->u, b->bx,
+                   b->hh, m->pre_h};
+        if (phi->per_byte == 2)
+            hipLaunchKernelGGL(k_layer_in<2>, dim3(B), dim3(kT), 0, st, in);
+        else
+            hipLaunchKernelGGL(k_layer_in<4>, dim3(B), dim3(kT), 0, st, in);
+        LCHK("k_layer_in");
+        // side stream: this layer's scatter-up gates from the prepared lanes
+        ND_HIP(hipEventRecord(b->ev_in[li & 1], st));
+        ND_HIP(hipStreamWaitEvent(side, b->ev_in[li & 1], 0));
+        {
+            const nd_cq *ws[2] = {m->phi_post, m->phi_res};
+            const size_t r0[2] = {size_t(li) * nl, size_t(li) * nl * nl};
+            const size_t nr[2] = {size_t(nl), size_t(nl) * nl};
+            float *ys[2] = {b->hpost, b->hres};
+            CK(nd_cq_exact_set(ctx, side, 2, ws, b->nxh, size_t(B), r0, nr, ys, "v3 phi post/res"));
+        }
+        MhcGates mg{b->hpost, b->hres, m->b_post + size_t(li) * nl, m->b_res + size_t(li) * nl * nl,
+                    m->a_post[li], m->a_res[li], li, nl, b->gp, b->gr};
+        hipLaunchKernelGGL(k_mhc_gates, dim3(B), dim3(64), 0, side, mg);
+        LCHK("k_mhc_gates");
+        ND_HIP(hipEventRecord(b->ev_gates[li & 1], side));
+        // q, k, v and gate projections of the prepared h, one launch
+        {
+            const nd_cq *ws[4] = {l.q, l.k, l.v, l.gate};
+            const size_t r0[4] = {0, 0, 0, 0};
+            const size_t nr[4] = {size_t(qd), size_t(kd), size_t(vd), size_t(od)};
+            float *ys[4] = {b->q, b->k, b->v, b->gate};
+            CK(nd_cq_exact_set(ctx, st, 4, ws, b->hh, size_t(B), r0, nr, ys, "v3 qkv/gate"));
+        }
+        // conv, norm + RoPE, int8 KV append
+        {
+            const nd_kv_geom &g = b->geom[li];
+            QkvKv qk{b->q, b->k, b->v, b->qt[li], b->kt[li], b->vt[li], l.q_taps, l.k_taps,
+                     l.v_taps, l.q_norm, l.k_norm, b->rope_dev, b->pos_dev, qd, kd, vd,
+                     c.qkv_conv_taps, c.num_heads, c.num_kv_heads, c.qk_head_dim, c.v_head_dim,
+                     b->kv[li], b->kv_stride[li], nd_kv_v_offset(&g), nd_kv_ks_offset(&g),
+                     nd_kv_vs_offset(&g), g.cap};
+            hipLaunchKernelGGL(k_qkv_kv, dim3(B), dim3(kT), 0, st, qk);
+            LCHK("k_qkv_kv");
+        }
+        // attention over the int8 ring (query fake-quant fused)
         CK(nd_attend_step_i8_exact(ctx, &b->geom[li], b->kv[li], b->kv_stride[li], size_t(B),
                                    b->lo_dev + size_t(li) * B, b->hi_dev, b->q, qk_scale, 1,
                                    b->attn));
-        hipLaunchKernelGGL(k_gate_mul, dim3(unsigned((size_t(B) * od + 255) / 256)), dim3(256), 0, st,
-                           b->attn, b->gate, size_t(B) * od);
-        LCHK("k_gate_mul");
-        CK(nd_cq_prepare_input(ctx, l.out, b->attn, B, b->ah));
+        hipLaunchKernelGGL(k_gate_prep, dim3(B), dim3(kT), 0, st, b->attn, b->gate, b->ah, od,
+                           m->pre_attn);
+        LCHK("k_gate_prep");
         CK(project(ctx, l.out, b->ah, B, 0, d, b->proj));
-        const float agate = nd_sigmoidf(l.attn_gate);
-        hipLaunchKernelGGL(k_post_attn, dim3(B), dim3(kT), 0, st, b->proj, b->bx, l.post_norm,
-                           l.pre_hada, agate, b->p2, d);
-        LCHK("k_post_attn");
-        HadaArgs ha{b->p2, b->u, b->bx, b->y, l.d1, l.d2, l.b2, l.d3, l.d4, l.w1a, l.w1b,
-                    l.w2a, l.w2b, l.w3a, l.w3b, l.cond_v, l.cond_u, m->p1, m->p2, d, l.cond_rank};
-        hipLaunchKernelGGL(k_hada_mlp, dim3(B), dim3(1024), 0, st, ha);
-        LCHK("k_hada_mlp");
-        // scatter up: lanes are unchanged since the mix down, so the prepared
-        // rms_unit(lanes) serves phi_post and phi_res too.
-        CK(project(ctx, m->phi_post, b->nxh, B, size_t(li) * nl, nl, b->hpost));
-        CK(project(ctx, m->phi_res, b->nxh, B, size_t(li) * nl * nl, size_t(nl) * nl, b->hres));
-        MhcOut mo2{b->lanes, b->hpost, b->hres, b->y, m->b_post + size_t(li) * nl,
-                   m->b_res + size_t(li) * nl * nl, m->a_post[li], m->a_res[li], li, nl, d};
-        hipLaunchKernelGGL(k_mhc_out, dim3(B), dim3(kT), 0, st, mo2);
-        LCHK("k_mhc_out");
+        HadaArgs ha{b->proj, l.post_norm, l.pre_hada, nd_sigmoidf(l.attn_gate), b->u, b->bx, b->y,
+                    l.d1, l.d2, l.b2, l.d3, l.d4, l.w1a, l.w1b, l.w2a, l.w2b, l.w3a, l.w3b,
+                    l.cond_v, l.cond_u, m->p1, m->p2, d, l.cond_rank};
+        hipLaunchKernelGGL(k_post_hada, dim3(B), dim3(1024), 0, st, ha);
+        LCHK("k_post_hada");
     }
     // ---- head ---------------------------------------------------------------
-    hipLaunchKernelGGL(k_final, dim3(B), dim3(kT), 0, st, b->lanes, m->final_norm, b->x, nl, d);
+    ND_HIP(hipStreamWaitEvent(st, b->ev_gates[(L - 1) & 1], 0));
+    hipLaunchKernelGGL(k_final, dim3(B), dim3(kT), 0, st, b->lanes, b->y, b->gp, b->gr,
+                       m->final_norm, b->xh, nl, d, m->pre_x);
     LCHK("k_final");
-    CK(nd_cq_prepare_input(ctx, m->embedding, b->x, B, b->xh));
     CK(project(ctx, m->embedding, b->xh, B, 0, rows, b->logits));
     if (logits)
         ND_HIP(hipMemcpyAsync(logits, b->logits, size_t(B) * rows * 4, hipMemcpyDeviceToDevice, st));
