@@ -222,7 +222,7 @@ int or_ngram_valid(size_t p, size_t table, const size_t *orders, size_t heads)
 }
 
 /* v3/engram.rs:111-132 */
-static void apply_site(float *x, const float *k, const float *v, size_t d)
+void or_v3_apply_site(float *x, const float *k, const float *v, size_t d)
 {
     float sx = 0.0f, sk = 0.0f;
     for (size_t i = 0; i < d; i++)
@@ -468,10 +468,11 @@ static void push_token(or_v3_cache *k, uint32_t tok)
     k->tokens[k->n_tokens++] = tok;
 }
 
-/* cache.rs:401-438: conv over Q/K/V with the retained raw tail. */
-static void conv_step(or_v3_cache *k, float *tail, const float *taps, float *raw, size_t dim)
+/* cache.rs:401-438: conv over Q/K/V at position `pos` with the retained raw
+ * tail ((n_taps - 1) x dim, oldest first). */
+void or_v3_conv_step(float *tail, const float *taps, float *raw, size_t dim, size_t n_taps,
+                     size_t pos)
 {
-    size_t n_taps = k->cfg.qkv_conv_taps, pos = k->pos;
     if (n_taps == 0)
         return;
     float *out = malloc(dim * sizeof(float));
@@ -493,13 +494,17 @@ static void conv_step(or_v3_cache *k, float *tail, const float *taps, float *raw
     free(out);
 }
 
-/* cache.rs:445-482 */
-static void engram_conv_step(or_v3_cache *k, size_t site, const float *taps, float *raw)
+static void conv_step(or_v3_cache *k, float *tail, const float *taps, float *raw, size_t dim)
 {
-    const or_v3_cfg *c = &k->cfg;
-    size_t n_taps = c->e_conv_taps, dil = c->e_conv_dilation, mo = max_order(c);
-    size_t d = c->d_model, pos = k->pos, reach = (n_taps - 1) * dil;
-    float *tail = k->engram_tail[site];
+    or_v3_conv_step(tail, taps, raw, dim, k->cfg.qkv_conv_taps, k->pos);
+}
+
+/* cache.rs:445-482: the Engram value conv at position `pos`, retained tail of
+ * (n_taps - 1) * dil rows. */
+void or_v3_engram_conv_step(float *tail, const float *taps, float *raw, size_t d, size_t n_taps,
+                            size_t dil, size_t mo, size_t pos)
+{
+    size_t reach = (n_taps - 1) * dil;
     float *out = malloc(d * sizeof(float));
     for (size_t ch = 0; ch < d; ch++) {
         float acc = 0.0f;
@@ -520,8 +525,15 @@ static void engram_conv_step(or_v3_cache *k, size_t site, const float *taps, flo
     free(out);
 }
 
+static void engram_conv_step(or_v3_cache *k, size_t site, const float *taps, float *raw)
+{
+    const or_v3_cfg *c = &k->cfg;
+    or_v3_engram_conv_step(k->engram_tail[site], taps, raw, c->d_model, c->e_conv_taps,
+                           c->e_conv_dilation, max_order(c), k->pos);
+}
+
 /* attention.rs:108-150 with seq = 1. */
-static void norm_and_rope(float *buf, const float *scale, const float *cs, const float *sn,
+void or_v3_norm_and_rope(float *buf, const float *scale, const float *cs, const float *sn,
                           size_t heads, size_t hd)
 {
     size_t half = hd / 2;
@@ -562,6 +574,46 @@ static float pre_off(size_t layer, size_t lane, size_t lanes)
 static float post_off(size_t layer, size_t lane, size_t lanes)
 {
     return lane == layer % lanes ? 0.0f : -4.0f;
+}
+
+/* mhc.rs:79-102: rows (in: nx . phi_pre, out: the gates) and u, the gated
+ * lane sum. */
+void or_v3_mix_down(const float *lanes, float *rows, float a_pre, const float *b_pre,
+                    size_t layer, size_t n, size_t d, float *u)
+{
+    for (size_t lane = 0; lane < n; lane++)
+        rows[lane] = sigmoid(a_pre * rows[lane] + b_pre[lane] + pre_off(layer, lane, n));
+    for (size_t c = 0; c < d; c++) {
+        float acc = 0.0f;
+        for (size_t lane = 0; lane < n; lane++)
+            acc += rows[lane] * lanes[lane * d + c];
+        u[c] = acc;
+    }
+}
+
+/* mhc.rs:109-152: post (n) and res (n*n) in: nx . phi rows, out: the gates
+ * applied; lanes (n x d) get the doubly-stochastic remix plus post * y. */
+void or_v3_scatter_up(float *lanes, float *post, float *res, const float *y, float a_post,
+                      const float *b_post, float a_res, const float *b_res, size_t layer, size_t n,
+                      size_t d)
+{
+    for (size_t lane = 0; lane < n; lane++)
+        post[lane] = 2.0f * sigmoid(a_post * post[lane] + b_post[lane] + post_off(layer, lane, n));
+    for (size_t x = 0; x < n * n; x++)
+        res[x] = a_res * res[x] + b_res[x];
+    or_sinkhorn(res, n);
+    float *scratch = malloc(n * d * sizeof(float));
+    memcpy(scratch, lanes, n * d * sizeof(float));
+    for (size_t i = 0; i < n; i++) {
+        float hp = post[i];
+        for (size_t c = 0; c < d; c++) {
+            float acc = 0.0f;
+            for (size_t j = 0; j < n; j++)
+                acc += res[i * n + j] * scratch[j * d + c];
+            lanes[i * d + c] = acc + hp * y[c];
+        }
+    }
+    free(scratch);
 }
 
 /* model.rs:150-375: one decode position; logits (logit_rows) into `out`. */
@@ -627,18 +679,11 @@ void or_v3_decode_step(const or_v3_model *m, or_v3_cache *cache, uint32_t token,
         rms_unit_to(lanes, nx, n * d);
         or_cq_prepare_input(m->phi_pre, nx, nx_prep);
         or_cq_matvec_rows_prepared(m->phi_pre, nx_prep, li * n, n, hpre);
-        for (size_t lane = 0; lane < n; lane++)
-            hpre[lane] = sigmoid(m->a_pre[li] * hpre[lane] + m->b_pre[li * n + lane] + pre_off(li, lane, n));
-        for (size_t c = 0; c < d; c++) {
-            float acc = 0.0f;
-            for (size_t lane = 0; lane < n; lane++)
-                acc += hpre[lane] * lanes[lane * d + c];
-            u[c] = acc;
-        }
+        or_v3_mix_down(lanes, hpre, m->a_pre[li], m->b_pre + li * n, li, n, d, u);
         memcpy(bx, u, d * sizeof(float));
         for (size_t s = 0; s < ns; s++)
             if (cfg->sites[s] == li) {
-                apply_site(bx, ek + s * d, ev + s * d, d);
+                or_v3_apply_site(bx, ek + s * d, ev + s * d, d);
                 break;
             }
 
@@ -652,8 +697,8 @@ void or_v3_decode_step(const or_v3_model *m, or_v3_cache *cache, uint32_t token,
             conv_step(cache, cache->k_tail[li], L->k_taps, k, kd);
             conv_step(cache, cache->v_tail[li], L->v_taps, v, vd);
         }
-        norm_and_rope(q, L->q_norm, cs, sn, cfg->num_heads, cfg->qk_head_dim);
-        norm_and_rope(k, L->k_norm, cs, sn, cfg->num_kv_heads, cfg->qk_head_dim);
+        or_v3_norm_and_rope(q, L->q_norm, cs, sn, cfg->num_heads, cfg->qk_head_dim);
+        or_v3_norm_and_rope(k, L->k_norm, cs, sn, cfg->num_kv_heads, cfg->qk_head_dim);
         if (cache->int8)
             or_quant_rows(q, 1, cfg->num_heads, cfg->qk_head_dim);
         or_ring_write_kv(cache->rings[li], pos, k, v);
@@ -684,22 +729,8 @@ void or_v3_decode_step(const or_v3_model *m, or_v3_cache *cache, uint32_t token,
         or_cq_matvec_rows_prepared(m->phi_post, nx_prep, li * n, n, hpost);
         or_cq_prepare_input(m->phi_res, nx, nx_prep);
         or_cq_matvec_rows_prepared(m->phi_res, nx_prep, li * n * n, n * n, hres);
-        for (size_t lane = 0; lane < n; lane++)
-            hpost[lane] = 2.0f * sigmoid(m->a_post[li] * hpost[lane] + m->b_post[li * n + lane] +
-                                         post_off(li, lane, n));
-        for (size_t x = 0; x < n * n; x++)
-            hres[x] = m->a_res[li] * hres[x] + m->b_res[li * n * n + x];
-        or_sinkhorn(hres, n);
-        memcpy(scratch, lanes, n * d * sizeof(float));
-        for (size_t i = 0; i < n; i++) {
-            float hp = hpost[i];
-            for (size_t c = 0; c < d; c++) {
-                float acc = 0.0f;
-                for (size_t j = 0; j < n; j++)
-                    acc += hres[i * n + j] * scratch[j * d + c];
-                lanes[i * d + c] = acc + hp * y[c];
-            }
-        }
+        or_v3_scatter_up(lanes, hpost, hres, y, m->a_post[li], m->b_post + li * n, m->a_res[li],
+                         m->b_res + li * n * n, li, n, d);
     }
     cache->pos++;
 

@@ -108,6 +108,18 @@ void or_engram_indices(const uint32_t *tokens, size_t seq, const size_t *orders,
                        uint32_t *out);
 int or_ngram_valid(size_t p, size_t table, const size_t *orders, size_t heads);
 void or_v3_rope_at(const or_v3_cfg *c, size_t pos, float *cs, float *sn);
+void or_v3_apply_site(float *x, const float *k, const float *v, size_t d);
+void or_v3_conv_step(float *tail, const float *taps, float *raw, size_t dim, size_t n_taps,
+                     size_t pos);
+void or_v3_engram_conv_step(float *tail, const float *taps, float *raw, size_t d, size_t n_taps,
+                            size_t dil, size_t max_order, size_t pos);
+void or_v3_norm_and_rope(float *buf, const float *scale, const float *cs, const float *sn,
+                         size_t heads, size_t hd);
+void or_v3_mix_down(const float *lanes, float *rows, float a_pre, const float *b_pre,
+                    size_t layer, size_t n, size_t d, float *u);
+void or_v3_scatter_up(float *lanes, float *post, float *res, const float *y, float a_post,
+                      const float *b_post, float a_res, const float *b_res, size_t layer, size_t n,
+                      size_t d);
 
 #ifdef __cplusplus
 }

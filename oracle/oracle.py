@@ -454,6 +454,16 @@ def _v3_lib():
         L.or_ngram_valid.argtypes = [_sz, _sz, np.ctypeslib.ndpointer(np.uintp), _sz]
         L.or_ngram_valid.restype = C.c_int
         L.or_v3_rope_at.argtypes = [C.POINTER(V3Cfg), _sz, _f32p, _f32p]
+        L.or_v3_apply_site.argtypes = [_f32p, _f32p, _f32p, _sz]
+        L.or_v3_conv_step.argtypes = [_f32p, _f32p, _f32p, _sz, _sz, _sz]
+        L.or_v3_engram_conv_step.argtypes = [_f32p, _f32p, _f32p, _sz, _sz, _sz, _sz, _sz]
+        L.or_v3_norm_and_rope.argtypes = [_f32p, _f32p, _f32p, _f32p, _sz, _sz]
+        L.or_v3_mix_down.argtypes = [_f32p, _f32p, C.c_float, _f32p, _sz, _sz, _sz, _f32p]
+        L.or_v3_scatter_up.argtypes = [_f32p, _f32p, _f32p, _f32p, C.c_float, _f32p, C.c_float,
+                                       _f32p, _sz, _sz, _sz]
+        L.or_hadamard_mlp.argtypes = [_f32p, _sz, C.c_void_p, np.ctypeslib.ndpointer(np.uint32),
+                                      np.ctypeslib.ndpointer(np.uint32), _sz, _f32p]
+        L.or_hada_blocks.argtypes = [_sz, C.POINTER(_sz), C.POINTER(_sz)]
         _v3_bound = True
     return L
 
@@ -543,3 +553,92 @@ def rope_at(geom, pos):
     c, s = np.zeros(half, np.float32), np.zeros(half, np.float32)
     _v3_lib().or_v3_rope_at(C.byref(v3_cfg(geom)), pos, c, s)
     return c, s
+
+
+# ---- v3 helper steps (mhc.rs, engram.rs, cache.rs, attention.rs) -----------
+
+def apply_site(x, k, v):
+    """engram.rs:111-132 on copies; returns the updated x."""
+    x = _f32(x).copy()
+    _v3_lib().or_v3_apply_site(x, _f32(k), _f32(v), x.size)
+    return x
+
+
+def conv_step(tail, taps, raw, pos):
+    """cache.rs:401-438: (out, new tail); tail is (taps - 1) x dim."""
+    taps = _f32(taps)
+    n_taps, dim = taps.shape
+    tail = _f32(tail).copy().reshape(-1)
+    x = _f32(raw).copy()
+    if tail.size == 0:
+        tail = np.zeros(1, np.float32)
+    _v3_lib().or_v3_conv_step(tail, taps.reshape(-1), x, dim, n_taps, pos)
+    return x, tail[:max(n_taps - 1, 0) * dim].reshape(max(n_taps - 1, 0), dim)
+
+
+def engram_conv_step(tail, taps, raw, dil, max_order, pos):
+    """cache.rs:445-482: (out, new tail); tail is (taps - 1) * dil x d."""
+    taps = _f32(taps)
+    n_taps, d = taps.shape
+    reach = (n_taps - 1) * dil
+    tail = _f32(tail).copy().reshape(-1)
+    if tail.size == 0:
+        tail = np.zeros(1, np.float32)
+    x = _f32(raw).copy()
+    _v3_lib().or_v3_engram_conv_step(tail, taps.reshape(-1), x, d, n_taps, dil, max_order, pos)
+    return x, tail[:reach * d].reshape(reach, d)
+
+
+def norm_and_rope(buf, scale, cs, sn):
+    """attention.rs:108-150 for one position: buf is (heads, head_dim)."""
+    buf = _f32(buf).copy()
+    heads, hd = buf.shape
+    _v3_lib().or_v3_norm_and_rope(buf.reshape(-1), _f32(scale), _f32(cs), _f32(sn), heads, hd)
+    return buf
+
+
+def mix_down(lanes, rows, a_pre, b_pre, layer):
+    """mhc.rs:79-102: (gates, u) for lanes (n x d) and raw rows (n)."""
+    lanes = _f32(lanes)
+    n, d = lanes.shape
+    rows = _f32(rows).copy()
+    u = np.zeros(d, np.float32)
+    _v3_lib().or_v3_mix_down(lanes.reshape(-1), rows, float(a_pre), _f32(b_pre), layer, n, d, u)
+    return rows, u
+
+
+def scatter_up(lanes, post, res, y, a_post, b_post, a_res, b_res, layer):
+    """mhc.rs:109-152: (lanes, post gates, res gates) after the scatter."""
+    lanes = _f32(lanes).copy()
+    n, d = lanes.shape
+    post = _f32(post).copy()
+    res = _f32(res).copy().reshape(-1)
+    _v3_lib().or_v3_scatter_up(lanes.reshape(-1), post, res, _f32(y), float(a_post), _f32(b_post),
+                               float(a_res), _f32(b_res).reshape(-1), layer, n, d)
+    return lanes, post, res.reshape(n, n)
+
+
+class _V3Mlp(C.Structure):
+    _fields_ = [(n, C.POINTER(C.c_float)) for n in
+                ("d1", "d2", "b2", "d3", "d4", "w1a", "w1b", "w2a", "w2b", "w3a", "w3b",
+                 "cond_v", "cond_u")] + [("cond_rank", _sz)]
+
+
+def hada_blocks(n):
+    a, b = _sz(), _sz()
+    _v3_lib().or_hada_blocks(n, C.byref(a), C.byref(b))
+    return a.value, b.value
+
+
+def hadamard_mlp(x, w, p1, p2, hada_n):
+    """v3/kernels.rs:119-180.  w: dict of d1 d2 b2 d3 d4 (hada_n), w1a..w3b
+    (square factors), cond_v (d x r), cond_u (r x hada_n)."""
+    x = _f32(x)
+    keep = {k: _f32(v).reshape(-1) for k, v in w.items()}
+    m = _V3Mlp(*[keep[k].ctypes.data_as(C.POINTER(C.c_float)) for k in
+                 ("d1", "d2", "b2", "d3", "d4", "w1a", "w1b", "w2a", "w2b", "w3a", "w3b",
+                  "cond_v", "cond_u")], np.asarray(w["cond_v"]).shape[1])
+    out = np.zeros(x.size, np.float32)
+    _v3_lib().or_hadamard_mlp(x, x.size, C.byref(m), np.ascontiguousarray(p1, np.uint32),
+                              np.ascontiguousarray(p2, np.uint32), hada_n, out)
+    return out
