@@ -1,14 +1,19 @@
 """Benchmark of the Needle-3 hot path on one MI355X.
 
-Headline (BASELINE metric "codebook GEMV GB/s (% HBM peak)"): the codebook
-dequant-GEMV at config 1's shape -- W [3072 x 768] uint8 codes, one 256-entry
-fp32 codebook per 64 rows, x [768], batch 1 -- over R = 448 distinct weight
-copies per step (1.09 GB, beyond the 256 MB MALL), as one strided launch.
-A step is one such launch; value = algorithmic bytes / time.
+Headline ("codebook GEMV GB/s (% HBM peak)"): the codebook dequant-GEMV,
+W [3072 x 768] uint8 codes, one 256-entry fp32 codebook per 64 rows, x [768],
+batch 1 -- over R = 448 distinct weight copies per step (1.09 GB, beyond the
+256 MB MALL), as one strided launch.  A step is one such launch; value =
+algorithmic bytes / time.
 
-Also reported ("secondary"): int8-KV decode attention at ctx 2048 (config 3,
-12 heads x 64) over 320 independent session caches per step (append one
-token + attend), and the batch-1 latencies of both kernels.
+Also reported ("secondary"):
+  - int8-KV decode attention at ctx 2048, 12 heads x 64, over 320
+    independent session caches per step (append one token + attend), and
+    the batch-1 latencies of both kernels;
+  - the Needle-3 forward (shipped geometry, random init, int8 KV cache),
+    bit-identical to the CPU oracle: one session with a 128-token prompt and
+    256 greedy tokens, and 64 sessions each prefilled with 2048 tokens then
+    128 greedy tokens in lockstep ("decode tok/s @ ctx2048 int8 KV").
 
 cpu_baseline: the oracle's Format-B GEMV (the closed form, fp32, row-parallel
 with OpenMP like the reference's rayon row bands) on the host cores, on a
@@ -56,6 +61,9 @@ def parse():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-secondary", action="store_true")
+    p.add_argument("--no-forward", action="store_true", help="skip the Needle-3 forward runs")
+    p.add_argument("--forward-sessions", type=int, default=64)
+    p.add_argument("--forward-ctx", type=int, default=2048)
     p.add_argument("--only", choices=["gemv", "attn"], default=None,
                    help="run one workload only, without the batch-1 latency probes "
                         "(for per-kernel profiles)")
@@ -118,6 +126,72 @@ def cpu_baseline(seconds=12.0):
             "kind": "port",
             "sample": f"{calls} GEMVs of 3072x768 u8 over 64 distinct weight copies in "
                       f"{el:.1f} s (oracle or_cb8_gemv_omp, {threads} OpenMP threads)"}
+
+
+def forward_runs(torch, nd, ctx, sessions, ctx_len, cpu_tokens=8):
+    """The Needle-3 forward on the device: batch 1 (128-token prompt, 256
+    greedy steps) and `sessions` sessions prefilled with `ctx_len` tokens
+    then 128 greedy steps.  Wall-clock over host-driven steps, each greedy
+    step ending with its tokens back on the host."""
+    import numpy as np
+    import v3_synth as S
+    g, recs = S.build_records(None, seed=0)
+    model = nd.V3Model(ctx, g, recs, S.CODEBOOK)
+    out = {}
+
+    def run(B, prompt_len, steps):
+        batch = nd.V3Batch(model, B, max_len=prompt_len + steps)
+        prompts = np.stack([S.prompt_tokens(prompt_len, 100 + i) for i in range(B)]).astype(np.int32)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        nxt = None
+        for t in range(prompt_len):
+            nxt = batch.step(prompts[:, t], want_next=(t == prompt_len - 1))
+        torch.cuda.synchronize()
+        t_pre = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            nxt = batch.step(nxt)
+        t_dec = time.perf_counter() - t0
+        batch.close()
+        return t_pre, t_dec
+
+    run(1, 16, 16)  # warm: code objects, clocks
+    t_pre, t_dec = run(1, 128, 256)
+    out["batch1_prompt128_greedy256"] = {
+        "workload": "shipped Needle-3 geometry (20 layers, d 768, 12 q / 2 kv heads, vocab "
+                    "8192), random init, Cactus-Quants weights, int8 KV; one session, "
+                    "128-token uniform prompt stepped, then 256 greedy tokens",
+        "prefill_ms_per_token": round(t_pre / 128 * 1e3, 3),
+        "decode_ms_per_token": round(t_dec / 256 * 1e3, 3),
+        "decode_tok_per_s": round(256 / t_dec, 1),
+    }
+    t_pre, t_dec = run(sessions, ctx_len, 128)
+    out[f"sessions{sessions}_ctx{ctx_len}_greedy128"] = {
+        "workload": f"{sessions} sessions of the same model in lockstep, each prefilled by "
+                    f"stepping {ctx_len} uniform prompt tokens, then 128 greedy steps; "
+                    "projections batched over sessions, attention per session",
+        "decode_tok_per_s": round(sessions * 128 / t_dec, 1),
+        "decode_ms_per_step": round(t_dec / 128 * 1e3, 3),
+        "prefill_tok_per_s": round(sessions * ctx_len / t_pre, 1),
+    }
+    # the oracle's decode step on one host core, for scale
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    om = O.V3Model(g, recs, S.CODEBOOK)
+    cache = om.new_cache(64, True)
+    toks = S.prompt_tokens(cpu_tokens, 7)
+    cache.decode_step(toks[0])
+    t0 = time.perf_counter()
+    for t in toks[1:]:
+        cache.decode_step(t)
+    out["cpu_oracle_decode_ms_per_token"] = round((time.perf_counter() - t0) / (cpu_tokens - 1) * 1e3, 2)
+    out["cpu_oracle_note"] = ("the oracle's scalar decode step (1 host core, reference float "
+                              "order) on the same model; the reference publishes 8.72 ms/token "
+                              "for its own multi-threaded NEON build on an M5 Max")
+    out["bit_identical_to_oracle"] = "yes (tests/test_gpu_v3.py)"
+    model.close()
+    return out
 
 
 def main():
@@ -243,6 +317,10 @@ def main():
                 "single_session_attention_us": round(ms_att1 * 1e3, 2),
             }
         }
+
+    if not args.no_secondary and not args.no_forward and args.only is None:
+        result.setdefault("secondary", {})["needle3_forward"] = forward_runs(
+            torch, nd, ctx, args.forward_sessions, args.forward_ctx)
 
     if args.calibrate_copy:
         # A plain device copy of exactly 1 GiB: the byte counters' reference.

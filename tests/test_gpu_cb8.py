@@ -21,7 +21,7 @@ def _problem(rng, out, inn):
     return w, cb, x
 
 
-def test_gemv_config1_shape(ctx):
+def test_gemv_3072x768_shape(ctx):
     """3072 x 768, 48 codebooks, x ~ N(0,1), seed 1."""
     rng = np.random.default_rng(1)
     w, cb, x = _problem(rng, 3072, 768)
