@@ -259,12 +259,17 @@ int nd_v3_positions(const nd_v3_batch *b, int32_t *pos);
 
 /* One decode position for every session: tokens[i] (host) is fed to
  * session i, exactly as V3Model::decode_step (v3/model.rs:150-375) with an
- * int8 cache.  When `next` (host, per session) is given it receives the
- * greedy argmax of the logits, first maximum winning
- * (needle-infer/src/v3_engine.rs:410-420); when `logits` (device,
- * [sessions][logit_rows]) is given the logits are copied there.  A prompt is
- * prefilled by stepping it: the reference's batched prefill is
- * bit-identical to stepping (needle-infer/tests/v3_kv_int8.rs:190-302). */
+ * int8 cache -- the logits are bit-identical to the reference's CPU order.
+ * When `next` (host, per session) is given it receives the greedy argmax of
+ * the logits, first maximum winning (needle-infer/src/v3_engine.rs:410-420),
+ * and the call returns once it is known; otherwise the step is only queued
+ * on the context's stream (a side stream of the batch carries the mHC
+ * gates, joined by events).  When `logits` (device, [sessions][logit_rows])
+ * is given the logits are copied there.  A prompt is prefilled by stepping
+ * it: the reference's batched prefill is bit-identical to stepping
+ * (needle-infer/tests/v3_kv_int8.rs:190-302).  Steps on one batch must not
+ * be issued from two threads at once.  After an error the batch's state is
+ * undefined; free it. */
 int nd_v3_step(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *tokens,
                int32_t *next, float *logits);
 
