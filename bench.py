@@ -64,7 +64,7 @@ def parse():
     p.add_argument("--no-forward", action="store_true", help="skip the Needle-3 forward runs")
     p.add_argument("--forward-sessions", type=int, default=64)
     p.add_argument("--forward-ctx", type=int, default=2048)
-    p.add_argument("--only", choices=["gemv", "attn"], default=None,
+    p.add_argument("--only", choices=["gemv", "attn", "forward"], default=None,
                    help="run one workload only, without the batch-1 latency probes "
                         "(for per-kernel profiles)")
     p.add_argument("--min-warm", type=float, default=0.5,
@@ -212,6 +212,12 @@ def main():
 
     # ---- headline: batched codebook GEMV ------------------------------------
     R = GEMV_COPIES if args.only in (None, "gemv") else 1
+    if args.only == "forward":
+        out = {"secondary": {"needle3_forward": forward_runs(
+            torch, nd, ctx, args.forward_sessions, args.forward_ctx)}}
+        ctx.close()
+        print(json.dumps(out))
+        return
     W = torch.randint(0, 256, (R, GEMV_OUT, GEMV_IN), dtype=torch.uint8, device="cuda", generator=gen)
     CB = torch.randn(R, GEMV_OUT // 64, 256, device="cuda", generator=gen) * 0.02
     X = torch.randn(R, GEMV_IN, device="cuda", generator=gen)
