@@ -79,10 +79,13 @@ __global__ __launch_bounds__(kThreads) void cq_exact_kernel(CqExactSet set)
     constexpr int PER_DW = 32 / W;          // codes per dword (8 or 16)
     constexpr int NDW = GR ? GR / PER_DW : 1;
     extern __shared__ __align__(16) float sm[];
+    // activations in LDS with each group padded by 4 floats, so that the
+    // groups a wave reads at once fall in different banks
+    const int gstride = a.group + 4, xstride = a.G * gstride;
     float *lvl = sm;                        // [16] code -> level
     float *ns = sm + 16;                    // [kThreads] this block's norms
-    float *xs = sm + 16 + kThreads;         // [BT][in_padded]
-    float *gs = xs + BT * a.in_padded;      // [BT][rpb * G] group sums
+    float *xs = sm + 16 + kThreads;         // [BT][G][group + 4]
+    float *gs = xs + BT * xstride;          // [BT][rpb * G] group sums
     const int tid = threadIdx.x;
     const int b0 = blockIdx.y * BT;
     const int nb = a.batch - b0 < BT ? a.batch - b0 : BT;
@@ -94,8 +97,10 @@ __global__ __launch_bounds__(kThreads) void cq_exact_kernel(CqExactSet set)
     if (tid < nrows * a.G) ns[tid] = a.norms[size_t(r0) * a.G + tid];
     for (int bb = 0; bb < nb; ++bb) {
         const float4 *src = reinterpret_cast<const float4 *>(a.xh + size_t(b0 + bb) * a.in_padded);
-        float4 *dst = reinterpret_cast<float4 *>(xs + bb * a.in_padded);
-        for (int e = tid; e < a.in_padded / 4; e += kThreads) dst[e] = src[e];
+        for (int e = tid; e < a.in_padded / 4; e += kThreads) {
+            const int g = (4 * e) / a.group, k = 4 * e - g * a.group;
+            *reinterpret_cast<float4 *>(xs + bb * xstride + g * gstride + k) = src[e];
+        }
     }
     // this thread's (row, group) and its codes
     const int rl = tid / a.G, g = tid - rl * a.G;
@@ -121,7 +126,7 @@ __global__ __launch_bounds__(kThreads) void cq_exact_kernel(CqExactSet set)
         for (int bb = 0; bb < BT; ++bb)
 #pragma unroll
             for (int k = 0; k < 8; ++k) lanes[bb][k] = 0.0f;
-        const float *xg = xs + g * a.group;
+        const float *xg = xs + g * gstride;
         // iteration i: elements 8i..8i+7 of the group, element 8i+k into lane k
         auto step = [&](int i, uint32_t dw) {
             const int sh = (i * 8 * W) & 31;
@@ -131,8 +136,8 @@ __global__ __launch_bounds__(kThreads) void cq_exact_kernel(CqExactSet set)
 #pragma unroll
             for (int bb = 0; bb < BT; ++bb) {
                 if (bb < nb) {
-                    const float4 xa = *reinterpret_cast<const float4 *>(xg + bb * a.in_padded + i * 8);
-                    const float4 xb = *reinterpret_cast<const float4 *>(xg + bb * a.in_padded + i * 8 + 4);
+                    const float4 xa = *reinterpret_cast<const float4 *>(xg + bb * xstride + i * 8);
+                    const float4 xb = *reinterpret_cast<const float4 *>(xg + bb * xstride + i * 8 + 4);
                     lanes[bb][0] += v[0] * xa.x;
                     lanes[bb][1] += v[1] * xa.y;
                     lanes[bb][2] += v[2] * xa.z;
@@ -230,9 +235,10 @@ __global__ __launch_bounds__(kThreads) void cq_exact_serial_kernel(CqSerial a)
     a.y[size_t(b) * a.rows + rl] = total;
 }
 
-size_t exact_lds(int bt, size_t in_padded, size_t pairs)
+size_t exact_lds(int bt, size_t in_padded, size_t group, size_t pairs)
 {
-    return 4 * (16 + size_t(kThreads) + size_t(bt) * in_padded + size_t(bt) * pairs);
+    const size_t padded = in_padded / group * (group + 4);
+    return 4 * (16 + size_t(kThreads) + size_t(bt) * padded + size_t(bt) * pairs);
 }
 
 template <int P, int BT>
@@ -240,7 +246,7 @@ void launch_exact(const CqExactSet &set, hipStream_t s)
 {
     const CqExact &a = set.w[0];
     const unsigned gy = unsigned((a.batch + BT - 1) / BT);
-    const size_t lds = exact_lds(BT, a.in_padded, size_t(a.rpb) * a.G);
+    const size_t lds = exact_lds(BT, a.in_padded, a.group, size_t(a.rpb) * a.G);
     const dim3 grid(unsigned(set.tile0[set.n]), gy);
     if (a.group == 128)
         hipLaunchKernelGGL((cq_exact_kernel<P, BT, 128>), grid, dim3(kThreads), lds, s, set);
@@ -306,9 +312,10 @@ int nd_cq_exact_set(nd_ctx *ctx, hipStream_t stream, int n, const nd_cq *const *
         const int rpb = int(kThreads / G);
         const size_t pairs = size_t(rpb) * G;
         int bt = kMaxBt;
-        while (bt > 1 && (size_t(bt) / 2 >= batch || exact_lds(bt, w0->in_padded, pairs) > kLdsBudget))
+        while (bt > 1 &&
+               (size_t(bt) / 2 >= batch || exact_lds(bt, w0->in_padded, w0->group, pairs) > kLdsBudget))
             bt /= 2;
-        if (exact_lds(bt, w0->in_padded, pairs) <= kLdsBudget) {
+        if (exact_lds(bt, w0->in_padded, w0->group, pairs) <= kLdsBudget) {
             CqExactSet set{};
             set.n = 0;
             int tiles = 0;

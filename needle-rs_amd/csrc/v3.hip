@@ -51,27 +51,17 @@ __device__ inline float chain_sum(const float *p, int n)
 {
     float s = 0.0f;
     int i = 0;
-    if ((reinterpret_cast<uintptr_t>(p) & 15) == 0 && n >= 16) {
-        // the next 16 values load while the current 16 are added
+    if ((reinterpret_cast<uintptr_t>(p) & 15) == 0) {
+        // four 16-byte reads, then sixteen adds: the compiler overlaps the
+        // next reads with the adds (measured faster than hand pipelining)
         const float4 *q = reinterpret_cast<const float4 *>(p);
-        float4 a = q[0], b = q[1], c = q[2], e = q[3];
-        for (; i + 32 <= n; i += 16) {
-            const float4 a2 = q[(i >> 2) + 4], b2 = q[(i >> 2) + 5], c2 = q[(i >> 2) + 6],
-                         e2 = q[(i >> 2) + 7];
+        for (; i + 16 <= n; i += 16) {
+            const float4 a = q[i >> 2], b = q[(i >> 2) + 1], c = q[(i >> 2) + 2], e = q[(i >> 2) + 3];
             s += a.x; s += a.y; s += a.z; s += a.w;
             s += b.x; s += b.y; s += b.z; s += b.w;
             s += c.x; s += c.y; s += c.z; s += c.w;
             s += e.x; s += e.y; s += e.z; s += e.w;
-            a = a2;
-            b = b2;
-            c = c2;
-            e = e2;
         }
-        s += a.x; s += a.y; s += a.z; s += a.w;
-        s += b.x; s += b.y; s += b.z; s += b.w;
-        s += c.x; s += c.y; s += c.z; s += c.w;
-        s += e.x; s += e.y; s += e.z; s += e.w;
-        i += 16;
     }
     for (; i < n; ++i) s += p[i];
     return s;
@@ -96,6 +86,52 @@ __device__ inline void fwht_groups_lds(float *buf, int n, int group, float inv)
         __syncthreads();
     }
     for (int e = threadIdx.x; e < n; e += blockDim.x) buf[e] *= inv;
+    __syncthreads();
+}
+
+// The same transform for one 128-wide group held by one wave: element e
+// sits in lane e % 64, slot e / 64.  Stage h pairs lanes l and l ^ h (h <
+// 64) or the two slots (h = 64); the lane with bit h clear forms a + b, the
+// other a - b, exactly the butterfly's two results.  No block barrier.
+__device__ inline void fwht128_wave(float &x0, float &x1, float inv)
+{
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int h = 1; h < 64; h <<= 1) {
+        const float p0 = __shfl_xor(x0, h, 64), p1 = __shfl_xor(x1, h, 64);
+        const bool hi = (lane & h) != 0;
+        x0 = hi ? p0 - x0 : x0 + p0;
+        x1 = hi ? p1 - x1 : x1 + p1;
+    }
+    const float a = x0, b = x1;
+    x0 = (a + b) * inv;
+    x1 = (a - b) * inv;
+}
+
+// prepare_input of `buf` (LDS, pp.in_padded floats, written and synchronised)
+// into `out` (global, and back into buf when `keep`): one wave per 128-group
+// when the group is 128, else the block-wide butterfly.  Every thread of the
+// block calls it; it ends synchronised.
+__device__ inline void prepare_lds(float *buf, float *out, int in_padded, int group, float inv,
+                                   bool keep)
+{
+    if (group == 128) {
+        const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+        for (int g = wave; g < in_padded / 128; g += nw) {
+            float x0 = buf[g * 128 + lane], x1 = buf[g * 128 + 64 + lane];
+            fwht128_wave(x0, x1, inv);
+            out[g * 128 + lane] = x0;
+            out[g * 128 + 64 + lane] = x1;
+            if (keep) {
+                buf[g * 128 + lane] = x0;
+                buf[g * 128 + 64 + lane] = x1;
+            }
+        }
+        __syncthreads();
+        return;
+    }
+    fwht_groups_lds(buf, in_padded, group, inv);
+    for (int e = threadIdx.x; e < in_padded; e += blockDim.x) out[e] = buf[e];
     __syncthreads();
 }
 
@@ -165,6 +201,7 @@ __global__ void k_engram_conv(float *__restrict__ ev, const float *__restrict__ 
 // q/k/v/gate projections.  One workgroup per session.
 constexpr int kMaxLanesD = 4096;  // mhc_lanes * d_model
 constexpr int kMaxPhiPairs = 512; // mhc_lanes * (phi input groups)
+constexpr int kPadGroup = 132;    // a 128-group's stride in LDS, padded
 
 struct LayerIn {
     float *lanes;             // [B][n][d]
@@ -219,12 +256,44 @@ __global__ __launch_bounds__(kT) void k_layer_in(LayerIn a)
         evv[k] = ek && c < d ? a.ev[b * d + c] : 0.0f;
     }
     const float bpre = tid < n ? a.b_pre[tid] : 0.0f;
+    // the previous layer's lanes and block delta for this thread's channels
+    constexpr int kUpLanes = 4;
+    const bool up_regs = a.update && n <= kUpLanes;
+    float old[kCh][kUpLanes], yv[kCh];
+#pragma unroll
+    for (int k = 0; k < kCh; ++k) {
+        const int c = tid + k * kT;
+        const bool on = up_regs && c < d;
+        yv[k] = on ? a.y[b * d + c] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < kUpLanes; ++j) old[k][j] = on && j < n ? lg[size_t(j) * d + c] : 0.0f;
+    }
     if (tid < 16) lvl[tid] = a.phi_lv[a.phi_ternary ? (tid == 3 ? 0 : (tid == 1 ? 2 : 1)) : tid];
     if (a.update) {
         if (tid < n) gpp[tid] = a.gp[b * n + tid];
         if (tid < n * n) grr[tid] = a.gr[b * n * n + tid];
         __syncthreads();
-        scatter_up(lg, ln, gpp, grr, a.y + b * d, n, d);
+        if (up_regs) {
+            // mhc.rs:140-151 from the preloaded values
+#pragma unroll
+            for (int k = 0; k < kCh; ++k) {
+                const int c = tid + k * kT;
+                if (c >= d) continue;
+#pragma unroll
+                for (int i = 0; i < kUpLanes; ++i) {
+                    if (i >= n) break;
+                    float acc = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < kUpLanes; ++j)
+                        if (j < n) acc += grr[i * n + j] * old[k][j];
+                    const float v = acc + gpp[i] * yv[k];
+                    lg[size_t(i) * d + c] = v;
+                    ln[i * d + c] = v;
+                }
+            }
+        } else {
+            scatter_up(lg, ln, gpp, grr, a.y + b * d, n, d);
+        }
     } else {
         for (int e = tid; e < nd; e += kT) ln[e] = lg[e];
     }
@@ -235,21 +304,33 @@ __global__ __launch_bounds__(kT) void k_layer_in(LayerIn a)
     if (tid == 0) tot[0] = chain_sum(nb, nd);
     __syncthreads();
     {
+        // prepare_input of rms_unit(lanes): one wave per 128-group straight
+        // from the lanes; the result goes to global nxh and, each group
+        // padded by 4 floats (so a wave's reads of different groups fall in
+        // different banks), to nb for the phi_pre dots
         const float inv = 1.0f / sqrtf(tot[0] / float(nd) + 1e-6f);
-        for (int e = tid; e < a.pnx.in_padded; e += kT) nb[e] = e < nd ? ln[e] * inv : 0.0f;
+        const int wave = tid >> 6, lane = tid & 63;
+        float *xo = a.nxh + b * a.pnx.in_padded;
+        for (int g = wave; g < G; g += kT / 64) {
+            const int e0 = g * 128 + lane, e1 = e0 + 64;
+            float x0 = e0 < nd ? ln[e0] * inv : 0.0f, x1 = e1 < nd ? ln[e1] * inv : 0.0f;
+            fwht128_wave(x0, x1, a.pnx.inv);
+            xo[e0] = x0;
+            xo[e1] = x1;
+            nb[g * kPadGroup + lane] = x0;
+            nb[g * kPadGroup + 64 + lane] = x1;
+        }
     }
     __syncthreads();
-    fwht_groups_lds(nb, a.pnx.in_padded, a.pnx.group, a.pnx.inv);
-    for (int e = tid; e < a.pnx.in_padded; e += kT) a.nxh[b * a.pnx.in_padded + e] = nb[e];
     // phi_pre rows of this layer (matvec_rows_prepared, reference order)
-    if (has_pair) gs[tid] = cq_group_dot128<PP>(codes, lvl, nb + (tid % G) * 128);
+    if (has_pair) gs[tid] = cq_group_dot128<PP>(codes, lvl, nb + (tid % G) * kPadGroup);
     for (int t = tid + kT; t < pairs; t += kT) {  // more pairs than threads
         const int r = t / G, g = t - r * G;
         CqGroupCodes<PP> more;
         cq_group_codes128<PP>(a.phi_packed + size_t(a.phi_row0 + r) * a.phi_row_bytes +
                                   size_t(g) * (128 / PP),
                               more);
-        gs[t] = cq_group_dot128<PP>(more, lvl, nb + g * 128);
+        gs[t] = cq_group_dot128<PP>(more, lvl, nb + g * kPadGroup);
         pn[t] = a.phi_norms[size_t(a.phi_row0 + r) * G + g];
     }
     __syncthreads();
@@ -311,8 +392,7 @@ __global__ __launch_bounds__(kT) void k_layer_in(LayerIn a)
     }
     for (int c = d + tid; c < a.ph.in_padded; c += kT) pa[c] = 0.0f;
     __syncthreads();
-    fwht_groups_lds(pa, a.ph.in_padded, a.ph.group, a.ph.inv);
-    for (int c = tid; c < a.ph.in_padded; c += kT) a.hh[b * a.ph.in_padded + c] = pa[c];
+    prepare_lds(pa, a.hh + b * a.ph.in_padded, a.ph.in_padded, a.ph.group, a.ph.inv, false);
 }
 
 // ---- after the projections: causal conv step over q/k/v with the retained
@@ -432,8 +512,7 @@ __global__ __launch_bounds__(kT) void k_gate_prep(const float *__restrict__ attn
     for (int c = threadIdx.x; c < pp.in_padded; c += kT)
         buf[c] = c < od ? attn[b * od + c] * sigmoidf_(gate[b * od + c]) : 0.0f;
     __syncthreads();
-    fwht_groups_lds(buf, pp.in_padded, pp.group, pp.inv);
-    for (int c = threadIdx.x; c < pp.in_padded; c += kT) ah[b * pp.in_padded + c] = buf[c];
+    prepare_lds(buf, ah + b * pp.in_padded, pp.in_padded, pp.group, pp.inv, false);
 }
 
 // ---- post-norm, gated residual, pre-MLP norm (model.rs:313-321), then the
@@ -462,20 +541,22 @@ __device__ inline void kron32(const float *z, const float *a, const float *bm, f
     const int r = tid >> 5, c = tid & 31;
     {
         float acc = 0.0f;
+#pragma unroll 8
         for (int i = 0; i < 32; ++i) {
             const float aik = a[i * 32 + r];
-            if (aik == 0.0f) continue;
-            acc += z[i * 32 + c] * aik;
+            const float p = z[i * 32 + c] * aik;
+            acc = aik == 0.0f ? acc : acc + p;  // a zero factor adds nothing, as skipped
         }
         t[r * 32 + c] = acc;
     }
     __syncthreads();
     {
         float acc = 0.0f;
+#pragma unroll 8
         for (int j = 0; j < 32; ++j) {
             const float tkj = t[r * 32 + j];
-            if (tkj == 0.0f) continue;
-            acc += tkj * bm[j * 32 + c];
+            const float p = tkj * bm[j * 32 + c];
+            acc = tkj == 0.0f ? acc : acc + p;
         }
         out[r * 32 + c] = acc;
     }
@@ -556,14 +637,16 @@ __global__ __launch_bounds__(1024) void k_post_hada(HadaArgs a)
         if (tid < r) proj[tid] = acc;
     }
     __syncthreads();
-    if (tid == 0) {
-        float mx = -INFINITY;
-        for (int j = 0; j < r; ++j) mx = fmaxf(mx, proj[j]);
-#pragma unroll 8
-        for (int j = 0; j < r; ++j) proj[j] = nd_expf(proj[j] - mx);  // independent of each other
+    if (tid < 64) {
+        // softmax over the r projections: the max is order-free, each exp
+        // on its own lane, the sum one chain in j order (every lane folds it)
+        const float pj = tid < r ? proj[tid] : -INFINITY;
+        float mx = pj;
+        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+        const float e = tid < r ? nd_expf(pj - mx) : 0.0f;
         float sum = 0.0f;
-        for (int j = 0; j < r; ++j) sum += proj[j];
-        for (int j = 0; j < r; ++j) proj[j] /= sum;
+        for (int j = 0; j < r; ++j) sum += __shfl(e, j, 64);
+        if (tid < r) proj[tid] = e / sum;
     }
     __syncthreads();
     {
@@ -726,8 +809,7 @@ __global__ __launch_bounds__(kT) void k_final(float *__restrict__ lanes, const f
     for (int c = threadIdx.x; c < pp.in_padded; c += kT)
         sq[c] = c < d ? (1.0f + final_norm[c]) * ms[c] * inv : 0.0f;
     __syncthreads();
-    fwht_groups_lds(sq, pp.in_padded, pp.group, pp.inv);
-    for (int c = threadIdx.x; c < pp.in_padded; c += kT) xh[b * pp.in_padded + c] = sq[c];
+    prepare_lds(sq, xh + b * pp.in_padded, pp.in_padded, pp.group, pp.inv, false);
 }
 
 // ---- greedy argmax, first maximum wins (v3_engine.rs:410-420) -----------------
@@ -1139,7 +1221,8 @@ int nd_v3_model_create(nd_ctx *ctx, const nd_v3_cfg *cfg, const float *codebook,
         }
         const nd_cq *phi = m->phi_pre;
         if (phi->group != 128 || !(phi->per_byte == 2 || phi->per_byte == 4) ||
-            nl * phi->num_groups > size_t(kMaxPhiPairs)) {
+            nl * phi->num_groups > size_t(kMaxPhiPairs) ||
+            phi->num_groups * kPadGroup > size_t(kMaxLanesD)) {
             rc = nd::fail(ND_ERR_ARG, "phi_pre must be 2- or 4-bit with 128-wide groups");
             goto fail;
         }
