@@ -311,9 +311,15 @@ int nd_cq_exact_set(nd_ctx *ctx, hipStream_t stream, int n, const nd_cq *const *
     if (fast) {
         const int rpb = int(kThreads / G);
         const size_t pairs = size_t(rpb) * G;
+        size_t tiles = 0;
+        for (int k = 0; k < n; ++k) tiles += (rows[k] + rpb - 1) / rpb;
+        // fewest activation rows per workgroup that still leave two
+        // workgroups per CU, so a large batch fills the GPU
+        const size_t want = 2 * size_t(ctx->num_cus > 0 ? ctx->num_cus : 256);
         int bt = kMaxBt;
         while (bt > 1 &&
-               (size_t(bt) / 2 >= batch || exact_lds(bt, w0->in_padded, w0->group, pairs) > kLdsBudget))
+               (size_t(bt) / 2 >= batch || exact_lds(bt, w0->in_padded, w0->group, pairs) > kLdsBudget ||
+                tiles * ((batch + bt - 1) / bt) < want))
             bt /= 2;
         if (exact_lds(bt, w0->in_padded, w0->group, pairs) <= kLdsBudget) {
             CqExactSet set{};
@@ -458,15 +464,21 @@ __global__ __launch_bounds__(kThreads) void attn_exact_kernel(ndkv::Geom g,
         }
         __syncthreads();
         if (tid < g.VD) {
-            const float *w = sc + c0;
+            const float *w = sc + c0;  // c0 is a multiple of the chunk: 16-byte aligned
             const int8_t *col = vl + tid;
             int t = 0;
-            for (; t + 8 <= cn; t += 8) {
-                float p[8];
+            for (; t + 16 <= cn; t += 16) {
+                const float4 w0 = *reinterpret_cast<const float4 *>(w + t);
+                const float4 w1 = *reinterpret_cast<const float4 *>(w + t + 4);
+                const float4 w2 = *reinterpret_cast<const float4 *>(w + t + 8);
+                const float4 w3 = *reinterpret_cast<const float4 *>(w + t + 12);
+                const float ws[16] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w,
+                                      w2.x, w2.y, w2.z, w2.w, w3.x, w3.y, w3.z, w3.w};
+                float p[16];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) p[u] = w[t + u] * float(col[(t + u) * g.VD]);
+                for (int u = 0; u < 16; ++u) p[u] = ws[u] * float(col[(t + u) * g.VD]);
 #pragma unroll
-                for (int u = 0; u < 8; ++u) acc += p[u];
+                for (int u = 0; u < 16; ++u) acc += p[u];
             }
             for (; t < cn; ++t) acc += w[t] * float(col[t * g.VD]);
         }
