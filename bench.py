@@ -64,7 +64,7 @@ def parse():
     p.add_argument("--no-forward", action="store_true", help="skip the Needle-3 forward runs")
     p.add_argument("--forward-sessions", type=int, default=64)
     p.add_argument("--forward-ctx", type=int, default=2048)
-    p.add_argument("--only", choices=["gemv", "attn", "forward"], default=None,
+    p.add_argument("--only", choices=["gemv", "attn", "forward", "gemm"], default=None,
                    help="run one workload only, without the batch-1 latency probes "
                         "(for per-kernel profiles)")
     p.add_argument("--min-warm", type=float, default=0.5,
@@ -126,6 +126,32 @@ def cpu_baseline(seconds=12.0):
             "kind": "port",
             "sample": f"{calls} GEMVs of 3072x768 u8 over 64 distinct weight copies in "
                       f"{el:.1f} s (oracle or_cb8_gemv_omp, {threads} OpenMP threads)"}
+
+
+BF16_MFMA_PEAK_TFLOPS = 2500.0
+
+
+def gemm_runs(torch, nd, ctx, gen, steps):
+    """Format B prefill GEMM, Y [512 x N] = X [512 x 768] . decode(W [N x 768]),
+    bf16 MFMA with fp32 accumulate, for the two projection widths; R
+    distinct problems per launch (one launch per step) so the step is long
+    enough to time on the device."""
+    out = {}
+    M, K = 512, 768
+    for N, R in ((3072, 32), (768, 64)):
+        X = torch.randn(R, M, K, device="cuda", generator=gen)
+        W = torch.randint(0, 256, (R, N, K), dtype=torch.uint8, device="cuda", generator=gen)
+        CB = torch.randn(R, N // 64, 256, device="cuda", generator=gen) * 0.02
+        Y = torch.empty(R, M, N, device="cuda")
+        ms = timed_loop(torch, lambda: nd.cb8_gemm_batched(ctx, X, W, CB, Y), steps, 10)
+        flops = 2.0 * M * N * K * R
+        tf = flops / (ms * 1e-3) / 1e12
+        out[f"m{M}_n{N}_k{K}"] = {"problems_per_launch": R, "us_per_launch": round(ms * 1e3, 2),
+                                  "us_per_gemm": round(ms * 1e3 / R, 3), "TFLOPs": round(tf, 2),
+                                  "frac_bf16_mfma_dense_peak": round(tf / BF16_MFMA_PEAK_TFLOPS, 4),
+                                  "flops_per_gemm": 2 * M * N * K}
+        del X, W, CB, Y
+    return out
 
 
 def forward_runs(torch, nd, ctx, sessions, ctx_len, cpu_tokens=8):
@@ -212,6 +238,10 @@ def main():
 
     # ---- headline: batched codebook GEMV ------------------------------------
     R = GEMV_COPIES if args.only in (None, "gemv") else 1
+    if args.only == "gemm":
+        print(json.dumps({"secondary": {"prefill_gemm_bf16": gemm_runs(torch, nd, ctx, gen, args.steps)}}))
+        ctx.close()
+        return
     if args.only == "forward":
         out = {"secondary": {"needle3_forward": forward_runs(
             torch, nd, ctx, args.forward_sessions, args.forward_ctx)}}
@@ -323,6 +353,9 @@ def main():
                 "single_session_attention_us": round(ms_att1 * 1e3, 2),
             }
         }
+
+    if not args.no_secondary and args.only is None:
+        result.setdefault("secondary", {})["prefill_gemm_bf16"] = gemm_runs(torch, nd, ctx, gen, 50)
 
     if not args.no_secondary and not args.no_forward and args.only is None:
         result.setdefault("secondary", {})["needle3_forward"] = forward_runs(

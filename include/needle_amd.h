@@ -85,6 +85,14 @@ int nd_cb8_gemv_batched(nd_ctx *ctx, size_t count,
 int nd_cb8_gemm(nd_ctx *ctx, const float *x, const uint8_t *w,
                 const float *cb, float *y, size_t m, size_t out, size_t in);
 
+/* `count` independent GEMMs in one launch: problem i reads x + i*x_stride,
+ * w + i*w_stride, cb + i*cb_stride and writes y + i*y_stride (strides in
+ * elements), e.g. the several projections of one prefill chunk. */
+int nd_cb8_gemm_batched(nd_ctx *ctx, size_t count, const float *x, size_t x_stride,
+                        const uint8_t *w, size_t w_stride, const float *cb,
+                        size_t cb_stride, float *y, size_t y_stride, size_t m,
+                        size_t out, size_t in);
+
 /* ---- Format A: Cactus-Quants weights (cq.rs) ----------------------------- */
 typedef struct nd_cq nd_cq;
 

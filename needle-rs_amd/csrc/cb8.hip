@@ -237,18 +237,52 @@ __device__ inline unsigned short f32_to_bf16_rne(float f)
     return static_cast<unsigned short>(u >> 16);
 }
 
-constexpr int kGM = 64, kGN = 64, kGK = 32;
+constexpr int kGM = 64, kGN = 64, kGK = 128;
 constexpr int kLdsPad = 8;  // bf16 elements of padding per LDS row
 
-__global__ __launch_bounds__(256) void cb8_gemm_kernel(const float *__restrict__ X,
+// X (f32) to bf16, round to nearest even, 8 elements per thread; problem
+// blockIdx.y of a batch at element stride xs (input) and n (output).
+__global__ __launch_bounds__(256) void x_to_bf16_kernel(const float *__restrict__ X, size_t xs,
+                                                        unsigned short *__restrict__ Xb, size_t n)
+{
+    const size_t i = (size_t(blockIdx.x) * 256 + threadIdx.x) * 8;
+    if (i >= n) return;
+    const float *src = X + blockIdx.y * xs + i;
+    unsigned short *dst = Xb + blockIdx.y * n + i;
+    if (i + 8 <= n) {
+        const float4 a = *reinterpret_cast<const float4 *>(src);
+        const float4 b = *reinterpret_cast<const float4 *>(src + 4);
+        *reinterpret_cast<uint4 *>(dst) =
+            make_uint4(f32_to_bf16_rne(a.x) | (uint32_t(f32_to_bf16_rne(a.y)) << 16),
+                       f32_to_bf16_rne(a.z) | (uint32_t(f32_to_bf16_rne(a.w)) << 16),
+                       f32_to_bf16_rne(b.x) | (uint32_t(f32_to_bf16_rne(b.y)) << 16),
+                       f32_to_bf16_rne(b.z) | (uint32_t(f32_to_bf16_rne(b.w)) << 16));
+    } else {
+        for (size_t k = 0; i + k < n; ++k) dst[k] = f32_to_bf16_rne(src[k]);
+    }
+}
+
+// Y[M][N] = X[M][K] . decode(W[N][K])^T, X already bf16.  A 256-thread block
+// owns a 64x64 output tile (4 waves of 32x32, 2x2 MFMA 16x16x32 tiles each)
+// and walks K 128 at a time: the next step's X rows and codes are loaded
+// into registers while the current step's 16 MFMAs per wave run from LDS.
+// The block's codebook sits in LDS already rounded to bf16, so decoding a
+// code is one LDS read.
+__global__ __launch_bounds__(256) void cb8_gemm_kernel(const unsigned short *__restrict__ Xb,
                                                        const uint8_t *__restrict__ W,
                                                        const float *__restrict__ cb,
                                                        float *__restrict__ Y, int M, int N,
-                                                       int K)
+                                                       int K, size_t ws, size_t cs, size_t ys)
 {
-    __shared__ float cbs[256];
-    __shared__ unsigned short As[kGM][kGK + kLdsPad];
-    __shared__ unsigned short Bs[kGN][kGK + kLdsPad];
+    __shared__ unsigned short cbh[256];
+    __shared__ __align__(16) unsigned short As[kGM][kGK + kLdsPad];
+    __shared__ __align__(16) unsigned short Bs[kGN][kGK + kLdsPad];
+
+    // problem blockIdx.z of a batch: X at M*K, the rest at element strides
+    Xb += blockIdx.z * size_t(M) * K;
+    W += blockIdx.z * ws;
+    cb += blockIdx.z * cs;
+    Y += blockIdx.z * ys;
 
     const int t = threadIdx.x;
     const int lane = t & 63;
@@ -258,7 +292,7 @@ __global__ __launch_bounds__(256) void cb8_gemm_kernel(const float *__restrict__
     const int wm = (wave >> 1) * 32;  // wave's row offset within the tile
     const int wn = (wave & 1) * 32;   // wave's column offset
 
-    cbs[t] = cb[size_t(n0 / 64) * 256 + t];
+    cbh[t] = f32_to_bf16_rne(cb[size_t(n0 / 64) * 256 + t]);
 
     floatx4_t acc[2][2];
 #pragma unroll
@@ -266,57 +300,66 @@ __global__ __launch_bounds__(256) void cb8_gemm_kernel(const float *__restrict__
 #pragma unroll
         for (int b = 0; b < 2; ++b) acc[a][b] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // Staging assignment: A tile 64x32 f32 = 2048 floats -> 8 per thread;
-    // B tile 64x32 bytes = 2048 codes -> 8 per thread.
-    const int ar = t >> 2;          // row 0..63
-    const int ac = (t & 3) * 8;     // col 0,8,16,24
-    __syncthreads();
-
+    const int sr = t >> 2;          // staged row 0..63 (of A and of B)
+    const int sc = (t & 3) * 32;    // staged columns sc..sc+31 of the K step
+    const bool mrow = m0 + sr < M;
+    const unsigned short *xrow = Xb + size_t(mrow ? m0 + sr : 0) * K;
+    const uint8_t *wrow = W + size_t(n0 + sr) * K;  // N is a multiple of 64
+    uint4 xa[4];
+    uint2 wc[4];
+    auto load = [&](int k0) {
+        const bool on = k0 + sc < K;  // K is a multiple of 32: a 32-column run is all in or out
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            xa[q] = on && mrow ? *reinterpret_cast<const uint4 *>(xrow + k0 + sc + 8 * q)
+                               : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            wc[q] = on ? *reinterpret_cast<const uint2 *>(wrow + k0 + sc + 8 * q) : make_uint2(0, 0);
+        return on;
+    };
+    auto store = [&](bool on) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) *reinterpret_cast<uint4 *>(&As[sr][sc + 8 * q]) = xa[q];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t d[2] = {wc[q].x, wc[q].y};
+            uint32_t h[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t lo = cbh[(d[e >> 1] >> (16 * (e & 1))) & 0xffu];
+                const uint32_t hi = cbh[(d[e >> 1] >> (16 * (e & 1) + 8)) & 0xffu];
+                h[e] = on ? lo | (hi << 16) : 0u;
+            }
+            *reinterpret_cast<uint4 *>(&Bs[sr][sc + 8 * q]) = make_uint4(h[0], h[1], h[2], h[3]);
+        }
+    };
+    __syncthreads();  // codebook in LDS
+    bool on = load(0);
+    // MFMA 16x16x32 bf16: lane l supplies A[row l%16][k 8*(l/16) .. +8]
+    // and B[k 8*(l/16) .. +8][col l%16].
+    const int r16 = lane & 15;
+    const int kq = (lane >> 4) * 8;
     for (int k0 = 0; k0 < K; k0 += kGK) {
-        {
-            const int m = m0 + ar;
-            float v[8];
-            if (m < M) {
-                const float4 *xp = reinterpret_cast<const float4 *>(X + size_t(m) * K + k0 + ac);
-                float4 a = xp[0], b = xp[1];
-                v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-                v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-            } else {
-#pragma unroll
-                for (int q = 0; q < 8; ++q) v[q] = 0.0f;
-            }
-#pragma unroll
-            for (int q = 0; q < 8; ++q) As[ar][ac + q] = f32_to_bf16_rne(v[q]);
-        }
-        {
-            const int n = n0 + ar;
-            uint2 c = make_uint2(0, 0);
-            if (n < N) c = *reinterpret_cast<const uint2 *>(W + size_t(n) * K + k0 + ac);
-            const uint32_t d[2] = {c.x, c.y};
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                const uint32_t e = (d[q >> 2] >> (8 * (q & 3))) & 0xffu;
-                Bs[ar][ac + q] = f32_to_bf16_rne(n < N ? cbs[e] : 0.0f);
-            }
-        }
+        store(on);
         __syncthreads();
-        // MFMA 16x16x32 bf16: lane l supplies A[row l%16][k 8*(l/16) .. +8]
-        // and B[k 8*(l/16) .. +8][col l%16].
-        const int r16 = lane & 15;
-        const int kq = (lane >> 4) * 8;
-        bf16x8_t afrag[2], bfrag[2];
+        if (k0 + kGK < K) on = load(k0 + kGK);
+        const int steps = (K - k0 < kGK ? K - k0 : kGK) / 32;
+        for (int kk = 0; kk < steps; ++kk) {
+            bf16x8_t afrag[2], bfrag[2];
 #pragma unroll
-        for (int a = 0; a < 2; ++a)
-            afrag[a] = *reinterpret_cast<const bf16x8_t *>(&As[wm + a * 16 + r16][kq]);
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-            bfrag[b] = *reinterpret_cast<const bf16x8_t *>(&Bs[wn + b * 16 + r16][kq]);
-#pragma unroll
-        for (int a = 0; a < 2; ++a)
+            for (int a = 0; a < 2; ++a)
+                afrag[a] = *reinterpret_cast<const bf16x8_t *>(&As[wm + a * 16 + r16][kk * 32 + kq]);
 #pragma unroll
             for (int b = 0; b < 2; ++b)
-                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afrag[a], bfrag[b], acc[a][b],
-                                                                    0, 0, 0);
+                bfrag[b] = *reinterpret_cast<const bf16x8_t *>(&Bs[wn + b * 16 + r16][kk * 32 + kq]);
+#pragma unroll
+            for (int a = 0; a < 2; ++a)
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afrag[a], bfrag[b],
+                                                                        acc[a][b], 0, 0, 0);
+        }
         __syncthreads();
     }
     // C layout: lane l holds C[4*(l/16) + i][l%16], i < 4.
@@ -330,7 +373,121 @@ __global__ __launch_bounds__(256) void cb8_gemm_kernel(const float *__restrict__
             for (int i = 0; i < 4; ++i) {
                 const int m = m0 + wm + a * 16 + rb + i;
                 const int n = n0 + wn + b * 16 + col;
-                if (m < M && n < N) Y[size_t(m) * N + n] = acc[a][b][i];
+                if (m < M) Y[size_t(m) * N + n] = acc[a][b][i];
+            }
+}
+
+// The same product with 128x128 tiles for M >= 96: 4 waves of 64x64 (4x4
+// MFMA tiles each), K steps of 64, each thread staging half a row of A
+// (32 bf16) and of B (32 codes).  A decoded code strip serves twice the
+// rows of the 64x64 kernel, halving the decode work per MFMA.
+constexpr int kBM = 128, kBN = 128, kBK = 64;
+
+__global__ __launch_bounds__(256) void cb8_gemm128_kernel(const unsigned short *__restrict__ Xb,
+                                                          const uint8_t *__restrict__ W,
+                                                          const float *__restrict__ cb,
+                                                          float *__restrict__ Y, int M, int N,
+                                                          int K, size_t ws, size_t cs, size_t ys)
+{
+    __shared__ unsigned short cbh[2][256];
+    __shared__ __align__(16) unsigned short As[kBM][kBK + kLdsPad];
+    __shared__ __align__(16) unsigned short Bs[kBN][kBK + kLdsPad];
+
+    Xb += blockIdx.z * size_t(M) * K;
+    W += blockIdx.z * ws;
+    cb += blockIdx.z * cs;
+    Y += blockIdx.z * ys;
+
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int n0 = blockIdx.x * kBN;
+    const int m0 = blockIdx.y * kBM;
+    const int wm = (wave >> 1) * 64;
+    const int wn = (wave & 1) * 64;
+
+    // the tile's two 64-row codebooks, rounded to bf16
+    cbh[0][t] = f32_to_bf16_rne(cb[size_t(n0 / 64) * 256 + t]);
+    cbh[1][t] = f32_to_bf16_rne(cb[size_t(n0 / 64 + 1) * 256 + t]);
+
+    floatx4_t acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int sr = t >> 1;          // staged row 0..127 (of A and of B)
+    const int sc = (t & 1) * 32;    // staged columns sc..sc+31 of the K step
+    const bool mrow = m0 + sr < M;
+    const unsigned short *xrow = Xb + size_t(mrow ? m0 + sr : 0) * K;
+    const uint8_t *wrow = W + size_t(n0 + sr) * K;  // N is a multiple of 128 here
+    const unsigned short *cbr = cbh[sr >> 6];
+    uint4 xa[4];
+    uint2 wc[4];
+    auto load = [&](int k0) {
+        const bool on = k0 + sc < K;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            xa[q] = on && mrow ? *reinterpret_cast<const uint4 *>(xrow + k0 + sc + 8 * q)
+                               : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            wc[q] = on ? *reinterpret_cast<const uint2 *>(wrow + k0 + sc + 8 * q) : make_uint2(0, 0);
+        return on;
+    };
+    auto store = [&](bool on) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) *reinterpret_cast<uint4 *>(&As[sr][sc + 8 * q]) = xa[q];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t d[2] = {wc[q].x, wc[q].y};
+            uint32_t h[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t lo = cbr[(d[e >> 1] >> (16 * (e & 1))) & 0xffu];
+                const uint32_t hi = cbr[(d[e >> 1] >> (16 * (e & 1) + 8)) & 0xffu];
+                h[e] = on ? lo | (hi << 16) : 0u;
+            }
+            *reinterpret_cast<uint4 *>(&Bs[sr][sc + 8 * q]) = make_uint4(h[0], h[1], h[2], h[3]);
+        }
+    };
+    __syncthreads();
+    bool on = load(0);
+    const int r16 = lane & 15;
+    const int kq = (lane >> 4) * 8;
+    for (int k0 = 0; k0 < K; k0 += kBK) {
+        store(on);
+        __syncthreads();
+        if (k0 + kBK < K) on = load(k0 + kBK);
+        const int steps = (K - k0 < kBK ? K - k0 : kBK) / 32;
+        for (int kk = 0; kk < steps; ++kk) {
+            bf16x8_t afrag[4], bfrag[4];
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+                afrag[a] = *reinterpret_cast<const bf16x8_t *>(&As[wm + a * 16 + r16][kk * 32 + kq]);
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+                bfrag[b] = *reinterpret_cast<const bf16x8_t *>(&Bs[wn + b * 16 + r16][kk * 32 + kq]);
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+#pragma unroll
+                for (int b = 0; b < 4; ++b)
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afrag[a], bfrag[b],
+                                                                        acc[a][b], 0, 0, 0);
+        }
+        __syncthreads();
+    }
+    const int col = lane & 15;
+    const int rb = (lane >> 4) * 4;
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = m0 + wm + a * 16 + rb + i;
+                const int n = n0 + wn + b * 16 + col;
+                if (m < M) Y[size_t(m) * N + n] = acc[a][b][i];
             }
 }
 
@@ -392,22 +549,48 @@ int nd_cb8_gemv_batched(nd_ctx *ctx, size_t count, const uint8_t *w, size_t w_st
     return launch_gemv(ctx, count, w, w_stride, cb, cb_stride, x, x_stride, y, y_stride, out, in);
 }
 
+int nd_cb8_gemm_batched(nd_ctx *ctx, size_t count, const float *x, size_t x_stride,
+                        const uint8_t *w, size_t w_stride, const float *cb, size_t cb_stride,
+                        float *y, size_t y_stride, size_t m, size_t out, size_t in)
+{
+    if (int rc = nd::enter(ctx)) return rc;
+    if (count == 0) return ND_OK;
+    ND_REQUIRE(x && w && cb && y, "null buffer");
+    ND_REQUIRE(m > 0 && out > 0 && in > 0, "empty shape");
+    ND_REQUIRE(count <= 65535, "count %zu above 65535", count);
+    ND_REQUIRE(out % kGN == 0, "out (%zu) must be a multiple of %d", out, kGN);
+    ND_REQUIRE(in % 32 == 0, "in (%zu) must be a multiple of 32", in);
+    ND_REQUIRE(m <= (size_t(1) << 24) && out <= (size_t(1) << 24) && in <= (size_t(1) << 24),
+               "shape too large");
+    ND_REQUIRE((reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(w) & 7) == 0 &&
+                   x_stride % 4 == 0 && w_stride % 8 == 0,
+               "x must be 16-byte and w 8-byte aligned, problem by problem");
+    // X to bf16 once per call, into the context workspace
+    const size_t mk = m * in;
+    void *wsp = nullptr;
+    if (int rc = nd::workspace(ctx, count * mk * sizeof(unsigned short), &wsp)) return rc;
+    unsigned short *xb = static_cast<unsigned short *>(wsp);
+    hipLaunchKernelGGL(x_to_bf16_kernel, dim3(unsigned((mk + 2047) / 2048), unsigned(count)),
+                       dim3(256), 0, ctx->stream, x, x_stride, xb, mk);
+    if (int rc = nd::check_launch("x_to_bf16")) return rc;
+    if (m >= 96 && out % kBN == 0) {
+        dim3 grid(static_cast<unsigned>(out / kBN), static_cast<unsigned>((m + kBM - 1) / kBM),
+                  static_cast<unsigned>(count));
+        hipLaunchKernelGGL(cb8_gemm128_kernel, grid, dim3(256), 0, ctx->stream, xb, w, cb, y,
+                           int(m), int(out), int(in), w_stride, cb_stride, y_stride);
+    } else {
+        dim3 grid(static_cast<unsigned>(out / kGN), static_cast<unsigned>((m + kGM - 1) / kGM),
+                  static_cast<unsigned>(count));
+        hipLaunchKernelGGL(cb8_gemm_kernel, grid, dim3(256), 0, ctx->stream, xb, w, cb, y, int(m),
+                           int(out), int(in), w_stride, cb_stride, y_stride);
+    }
+    return nd::check_launch("cb8_gemm");
+}
+
 int nd_cb8_gemm(nd_ctx *ctx, const float *x, const uint8_t *w, const float *cb, float *y,
                 size_t m, size_t out, size_t in)
 {
-    if (int rc = nd::enter(ctx)) return rc;
-    ND_REQUIRE(x && w && cb && y, "null buffer");
-    ND_REQUIRE(m > 0 && out > 0 && in > 0, "empty shape");
-    ND_REQUIRE(out % kGN == 0, "out (%zu) must be a multiple of %d", out, kGN);
-    ND_REQUIRE(in % kGK == 0, "in (%zu) must be a multiple of %d", in, kGK);
-    ND_REQUIRE(m <= (size_t(1) << 24) && out <= (size_t(1) << 24) && in <= (size_t(1) << 24),
-               "shape too large");
-    ND_REQUIRE((reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(w) & 7) == 0,
-               "x must be 16-byte and w 8-byte aligned");
-    dim3 grid(static_cast<unsigned>(out / kGN), static_cast<unsigned>((m + kGM - 1) / kGM));
-    hipLaunchKernelGGL(cb8_gemm_kernel, grid, dim3(256), 0, ctx->stream, x, w, cb, y, int(m),
-                       int(out), int(in));
-    return nd::check_launch("cb8_gemm");
+    return nd_cb8_gemm_batched(ctx, 1, x, 0, w, 0, cb, 0, y, 0, m, out, in);
 }
 
 }  // extern "C"

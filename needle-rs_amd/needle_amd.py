@@ -54,6 +54,7 @@ _SIGS = [
     ("nd_cb8_gemv", C.c_int, [_vp, _vp, _vp, _vp, _vp, _sz, _sz]),
     ("nd_cb8_gemv_batched", C.c_int, [_vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _sz]),
     ("nd_cb8_gemm", C.c_int, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz]),
+    ("nd_cb8_gemm_batched", C.c_int, [_vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _sz, _sz]),
     ("nd_cq_from_blob", C.c_int, [_vp, _vp, _sz, _sz, _sz, _sz, C.c_uint8, _vp, _sz, C.POINTER(_vp)]),
     ("nd_cq_free", None, [_vp]),
     ("nd_cq_shape", C.c_int, [_vp, C.POINTER(_sz), C.POINTER(_sz), C.POINTER(_sz), C.POINTER(_sz),
@@ -178,6 +179,16 @@ def cb8_gemm(ctx, x, w, cb, y=None):
     if y is None:
         y = torch.empty(m, out, dtype=torch.float32, device=x.device)
     _check(lib().nd_cb8_gemm(ctx.h, _ptr(x), _ptr(w), _ptr(cb), _ptr(y), m, out, inn))
+    return y
+
+
+def cb8_gemm_batched(ctx, x, w, cb, y):
+    """x [count][m][in] f32, w [count][out][in] u8, cb [count][out/64][256],
+    y [count][m][out]: one launch."""
+    count, m, inn = x.shape
+    out = w.shape[1]
+    _check(lib().nd_cb8_gemm_batched(ctx.h, count, _ptr(x), x.stride(0), _ptr(w), w.stride(0),
+                                     _ptr(cb), cb.stride(0), _ptr(y), y.stride(0), m, out, inn))
     return y
 
 

@@ -74,10 +74,13 @@ def test_gemv_rejects_misaligned_width(ctx):
     assert e.value.code == 1 and "multiple of 16" in str(e.value)
 
 
-@pytest.mark.parametrize("m,out", [(512, 3072), (512, 768), (1, 64), (100, 192)])
-def test_gemm_bf16_mfma(ctx, m, out):
-    rng = np.random.default_rng(m + out)
-    inn = 768
+@pytest.mark.parametrize("m,out,inn", [(512, 3072, 768), (512, 768, 768), (1, 64, 768),
+                                       (100, 192, 768), (200, 256, 96), (130, 384, 160),
+                                       (96, 128, 32)])
+def test_gemm_bf16_mfma(ctx, m, out, inn):
+    """Both tile shapes (64x64 below M = 96 or when out is not a multiple of
+    128, else 128x128), K not a multiple of the K step, ragged M."""
+    rng = np.random.default_rng(m + out + inn)
     w = rng.integers(0, 256, size=(out, inn), dtype=np.uint8)
     cb = rng.normal(0, 0.02, size=(out // 64, 256)).astype(np.float32)
     X = rng.normal(size=(m, inn)).astype(np.float32)
@@ -87,3 +90,20 @@ def test_gemm_bf16_mfma(ctx, m, out):
     assert rel <= 2e-2, rel
     # bf16 inputs, fp32 accumulation: far tighter than the gate in practice
     assert np.linalg.norm(Y - ref) / np.linalg.norm(ref) <= 5e-3
+
+
+def test_gemm_batched_equals_single(ctx):
+    """Problem i of one batched launch is bit-identical to its own launch."""
+    rng = np.random.default_rng(21)
+    R, M, N, K = 3, 70, 128, 96
+    X = rng.normal(size=(R, M, K)).astype(np.float32)
+    W = rng.integers(0, 256, size=(R, N, K), dtype=np.uint8)
+    CB = (rng.normal(size=(R, N // 64, 256)) * 0.02).astype(np.float32)
+    Y = torch.empty(R, M, N, device="cuda")
+    nd.cb8_gemm_batched(ctx, dev(X), dev(W), dev(CB), Y)
+    got = host(Y)
+    for i in range(R):
+        one = host(nd.cb8_gemm(ctx, dev(X[i]), dev(W[i]), dev(CB[i])))
+        assert np.array_equal(got[i], one)
+        want = O.cb8_gemm(X[i], W[i], CB[i])
+        assert np.max(np.abs(got[i] - want)) <= 2e-2 * np.max(np.abs(want))
