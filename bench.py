@@ -64,7 +64,7 @@ def parse():
     p.add_argument("--no-forward", action="store_true", help="skip the Needle-3 forward runs")
     p.add_argument("--forward-sessions", type=int, default=64)
     p.add_argument("--forward-ctx", type=int, default=2048)
-    p.add_argument("--only", choices=["gemv", "attn", "forward", "gemm"], default=None,
+    p.add_argument("--only", choices=["gemv", "attn", "forward", "gemm", "cqa"], default=None,
                    help="run one workload only, without the batch-1 latency probes "
                         "(for per-kernel profiles)")
     p.add_argument("--min-warm", type=float, default=0.5,
@@ -154,6 +154,68 @@ def gemm_runs(torch, nd, ctx, gen, steps):
     return out
 
 
+def _cq_blob(rng, rows, inn, bits, group=128):
+    """A Cactus-Quants blob (cq.rs:181-238): uniform random packed codes, then
+    FP16 norms ~ N(0, 0.02) * sqrt(group)."""
+    import numpy as np
+    per = {2: 4, 4: 2}[bits]
+    row_bytes = inn // per
+    ng = inn // group
+    packed = rng.integers(0, 256, size=rows * row_bytes, dtype=np.uint8)
+    norms = (rng.standard_normal(rows * ng, dtype=np.float32) * np.float32(0.02 * math.sqrt(group)))
+    return np.concatenate([packed, norms.astype(np.float16).view(np.uint8)]), row_bytes, ng
+
+
+def format_a_runs(torch, nd, steps):
+    """Cactus-Quants (Format A) decode GEMV, batch 1, in 768, group 128.
+
+    Streaming: one tall weight of the q projection's shape stacked 4096 times
+    (2-bit, 2,359,296 rows) and one of the LM head's shape stacked 160 times
+    (4-bit, 1,310,720 rows) -- each over 450 MB, beyond the MALL -- timed as
+    one call over all rows; bytes = packed + f32 norms + xh + y.  Both the
+    tolerance kernel and the reference-order (bit-exact) kernel.
+    Latency: one call on each projection shape of the shipped Needle-3 model."""
+    import numpy as np
+    import v3_synth as S
+    rng = np.random.default_rng(11)
+    ctx = nd.Ctx(0)
+    inn = 768
+    out = {}
+    for name, shape_rows, copies, bits in (("q576x768_2bit", 576, 4096, 2),
+                                           ("lm_head8192x768_4bit", 8192, 160, 4)):
+        rows = shape_rows * copies
+        blob, row_bytes, ng = _cq_blob(rng, rows, inn, bits)
+        w = nd.CqWeight(ctx, blob, rows, inn, 128, bits, S.CODEBOOK)
+        del blob
+        xh = torch.randn(inn, device="cuda")
+        y = torch.empty(rows, device="cuda")
+        nbytes = rows * (row_bytes + 4 * ng + 4) + 4 * inn
+        rec = {"rows": rows, "bytes_per_call": nbytes}
+        for tag, exact in (("tolerance", False), ("exact", True)):
+            ms = timed_loop(torch, lambda: w.matvec_rows_prepared(xh, 0, rows, y, exact=exact),
+                            max(10, steps // 2), 3)
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            rec[tag] = {"us": round(ms * 1e3, 1), "GBps": round(gbs, 1),
+                        "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+        out[name + "_stream"] = rec
+        w.close()
+        del y
+    lat = {}
+    for name, rows, bits in (("q", 576, 2), ("k", 96, 2), ("v", 128, 2), ("gate_out", 768, 2),
+                             ("lm_head", 8192, 4)):
+        blob, row_bytes, ng = _cq_blob(rng, rows, inn, bits)
+        w = nd.CqWeight(ctx, blob, rows, inn, 128, bits, S.CODEBOOK)
+        xh = torch.randn(inn, device="cuda")
+        y = torch.empty(rows, device="cuda")
+        lat[name] = {tag: round(timed_loop(torch, lambda: w.matvec_rows_prepared(
+            xh, 0, rows, y, exact=exact), 200, 20, 0.1) * 1e3, 2)
+            for tag, exact in (("tolerance_us", False), ("exact_us", True))}
+        w.close()
+    out["single_call_latency"] = lat
+    ctx.close()
+    return out
+
+
 def forward_runs(torch, nd, ctx, sessions, ctx_len, cpu_tokens=8):
     """The Needle-3 forward on the device: batch 1 (128-token prompt, 256
     greedy steps) and `sessions` sessions prefilled with `ctx_len` tokens
@@ -240,6 +302,10 @@ def main():
     R = GEMV_COPIES if args.only in (None, "gemv") else 1
     if args.only == "gemm":
         print(json.dumps({"secondary": {"prefill_gemm_bf16": gemm_runs(torch, nd, ctx, gen, args.steps)}}))
+        ctx.close()
+        return
+    if args.only == "cqa":
+        print(json.dumps({"secondary": {"format_a_gemv": format_a_runs(torch, nd, args.steps)}}))
         ctx.close()
         return
     if args.only == "forward":
@@ -356,6 +422,9 @@ def main():
 
     if not args.no_secondary and args.only is None:
         result.setdefault("secondary", {})["prefill_gemm_bf16"] = gemm_runs(torch, nd, ctx, gen, 50)
+
+    if not args.no_secondary and args.only is None:
+        result.setdefault("secondary", {})["format_a_gemv"] = format_a_runs(torch, nd, 50)
 
     if not args.no_secondary and not args.no_forward and args.only is None:
         result.setdefault("secondary", {})["needle3_forward"] = forward_runs(

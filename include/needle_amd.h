@@ -211,8 +211,8 @@ int nd_attend_step_i8(nd_ctx *ctx, const nd_kv_geom *g, const void *kv,
  * (attention.rs:327-377): each score is one dot chain over the head dim,
  * scaled by the key scale and then `scale`; the softmax sum and every
  * output column are single chains over the span in position order; exp is
- * libm's expf algorithm.  Also requires cap <= 16384 (one span's scores sit
- * in LDS).  The Needle-3 forward uses this. */
+ * libm's expf algorithm.  Also requires cap <= 12288 (one span's scores and
+ * a 16 KB chunk of V rows sit in LDS).  The Needle-3 forward uses this. */
 int nd_attend_step_i8_exact(nd_ctx *ctx, const nd_kv_geom *g, const void *kv,
                             size_t kv_stride, size_t count, const int32_t *lo,
                             const int32_t *hi, const float *q, float scale,

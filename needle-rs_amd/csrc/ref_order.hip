@@ -486,6 +486,342 @@ __global__ __launch_bounds__(kThreads) void attn_exact_kernel(ndkv::Geom g,
     if (tid < g.VD) out[(i * g.H + h) * size_t(g.VD) + tid] = acc;
 }
 
+// The same arithmetic, with the value pass split between roles.  Of the 256
+// threads, CW consumer waves hold one output column per lane and run the
+// column chains; the other 4 - CW producer waves stream V a chunk of
+// positions ahead, form each product ((e * inv) * v_scale) * v into an LDS
+// double buffer, and keep kPrefetch chunks of V loads in flight.  A chain
+// then costs one add per position.  At most 128 VGPRs, so four workgroups fit
+// a CU and a 64-session layer (768 workgroups) is resident at once.
+// Blocks are numbered so that the heads sharing a kv head run on one XCD
+// (workgroups are dealt to the 8 XCDs round-robin), where they share that
+// XCD's L2 copy of the span.
+constexpr int kAttn2Threads = 256;
+constexpr int kProdBuf = 64 * 52;  // products per buffer: VD x (T + 4) <= 64 x 52, 128 x 20
+constexpr int kPrefetch = 8;
+constexpr int kAttn2MaxCap = 8192;  // scores 32 KB + two product buffers 26 KB
+constexpr int kScoreBatch = 4;      // positions per thread whose K rows load together
+
+// One (q, key) score chain per position, QC = qk / 16 pieces of 16 codes
+// (0: any qk, read piece by piece).  With QC set, a thread loads the K rows
+// of kScoreBatch positions at once and runs their chains interleaved.
+template <int QC, int NT>
+__device__ __forceinline__ float attn_scores(const ndkv::Geom &g, const float *qs, const int8_t *kb,
+                                    const float *ks, int base, int span, float scale, float *sc)
+{
+    const int tid = threadIdx.x;
+    float mx = -INFINITY;
+    if constexpr (QC > 0) {
+        for (int t0 = tid; t0 < span; t0 += NT * kScoreBatch) {
+            uint4 kw[kScoreBatch][QC];
+            float ksv[kScoreBatch];
+#pragma unroll
+            for (int u = 0; u < kScoreBatch; ++u) {
+                const int t = t0 + u * NT;
+                int slot = base + (t < span ? t : 0);
+                if (slot >= g.cap) slot -= g.cap;
+                const uint4 *kr = reinterpret_cast<const uint4 *>(kb + size_t(slot) * (16 * QC));
+#pragma unroll
+                for (int c = 0; c < QC; ++c) kw[u][c] = kr[c];
+                ksv[u] = ks[slot];
+            }
+            float acc[kScoreBatch];
+#pragma unroll
+            for (int u = 0; u < kScoreBatch; ++u) acc[u] = 0.0f;
+#pragma unroll
+            for (int c = 0; c < QC; ++c) {
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) {
+                        const float qv = qs[c * 16 + d * 4 + b];
+#pragma unroll
+                        for (int u = 0; u < kScoreBatch; ++u) {
+                            const uint32_t dw = d == 0 ? kw[u][c].x
+                                              : d == 1 ? kw[u][c].y
+                                              : d == 2 ? kw[u][c].z
+                                                       : kw[u][c].w;
+                            acc[u] += qv * i8_lane(dw, b);
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kScoreBatch; ++u) {
+                const int t = t0 + u * NT;
+                if (t < span) {
+                    const float s = acc[u] * ksv[u] * scale;
+                    sc[t] = s;
+                    if (s > mx) mx = s;
+                }
+            }
+        }
+    } else {
+        for (int t = tid; t < span; t += NT) {
+            int slot = base + t;
+            if (slot >= g.cap) slot -= g.cap;
+            const uint4 *kr = reinterpret_cast<const uint4 *>(kb + size_t(slot) * g.QK);
+            float acc = 0.0f;
+            for (int c = 0; c < g.QK / 16; ++c) {
+                const uint4 w = kr[c];
+                const uint32_t dws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                for (int d = 0; d < 4; ++d)
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) acc += qs[c * 16 + d * 4 + b] * i8_lane(dws[d], b);
+            }
+            const float s = acc * ks[slot] * scale;
+            sc[t] = s;
+            if (s > mx) mx = s;
+        }
+    }
+    return mx;
+}
+
+// acc += a[0].x; acc += a[0].y; ... acc += a[3].w, as 16 dependent adds in
+// one asm block: the compiler can neither reorder the terms nor move LDS
+// reads across the block (left to itself it hoists the next group's reads
+// and copies this group's registers to make room).
+__device__ __forceinline__ float add16(float acc, const float4 (&a)[4])
+{
+    asm volatile(
+        "v_add_f32 %0, %1, %0\n\tv_add_f32 %0, %2, %0\n\tv_add_f32 %0, %3, %0\n\t"
+        "v_add_f32 %0, %4, %0\n\tv_add_f32 %0, %5, %0\n\tv_add_f32 %0, %6, %0\n\t"
+        "v_add_f32 %0, %7, %0\n\tv_add_f32 %0, %8, %0\n\tv_add_f32 %0, %9, %0\n\t"
+        "v_add_f32 %0, %10, %0\n\tv_add_f32 %0, %11, %0\n\tv_add_f32 %0, %12, %0\n\t"
+        "v_add_f32 %0, %13, %0\n\tv_add_f32 %0, %14, %0\n\tv_add_f32 %0, %15, %0\n\t"
+        "v_add_f32 %0, %16, %0"
+        : "+v"(acc)
+        : "v"(a[0].x), "v"(a[0].y), "v"(a[0].z), "v"(a[0].w), "v"(a[1].x), "v"(a[1].y),
+          "v"(a[1].z), "v"(a[1].w), "v"(a[2].x), "v"(a[2].y), "v"(a[2].z), "v"(a[2].w),
+          "v"(a[3].x), "v"(a[3].y), "v"(a[3].z), "v"(a[3].w)
+        : "memory");
+    return acc;
+}
+
+// acc += the first m terms of a (m <= 16, uniform), in order.
+__device__ __forceinline__ float add_first(float acc, const float4 (&a)[4], int m)
+{
+    if (m >= 16) return add16(acc, a);
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+        const float4 &q = a[u / 4];
+        const float t = (u & 3) == 0 ? q.x : (u & 3) == 1 ? q.y : (u & 3) == 2 ? q.z : q.w;
+        if (u < m) acc += t;
+    }
+    return acc;
+}
+
+__device__ __forceinline__ void lds_read16(float4 (&a)[4], const float *v)
+{
+    const float4 *v4 = reinterpret_cast<const float4 *>(v);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) a[u] = v4[u];
+}
+
+// acc += v[0]; acc += v[1]; ... acc += v[n-1] in index order, v 16-byte
+// aligned LDS with at least 32 readable floats past v[n-1].  Terms go in
+// groups of 32, read into two register sets in turn, so that a group's
+// reads are in flight while the group before it is added.
+__device__ inline float lds_chain(float acc, const float *v, int n)
+{
+    const int G = (n + 31) / 32;
+    if (G == 0) return acc;
+    float4 a[8], b[8];
+    auto rd = [&](float4 (&r)[8], int gi) {
+        const float4 *v4 = reinterpret_cast<const float4 *>(v + gi * 32);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) r[u] = v4[u];
+    };
+    auto add32 = [&](float s, const float4 (&r)[8], int m) {
+        const float4 lo[4] = {r[0], r[1], r[2], r[3]};
+        const float4 hi[4] = {r[4], r[5], r[6], r[7]};
+        if (m >= 32) return add16(add16(s, lo), hi);
+        s = add_first(s, lo, m);
+        return m > 16 ? add_first(s, hi, m - 16) : s;
+    };
+    rd(a, 0);
+    int gi = 0;
+    for (; gi + 2 < G; gi += 2) {
+        rd(b, gi + 1);
+        acc = add32(acc, a, 32);
+        rd(a, gi + 2);
+        acc = add32(acc, b, 32);
+    }
+    if (gi + 1 < G) {
+        rd(b, gi + 1);
+        acc = add32(acc, a, 32);
+        acc = add32(acc, b, n - (gi + 1) * 32);
+    } else {
+        acc = add32(acc, a, n - gi * 32);
+    }
+    return acc;
+}
+
+template <int CW, int QC>
+__global__ __launch_bounds__(kAttn2Threads, 4) void attn_exact2_kernel(
+    ndkv::Geom g, const uint8_t *__restrict__ kv, size_t stride, const int32_t *__restrict__ lo,
+    const int32_t *__restrict__ hi, const float *__restrict__ q, float scale, int quant_query,
+    float *__restrict__ out, int groups)
+{
+    constexpr int NT = kAttn2Threads;
+    extern __shared__ __align__(16) float sm[];
+    __shared__ float qs[ndkv::kMaxDim];
+    __shared__ float red[NT / 64];
+    __shared__ float total;
+    const int tid = threadIdx.x;
+    const int R = g.H / g.KVH;
+    const int xcd = int(blockIdx.x) & 7, slot8 = int(blockIdx.x) >> 3;
+    const int grp = (slot8 / R) * 8 + xcd;
+    if (grp >= groups) return;  // padding block: the whole block leaves
+    const int i = grp / g.KVH, kvh = grp - (grp / g.KVH) * g.KVH;
+    const int h = kvh * R + slot8 % R;
+    const uint8_t *blk = kv + size_t(i) * stride;
+    const int p0 = lo[i];
+    const int span = hi[i] - p0 + 1;
+    if (p0 < 0 || span < 1 || span > g.cap) {
+        for (int j = tid; j < g.VD; j += NT) out[(size_t(i) * g.H + h) * g.VD + j] = NAN;
+        return;
+    }
+    float *sc = sm;                                   // [span] scores, then exps
+    float *prod = sm + ((g.cap + 3) & ~3);            // [2][kProdBuf] products
+    const float *qv = q + (size_t(i) * g.H + h) * g.QK;
+    if (tid < 64) {
+        // quant_rows (v3/model.rs:289-293): fake-quantised query head
+        if (quant_query) {
+            float s, inv;
+            ndkv::quant_scale_wave(qv, g.QK, s, inv);
+            for (int e = tid; e < g.QK; e += 64) qs[e] = ndkv::quant_code(qv[e], inv) * s;
+        } else {
+            for (int e = tid; e < g.QK; e += 64) qs[e] = qv[e];
+        }
+    }
+    __syncthreads();
+    const int8_t *kb = reinterpret_cast<const int8_t *>(blk) + size_t(kvh) * g.cap * g.QK;
+    const float *ks = reinterpret_cast<const float *>(blk + g.ks_off) + size_t(kvh) * g.cap;
+    const int base = p0 % g.cap;
+    float mx = attn_scores<QC, NT>(g, qs, kb, ks, base, span, scale, sc);
+    mx = ndkv::wave_max(mx);
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
+    __syncthreads();
+    mx = red[0];
+    for (int w = 1; w < NT / 64; ++w) mx = red[w] > mx ? red[w] : mx;
+    for (int t0 = tid; t0 < span; t0 += 4 * NT) {
+        // four independent exps per thread in flight
+        float e[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int t = t0 + u * NT;
+            e[u] = nd_expf(sc[t < span ? t : 0] - mx);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (t0 + u * NT < span) sc[t0 + u * NT] = e[u];
+    }
+    __syncthreads();
+
+    // Products sit column-major, [VD][T + 4] per buffer: a consumer lane reads
+    // four positions of its column per 16-byte read, and the 4-float pad puts
+    // the columns of one read in different banks.  Producer item (pc, tl) of a
+    // chunk is position tl, columns pc*16..+15; a wave's items are consecutive
+    // positions of one column piece.
+    constexpr int T = CW == 1 ? 48 : 16;  // positions per chunk: one item per producer
+    constexpr int TS = T + 4;
+    const int pieces = g.VD / 16;
+    const int nch = (span + T - 1) / T;
+    const bool producer = tid >= 64 * CW;
+    const int pt = tid - 64 * CW;
+    const int pc = pt / T, tl = pt - (pt / T) * T;
+    const bool has_item = producer && pc < pieces;
+    const int8_t *vbase = reinterpret_cast<const int8_t *>(blk + g.v_off) + size_t(kvh) * g.cap * g.VD;
+    const float *vs = reinterpret_cast<const float *>(blk + g.vs_off) + size_t(kvh) * g.cap;
+    uint4 vb[kPrefetch];
+    float vsb[kPrefetch];
+    // Every load is issued unconditionally (a position past the span reads
+    // position 0 and is never used), so the compiler can count the loads in
+    // flight and wait for the oldest one only.
+    auto load = [&](int k, uint4 &v, float &f) {
+        int t = k * T + tl;
+        t = has_item && t < span ? t : 0;
+        int slot = base + t;
+        if (slot >= g.cap) slot -= g.cap;
+        v = *reinterpret_cast<const uint4 *>(vbase + size_t(slot) * g.VD + pc * 16);
+        f = vs[slot];
+    };
+#pragma unroll
+    for (int j = 0; j < kPrefetch; ++j) load(j, vb[j], vsb[j]);
+    if (tid == 0) {
+        // the softmax sum: one chain in position order
+        __builtin_amdgcn_s_setprio(2);
+        const float s = lds_chain(0.0f, sc, span);
+        total = s;
+        __builtin_amdgcn_s_setprio(0);
+    }
+    __syncthreads();
+    const float inv = 1.0f / total;
+    float acc = 0.0f;
+    // Step k: producers fill chunk k, consumers add chunk k - 1.  Each role
+    // runs its own loop; the roles are whole waves and both pass the same
+    // number of barriers (a multiple of kPrefetch, the last few empty).
+    const int steps = (nch + 1 + kPrefetch - 1) / kPrefetch * kPrefetch;
+    if (producer) {
+        // this item's exp for the step after the current one, read ahead
+        float e_next = sc[tl < span ? tl : 0];
+        for (int k0 = 0; k0 < steps; k0 += kPrefetch) {
+#pragma unroll
+            for (int j = 0; j < kPrefetch; ++j) {
+                const int k = k0 + j;
+                const int t = k * T + tl;
+                const float e = e_next;
+                const int tn = t + T;
+                e_next = sc[tn < span ? tn : 0];
+                if (has_item && k < nch && t < span) {
+                    const float w = e * inv * vsb[j];
+                    const uint32_t dws[4] = {vb[j].x, vb[j].y, vb[j].z, vb[j].w};
+                    float p[16];
+#pragma unroll
+                    for (int d = 0; d < 4; ++d)
+#pragma unroll
+                        for (int b = 0; b < 4; ++b) p[d * 4 + b] = w * i8_lane(dws[d], b);
+                    float *dst = prod + (k & 1) * kProdBuf + (pc * 16) * TS + tl;
+#pragma unroll
+                    for (int u = 0; u < 16; ++u) dst[u * TS] = p[u];
+                }
+                load(k + kPrefetch, vb[j], vsb[j]);
+                __syncthreads();
+            }
+        }
+    } else {
+        const float *col = prod + (tid < g.VD ? tid : 0) * TS;
+        for (int k = 0; k < steps; ++k) {
+            const int c = k - 1;
+            if (c >= 0 && c < nch && tid < g.VD) {
+                __builtin_amdgcn_s_setprio(2);
+                // T / 16 groups of 16 products, read into two register sets
+                // in turn so that a group's reads are in flight while the one
+                // before it is added
+                const float *buf = col + (c & 1) * kProdBuf;
+                const int rem = span - c * T;
+                float4 a[4], b[4];
+                lds_read16(a, buf);
+#pragma unroll
+                for (int gi = 0; gi < T / 16; ++gi) {
+                    if (gi % 2 == 0) {
+                        if (gi + 1 < T / 16) lds_read16(b, buf + (gi + 1) * 16);
+                        acc = add_first(acc, a, rem - gi * 16);
+                    } else {
+                        if (gi + 1 < T / 16) lds_read16(a, buf + (gi + 1) * 16);
+                        acc = add_first(acc, b, rem - gi * 16);
+                    }
+                }
+                __builtin_amdgcn_s_setprio(0);
+            }
+            __syncthreads();
+        }
+    }
+    if (tid < g.VD) out[(size_t(i) * g.H + h) * g.VD + tid] = acc;
+}
+
 }  // namespace
 
 extern "C" {
@@ -517,6 +853,36 @@ int nd_attend_step_i8_exact(nd_ctx *ctx, const nd_kv_geom *g, const void *kv, si
                kAttnMaxCap);
     ND_REQUIRE((reinterpret_cast<uintptr_t>(kv) & 255) == 0 && kv_stride % 256 == 0,
                "kv blocks must be 256-byte aligned");
+    if (g->v_head_dim <= 128 && g->cap <= kAttn2MaxCap) {
+        const int R = g->num_heads / g->num_kv_heads;
+        const size_t groups = count * size_t(g->num_kv_heads);
+        const size_t blocks = 8 * size_t(R) * ((groups + 7) / 8);
+        ND_REQUIRE(blocks <= 0x7fffffffu, "count %zu too large", count);
+        const size_t lds = size_t((g->cap + 3) & ~3) * 4 + 2 * kProdBuf * sizeof(float);
+        const int cw = g->v_head_dim <= 64 ? 1 : 2;
+        const int qc = g->qk_head_dim <= 64 ? g->qk_head_dim / 16 : 0;
+#define ND_ATTN2(CW, QC)                                                                       \
+    hipLaunchKernelGGL((attn_exact2_kernel<CW, QC>), dim3(unsigned(blocks)),                   \
+                       dim3(kAttn2Threads), lds, ctx->stream, ndkv::make_geom(g),               \
+                       static_cast<const uint8_t *>(kv), kv_stride, lo, hi, q, scale, quant_query, \
+                       out, int(groups))
+#define ND_ATTN2_QC(CW)                    \
+    switch (qc) {                          \
+    case 1: ND_ATTN2(CW, 1); break;        \
+    case 2: ND_ATTN2(CW, 2); break;        \
+    case 3: ND_ATTN2(CW, 3); break;        \
+    case 4: ND_ATTN2(CW, 4); break;        \
+    default: ND_ATTN2(CW, 0); break;       \
+    }
+        if (cw == 1) {
+            ND_ATTN2_QC(1)
+        } else {
+            ND_ATTN2_QC(2)
+        }
+#undef ND_ATTN2_QC
+#undef ND_ATTN2
+        return nd::check_launch("attn_exact2");
+    }
     dim3 grid(unsigned(g->num_heads), unsigned(count));
     const size_t lds = size_t((g->cap + 3) & ~3) * 4 + kVChunk;
     hipLaunchKernelGGL(attn_exact_kernel, grid, dim3(kThreads), lds, ctx->stream,

@@ -94,7 +94,8 @@ def _oracle(g, block_np, q, lo, hi):
                             g.v_head_dim)
 
 
-@pytest.mark.parametrize("H,KVH,QK,VD", [(12, 2, 48, 64), (12, 12, 64, 64), (4, 2, 16, 32)])
+@pytest.mark.parametrize("H,KVH,QK,VD", [(12, 2, 48, 64), (12, 12, 64, 64), (4, 2, 16, 32),
+                                         (4, 2, 32, 128), (6, 3, 16, 48), (2, 1, 16, 16)])
 @pytest.mark.parametrize("n", [1, 2, 33, 384, 2048])
 def test_attend_exact_causal(ctx, H, KVH, QK, VD, n):
     rng = np.random.default_rng(n * 13 + H + QK)
@@ -151,3 +152,44 @@ def test_attend_exact_bad_span_is_nan(ctx):
         out = host(nd.attend_step_i8(ctx, g, blk, nb, dev(np.array([lo], np.int32)),
                                      dev(np.array([hi], np.int32)), q, exact=True))
         assert np.isnan(out).all()
+
+
+def test_attend_exact_many_sessions_ragged(ctx):
+    """13 sessions x 2 kv heads: 26 head groups, a grid padded to whole XCD rounds."""
+    H, KVH, QK, VD, cap, count = 12, 2, 48, 64, 640, 13
+    rng = np.random.default_rng(23)
+    g, blk, nb = _fill(ctx, rng, H, KVH, QK, VD, cap, cap, count)
+    q = rng.normal(size=(count, H * QK)).astype(np.float32)
+    hi = rng.integers(0, cap, size=count).astype(np.int32)
+    lo = np.maximum(hi - rng.integers(0, cap, size=count), 0).astype(np.int32)
+    out = host(nd.attend_step_i8(ctx, g, blk, nb, dev(lo), dev(hi), dev(q), quant_query=True,
+                                 exact=True))
+    blocks = host(blk)
+    for i in range(count):
+        want = _oracle(g, blocks[i * nb:(i + 1) * nb], O.quant_rows(q[i], 1, H, QK),
+                       int(lo[i]), int(hi[i]))
+        assert _same_bits(out[i], want), i
+
+
+def test_attend_exact_large_cap(ctx):
+    """cap above 8192 takes the single-role kernel; same bits."""
+    H, KVH, QK, VD, cap = 4, 2, 16, 32, 9000
+    rng = np.random.default_rng(29)
+    g, blk, nb = _fill(ctx, rng, H, KVH, QK, VD, cap, cap)
+    q = rng.normal(size=H * QK).astype(np.float32)
+    for lo, hi in [(0, 8999), (4000, 4100)]:
+        out = host(nd.attend_step_i8(ctx, g, blk, nb, dev(np.array([lo], np.int32)),
+                                     dev(np.array([hi], np.int32)), dev(q)[None], exact=True))[0]
+        assert _same_bits(out, _oracle(g, host(blk), q, lo, hi))
+
+
+def test_attend_exact_cap_8192(ctx):
+    """The largest cap of the split-role kernel (scores and products fill 68 KB of LDS)."""
+    H, KVH, QK, VD, cap = 12, 2, 48, 64, 8192
+    rng = np.random.default_rng(31)
+    g, blk, nb = _fill(ctx, rng, H, KVH, QK, VD, cap, cap)
+    q = rng.normal(size=H * QK).astype(np.float32)
+    for lo, hi in [(0, 8191), (100, 8191), (0, 31)]:
+        out = host(nd.attend_step_i8(ctx, g, blk, nb, dev(np.array([lo], np.int32)),
+                                     dev(np.array([hi], np.int32)), dev(q)[None], exact=True))[0]
+        assert _same_bits(out, _oracle(g, host(blk), q, lo, hi))
