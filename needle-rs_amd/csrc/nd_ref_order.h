@@ -70,3 +70,91 @@ __device__ inline float cq_group_dot128(const CqGroupCodes<P> &c, const float *l
     for (int k = 0; k < 8; ++k) acc += lanes[k];
     return acc;
 }
+
+// acc += a[0].x; acc += a[0].y; ... acc += a[3].w: 16 dependent adds in one
+// asm block, so the compiler can neither reorder the terms nor move LDS
+// reads across the block (left to itself it hoists the next group's reads
+// and copies this group's registers to make room).
+__device__ __forceinline__ float nd_add16(float acc, const float4 (&a)[4])
+{
+    asm volatile(
+        "v_add_f32 %0, %1, %0\n\tv_add_f32 %0, %2, %0\n\tv_add_f32 %0, %3, %0\n\t"
+        "v_add_f32 %0, %4, %0\n\tv_add_f32 %0, %5, %0\n\tv_add_f32 %0, %6, %0\n\t"
+        "v_add_f32 %0, %7, %0\n\tv_add_f32 %0, %8, %0\n\tv_add_f32 %0, %9, %0\n\t"
+        "v_add_f32 %0, %10, %0\n\tv_add_f32 %0, %11, %0\n\tv_add_f32 %0, %12, %0\n\t"
+        "v_add_f32 %0, %13, %0\n\tv_add_f32 %0, %14, %0\n\tv_add_f32 %0, %15, %0\n\t"
+        "v_add_f32 %0, %16, %0"
+        : "+v"(acc)
+        : "v"(a[0].x), "v"(a[0].y), "v"(a[0].z), "v"(a[0].w), "v"(a[1].x), "v"(a[1].y),
+          "v"(a[1].z), "v"(a[1].w), "v"(a[2].x), "v"(a[2].y), "v"(a[2].z), "v"(a[2].w),
+          "v"(a[3].x), "v"(a[3].y), "v"(a[3].z), "v"(a[3].w)
+        : "memory");
+    return acc;
+}
+
+// acc += the first m terms of a (m uniform; m >= 16 adds all 16), in order.
+__device__ __forceinline__ float nd_add_first(float acc, const float4 (&a)[4], int m)
+{
+    if (m >= 16) return nd_add16(acc, a);
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+        const float4 &q = a[u / 4];
+        const float t = (u & 3) == 0 ? q.x : (u & 3) == 1 ? q.y : (u & 3) == 2 ? q.z : q.w;
+        if (u < m) acc += t;
+    }
+    return acc;
+}
+
+__device__ __forceinline__ void nd_lds_read16(float4 (&a)[4], const float *v)
+{
+    const float4 *v4 = reinterpret_cast<const float4 *>(v);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) a[u] = v4[u];
+}
+
+// ((acc + v[0]) + v[1]) + ... + v[n-1]: the reference's sequential fold, by
+// one thread over n floats in LDS (v 16-byte aligned; nothing past v[n-1] is
+// read).  Whole groups of 32 are read into two register sets in turn, so a
+// group's reads are in flight while the group before it is added.
+__device__ inline float nd_lds_fold(float acc, const float *v, int n)
+{
+    const int G = n / 32;
+    if (G > 0) {
+        float4 a[8], b[8];
+        auto rd = [&](float4 (&r)[8], int gi) {
+            const float4 *v4 = reinterpret_cast<const float4 *>(v + gi * 32);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) r[u] = v4[u];
+        };
+        auto add32 = [&](float s, const float4 (&r)[8]) {
+            const float4 lo[4] = {r[0], r[1], r[2], r[3]};
+            const float4 hi[4] = {r[4], r[5], r[6], r[7]};
+            return nd_add16(nd_add16(s, lo), hi);
+        };
+        rd(a, 0);
+        int gi = 0;
+        for (; gi + 2 <= G; gi += 2) {
+            // Wait for the LDS reads in flight (group gi, issued 32 adds ago)
+            // before issuing the next group's: at the loop head the compiler
+            // would otherwise wait for all reads after issuing them.
+            // 0xc07f: lgkmcnt(0), vmcnt and expcnt not waited on.
+            __builtin_amdgcn_s_waitcnt(0xc07f);
+            rd(b, gi + 1);
+            acc = add32(acc, a);
+            rd(a, gi + 2 < G ? gi + 2 : gi + 1);  // past the end: a harmless re-read
+            acc = add32(acc, b);
+        }
+        if (gi < G) acc = add32(acc, a);
+    }
+    int i = G * 32;
+    const float4 *v4 = reinterpret_cast<const float4 *>(v);
+    for (; i + 4 <= n; i += 4) {
+        const float4 q = v4[i / 4];
+        acc += q.x;
+        acc += q.y;
+        acc += q.z;
+        acc += q.w;
+    }
+    for (; i < n; ++i) acc += v[i];
+    return acc;
+}

@@ -578,47 +578,6 @@ __device__ __forceinline__ float attn_scores(const ndkv::Geom &g, const float *q
     return mx;
 }
 
-// acc += a[0].x; acc += a[0].y; ... acc += a[3].w, as 16 dependent adds in
-// one asm block: the compiler can neither reorder the terms nor move LDS
-// reads across the block (left to itself it hoists the next group's reads
-// and copies this group's registers to make room).
-__device__ __forceinline__ float add16(float acc, const float4 (&a)[4])
-{
-    asm volatile(
-        "v_add_f32 %0, %1, %0\n\tv_add_f32 %0, %2, %0\n\tv_add_f32 %0, %3, %0\n\t"
-        "v_add_f32 %0, %4, %0\n\tv_add_f32 %0, %5, %0\n\tv_add_f32 %0, %6, %0\n\t"
-        "v_add_f32 %0, %7, %0\n\tv_add_f32 %0, %8, %0\n\tv_add_f32 %0, %9, %0\n\t"
-        "v_add_f32 %0, %10, %0\n\tv_add_f32 %0, %11, %0\n\tv_add_f32 %0, %12, %0\n\t"
-        "v_add_f32 %0, %13, %0\n\tv_add_f32 %0, %14, %0\n\tv_add_f32 %0, %15, %0\n\t"
-        "v_add_f32 %0, %16, %0"
-        : "+v"(acc)
-        : "v"(a[0].x), "v"(a[0].y), "v"(a[0].z), "v"(a[0].w), "v"(a[1].x), "v"(a[1].y),
-          "v"(a[1].z), "v"(a[1].w), "v"(a[2].x), "v"(a[2].y), "v"(a[2].z), "v"(a[2].w),
-          "v"(a[3].x), "v"(a[3].y), "v"(a[3].z), "v"(a[3].w)
-        : "memory");
-    return acc;
-}
-
-// acc += the first m terms of a (m <= 16, uniform), in order.
-__device__ __forceinline__ float add_first(float acc, const float4 (&a)[4], int m)
-{
-    if (m >= 16) return add16(acc, a);
-#pragma unroll
-    for (int u = 0; u < 16; ++u) {
-        const float4 &q = a[u / 4];
-        const float t = (u & 3) == 0 ? q.x : (u & 3) == 1 ? q.y : (u & 3) == 2 ? q.z : q.w;
-        if (u < m) acc += t;
-    }
-    return acc;
-}
-
-__device__ __forceinline__ void lds_read16(float4 (&a)[4], const float *v)
-{
-    const float4 *v4 = reinterpret_cast<const float4 *>(v);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) a[u] = v4[u];
-}
-
 // acc += v[0]; acc += v[1]; ... acc += v[n-1] in index order, v 16-byte
 // aligned LDS with at least 32 readable floats past v[n-1].  Terms go in
 // groups of 32, read into two register sets in turn, so that a group's
@@ -636,9 +595,9 @@ __device__ inline float lds_chain(float acc, const float *v, int n)
     auto add32 = [&](float s, const float4 (&r)[8], int m) {
         const float4 lo[4] = {r[0], r[1], r[2], r[3]};
         const float4 hi[4] = {r[4], r[5], r[6], r[7]};
-        if (m >= 32) return add16(add16(s, lo), hi);
-        s = add_first(s, lo, m);
-        return m > 16 ? add_first(s, hi, m - 16) : s;
+        if (m >= 32) return nd_add16(nd_add16(s, lo), hi);
+        s = nd_add_first(s, lo, m);
+        return m > 16 ? nd_add_first(s, hi, m - 16) : s;
     };
     rd(a, 0);
     int gi = 0;
@@ -803,15 +762,15 @@ __global__ __launch_bounds__(kAttn2Threads, 4) void attn_exact2_kernel(
                 const float *buf = col + (c & 1) * kProdBuf;
                 const int rem = span - c * T;
                 float4 a[4], b[4];
-                lds_read16(a, buf);
+                nd_lds_read16(a, buf);
 #pragma unroll
                 for (int gi = 0; gi < T / 16; ++gi) {
                     if (gi % 2 == 0) {
-                        if (gi + 1 < T / 16) lds_read16(b, buf + (gi + 1) * 16);
-                        acc = add_first(acc, a, rem - gi * 16);
+                        if (gi + 1 < T / 16) nd_lds_read16(b, buf + (gi + 1) * 16);
+                        acc = nd_add_first(acc, a, rem - gi * 16);
                     } else {
-                        if (gi + 1 < T / 16) lds_read16(a, buf + (gi + 1) * 16);
-                        acc = add_first(acc, b, rem - gi * 16);
+                        if (gi + 1 < T / 16) nd_lds_read16(a, buf + (gi + 1) * 16);
+                        acc = nd_add_first(acc, b, rem - gi * 16);
                     }
                 }
                 __builtin_amdgcn_s_setprio(0);

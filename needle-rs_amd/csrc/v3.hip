@@ -44,26 +44,14 @@ constexpr int kT = 256;
 __device__ inline float sigmoidf_(float x) { return nd_sigmoidf(x); }
 
 // ((0 + p[0]) + p[1]) + ... + p[n-1]: a sequential fold, as the reference's
-// loops and iterator sums, run by one thread over values already in LDS
-// (16-byte aligned).  Products are formed in parallel beforehand; a product
-// rounds the same whether it is formed here or inside the fold.
+// loops and iterator sums, run by one thread over values already in LDS.
+// Products are formed in parallel beforehand; a product rounds the same
+// whether it is formed here or inside the fold.
 __device__ inline float chain_sum(const float *p, int n)
 {
+    if ((reinterpret_cast<uintptr_t>(p) & 15) == 0) return nd_lds_fold(0.0f, p, n);
     float s = 0.0f;
-    int i = 0;
-    if ((reinterpret_cast<uintptr_t>(p) & 15) == 0) {
-        // four 16-byte reads, then sixteen adds: the compiler overlaps the
-        // next reads with the adds (measured faster than hand pipelining)
-        const float4 *q = reinterpret_cast<const float4 *>(p);
-        for (; i + 16 <= n; i += 16) {
-            const float4 a = q[i >> 2], b = q[(i >> 2) + 1], c = q[(i >> 2) + 2], e = q[(i >> 2) + 3];
-            s += a.x; s += a.y; s += a.z; s += a.w;
-            s += b.x; s += b.y; s += b.z; s += b.w;
-            s += c.x; s += c.y; s += c.z; s += c.w;
-            s += e.x; s += e.y; s += e.z; s += e.w;
-        }
-    }
-    for (; i < n; ++i) s += p[i];
+    for (int i = 0; i < n; ++i) s += p[i];
     return s;
 }
 
