@@ -202,6 +202,113 @@ __global__ __launch_bounds__(kThreads) void cq_gemv_kernel(
     }
 }
 
+// The streaming form of the same GEMV: a workgroup owns a contiguous run of
+// 16-row tiles, builds the LUT replicas and loads its activations once, and
+// keeps the codes and norms of the next D tiles in registers while it works
+// on the current one.  Lane j of a row owns the ND consecutive code dwords
+// from j * ND, read as one run (wide loads).  Past the last row a lane reads the
+// last row again and stores nothing, so every load is unconditional and the
+// compiler waits for the oldest tile only.  Needs row_dwords == 16 * ND.
+template <int ND>
+struct CodeRun {
+    uint32_t v[ND];
+};
+
+template <int P, int ND, int REPL, int D>
+__global__ __launch_bounds__(kThreads) void cq_gemv_stream_kernel(
+    const uint8_t *__restrict__ packed, const float *__restrict__ norms,
+    const float *__restrict__ lut, const float *__restrict__ xh, float *__restrict__ y,
+    int row_start, int rows, int row_bytes, int num_groups, int group, int tiles_per_block)
+{
+    using V = typename LutVec<P>::T;
+    using CV = CodeRun<ND>;
+    constexpr int E = 4 * P;  // elements per code dword
+    __shared__ V rep[256 * REPL];
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int j = t & (kLanesPerRow - 1);
+    const int rg = t / kLanesPerRow;
+
+    for (int f = t; f < 256 * REPL; f += kThreads) {
+        const int e = f / REPL;
+        rep[f] = *reinterpret_cast<const V *>(lut + e * P);
+    }
+    // lane j's activations: elements [j * ND * E, (j + 1) * ND * E)
+    // the lane's ND * E <= group elements span groups g0 and g0 + 1 at most
+    float xr[ND][E];
+    const int g0 = (j * ND * E) / group;
+    bool second[ND];
+#pragma unroll
+    for (int i = 0; i < ND; ++i) {
+        const int d = j * ND + i;
+        second[i] = (d * E) / group != g0;
+        const float4 *xp = reinterpret_cast<const float4 *>(xh + d * E);
+#pragma unroll
+        for (int q = 0; q < E / 4; ++q) {
+            const float4 v = xp[q];
+            xr[i][4 * q + 0] = v.x;
+            xr[i][4 * q + 1] = v.y;
+            xr[i][4 * q + 2] = v.z;
+            xr[i][4 * q + 3] = v.w;
+        }
+    }
+    __syncthreads();
+
+    const V *lutl = rep + (lane & (REPL - 1));
+    const int ntiles = (rows + kRowsPerPass - 1) / kRowsPerPass;
+    const int tile0 = blockIdx.x * tiles_per_block;
+    const int tile1 = tile0 + tiles_per_block < ntiles ? tile0 + tiles_per_block : ntiles;
+    const int g1 = g0 + 1 < num_groups ? g0 + 1 : g0;
+    CV cb[D];
+    float nb[D][2];
+    auto load = [&](int tile, CV &c, float (&nr)[2]) {
+        int r = tile * kRowsPerPass + rg;
+        r = r < rows ? r : rows - 1;
+        const uint8_t *wr = packed + size_t(row_start + r) * row_bytes;
+        __builtin_memcpy(&c, wr + size_t(j) * (4 * ND), 4 * ND);
+        const float *nrow = norms + size_t(row_start + r) * num_groups;
+        nr[0] = nrow[g0];
+        nr[1] = nrow[g1];
+    };
+#pragma unroll
+    for (int k = 0; k < D; ++k) load(tile0 + k, cb[k], nb[k]);
+    for (int tile = tile0; tile < tile1; tile += D) {
+#pragma unroll
+        for (int k = 0; k < D; ++k) {
+            const int tt = tile + k;
+            if (tt < tile1) {
+                float total = 0.0f;
+#pragma unroll
+                for (int i = 0; i < ND; ++i) {
+                    const uint32_t dw = cb[k].v[i];
+                    float acc[P];
+#pragma unroll
+                    for (int q = 0; q < P; ++q) acc[q] = 0.0f;
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) {
+                        const uint32_t e = (dw >> (8 * b)) & 0xffu;
+                        const V v = lutl[e * REPL];
+                        const float *vf = reinterpret_cast<const float *>(&v);
+#pragma unroll
+                        for (int q = 0; q < P; ++q) acc[q] += vf[q] * xr[i][b * P + q];
+                    }
+                    float dot = acc[0];
+#pragma unroll
+                    for (int q = 1; q < P; ++q) dot += acc[q];
+                    total += (second[i] ? nb[k][1] : nb[k][0]) * dot;
+                }
+                total += __shfl_xor(total, 8, kLanesPerRow);
+                total += __shfl_xor(total, 4, kLanesPerRow);
+                total += __shfl_xor(total, 2, kLanesPerRow);
+                total += __shfl_xor(total, 1, kLanesPerRow);
+                const int r = tt * kRowsPerPass + rg;
+                if (j == 0 && r < rows) y[r] = total;
+            }
+            load(tt + D, cb[k], nb[k]);
+        }
+    }
+}
+
 // Reads code k of a row with the bit reader of cq.rs:914-925 (any width).
 __device__ inline uint32_t read_code(const uint8_t *row, int k, int w, int row_bytes)
 {
@@ -548,6 +655,43 @@ int nd_cq_matvec_rows_prepared(nd_ctx *ctx, const nd_cq *w, const float *xh, siz
     const int E = int(4 * w->per_byte);
     const bool fast = w->per_byte != 0 && w->row_bytes % 4 == 0 && size_t(E) <= w->group &&
                       row_dwords <= 16 * 6;
+    // the streaming kernel: rows of 16 * ND code dwords, ND <= 6 (in 768: 48
+    // dwords at 2 bits, 96 at 4 bits); other rows take the per-dword kernel
+    const bool stream = w->per_byte != 0 && w->row_bytes % 64 == 0 && row_dwords / 16 >= 1 &&
+                        row_dwords / 16 <= 6 && size_t(E) * (row_dwords / 16) <= w->group;
+    if (stream) {
+        const size_t tiles = (rows + kRowsPerPass - 1) / kRowsPerPass;
+        const size_t slots = 4 * size_t(ctx->num_cus > 0 ? ctx->num_cus : 256);
+        const int tpb = int(tiles > slots ? (tiles + slots - 1) / slots : 1);
+        dim3 grid(unsigned((tiles + tpb - 1) / tpb));
+        const int args_rb = int(w->row_bytes), ng = int(w->num_groups), gr = int(w->group);
+#define ND_CQS(P, NDV, REPL)                                                                   \
+    hipLaunchKernelGGL((cq_gemv_stream_kernel<P, NDV, REPL, 4>), grid, dim3(kThreads), 0,       \
+                       ctx->stream, w->packed, w->norms, w->lut, xh, y, int(row_start), int(rows), \
+                       args_rb, ng, gr, tpb)
+        const int nd = row_dwords / 16;
+        if (w->per_byte == 4) {
+            switch (nd) {
+            case 1: ND_CQS(4, 1, 8); break;
+            case 2: ND_CQS(4, 2, 8); break;
+            case 3: ND_CQS(4, 3, 8); break;
+            case 4: ND_CQS(4, 4, 8); break;
+            case 5: ND_CQS(4, 5, 8); break;
+            default: ND_CQS(4, 6, 8); break;
+            }
+        } else {
+            switch (nd) {
+            case 1: ND_CQS(2, 1, 16); break;
+            case 2: ND_CQS(2, 2, 16); break;
+            case 3: ND_CQS(2, 3, 16); break;
+            case 4: ND_CQS(2, 4, 16); break;
+            case 5: ND_CQS(2, 5, 16); break;
+            default: ND_CQS(2, 6, 16); break;
+            }
+        }
+#undef ND_CQS
+        return nd::check_launch("cq_gemv_stream");
+    }
     if (fast) {
         const int nd = (row_dwords + 15) / 16;
         dim3 grid(unsigned((rows + 63) / 64));

@@ -110,3 +110,21 @@ def test_errors_match_cqerror(ctx):
         with pytest.raises(nd.NeedleError) as e:
             nd.CqWeight(ctx, *args)
         assert e.value.code == code
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_matvec_tall_multi_tile(ctx, bits):
+    """40,003 rows: several 16-row tiles per workgroup and a ragged last tile."""
+    rng = np.random.default_rng(40003 + bits)
+    out, inn = 40003, 768
+    packed = rng.integers(0, 256, size=out * inn * bits // 8, dtype=np.uint8)
+    norms = (np.abs(rng.normal(0.0, 0.02, size=out * (inn // 128))) * np.sqrt(128.0))
+    blob = np.concatenate([packed, norms.astype(np.float16).view(np.uint8)])
+    g = nd.CqWeight(ctx, blob, out, inn, 128, bits, REAL_CB)
+    o = O.CqWeight(blob, out, inn, 128, bits, REAL_CB)
+    x = rng.normal(size=768).astype(np.float32)
+    xh = g.prepare_input(dev(x))[0]
+    y = host(g.matvec_prepared(xh))
+    assert _close(y, o.matvec(x))
+    band = host(g.matvec_rows_prepared(xh, 17, 39000))
+    assert _close(band, y[17:17 + 39000])
