@@ -71,7 +71,41 @@ def parse():
                    help="seconds of untimed warm-up before each timed loop (0 for counter runs)")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="also run a plain 1 GiB device copy (PMC byte-counter scale)")
+    p.add_argument("--summarize-trace", metavar="CSV", default=None,
+                   help="no GPU: print per-kernel statistics of the last --tail-steps forward "
+                        "steps of a rocprofv3 kernel-trace CSV (steps end at k_final)")
+    p.add_argument("--tail-steps", type=int, default=128)
     return p.parse_args()
+
+
+def summarize_trace(path, nsteps):
+    """Per-kernel durations over the last `nsteps` forward steps of a
+    rocprofv3 --kernel-trace CSV.  Each step launches k_final once, so the
+    window starts after the (nsteps + 1)-th last k_final ends; kernels of the
+    side stream in that window are included."""
+    import collections
+    import csv
+    rows = []
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]))
+    rows.sort()
+    finals = [i for i, r in enumerate(rows) if "::k_final(" in r[2]]
+    t0 = rows[finals[-(nsteps + 1)]][1]
+    sel = [r for r in rows if r[0] > t0]
+    agg = collections.defaultdict(list)
+    for a, b, n in sel:
+        agg[n].append(b - a)
+    span = (max(r[1] for r in sel) - t0) / 1e3
+    print(f"last {nsteps} steps: {span / nsteps:.1f} us per step (profiler on), {len(sel)} kernels")
+    print("| kernel | per step | avg us | min us | max us | us per step |")
+    print("|---|---|---|---|---|---|")
+    for n, v in sorted(agg.items(), key=lambda kv: -sum(kv[1])):
+        name = n.replace("(anonymous namespace)::", "").split("(")[0]
+        if name.startswith("void "):
+            name = name[5:]
+        print(f"| `{name}` | {len(v) / nsteps:.2f} | {sum(v) / len(v) / 1e3:.2f} | "
+              f"{min(v) / 1e3:.2f} | {max(v) / 1e3:.2f} | {sum(v) / nsteps / 1e3:.1f} |")
 
 
 MIN_WARM_S = 0.5
@@ -286,6 +320,9 @@ def main():
     global MIN_WARM_S
     args = parse()
     MIN_WARM_S = args.min_warm
+    if args.summarize_trace:
+        summarize_trace(args.summarize_trace, args.tail_steps)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1",
                           "n_gpus": args.gpus}))
