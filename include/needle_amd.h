@@ -32,7 +32,14 @@ enum nd_status {
     ND_ERR_CQ_BAD_GROUP = 12,
     ND_ERR_CQ_BAD_CODEBOOK_LEN = 13,
     ND_ERR_CQ_SHORT_BLOB = 14,
-    ND_ERR_CQ_EMPTY_SHAPE = 15
+    ND_ERR_CQ_EMPTY_SHAPE = 15,
+    /* .cact v3 container: CactError (needle-infer/src/cact.rs:58-108), a
+     * header that contradicts itself (V3GeometryError, v3.rs:84-90) and a
+     * directory that contradicts the header (V3LayoutError, v3.rs:180-190);
+     * the message names the variant and its fields */
+    ND_ERR_CACT = 20,
+    ND_ERR_V3_GEOMETRY = 21,
+    ND_ERR_V3_LAYOUT = 22
 };
 
 /* Last error message on this thread, or NULL.  Borrowed; valid until the
@@ -280,6 +287,24 @@ int nd_v3_positions(const nd_v3_batch *b, int32_t *pos);
  * undefined; free it. */
 int nd_v3_step(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *tokens,
                int32_t *next, float *logits);
+
+/* ---- the .cact v3 container (needle-infer/src/cact.rs, v3.rs) ----------- */
+
+/* Reads a Needle-3 container held in host memory (`bytes`, `len`): the
+ * 49-word header, the 28-float codebook, the 44-byte directory records,
+ * then the nameless canon walked and shape-checked as V3Layout::derive and
+ * validate do (v3.rs:236-330), with every float slot decoded (FP16 widened
+ * exactly).  Fills `cfg` as config_from_geometry does (v3.rs:25-82) and
+ * `canon_records` (optional) with the number of records up to final_norm;
+ * the heads manifest, probe-head tensors and tokenizer that may follow are
+ * not read.  Host only.  Replaces CactV3::from_bytes (cact.rs:994-1030) with
+ * config_from_geometry and V3Layout::derive. */
+int nd_v3_cact_config(const void *bytes, size_t len, nd_v3_cfg *cfg, size_t *canon_records);
+
+/* As nd_v3_cact_config, then uploads the model: the CQ blobs go up as
+ * stored (no repacking), the float tensors widened to f32.  Replaces
+ * model_from_cact (v3.rs:438-482). */
+int nd_v3_model_from_cact(nd_ctx *ctx, const void *bytes, size_t len, nd_v3_model **out);
 
 #ifdef __cplusplus
 }

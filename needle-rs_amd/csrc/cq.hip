@@ -40,25 +40,6 @@ __host__ __device__ inline int ternary_index(uint32_t code)
     return code == 3 ? 0 : (code == 1 ? 2 : 1);
 }
 
-// f16 -> f32, exact (math.rs:53-68).
-float f16_to_f32(uint16_t bits)
-{
-    uint32_t sign = uint32_t(bits >> 15) << 31;
-    uint32_t exp = (bits >> 10) & 0x1F;
-    uint32_t mant = bits & 0x3FF;
-    uint32_t out;
-    if (exp == 0) {
-        float val = float(mant) / float(1u << 24);
-        return sign ? -val : val;
-    }
-    if (exp == 31)
-        out = sign | 0x7F800000u | (mant << 13);
-    else
-        out = sign | ((exp + 127 - 15) << 23) | (mant << 13);
-    float f;
-    std::memcpy(&f, &out, 4);
-    return f;
-}
 
 // ---------------------------------------------------------------------------
 // prepare_input: one block per (group, batch row).
@@ -569,7 +550,7 @@ int nd_cq_from_blob(nd_ctx *ctx, const uint8_t *blob, size_t blob_len, size_t ou
     std::vector<float> norms(out_feat * num_groups);
     for (size_t i = 0; i < norms.size(); ++i) {
         const uint8_t *c = blob + n_packed + 2 * i;
-        norms[i] = f16_to_f32(uint16_t(c[0] | (c[1] << 8)));
+        norms[i] = nd_f16_to_f32(uint16_t(c[0] | (c[1] << 8)));
     }
     std::vector<float> lut;
     if (w->per_byte) {

@@ -1,6 +1,8 @@
 // The device-side Cactus-Quants weight, shared by the projection kernels.
 #pragma once
 
+#include <cstring>
+
 #include "nd_internal.h"
 
 struct nd_cq {
@@ -16,3 +18,20 @@ struct nd_cq {
     float *lut = nullptr;         // device [256][per_byte] (empty for 3-bit)
     float *lv = nullptr;          // device levels[16]
 };
+
+// f16 -> f32, exact: subnormals, infinities and NaN included (math.rs:53-68).
+inline float nd_f16_to_f32(uint16_t bits)
+{
+    const uint32_t sign = uint32_t(bits >> 15) << 31;
+    const uint32_t exp = (bits >> 10) & 0x1F;
+    const uint32_t mant = bits & 0x3FF;
+    if (exp == 0) {
+        const float val = float(mant) / float(1u << 24);
+        return sign ? -val : val;
+    }
+    const uint32_t out = exp == 31 ? (sign | 0x7F800000u | (mant << 13))
+                                   : (sign | ((exp + 127 - 15) << 23) | (mant << 13));
+    float f;
+    std::memcpy(&f, &out, 4);
+    return f;
+}

@@ -22,8 +22,10 @@ LIB_PATH = os.path.join(HERE, "libneedle_amd.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "needle_amd.h")
 
 ND_OK = 0
+ND_ERR_ARG, ND_ERR_CACT, ND_ERR_V3_GEOMETRY, ND_ERR_V3_LAYOUT = 1, 20, 21, 22
 ERRORS = {1: "ND_ERR_ARG", 2: "ND_ERR_HIP", 3: "ND_ERR_NOMEM", 11: "UnsupportedBits",
-          12: "BadGroup", 13: "BadCodebookLen", 14: "ShortBlob", 15: "EmptyShape"}
+          12: "BadGroup", 13: "BadCodebookLen", 14: "ShortBlob", 15: "EmptyShape",
+          20: "CactError", 21: "V3GeometryError", 22: "V3LayoutError"}
 
 
 class NeedleError(RuntimeError):
@@ -83,6 +85,8 @@ _SIGS = [
     ("nd_v3_batch_free", None, [_vp]),
     ("nd_v3_positions", C.c_int, [_vp, _vp]),
     ("nd_v3_step", C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp]),
+    ("nd_v3_cact_config", C.c_int, [_vp, _sz, _vp, C.POINTER(_sz)]),
+    ("nd_v3_model_from_cact", C.c_int, [_vp, _vp, _sz, C.POINTER(_vp)]),
 ]
 
 
@@ -430,9 +434,57 @@ def v3_cfg(g):
     return c
 
 
+def geom_of_cfg(c):
+    """The geometry dict (the keys v3_cfg reads) of an nd_v3_cfg."""
+    g = {k: getattr(c, k) for k in (
+        "vocab_size", "out_vocab", "d_model", "num_heads", "num_kv_heads", "num_layers",
+        "qk_head_dim", "v_head_dim", "max_seq_len", "hada_n", "mhc_lanes", "sliding_window",
+        "qkv_conv_taps", "e_heads", "e_slots", "e_sub_dim", "e_conv_taps", "e_conv_dilation",
+        "e_seed_heads")}
+    g["rope_theta"] = c.rope_theta
+    g["global_layers"] = [c.global_layers[i] for i in range(c.n_global)]
+    g["orders"] = [c.orders[i] for i in range(c.n_orders)]
+    g["sites"] = [c.sites[i] for i in range(c.n_sites)]
+    return g
+
+
+def _container_bytes(data):
+    if isinstance(data, (str, os.PathLike)):
+        with open(data, "rb") as f:
+            data = f.read()
+    return np.frombuffer(data, np.uint8) if not isinstance(data, np.ndarray) else \
+        np.ascontiguousarray(data, np.uint8)
+
+
+def cact_v3_config(data):
+    """A .cact v3 container (path or bytes) read as CactV3::from_bytes +
+    config_from_geometry + V3Layout::derive (needle-infer/src/cact.rs:994-1030,
+    v3.rs:25-386) do: returns (geometry dict, records up to final_norm).
+    Host only; raises NeedleError with the reference's error variant."""
+    buf = _container_bytes(data)
+    cfg, n = V3Cfg(), _sz()
+    _check(lib().nd_v3_cact_config(buf.ctypes.data_as(C.c_void_p), buf.size, C.byref(cfg),
+                                   C.byref(n)))
+    return geom_of_cfg(cfg), n.value
+
+
 class V3Model:
     """A Needle-3 model on the device, from canonical container records
-    (V3Layout::derive order, crates/needle-infer/src/v3.rs:236-330)."""
+    (V3Layout::derive order, crates/needle-infer/src/v3.rs:236-330), or from a
+    .cact v3 container with `from_cact` (model_from_cact, v3.rs:438-482)."""
+
+    @classmethod
+    def from_cact(cls, ctx, data):
+        buf = _container_bytes(data)
+        geom, _ = cact_v3_config(buf)
+        self = cls.__new__(cls)
+        self.ctx, self.geom = ctx, geom
+        h = C.c_void_p()
+        _check(lib().nd_v3_model_from_cact(ctx.h, buf.ctypes.data_as(C.c_void_p), buf.size,
+                                           C.byref(h)))
+        self.h = h
+        self.rows = lib().nd_v3_logit_rows(h)
+        return self
 
     def __init__(self, ctx, geom, records, codebook):
         self.ctx, self.geom = ctx, geom

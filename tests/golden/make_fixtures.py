@@ -4,7 +4,7 @@ self-contained data files under tests/golden/.
 Reads JSON data files only (no reference code is imported or run):
   tests/v3_kv_quant_vectors.json  -> kv_quant_vectors.json   (upstream fake_quant KAT)
   tests/cact_vectors.json         -> cq_codebook.json        (28-float cb2|cb3|cb4)
-  tests/cact_v3_vectors.json      -> v3_geometry.json, v3_cq_records.json
+  tests/cact_v3_vectors.json      -> v3_geometry.json, v3_cq_records.json, v3_directory.json
 Run from the repo root:  python tests/golden/make_fixtures.py [/root/reference]
 """
 import json
@@ -45,4 +45,15 @@ dump("v3_cq_records.json", {
     "provenance": "needle-rs tests/cact_v3_vectors.json 'records' with dtype 3 (CQ)",
     "records": cq,
 })
-print(f"wrote {len(kv['cases'])} kv cases, {len(cq)} CQ records")
+dump("v3_directory.json", {
+    "provenance": "needle-rs tests/cact_v3_vectors.json: the whole needle3.cact directory "
+                  "(every record's dtype, ndim, shape, offset, nbytes, group, bits) and sizes",
+    "container_bytes": v3["container_bytes"],
+    "header_bytes": v3["header_bytes"],
+    "record_bytes": v3["record_bytes"],
+    "codebook_len": v3["codebook_len"],
+    "records": [[r["index"], r["dtype"], r["ndim"], r["shape"], r["offset"], r["nbytes"],
+                 r["group"], r["bits"]] for r in v3["records"]],
+})
+print(f"wrote {len(kv['cases'])} kv cases, {len(cq)} CQ records, "
+      f"{len(v3['records'])} directory records")
