@@ -9,7 +9,11 @@ algorithmic bytes / time.
 Also reported ("secondary"):
   - int8-KV decode attention at ctx 2048, 12 heads x 64, over 320
     independent session caches per step (append one token + attend), and
-    the batch-1 latencies of both kernels;
+    the batch-1 latencies of both kernels; attention alone at ctx 512 and
+    8192 over 1 GiB of caches;
+  - the Cactus-Quants (Format A) decode GEMV, tolerance and reference order,
+    streaming and at the shipped shapes;
+  - the Format B prefill GEMM on bf16 MFMA;
   - the Needle-3 forward (shipped geometry, random init, int8 KV cache),
     bit-identical to the CPU oracle: one session with a 128-token prompt and
     256 greedy tokens, and 64 sessions each prefilled with 2048 tokens then
@@ -250,6 +254,43 @@ def format_a_runs(torch, nd, steps):
     return out
 
 
+def attention_ctx_runs(torch, nd, ctx, gen, steps):
+    """Decode attention over the int8 cache at ctx 512 and 8192 (12 heads x
+    64, MHA, scale 1/8): as many independent session caches as stream over
+    1 GiB per step, attention only; plus one session's latency."""
+    out = {}
+    for ctx_len in (512, 8192):
+        per = ctx_len * (2 * ATT_H * ATT_D + 2 * ATT_H * 4) + 2 * ATT_H * ATT_D * 4
+        S = -(-(1 << 30) // per)
+        g = nd.kv_geom(ATT_H, ATT_H, ATT_D, ATT_D, ctx_len)
+        nb = nd.kv_block_bytes(g)
+        off = nd.kv_offsets(g)
+        blk = torch.empty(S * nb, dtype=torch.uint8, device="cuda")
+        view = blk.view(S, nb)
+        view[:, :off["ks"]].copy_(torch.randint(-127, 128, (S, off["ks"]), dtype=torch.int8,
+                                                device="cuda", generator=gen).view(torch.uint8))
+        scales = torch.rand(S, 2 * ATT_H * ctx_len, device="cuda", generator=gen) * 0.03 + 1e-3
+        view[:, off["ks"]:off["ks"] + 8 * ATT_H * ctx_len].copy_(scales.view(torch.uint8).view(S, -1))
+        del scales
+        q = torch.randn(S, ATT_H * ATT_D, device="cuda", generator=gen)
+        hi = torch.full((S,), ctx_len - 1, dtype=torch.int32, device="cuda")
+        lo = torch.zeros(S, dtype=torch.int32, device="cuda")
+        o = torch.empty(S, ATT_H * ATT_D, device="cuda")
+        ms = timed_loop(torch, lambda: nd.attend_step_i8(ctx, g, blk, nb, lo, hi, q,
+                                                         quant_query=True, out=o),
+                        max(10, steps // 2), 5)
+        ms1 = timed_loop(torch, lambda: nd.attend_step_i8(ctx, g, blk, nb, lo[:1], hi[:1], q[:1],
+                                                          quant_query=True, out=o[:1]), 200, 20)
+        gbs = S * per / (ms * 1e-3) / 1e9
+        out[f"decode_attention_int8_ctx{ctx_len}"] = {
+            "workload": f"{S} sessions x 12 heads x 64, ctx {ctx_len}, int8 K/V + f32 scales",
+            "attention_GBps": round(gbs, 2), "attention_frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+            "bytes_per_session_decode": per, "sessions": S,
+            "single_session_attention_us": round(ms1 * 1e3, 2)}
+        del blk, view, q, o
+    return out
+
+
 def forward_runs(torch, nd, ctx, sessions, ctx_len, cpu_tokens=8):
     """The Needle-3 forward on the device: batch 1 (128-token prompt, 256
     greedy steps) and `sessions` sessions prefilled with `ctx_len` tokens
@@ -456,6 +497,9 @@ def main():
                 "single_session_attention_us": round(ms_att1 * 1e3, 2),
             }
         }
+
+    if not args.no_secondary and args.only in (None, "attn"):
+        result.setdefault("secondary", {}).update(attention_ctx_runs(torch, nd, ctx, gen, args.steps))
 
     if not args.no_secondary and args.only is None:
         result.setdefault("secondary", {})["prefill_gemm_bf16"] = gemm_runs(torch, nd, ctx, gen, 50)
