@@ -268,6 +268,16 @@ size_t nd_v3_logit_rows(const nd_v3_model *m);
  * positions each; `hint` sizes the reference's logical ring growth. */
 int nd_v3_batch_create(nd_ctx *ctx, const nd_v3_model *m, size_t sessions, size_t max_len,
                        size_t hint, nd_v3_batch **out);
+/* As nd_v3_batch_create, for steps of up to `max_chunk` consecutive
+ * positions per session (nd_v3_prefill): the per-row buffers hold
+ * sessions * max_chunk rows and each local layer's ring max_chunk - 1 more
+ * positions than its window, so that a step's own writes never reach a slot
+ * one of its rows still attends over.  No reference counterpart: it sizes
+ * the device state behind the reference's chunked prefill
+ * (V3Model::prefill, v3/model.rs:512-523). */
+int nd_v3_batch_create_chunked(nd_ctx *ctx, const nd_v3_model *m, size_t sessions,
+                               size_t max_len, size_t hint, size_t max_chunk,
+                               nd_v3_batch **out);
 void nd_v3_batch_free(nd_v3_batch *b);
 /* Each session's next write position (V3Cache::pos). */
 int nd_v3_positions(const nd_v3_batch *b, int32_t *pos);
@@ -287,6 +297,19 @@ int nd_v3_positions(const nd_v3_batch *b, int32_t *pos);
  * undefined; free it. */
 int nd_v3_step(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *tokens,
                int32_t *next, float *logits);
+
+/* `count` consecutive positions for every session in one pass over the
+ * layers: tokens (host) is [sessions][count], session-major.  Replaces the
+ * reference's chunked prefill (V3Model::prefill -> forward_impl_pooled,
+ * v3/model.rs:512-523, 550-980), which is bit-identical to stepping
+ * (needle-infer/tests/v3_kv_int8.rs:269-282): so is this -- the caches,
+ * the conv tails and the logits of the last position equal `count`
+ * nd_v3_step calls.  Every position's projections, attention and MLP run
+ * as rows of one batch; the causal conv and the Engram conv read the step's
+ * earlier rows.  `next` and `logits` as for nd_v3_step, for each session's
+ * last position.  count <= the batch's max_chunk. */
+int nd_v3_prefill(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *tokens,
+                  size_t count, int32_t *next, float *logits);
 
 /* ---- the .cact v3 container (needle-infer/src/cact.rs, v3.rs) ----------- */
 

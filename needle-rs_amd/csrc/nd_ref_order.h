@@ -14,6 +14,13 @@ int nd_cq_exact_set(nd_ctx *ctx, hipStream_t stream, int n, const nd_cq *const *
                     size_t batch, const size_t *row_start, const size_t *rows, float *const *y,
                     const char *what);
 
+// nd_attend_step_i8_exact with query row i reading the KV block of
+// kv + (i / rows_per_block) * kv_stride: several positions of one session
+// in one call.
+int nd_attend_exact_rows(nd_ctx *ctx, const nd_kv_geom *g, const void *kv, size_t kv_stride,
+                         size_t count, int rows_per_block, const int32_t *lo, const int32_t *hi,
+                         const float *q, float scale, int quant_query, float *out);
+
 // One 128-wide group of a Cactus-Quants row dotted with a prepared
 // activation group in the reference's order (cq.rs:838-873): element e into
 // lane e % 8, each lane a chain over the 16 elements it holds, the lanes

@@ -359,7 +359,7 @@ __device__ inline float i8_lane(uint32_t dw, int b) { return float(int32_t(dw <<
 
 __global__ __launch_bounds__(kThreads) void attn_exact_kernel(ndkv::Geom g,
                                                              const uint8_t *__restrict__ kv,
-                                                             size_t stride,
+                                                             size_t stride, int rows_per_block,
                                                              const int32_t *__restrict__ lo,
                                                              const int32_t *__restrict__ hi,
                                                              const float *__restrict__ q, float scale,
@@ -372,7 +372,7 @@ __global__ __launch_bounds__(kThreads) void attn_exact_kernel(ndkv::Geom g,
     const int h = blockIdx.x, tid = threadIdx.x;
     const size_t i = blockIdx.y;
     const int kvh = h / (g.H / g.KVH);
-    const uint8_t *blk = kv + i * stride;
+    const uint8_t *blk = kv + (i / size_t(rows_per_block)) * stride;
     const int p0 = lo[i];
     const int span = hi[i] - p0 + 1;
     if (p0 < 0 || span < 1 || span > g.cap) {
@@ -621,7 +621,7 @@ template <int CW, int QC>
 __global__ __launch_bounds__(kAttn2Threads, 4) void attn_exact2_kernel(
     ndkv::Geom g, const uint8_t *__restrict__ kv, size_t stride, const int32_t *__restrict__ lo,
     const int32_t *__restrict__ hi, const float *__restrict__ q, float scale, int quant_query,
-    float *__restrict__ out, int groups)
+    float *__restrict__ out, int groups, int rows_per_block)
 {
     constexpr int NT = kAttn2Threads;
     extern __shared__ __align__(16) float sm[];
@@ -635,7 +635,7 @@ __global__ __launch_bounds__(kAttn2Threads, 4) void attn_exact2_kernel(
     if (grp >= groups) return;  // padding block: the whole block leaves
     const int i = grp / g.KVH, kvh = grp - (grp / g.KVH) * g.KVH;
     const int h = kvh * R + slot8 % R;
-    const uint8_t *blk = kv + size_t(i) * stride;
+    const uint8_t *blk = kv + size_t(i / rows_per_block) * stride;
     const int p0 = lo[i];
     const int span = hi[i] - p0 + 1;
     if (p0 < 0 || span < 1 || span > g.cap) {
@@ -803,7 +803,17 @@ int nd_attend_step_i8_exact(nd_ctx *ctx, const nd_kv_geom *g, const void *kv, si
                             size_t count, const int32_t *lo, const int32_t *hi, const float *q,
                             float scale, int quant_query, float *out)
 {
+    return nd_attend_exact_rows(ctx, g, kv, kv_stride, count, 1, lo, hi, q, scale, quant_query, out);
+}
+
+}  // extern "C"
+
+int nd_attend_exact_rows(nd_ctx *ctx, const nd_kv_geom *g, const void *kv, size_t kv_stride,
+                         size_t count, int rows_per_block, const int32_t *lo, const int32_t *hi,
+                         const float *q, float scale, int quant_query, float *out)
+{
     if (int rc = nd::enter(ctx)) return rc;
+    ND_REQUIRE(rows_per_block >= 1, "rows_per_block %d", rows_per_block);
     if (int rc = ndkv::check_geom(g)) return rc;
     if (count == 0) return ND_OK;
     ND_REQUIRE(kv && lo && hi && q && out, "null buffer");
@@ -824,7 +834,7 @@ int nd_attend_step_i8_exact(nd_ctx *ctx, const nd_kv_geom *g, const void *kv, si
     hipLaunchKernelGGL((attn_exact2_kernel<CW, QC>), dim3(unsigned(blocks)),                   \
                        dim3(kAttn2Threads), lds, ctx->stream, ndkv::make_geom(g),               \
                        static_cast<const uint8_t *>(kv), kv_stride, lo, hi, q, scale, quant_query, \
-                       out, int(groups))
+                       out, int(groups), rows_per_block)
 #define ND_ATTN2_QC(CW)                    \
     switch (qc) {                          \
     case 1: ND_ATTN2(CW, 1); break;        \
@@ -845,9 +855,7 @@ int nd_attend_step_i8_exact(nd_ctx *ctx, const nd_kv_geom *g, const void *kv, si
     dim3 grid(unsigned(g->num_heads), unsigned(count));
     const size_t lds = size_t((g->cap + 3) & ~3) * 4 + kVChunk;
     hipLaunchKernelGGL(attn_exact_kernel, grid, dim3(kThreads), lds, ctx->stream,
-                       ndkv::make_geom(g), static_cast<const uint8_t *>(kv), kv_stride, lo, hi, q,
-                       scale, quant_query, out);
+                       ndkv::make_geom(g), static_cast<const uint8_t *>(kv), kv_stride,
+                       rows_per_block, lo, hi, q, scale, quant_query, out);
     return nd::check_launch("attn_exact");
 }
-
-}  // extern "C"

@@ -183,6 +183,32 @@ __global__ void k_engram_conv(float *__restrict__ ev, const float *__restrict__ 
     ev[b * d + c] = acc;
 }
 
+// k_engram_conv for a step of C consecutive positions per session: the raw
+// values of the step's rows in `raw` ([R][d], unchanged), the conv into
+// `out`, the tails as they stood before the step (updated after by
+// k_tails).
+__global__ void k_engram_conv_rows(const float *__restrict__ raw, float *__restrict__ out,
+                                   const float *__restrict__ taps, const float *__restrict__ tail,
+                                   const int32_t *__restrict__ pos, int taps_n, int dil,
+                                   int max_order, int reach, int d, int C)
+{
+    const size_t b = blockIdx.y;
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= d) return;
+    const size_t sess = b / C;
+    const int r = int(b % C);
+    const int p = pos[b];
+    const float *tb = tail + sess * size_t(reach) * d;
+    float acc = 0.0f;
+    for (int j = 0; j < taps_n; ++j) {
+        const int back = j * dil;
+        if (back > p || p < j * max_order) continue;
+        const float val = back <= r ? raw[(b - back) * d + c] : tb[size_t(reach - (back - r)) * d + c];
+        acc += taps[j * d + c] * val;
+    }
+    out[b * d + c] = acc;
+}
+
 // ---- layer input: the previous layer's scatter up, then this layer's mix
 // down (mhc.rs:80-103): rms_unit of the lanes, prepare_input, the phi_pre
 // rows, the gated lane sum, the Engram gate and ZCRMSNorm, prepared for the
@@ -388,17 +414,23 @@ __global__ __launch_bounds__(kT) void k_layer_in(LayerIn a)
 // (attention.rs:108-150), q to global, and k and v quantised straight into
 // the session's int8 KV block at slot pos % cap (write_kv, cache.rs:346-379).
 struct QkvKv {
-    float *q;                               // [B][qd] in: projection, out: normed + roped
-    const float *k, *v;                     // [B][kd], [B][vd] projections
+    float *q;                               // [R][qd] in: projection, out: normed + roped
+    const float *k, *v;                     // [R][kd], [R][vd] projections
     float *qt, *kt, *vt;                    // tails [B][taps-1][dim]
     const float *q_taps, *k_taps, *v_taps;  // [taps][dim]
     const float *q_norm, *k_norm;           // [hd]
-    const float *rope;                      // [B][2][hd/2]: cos then sin
-    const int32_t *pos;
+    const float *rope;                      // [R][2][hd/2]: cos then sin
+    const int32_t *pos;                     // [R]
     int qd, kd, vd, taps, H, KVH, hd, VD;
-    uint8_t *kv;                            // session b's block at kv + b * kv_stride
+    uint8_t *kv;                            // session s's block at kv + s * kv_stride
     size_t kv_stride, v_off, ks_off, vs_off;
     int cap;
+    // Several consecutive positions per session (prefill): row r of the C
+    // rows of a session is position pos[r]; earlier positions of the step
+    // are read from the projection rows before it, older ones from the
+    // tails, which this kernel does not change; the normed q goes to q_out.
+    int C;
+    float *q_out;
 };
 
 // cache.rs:401-438 for one channel: the conv output, with the tail shifted
@@ -416,32 +448,83 @@ __device__ inline float conv_one(float raw, float *tail, const float *taps, int 
     return acc;
 }
 
+// conv_one for row r (position p) of a step holding C consecutive positions
+// of one session: the value j positions back comes from row r - j of `rows`
+// (row stride `dim`) while it is in this step, else from the tail as it
+// stood before the step (tail[T - 2] the position just before the step).
+__device__ inline float conv_rows(const float *rows, const float *tail, const float *taps, int dim,
+                                  int c, int T, int p, int r)
+{
+    float acc = taps[c] * rows[size_t(r) * dim + c];
+    for (int j = 1; j < T; ++j) {
+        if (j > p) break;
+        const float prev = j <= r ? rows[size_t(r - j) * dim + c]
+                                  : tail[size_t(T - 1 - (j - r)) * dim + c];
+        acc += taps[j * dim + c] * prev;
+    }
+    return acc;
+}
+
+// After a step of C positions: each session's tail of the last `keep`
+// values of `rows` (row stride `dim`, the session's C rows consecutive),
+// older entries shifted in from the previous tail when C < keep.
+__global__ void k_tails(const float *__restrict__ rows, float *__restrict__ tail, int keep, int C,
+                        int dim)
+{
+    const size_t s = blockIdx.y;
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= dim || keep <= 0) return;
+    float *tb = tail + s * size_t(keep) * dim;
+    const float *rb = rows + s * size_t(C) * dim;
+    float old[16];
+    for (int k = 0; k < keep && k < 16; ++k) old[k] = tb[size_t(k) * dim + c];
+    for (int k = 0; k < keep && k < 16; ++k) {
+        const int from_row = C - keep + k;  // row of the step, or an older position
+        tb[size_t(k) * dim + c] = from_row >= 0 ? rb[size_t(from_row) * dim + c] : old[k + C];
+    }
+}
+
 constexpr int kMaxQkDims = 2048;  // (num_heads + num_kv_heads) * qk_head_dim
 constexpr int kMaxVDims = 1024;   // num_kv_heads * v_head_dim
 
+template <bool CHUNK>
 __global__ __launch_bounds__(kT) void k_qkv_kv(QkvKv a)
 {
     __shared__ __align__(16) float qk[kMaxQkDims], sq[kMaxQkDims], vl[kMaxVDims];
     __shared__ float rms[64];
     const size_t b = blockIdx.x;
+    const size_t sess = CHUNK ? b / a.C : b;
+    const int r = CHUNK ? int(b % a.C) : 0;
     const int p = a.pos[b], T = a.taps, hd = a.hd, half = hd / 2;
     const int nq = a.qd + a.kd, heads = a.H + a.KVH;
     for (int c = threadIdx.x; c < nq + a.vd; c += kT) {
         if (c < a.qd) {
             float v = a.q[b * a.qd + c];
-            if (T > 0) v = conv_one(v, a.qt + b * size_t(T - 1) * a.qd, a.q_taps, a.qd, c, T, p);
+            if (T > 0) {
+                const float *tl = a.qt + sess * size_t(T - 1) * a.qd;
+                v = CHUNK ? conv_rows(a.q + (b - r) * a.qd, tl, a.q_taps, a.qd, c, T, p, r)
+                          : conv_one(v, a.qt + b * size_t(T - 1) * a.qd, a.q_taps, a.qd, c, T, p);
+            }
             qk[c] = v;
             sq[c] = v * v;
         } else if (c < nq) {
             float v = a.k[b * a.kd + c - a.qd];
-            if (T > 0)
-                v = conv_one(v, a.kt + b * size_t(T - 1) * a.kd, a.k_taps, a.kd, c - a.qd, T, p);
+            if (T > 0) {
+                const float *tl = a.kt + sess * size_t(T - 1) * a.kd;
+                v = CHUNK ? conv_rows(a.k + (b - r) * a.kd, tl, a.k_taps, a.kd, c - a.qd, T, p, r)
+                          : conv_one(v, a.kt + b * size_t(T - 1) * a.kd, a.k_taps, a.kd, c - a.qd,
+                                     T, p);
+            }
             qk[c] = v;
             sq[c] = v * v;
         } else {
             float v = a.v[b * a.vd + c - nq];
-            if (T > 0)
-                v = conv_one(v, a.vt + b * size_t(T - 1) * a.vd, a.v_taps, a.vd, c - nq, T, p);
+            if (T > 0) {
+                const float *tl = a.vt + sess * size_t(T - 1) * a.vd;
+                v = CHUNK ? conv_rows(a.v + (b - r) * a.vd, tl, a.v_taps, a.vd, c - nq, T, p, r)
+                          : conv_one(v, a.vt + b * size_t(T - 1) * a.vd, a.v_taps, a.vd, c - nq,
+                                     T, p);
+            }
             vl[c - nq] = v;
         }
     }
@@ -461,7 +544,7 @@ __global__ __launch_bounds__(kT) void k_qkv_kv(QkvKv a)
         const float c = cs[i], s = sn[i];
         const float o1 = x1 * c - x2 * s, o2 = x2 * c + x1 * s;
         if (hh < a.H) {
-            float *o = a.q + b * a.qd + hh * hd;
+            float *o = (CHUNK ? a.q_out : a.q) + b * a.qd + hh * hd;
             o[i] = o1;
             o[half + i] = o2;
         } else {
@@ -472,7 +555,7 @@ __global__ __launch_bounds__(kT) void k_qkv_kv(QkvKv a)
     __syncthreads();
     // quantise (cache.rs:80-104): one wave per kv head vector, K then V
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    uint8_t *blk = a.kv + b * a.kv_stride;
+    uint8_t *blk = a.kv + sess * a.kv_stride;
     const int slot = p % a.cap;
     for (int vec = wave; vec < 2 * a.KVH; vec += kT / 64) {
         const bool isv = vec >= a.KVH;
@@ -773,15 +856,16 @@ __global__ __launch_bounds__(64) void k_mhc_gates(MhcGates a)
 __global__ __launch_bounds__(kT) void k_final(float *__restrict__ lanes, const float *__restrict__ y,
                                              const float *__restrict__ gp, const float *__restrict__ gr,
                                              const float *__restrict__ final_norm,
-                                             float *__restrict__ xh, int n, int d, Prep pp)
+                                             float *__restrict__ xh, int n, int d, Prep pp, int rstride)
 {
     __shared__ __align__(16) float ln[kMaxLanesD], ms[1024], sq[1024];
     __shared__ float gpp[16], grr[256], tot;
-    const size_t b = blockIdx.x;
-    if (threadIdx.x < n) gpp[threadIdx.x] = gp[b * n + threadIdx.x];
-    if (threadIdx.x < n * n) grr[threadIdx.x] = gr[b * n * n + threadIdx.x];
+    const size_t b = blockIdx.x;                       // output row: one per session
+    const size_t rw = b * rstride + (rstride - 1);     // the session's last position
+    if (threadIdx.x < n) gpp[threadIdx.x] = gp[rw * n + threadIdx.x];
+    if (threadIdx.x < n * n) grr[threadIdx.x] = gr[rw * n * n + threadIdx.x];
     __syncthreads();
-    scatter_up(lanes + b * size_t(n) * d, ln, gpp, grr, y + b * d, n, d);
+    scatter_up(lanes + rw * size_t(n) * d, ln, gpp, grr, y + rw * d, n, d);
     __syncthreads();
     for (int c = threadIdx.x; c < d; c += kT) {
         float acc = 0.0f;
@@ -911,6 +995,9 @@ struct SessionHost {
 struct nd_v3_batch {
     int device = 0;
     int B = 0, max_len = 0;
+    // positions one step may take per session (prefill), and the rows the
+    // per-row buffers hold: B * chunk
+    int chunk = 1, R = 0;
     std::vector<SessionHost> s;
     std::vector<uint8_t *> kv;        // per layer: B blocks
     std::vector<size_t> kv_stride;    // per layer
@@ -926,6 +1013,9 @@ struct nd_v3_batch {
           *hpost = nullptr, *hres = nullptr, *emb = nullptr, *fetched = nullptr, *fh = nullptr,
           *ek = nullptr, *ev = nullptr, *xh = nullptr, *logits = nullptr;
     float *gp = nullptr, *gr = nullptr;  // scatter-up gates of the latest layer
+    // several positions per step: the normed q ([R][qd]) and the Engram
+    // conv ([sites][R][d]) go here, the projections' rows stay as they are
+    float *qn = nullptr, *evc = nullptr;
     int32_t *next = nullptr;
     // The scatter-up gates of a layer depend only on its input lanes: they
     // run on `side` while the layer's attention and MLP run on the caller's
@@ -944,9 +1034,6 @@ struct nd_v3_batch {
     bool stage_pending[kStages] = {};
     int stage_next = 0;
     size_t step_bytes = 0;
-    int32_t *tok_dev = nullptr, *pos_dev = nullptr, *lo_dev = nullptr, *hi_dev = nullptr,
-            *rows_dev = nullptr;
-    float *rope_dev = nullptr;
     int32_t *next_host = nullptr;
     std::vector<void *> mem;
 
@@ -1241,6 +1328,12 @@ size_t nd_v3_logit_rows(const nd_v3_model *m)
 int nd_v3_batch_create(nd_ctx *ctx, const nd_v3_model *m, size_t sessions, size_t max_len,
                        size_t hint, nd_v3_batch **out)
 {
+    return nd_v3_batch_create_chunked(ctx, m, sessions, max_len, hint, 1, out);
+}
+
+int nd_v3_batch_create_chunked(nd_ctx *ctx, const nd_v3_model *m, size_t sessions, size_t max_len,
+                               size_t hint, size_t max_chunk, nd_v3_batch **out)
+{
     if (int rc = nd::enter(ctx)) return rc;
     ND_REQUIRE(m && out, "null argument");
     *out = nullptr;
@@ -1248,12 +1341,17 @@ int nd_v3_batch_create(nd_ctx *ctx, const nd_v3_model *m, size_t sessions, size_
     ND_REQUIRE(sessions >= 1 && sessions <= 4096, "sessions %zu out of 1..4096", sessions);
     ND_REQUIRE(max_len >= 1 && max_len <= size_t(c.max_seq_len), "max_len %zu out of 1..%d",
                max_len, c.max_seq_len);
+    ND_REQUIRE(max_chunk >= 1 && max_chunk <= 256 && sessions * max_chunk <= 16384,
+               "max_chunk %zu out of 1..256 (or sessions x max_chunk above 16384)", max_chunk);
     nd_v3_batch *b = new (std::nothrow) nd_v3_batch;
     if (!b) return nd::fail(ND_ERR_NOMEM, "host allocation failed");
     b->device = ctx->device;
     b->B = int(sessions);
     b->max_len = int(max_len);
-    const int B = b->B, L = c.num_layers, nl = c.mhc_lanes, d = c.d_model;
+    b->chunk = int(max_chunk);
+    b->R = int(sessions * max_chunk);
+    const int B = b->R, L = c.num_layers, nl = c.mhc_lanes, d = c.d_model;
+    const int S = b->B;  // sessions: per-session state
     const int qd = c.num_heads * c.qk_head_dim, kd = c.num_kv_heads * c.qk_head_dim;
     const int vd = c.num_kv_heads * c.v_head_dim, od = c.num_heads * c.v_head_dim;
     const int T = c.qkv_conv_taps, nt = c.n_orders * c.e_heads;
@@ -1261,7 +1359,7 @@ int nd_v3_batch_create(nd_ctx *ctx, const nd_v3_model *m, size_t sessions, size_
     const size_t rows = nd_v3_logit_rows(m);
     const size_t hnt = hint < 1 ? 1 : (hint > size_t(c.max_seq_len) ? size_t(c.max_seq_len) : hint);
     int rc = ND_OK;
-    b->s.resize(B);
+    b->s.resize(S);
     for (auto &sh : b->s) sh.slots.resize(L);
     b->kv.resize(L);
     b->kv_stride.resize(L);
@@ -1277,31 +1375,35 @@ int nd_v3_batch_create(nd_ctx *ctx, const nd_v3_model *m, size_t sessions, size_
                                 ? c.max_seq_len
                                 : (c.sliding_window < c.max_seq_len ? c.sliding_window : c.max_seq_len);
         b->cap[li] = ref_cap;
-        const int dev_cap = ref_cap < b->max_len ? ref_cap : b->max_len;
+        // a step of C positions writes C slots before its rows attend: the
+        // ring holds window + C - 1 positions so none of them is overwritten
+        // while a row of the step still reads it
+        const long wide = long(ref_cap) + long(b->chunk) - 1;
+        const int dev_cap = int(wide < b->max_len ? wide : b->max_len);
         for (auto &sh : b->s) sh.slots[li] = int(hnt < size_t(ref_cap) ? hnt : size_t(ref_cap));
         nd_kv_geom g{c.num_heads, c.num_kv_heads, c.qk_head_dim, c.v_head_dim, dev_cap};
         b->geom[li] = g;
         b->kv_stride[li] = nd_kv_block_bytes(&g);
-        if ((rc = dalloc(b->mem, &b->kv[li], b->kv_stride[li] * B))) goto fail;
+        if ((rc = dalloc(b->mem, &b->kv[li], b->kv_stride[li] * S))) goto fail;
         {
-            hipError_t e = hipMemsetAsync(b->kv[li], 0, b->kv_stride[li] * B, ctx->stream);
+            hipError_t e = hipMemsetAsync(b->kv[li], 0, b->kv_stride[li] * S, ctx->stream);
             if (e != hipSuccess) {
                 rc = nd::hip_fail(e, "hipMemsetAsync");
                 goto fail;
             }
         }
         const int tt = T > 0 ? T - 1 : 0;
-        if ((rc = dalloc(b->mem, &b->qt[li], size_t(B) * tt * qd + 1))) goto fail;
-        if ((rc = dalloc(b->mem, &b->kt[li], size_t(B) * tt * kd + 1))) goto fail;
-        if ((rc = dalloc(b->mem, &b->vt[li], size_t(B) * tt * vd + 1))) goto fail;
-        (void)hipMemsetAsync(b->qt[li], 0, (size_t(B) * tt * qd + 1) * 4, ctx->stream);
-        (void)hipMemsetAsync(b->kt[li], 0, (size_t(B) * tt * kd + 1) * 4, ctx->stream);
-        (void)hipMemsetAsync(b->vt[li], 0, (size_t(B) * tt * vd + 1) * 4, ctx->stream);
+        if ((rc = dalloc(b->mem, &b->qt[li], size_t(S) * tt * qd + 1))) goto fail;
+        if ((rc = dalloc(b->mem, &b->kt[li], size_t(S) * tt * kd + 1))) goto fail;
+        if ((rc = dalloc(b->mem, &b->vt[li], size_t(S) * tt * vd + 1))) goto fail;
+        (void)hipMemsetAsync(b->qt[li], 0, (size_t(S) * tt * qd + 1) * 4, ctx->stream);
+        (void)hipMemsetAsync(b->kt[li], 0, (size_t(S) * tt * kd + 1) * 4, ctx->stream);
+        (void)hipMemsetAsync(b->vt[li], 0, (size_t(S) * tt * vd + 1) * 4, ctx->stream);
     }
     b->et.resize(c.n_sites);
     for (int s = 0; s < c.n_sites; ++s) {
-        if ((rc = dalloc(b->mem, &b->et[s], size_t(B) * reach * d + 1))) goto fail;
-        (void)hipMemsetAsync(b->et[s], 0, (size_t(B) * reach * d + 1) * 4, ctx->stream);
+        if ((rc = dalloc(b->mem, &b->et[s], size_t(S) * reach * d + 1))) goto fail;
+        (void)hipMemsetAsync(b->et[s], 0, (size_t(S) * reach * d + 1) * 4, ctx->stream);
     }
 #define A(p, cnt) \
     if ((rc = dalloc(b->mem, &b->p, size_t(cnt)))) goto fail;
@@ -1331,11 +1433,15 @@ int nd_v3_batch_create(nd_ctx *ctx, const nd_v3_model *m, size_t sessions, size_
     A(fh, size_t(B) * nt * c.e_sub_dim);
     A(ek, size_t(c.n_sites > 0 ? c.n_sites : 1) * B * d);
     A(ev, size_t(c.n_sites > 0 ? c.n_sites : 1) * B * d);
-    A(xh, size_t(B) * m->pre_x.in_padded);
-    A(logits, size_t(B) * rows);
+    A(xh, size_t(S) * m->pre_x.in_padded);
+    A(logits, size_t(S) * rows);
     A(gp, size_t(B) * nl);
     A(gr, size_t(B) * nl * nl);
-    A(next, size_t(B));
+    A(next, size_t(S));
+    if (b->chunk > 1) {
+        A(qn, size_t(B) * qd);
+        A(evc, size_t(c.n_sites > 0 ? c.n_sites : 1) * B * d);
+    }
 #undef A
     {
         hipError_t e = hipStreamCreateWithFlags(&b->side, hipStreamNonBlocking);
@@ -1359,18 +1465,11 @@ int nd_v3_batch_create(nd_ctx *ctx, const nd_v3_model *m, size_t sessions, size_
             e = hipHostMalloc(&b->stage_host[i], b->step_bytes, hipHostMallocDefault);
             if (e == hipSuccess) e = hipEventCreateWithFlags(&b->stage_done[i], hipEventDisableTiming);
         }
-        if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void **>(&b->next_host), size_t(B) * 4, hipHostMallocDefault);
+        if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void **>(&b->next_host), size_t(S) * 4, hipHostMallocDefault);
         if (e != hipSuccess) {
             rc = nd::hip_fail(e, "hipHostMalloc");
             goto fail;
         }
-        int32_t *base = static_cast<int32_t *>(b->step_dev);
-        b->tok_dev = base;
-        b->pos_dev = base + B;
-        b->hi_dev = base + 2 * B;
-        b->lo_dev = base + 3 * B;
-        b->rows_dev = base + 3 * B + size_t(L) * B;
-        b->rope_dev = reinterpret_cast<float *>(base + ints);
     }
     {
         hipError_t e = hipStreamSynchronize(ctx->stream);
@@ -1397,20 +1496,30 @@ int nd_v3_positions(const nd_v3_batch *b, int32_t *pos)
     return ND_OK;
 }
 
-int nd_v3_step(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *tokens,
-               int32_t *next, float *logits)
+}  // extern "C"
+
+namespace {
+
+// C consecutive positions for every session (C = 1: one decode step).  Row
+// i * C + j of every per-row buffer is position pos + j of session i; the
+// layers run once over all rows; only each session's last row is scored.
+int step_impl(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *tokens, int C,
+              int32_t *next, float *logits)
 {
     if (int rc = nd::enter(ctx)) return rc;
     ND_REQUIRE(m && b && tokens, "null argument");
+    ND_REQUIRE(C >= 1 && C <= b->chunk, "%d positions per step; the batch takes at most %d", C,
+               b->chunk);
     const nd_v3_cfg &c = m->cfg;
-    const int B = b->B, L = c.num_layers, nl = c.mhc_lanes, d = c.d_model;
+    const int S = b->B, B = S * C, Rcap = b->R;
+    const int L = c.num_layers, nl = c.mhc_lanes, d = c.d_model;
     const int qd = c.num_heads * c.qk_head_dim, kd = c.num_kv_heads * c.qk_head_dim;
     const int vd = c.num_kv_heads * c.v_head_dim, od = c.num_heads * c.v_head_dim;
     const int nt = c.n_orders * c.e_heads, half = c.qk_head_dim / 2;
     const int mo = max_order(c);
     const size_t rows = nd_v3_logit_rows(m);
-    for (int i = 0; i < B; ++i)
-        ND_REQUIRE(b->s[i].pos < b->max_len, "session %d is full (%d positions)", i, b->max_len);
+    for (int i = 0; i < S; ++i)
+        ND_REQUIRE(b->s[i].pos + C <= b->max_len, "session %d is full (%d positions)", i, b->max_len);
 
     // ---- host bookkeeping (V3Cache state that only steers addressing) -------
     const int stage = b->stage_next;
@@ -1420,10 +1529,11 @@ int nd_v3_step(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t 
     int32_t *h_tok = si, *h_pos = si + B, *h_hi = si + 2 * B, *h_lo = si + 3 * B;
     int32_t *h_rows = si + 3 * B + size_t(L) * B;
     float *h_rope = reinterpret_cast<float *>(si + size_t(B) * (3 + L + nt));
-    for (int i = 0; i < B; ++i) {
-        SessionHost &sh = b->s[i];
-        const int pos = sh.pos;
-        const uint32_t tok = uint32_t(tokens[i]);
+    for (int row = 0; row < B; ++row) {
+        const int i = row;  // buffer row: session row / C, position pos + row % C
+        SessionHost &sh = b->s[row / C];
+        const int pos = sh.pos + row % C;
+        const uint32_t tok = uint32_t(tokens[row]);
         // cache.rs:283-289 push_token, keeping max(order) ids
         sh.hist.push_back(tok);
         if (int(sh.hist.size()) > mo) sh.hist.erase(sh.hist.begin());
@@ -1470,6 +1580,10 @@ int nd_v3_step(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t 
     }
     ND_HIP(hipMemcpyAsync(b->step_dev, b->stage_host[stage], b->step_bytes, hipMemcpyHostToDevice,
                           ctx->stream));
+    int32_t *tok_dev = static_cast<int32_t *>(b->step_dev);
+    int32_t *pos_dev = tok_dev + B, *hi_dev = tok_dev + 2 * B, *lo_dev = tok_dev + 3 * B;
+    int32_t *rows_dev = tok_dev + 3 * B + size_t(L) * B;
+    float *rope_dev = reinterpret_cast<float *>(tok_dev + size_t(B) * (3 + L + nt));
     ND_HIP(hipEventRecord(b->stage_done[stage], ctx->stream));
     b->stage_pending[stage] = true;
     b->stage_next = (stage + 1) % nd_v3_batch::kStages;
@@ -1483,23 +1597,35 @@ int nd_v3_step(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t 
     // ---- Engram for this position (model.rs:162-191) -------------------------
     for (int s = 0; s < c.n_sites; ++s) {
         const Site &site = m->sites[s];
-        CK(nd_cq_dequantize_rows(ctx, site.tables, b->rows_dev, size_t(B) * nt, b->fetched));
+        CK(nd_cq_dequantize_rows(ctx, site.tables, rows_dev, size_t(B) * nt, b->fetched));
         CK(nd_cq_prepare_input(ctx, site.key, b->fetched, B, b->fh));
         {
             const nd_cq *ws[2] = {site.key, site.value};
             const size_t r0[2] = {0, 0};
             const size_t nr[2] = {size_t(d), size_t(d)};
-            float *ys[2] = {b->ek + size_t(s) * B * d, b->ev + size_t(s) * B * d};
+            float *ys[2] = {b->ek + size_t(s) * Rcap * d, b->ev + size_t(s) * Rcap * d};
             CK(nd_cq_exact_set(ctx, st, 2, ws, b->fh, size_t(B), r0, nr, ys, "v3 engram key/value"));
         }
         const int reach = (c.e_conv_taps - 1) * c.e_conv_dilation;
-        hipLaunchKernelGGL(k_engram_conv, dim3((d + 255) / 256, B), dim3(256), 0, st,
-                           b->ev + size_t(s) * B * d, site.taps, b->et[s], b->pos_dev,
-                           c.e_conv_taps, c.e_conv_dilation, mo, reach, d);
-        LCHK("k_engram_conv");
+        if (C == 1) {
+            hipLaunchKernelGGL(k_engram_conv, dim3((d + 255) / 256, B), dim3(256), 0, st,
+                               b->ev + size_t(s) * Rcap * d, site.taps, b->et[s], pos_dev,
+                               c.e_conv_taps, c.e_conv_dilation, mo, reach, d);
+            LCHK("k_engram_conv");
+        } else {
+            hipLaunchKernelGGL(k_engram_conv_rows, dim3((d + 255) / 256, B), dim3(256), 0, st,
+                               b->ev + size_t(s) * Rcap * d, b->evc + size_t(s) * Rcap * d,
+                               site.taps, b->et[s], pos_dev, c.e_conv_taps, c.e_conv_dilation, mo,
+                               reach, d, C);
+            LCHK("k_engram_conv_rows");
+            hipLaunchKernelGGL(k_tails, dim3((d + 255) / 256, S), dim3(256), 0, st,
+                               b->ev + size_t(s) * Rcap * d, b->et[s], reach, C, d);
+            LCHK("k_tails");
+        }
     }
+    float *const ev_conv = C == 1 ? b->ev : b->evc;  // [sites][Rcap][d], after the conv
     // ---- lane stream (model.rs:194-203) --------------------------------------
-    CK(nd_cq_dequantize_rows(ctx, m->embedding, b->tok_dev, size_t(B), b->emb));
+    CK(nd_cq_dequantize_rows(ctx, m->embedding, tok_dev, size_t(B), b->emb));
     hipLaunchKernelGGL(k_embed, dim3((d + 255) / 256, B), dim3(256), 0, st, b->emb, b->lanes,
                        m->embed_scale, nl, d);
     LCHK("k_embed");
@@ -1515,8 +1641,8 @@ int nd_v3_step(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t 
         LayerIn in{b->lanes, b->y, b->gp, b->gr, li > 0, b->nxh, m->pre_nx, phi->packed,
                    phi->norms, phi->lv, phi->row_bytes, int(phi->num_groups), li * nl,
                    int(phi->bits == 5), m->b_pre + size_t(li) * nl, m->a_pre[li], li, nl, d,
-                   site >= 0 ? b->ek + size_t(site) * B * d : nullptr,
-                   site >= 0 ? b->ev + size_t(site) * B * d : nullptr, l.norm_in, b->u, b->bx,
+                   site >= 0 ? b->ek + size_t(site) * Rcap * d : nullptr,
+                   site >= 0 ? ev_conv + size_t(site) * Rcap * d : nullptr, l.norm_in, b->u, b->bx,
                    b->hh, m->pre_h};
         if (phi->per_byte == 2)
             hipLaunchKernelGGL(k_layer_in<2>, dim3(B), dim3(kT), 0, st, in);
@@ -1550,17 +1676,32 @@ int nd_v3_step(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t 
         {
             const nd_kv_geom &g = b->geom[li];
             QkvKv qk{b->q, b->k, b->v, b->qt[li], b->kt[li], b->vt[li], l.q_taps, l.k_taps,
-                     l.v_taps, l.q_norm, l.k_norm, b->rope_dev, b->pos_dev, qd, kd, vd,
+                     l.v_taps, l.q_norm, l.k_norm, rope_dev, pos_dev, qd, kd, vd,
                      c.qkv_conv_taps, c.num_heads, c.num_kv_heads, c.qk_head_dim, c.v_head_dim,
                      b->kv[li], b->kv_stride[li], nd_kv_v_offset(&g), nd_kv_ks_offset(&g),
-                     nd_kv_vs_offset(&g), g.cap};
-            hipLaunchKernelGGL(k_qkv_kv, dim3(B), dim3(kT), 0, st, qk);
-            LCHK("k_qkv_kv");
+                     nd_kv_vs_offset(&g), g.cap, C, b->qn};
+            if (C == 1) {
+                hipLaunchKernelGGL(k_qkv_kv<false>, dim3(B), dim3(kT), 0, st, qk);
+                LCHK("k_qkv_kv");
+            } else {
+                hipLaunchKernelGGL(k_qkv_kv<true>, dim3(B), dim3(kT), 0, st, qk);
+                LCHK("k_qkv_kv");
+                const int tt = c.qkv_conv_taps - 1;
+                if (tt > 0) {
+                    hipLaunchKernelGGL(k_tails, dim3((qd + 255) / 256, S), dim3(256), 0, st, b->q,
+                                       b->qt[li], tt, C, qd);
+                    hipLaunchKernelGGL(k_tails, dim3((kd + 255) / 256, S), dim3(256), 0, st, b->k,
+                                       b->kt[li], tt, C, kd);
+                    hipLaunchKernelGGL(k_tails, dim3((vd + 255) / 256, S), dim3(256), 0, st, b->v,
+                                       b->vt[li], tt, C, vd);
+                    LCHK("k_tails");
+                }
+            }
         }
         // attention over the int8 ring (query fake-quant fused)
-        CK(nd_attend_step_i8_exact(ctx, &b->geom[li], b->kv[li], b->kv_stride[li], size_t(B),
-                                   b->lo_dev + size_t(li) * B, b->hi_dev, b->q, qk_scale, 1,
-                                   b->attn));
+        CK(nd_attend_exact_rows(ctx, &b->geom[li], b->kv[li], b->kv_stride[li], size_t(B), C,
+                                lo_dev + size_t(li) * B, hi_dev, C == 1 ? b->q : b->qn, qk_scale,
+                                1, b->attn));
         hipLaunchKernelGGL(k_gate_prep, dim3(B), dim3(kT), 0, st, b->attn, b->gate, b->ah, od,
                            m->pre_attn);
         LCHK("k_gate_prep");
@@ -1573,23 +1714,42 @@ int nd_v3_step(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t 
     }
     // ---- head ---------------------------------------------------------------
     ND_HIP(hipStreamWaitEvent(st, b->ev_gates[(L - 1) & 1], 0));
-    hipLaunchKernelGGL(k_final, dim3(B), dim3(kT), 0, st, b->lanes, b->y, b->gp, b->gr,
-                       m->final_norm, b->xh, nl, d, m->pre_x);
+    hipLaunchKernelGGL(k_final, dim3(S), dim3(kT), 0, st, b->lanes, b->y, b->gp, b->gr,
+                       m->final_norm, b->xh, nl, d, m->pre_x, C);
     LCHK("k_final");
-    CK(project(ctx, m->embedding, b->xh, B, 0, rows, b->logits));
+    CK(project(ctx, m->embedding, b->xh, S, 0, rows, b->logits));
     if (logits)
-        ND_HIP(hipMemcpyAsync(logits, b->logits, size_t(B) * rows * 4, hipMemcpyDeviceToDevice, st));
+        ND_HIP(hipMemcpyAsync(logits, b->logits, size_t(S) * rows * 4, hipMemcpyDeviceToDevice, st));
     if (next) {
-        hipLaunchKernelGGL(k_argmax, dim3(B), dim3(kT), 0, st, b->logits, int(rows), b->next);
+        hipLaunchKernelGGL(k_argmax, dim3(S), dim3(kT), 0, st, b->logits, int(rows), b->next);
         LCHK("k_argmax");
-        ND_HIP(hipMemcpyAsync(b->next_host, b->next, size_t(B) * 4, hipMemcpyDeviceToHost, st));
+        ND_HIP(hipMemcpyAsync(b->next_host, b->next, size_t(S) * 4, hipMemcpyDeviceToHost, st));
         ND_HIP(hipStreamSynchronize(st));
-        std::memcpy(next, b->next_host, size_t(B) * 4);
+        std::memcpy(next, b->next_host, size_t(S) * 4);
     }
-    for (int i = 0; i < B; ++i) b->s[i].pos++;
+    for (int i = 0; i < S; ++i) b->s[i].pos += C;
 #undef CK
 #undef LCHK
     return ND_OK;
 }
+
+}  // namespace
+
+extern "C" {
+
+int nd_v3_step(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *tokens,
+               int32_t *next, float *logits)
+{
+    return step_impl(ctx, m, b, tokens, 1, next, logits);
+}
+
+int nd_v3_prefill(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *tokens,
+                  size_t count, int32_t *next, float *logits)
+{
+    nd::clear_error();
+    ND_REQUIRE(count >= 1 && count <= 256, "count %zu out of 1..256", count);
+    return step_impl(ctx, m, b, tokens, int(count), next, logits);
+}
+
 
 }  // extern "C"

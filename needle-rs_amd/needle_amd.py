@@ -85,6 +85,8 @@ _SIGS = [
     ("nd_v3_batch_free", None, [_vp]),
     ("nd_v3_positions", C.c_int, [_vp, _vp]),
     ("nd_v3_step", C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp]),
+    ("nd_v3_batch_create_chunked", C.c_int, [_vp, _vp, _sz, _sz, _sz, _sz, C.POINTER(_vp)]),
+    ("nd_v3_prefill", C.c_int, [_vp, _vp, _vp, _vp, _sz, _vp, _vp]),
     ("nd_v3_cact_config", C.c_int, [_vp, _sz, _vp, C.POINTER(_sz)]),
     ("nd_v3_model_from_cact", C.c_int, [_vp, _vp, _sz, C.POINTER(_vp)]),
 ]
@@ -510,13 +512,15 @@ class V3Model:
 
 
 class V3Batch:
-    """`sessions` int8-KV decode sessions stepped in lockstep on the device."""
+    """`sessions` int8-KV decode sessions stepped in lockstep on the device;
+    with max_chunk > 1 a prompt is prefilled up to max_chunk positions per
+    pass (the reference's chunked prefill, bit-identical to stepping)."""
 
-    def __init__(self, model, sessions, max_len, hint=None):
-        self.model, self.sessions = model, sessions
+    def __init__(self, model, sessions, max_len, hint=None, max_chunk=1):
+        self.model, self.sessions, self.max_chunk = model, sessions, max_chunk
         h = C.c_void_p()
-        _check(lib().nd_v3_batch_create(model.ctx.h, model.h, sessions, max_len,
-                                        hint or max_len, C.byref(h)))
+        _check(lib().nd_v3_batch_create_chunked(model.ctx.h, model.h, sessions, max_len,
+                                                hint or max_len, max_chunk, C.byref(h)))
         self.h = h
 
     def close(self):
@@ -542,13 +546,31 @@ class V3Batch:
                                 _ptr(logits) if logits is not None else None))
         return nxt
 
+    def prefill(self, tokens, logits=None, want_next=True):
+        """tokens [sessions][count]: count consecutive positions per session in
+        one pass (V3Model::prefill); returns the greedy token after the last."""
+        tok = np.ascontiguousarray(tokens, np.int32).reshape(self.sessions, -1)
+        nxt = np.zeros(self.sessions, np.int32) if want_next else None
+        _check(lib().nd_v3_prefill(self.model.ctx.h, self.model.h, self.h,
+                                   tok.ctypes.data_as(C.c_void_p), tok.shape[1],
+                                   nxt.ctypes.data_as(C.c_void_p) if want_next else None,
+                                   _ptr(logits) if logits is not None else None))
+        return nxt
+
     def generate(self, prompts, steps):
-        """Prefill by stepping each session's prompt (the reference's batched
-        prefill is bit-identical to stepping), then `steps` greedy tokens."""
+        """Prefill each session's prompt, max_chunk positions per pass (or by
+        stepping; the reference proves the two bit-identical), then `steps`
+        greedy tokens."""
         prompts = np.asarray(prompts, np.int32).reshape(self.sessions, -1)
         nxt = None
-        for t in range(prompts.shape[1]):
-            nxt = self.step(prompts[:, t], want_next=(t == prompts.shape[1] - 1))
+        n = prompts.shape[1]
+        for t0 in range(0, n, self.max_chunk):
+            t1 = min(n, t0 + self.max_chunk)
+            last = t1 == n
+            if t1 - t0 == 1:
+                nxt = self.step(prompts[:, t0], want_next=last)
+            else:
+                nxt = self.prefill(prompts[:, t0:t1], want_next=last)
         out = np.zeros((self.sessions, steps), np.int32)
         for s in range(steps):
             out[:, s] = nxt
