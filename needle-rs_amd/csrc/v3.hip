@@ -1578,7 +1578,9 @@ int step_impl(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *
             h_lo[size_t(li) * B + i] = lo > clamp ? lo : clamp;
         }
     }
-    ND_HIP(hipMemcpyAsync(b->step_dev, b->stage_host[stage], b->step_bytes, hipMemcpyHostToDevice,
+    // this step's rows only: the buffer is sized for a full pass of max_chunk
+    const size_t used = size_t(B) * (3 + L + nt) * 4 + size_t(B) * c.qk_head_dim * 4;
+    ND_HIP(hipMemcpyAsync(b->step_dev, b->stage_host[stage], used, hipMemcpyHostToDevice,
                           ctx->stream));
     int32_t *tok_dev = static_cast<int32_t *>(b->step_dev);
     int32_t *pos_dev = tok_dev + B, *hi_dev = tok_dev + 2 * B, *lo_dev = tok_dev + 3 * B;
