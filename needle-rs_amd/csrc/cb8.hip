@@ -491,6 +491,161 @@ __global__ __launch_bounds__(256) void cb8_gemm128_kernel(const unsigned short *
             }
 }
 
+// The same product on 256x256 tiles for launches with at least one tile per
+// CU.  8 waves, two per SIMD, each a 64x128 output (4x8 MFMA 16x16x32 tiles);
+// LDS holds two K steps of 64 so the next step is decoded while the current
+// one is multiplied.  Waves 0-3 multiply first and then stage, waves 4-7
+// stage first: the two waves sharing a SIMD are out of phase, so one keeps
+// the MFMA pipe fed while the other waits on global loads and codebook
+// gathers.  Loads read clamped, always valid addresses and are masked at the
+// LDS store, so no load sits behind a branch.  Tiles are numbered so that each
+// XCD (blocks are dealt round-robin to the 8 XCDs) owns a contiguous run,
+// M tiles fastest: blocks sharing an X row block or a W column block meet in
+// one L2.  Per output the K order is that of the 128x128 kernel, so the two
+// agree bit for bit.
+constexpr int kPM = 256, kPN = 256, kPK = 64;
+constexpr int kPWM = 64, kPWN = 128;  // wave tile: waves 4 (M) x 2 (N)
+
+__global__ __launch_bounds__(512) void cb8_gemm256_kernel(const unsigned short *__restrict__ Xb,
+                                                          const uint8_t *__restrict__ W,
+                                                          const float *__restrict__ cb,
+                                                          float *__restrict__ Y, int M, int N,
+                                                          int K, size_t ws, size_t cs, size_t ys,
+                                                          int tiles_n, int tiles_m, int xcd_run)
+{
+    constexpr int TA = kPWM / 16, TB = kPWN / 16;
+    constexpr int J = kPM / 64;  // staged 64-row slabs of A and of B
+    __shared__ __align__(16) unsigned short As[2][kPM][kPK + kLdsPad];
+    __shared__ __align__(16) unsigned short Bs[2][kPN][kPK + kLdsPad];
+    __shared__ unsigned short cbh[kPN / 64][256];
+
+    const int id = blockIdx.x;
+    const int u = xcd_run ? (id % 8) * xcd_run + id / 8 : id;
+    const int z = u / (tiles_n * tiles_m);
+    const int m0 = (u % tiles_m) * kPM;
+    const int n0 = ((u / tiles_m) % tiles_n) * kPN;
+    Xb += z * size_t(M) * K;
+    W += z * ws;
+    cb += z * cs;
+    Y += z * ys;
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int wm = (wave & 3) * kPWM;
+    const int wn = (wave >> 2) * kPWN;
+    for (int i = t; i < kPN / 64 * 256; i += 512)
+        cbh[i / 256][i % 256] = f32_to_bf16_rne(cb[size_t(n0 / 64 + i / 256) * 256 + i % 256]);
+
+    floatx4_t acc[TA][TB];
+#pragma unroll
+    for (int a = 0; a < TA; ++a)
+#pragma unroll
+        for (int b = 0; b < TB; ++b) acc[a][b] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int r8 = t >> 3;       // staged row within a 64-row slab
+    const int c8 = (t & 7) * 8;  // staged columns c8..c8+7 of the K step
+    bool mok[J];
+    const unsigned short *xp[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int m = m0 + r8 + 64 * j;
+        mok[j] = m < M;
+        xp[j] = Xb + size_t(m < M ? m : M - 1) * K + c8;
+    }
+    const uint8_t *wp = W + size_t(n0 + r8) * K + c8;  // N is a multiple of 256 here
+    uint4 xa[J];
+    uint2 wc[J];
+    bool on = true;
+    auto load = [&](int k0) {
+        on = k0 + c8 < K;
+        // K is a multiple of 32: a run past K belongs to a final half step,
+        // and the run 32 columns back is in range
+        const int kc = on ? k0 : k0 - 32;
+#pragma unroll
+        for (int j = 0; j < J; ++j) xa[j] = *reinterpret_cast<const uint4 *>(xp[j] + kc);
+#pragma unroll
+        for (int j = 0; j < J; ++j) wc[j] = *reinterpret_cast<const uint2 *>(wp + size_t(64 * j) * K + kc);
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+            *reinterpret_cast<uint4 *>(&As[buf][r8 + 64 * j][c8]) =
+                on && mok[j] ? xa[j] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const uint32_t d[2] = {wc[j].x, wc[j].y};
+            uint32_t h[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t lo = cbh[j][(d[e >> 1] >> (16 * (e & 1))) & 0xffu];
+                const uint32_t hi = cbh[j][(d[e >> 1] >> (16 * (e & 1) + 8)) & 0xffu];
+                h[e] = on ? lo | (hi << 16) : 0u;
+            }
+            *reinterpret_cast<uint4 *>(&Bs[buf][r8 + 64 * j][c8]) = make_uint4(h[0], h[1], h[2], h[3]);
+        }
+    };
+    const int r16 = lane & 15;
+    const int kq = (lane >> 4) * 8;
+    auto multiply = [&](int buf, int halves) {
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            if (kk < halves) {
+                bf16x8_t af[TA], bfv[TB];
+#pragma unroll
+                for (int a = 0; a < TA; ++a)
+                    af[a] = *reinterpret_cast<const bf16x8_t *>(&As[buf][wm + a * 16 + r16][kk * 32 + kq]);
+#pragma unroll
+                for (int b = 0; b < TB; ++b)
+                    bfv[b] = *reinterpret_cast<const bf16x8_t *>(&Bs[buf][wn + b * 16 + r16][kk * 32 + kq]);
+#pragma unroll
+                for (int a = 0; a < TA; ++a)
+#pragma unroll
+                    for (int b = 0; b < TB; ++b)
+                        acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[a], bfv[b], acc[a][b], 0, 0, 0);
+            }
+        }
+    };
+    const int nk = (K + kPK - 1) / kPK;
+    load(0);
+    __syncthreads();  // codebooks in LDS
+    store(0);
+    if (nk > 1) load(kPK);
+    __syncthreads();
+    const bool first = wave < 4;
+    for (int i = 0; i < nk; ++i) {
+        const int cur = i & 1;
+        const int halves = (K - i * kPK < kPK ? K - i * kPK : kPK) / 32;
+        // step i+1 into the other buffer (read last in step i-1, before the
+        // barrier that ended it); step i+2's loads go out behind it
+        if (first) {
+            multiply(cur, halves);
+            if (i + 1 < nk) {
+                store(cur ^ 1);
+                if (i + 2 < nk) load((i + 2) * kPK);
+            }
+        } else {
+            if (i + 1 < nk) {
+                store(cur ^ 1);
+                if (i + 2 < nk) load((i + 2) * kPK);
+            }
+            multiply(cur, halves);
+        }
+        __syncthreads();
+    }
+    const int col = lane & 15;
+    const int rb = (lane >> 4) * 4;
+#pragma unroll
+    for (int a = 0; a < TA; ++a)
+#pragma unroll
+        for (int b = 0; b < TB; ++b)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = m0 + wm + a * 16 + rb + i;
+                const int n = n0 + wn + b * 16 + col;
+                if (m < M) Y[size_t(m) * N + n] = acc[a][b][i];
+            }
+}
+
 constexpr int kRep = 32;
 
 int launch_gemv(nd_ctx *ctx, size_t count, const uint8_t *w, size_t w_stride, const float *cb,
@@ -573,7 +728,16 @@ int nd_cb8_gemm_batched(nd_ctx *ctx, size_t count, const float *x, size_t x_stri
     hipLaunchKernelGGL(x_to_bf16_kernel, dim3(unsigned((mk + 2047) / 2048), unsigned(count)),
                        dim3(256), 0, ctx->stream, x, x_stride, xb, mk);
     if (int rc = nd::check_launch("x_to_bf16")) return rc;
-    if (m >= 96 && out % kBN == 0) {
+    const size_t big_tiles = (out / kPN) * ((m + kPM - 1) / kPM) * count;
+    const size_t cus = size_t(ctx->num_cus > 0 ? ctx->num_cus : 256);
+    if (m >= 96 && out % kPN == 0 && big_tiles >= cus && big_tiles <= 0x7fffffff) {
+        // at least one 256x256 tile per CU: below that the 128x128 tiles fill
+        // the chip better
+        const int run = big_tiles % 8 == 0 ? int(big_tiles / 8) : 0;
+        hipLaunchKernelGGL(cb8_gemm256_kernel, dim3(unsigned(big_tiles)), dim3(512), 0, ctx->stream, xb,
+                           w, cb, y, int(m), int(out), int(in), w_stride, cb_stride, y_stride,
+                           int(out / kPN), int((m + kPM - 1) / kPM), run);
+    } else if (m >= 96 && out % kBN == 0) {
         dim3 grid(static_cast<unsigned>(out / kBN), static_cast<unsigned>((m + kBM - 1) / kBM),
                   static_cast<unsigned>(count));
         hipLaunchKernelGGL(cb8_gemm128_kernel, grid, dim3(256), 0, ctx->stream, xb, w, cb, y,

@@ -92,6 +92,28 @@ def test_gemm_bf16_mfma(ctx, m, out, inn):
     assert np.linalg.norm(Y - ref) / np.linalg.norm(ref) <= 5e-3
 
 
+@pytest.mark.parametrize("R,M,N,K", [(11, 512, 3072, 768), (43, 300, 768, 800)])
+def test_gemm_256_tiles_match_128_tiles(ctx, R, M, N, K):
+    """A batched launch with at least one 256x256 tile per CU runs the 256
+    kernel; each problem alone has too few tiles and runs the 128x128 one.
+    The K order per output is the same, so the two agree bit for bit (ragged
+    M, K with a final half step); two problems also against the oracle."""
+    rng = np.random.default_rng(R * 1000 + K)
+    X = rng.normal(size=(R, M, K)).astype(np.float32)
+    W = rng.integers(0, 256, size=(R, N, K), dtype=np.uint8)
+    CB = (rng.normal(size=(R, N // 64, 256)) * 0.02).astype(np.float32)
+    Y = torch.empty(R, M, N, device="cuda")
+    nd.cb8_gemm_batched(ctx, dev(X), dev(W), dev(CB), Y)
+    got = host(Y)
+    for i in range(R):
+        one = host(nd.cb8_gemm(ctx, dev(X[i]), dev(W[i]), dev(CB[i])))
+        assert np.array_equal(got[i], one), i
+    for i in (0, R - 1):
+        want = O.cb8_gemm(X[i], W[i], CB[i])
+        assert np.max(np.abs(got[i] - want)) <= 2e-2 * np.max(np.abs(want))
+        assert np.linalg.norm(got[i] - want) / np.linalg.norm(want) <= 5e-3
+
+
 def test_gemm_batched_equals_single(ctx):
     """Problem i of one batched launch is bit-identical to its own launch."""
     rng = np.random.default_rng(21)
