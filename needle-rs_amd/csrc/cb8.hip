@@ -15,8 +15,10 @@
 //   * code loads split in two halves so the second half is in flight while
 //     the first computes; nontemporal loads, since codes are read once.
 // Other widths fall back to a kernel with the activations in LDS.
-// GEMM (prefill) dequantises a 64x32 weight tile to bf16 in LDS and feeds
-// v_mfma_f32_16x16x32_bf16 with fp32 accumulation.
+// GEMM (prefill) converts X to bf16 once, dequantises weight tiles to bf16 in
+// LDS through the bf16-rounded codebook and feeds v_mfma_f32_16x16x32_bf16
+// with fp32 accumulation: 64x64 tiles below M = 96, 128x128 tiles, and
+// 256x256 tiles with two waves per SIMD once a launch has a tile per CU.
 #include "nd_internal.h"
 
 #include <hip/hip_bf16.h>
@@ -240,25 +242,48 @@ __device__ inline unsigned short f32_to_bf16_rne(float f)
 constexpr int kGM = 64, kGN = 64, kGK = 128;
 constexpr int kLdsPad = 8;  // bf16 elements of padding per LDS row
 
-// X (f32) to bf16, round to nearest even, 8 elements per thread; problem
-// blockIdx.y of a batch at element stride xs (input) and n (output).
+// X (f32) to bf16, round to nearest even; problem blockIdx.y of a batch at
+// element stride xs (input) and n (output).  A block converts kXRuns runs of
+// 2048 elements, 8 per thread per run, all loads issued before the stores.
+constexpr int kXRuns = 4;
+
+__device__ inline uint4 pack_bf16x8(float4 a, float4 b)
+{
+    return make_uint4(f32_to_bf16_rne(a.x) | (uint32_t(f32_to_bf16_rne(a.y)) << 16),
+                      f32_to_bf16_rne(a.z) | (uint32_t(f32_to_bf16_rne(a.w)) << 16),
+                      f32_to_bf16_rne(b.x) | (uint32_t(f32_to_bf16_rne(b.y)) << 16),
+                      f32_to_bf16_rne(b.z) | (uint32_t(f32_to_bf16_rne(b.w)) << 16));
+}
+
 __global__ __launch_bounds__(256) void x_to_bf16_kernel(const float *__restrict__ X, size_t xs,
                                                         unsigned short *__restrict__ Xb, size_t n)
 {
-    const size_t i = (size_t(blockIdx.x) * 256 + threadIdx.x) * 8;
-    if (i >= n) return;
-    const float *src = X + blockIdx.y * xs + i;
-    unsigned short *dst = Xb + blockIdx.y * n + i;
-    if (i + 8 <= n) {
-        const float4 a = *reinterpret_cast<const float4 *>(src);
-        const float4 b = *reinterpret_cast<const float4 *>(src + 4);
-        *reinterpret_cast<uint4 *>(dst) =
-            make_uint4(f32_to_bf16_rne(a.x) | (uint32_t(f32_to_bf16_rne(a.y)) << 16),
-                       f32_to_bf16_rne(a.z) | (uint32_t(f32_to_bf16_rne(a.w)) << 16),
-                       f32_to_bf16_rne(b.x) | (uint32_t(f32_to_bf16_rne(b.y)) << 16),
-                       f32_to_bf16_rne(b.z) | (uint32_t(f32_to_bf16_rne(b.w)) << 16));
-    } else {
-        for (size_t k = 0; i + k < n; ++k) dst[k] = f32_to_bf16_rne(src[k]);
+    const float *src = X + blockIdx.y * xs;
+    unsigned short *dst = Xb + blockIdx.y * n;
+    const size_t base = size_t(blockIdx.x) * (2048 * kXRuns) + threadIdx.x * 8;
+    if (base + 2048 * (kXRuns - 1) + 8 <= n) {
+        float4 a[kXRuns], b[kXRuns];
+#pragma unroll
+        for (int r = 0; r < kXRuns; ++r) {
+            a[r] = *reinterpret_cast<const float4 *>(src + base + 2048 * r);
+            b[r] = *reinterpret_cast<const float4 *>(src + base + 2048 * r + 4);
+        }
+#pragma unroll
+        for (int r = 0; r < kXRuns; ++r)
+            *reinterpret_cast<uint4 *>(dst + base + 2048 * r) = pack_bf16x8(a[r], b[r]);
+        return;
+    }
+    // a problem's last block: run by run, the ragged end element by element
+    for (int r = 0; r < kXRuns; ++r) {
+        const size_t i = base + 2048 * size_t(r);
+        if (i >= n) return;
+        if (i + 8 <= n) {
+            const float4 a = *reinterpret_cast<const float4 *>(src + i);
+            const float4 b = *reinterpret_cast<const float4 *>(src + i + 4);
+            *reinterpret_cast<uint4 *>(dst + i) = pack_bf16x8(a, b);
+        } else {
+            for (size_t k = i; k < n; ++k) dst[k] = f32_to_bf16_rne(src[k]);
+        }
     }
 }
 
@@ -725,7 +750,7 @@ int nd_cb8_gemm_batched(nd_ctx *ctx, size_t count, const float *x, size_t x_stri
     void *wsp = nullptr;
     if (int rc = nd::workspace(ctx, count * mk * sizeof(unsigned short), &wsp)) return rc;
     unsigned short *xb = static_cast<unsigned short *>(wsp);
-    hipLaunchKernelGGL(x_to_bf16_kernel, dim3(unsigned((mk + 2047) / 2048), unsigned(count)),
+    hipLaunchKernelGGL(x_to_bf16_kernel, dim3(unsigned((mk + 2048 * kXRuns - 1) / (2048 * kXRuns)), unsigned(count)),
                        dim3(256), 0, ctx->stream, x, x_stride, xb, mk);
     if (int rc = nd::check_launch("x_to_bf16")) return rc;
     const size_t big_tiles = (out / kPN) * ((m + kPM - 1) / kPM) * count;
