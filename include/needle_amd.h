@@ -329,6 +329,36 @@ int nd_v3_cact_config(const void *bytes, size_t len, nd_v3_cfg *cfg, size_t *can
  * model_from_cact (v3.rs:438-482). */
 int nd_v3_model_from_cact(nd_ctx *ctx, const void *bytes, size_t len, nd_v3_model **out);
 
+/* ---- ladder rungs: a shallower model sliced from the full container ------ */
+
+/* The `depth` blocks a rung of a `num_layers`-block stack keeps, ascending,
+ * into kept[0..depth): the first `depth` of the ladder order (both
+ * endpoints, then the widest remaining gap split at its midpoint, leftmost
+ * first).  ND_ERR_ARG ("depth is outside the ladder") unless
+ * 2 <= depth <= num_layers.  Host only.  Replaces ladder_layer_indices
+ * (crates/needle-core/src/v3/ladder.rs:67-74). */
+int nd_v3_ladder(size_t num_layers, size_t depth, int32_t *kept);
+
+/* As nd_v3_cact_config for the `depth`-block rung: the parent geometry is
+ * read and checked, the ladder applied, every block's shapes checked and
+ * the kept blocks' tensors decoded; `cfg` receives the rung's geometry (kept
+ * blocks renumbered, global layers and Engram sites following their blocks)
+ * and `kept` (optional, `depth` entries) the parent blocks kept.  depth ==
+ * num_layers is the ordinary read.  Host only.  Replaces config_at_depth
+ * (needle-infer/src/v3.rs:620-637) with model_from_cact_at_depth's checks
+ * (v3.rs:656-664). */
+int nd_v3_cact_config_at_depth(const void *bytes, size_t len, size_t depth, nd_v3_cfg *cfg,
+                               int32_t *kept);
+
+/* Uploads the `depth`-block rung of a full-depth container: the kept blocks
+ * whole, the mHC scalars of the kept blocks, the phi lane rows of the kept
+ * blocks (packed rows and FP16 norms copied unchanged: nothing is
+ * re-quantised), the Engram sites on kept blocks, the rest as stored.
+ * Replaces model_from_cact_at_depth (v3.rs:656-734) behind
+ * V3Engine::load_with_depth and needle_v3_load_with_depth. */
+int nd_v3_model_from_cact_at_depth(nd_ctx *ctx, const void *bytes, size_t len, size_t depth,
+                                   nd_v3_model **out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -18,6 +18,7 @@
 #include "nd_cq_internal.h"
 #include "nd_internal.h"
 
+#include <algorithm>
 #include <cstring>
 #include <vector>
 
@@ -174,8 +175,11 @@ struct Canon {
 // order (v3.rs:438-482, layer_from_layout v3.rs:396-436): CQ slots must be
 // CQ records (CactV3::cq, cact.rs:1076-1093; the blob itself is parsed by
 // the device upload, CqWeight::from_blob), float slots are decoded
-// (decode_floats, cact.rs:494-526).
-int walk(Container &c)
+// (decode_floats, cact.rs:494-526).  With `kept` (a ladder rung), the shapes
+// are still checked for every block but only the kept blocks and the Engram
+// sites on them are read, in model_from_cact_at_depth's order
+// (v3.rs:656-734): the embedding after the permutations.
+int walk(Container &c, const std::vector<int> *kept = nullptr)
 {
     const nd_v3_cfg &g = c.cfg;
     const size_t n = c.recs.size();
@@ -259,8 +263,16 @@ int walk(Container &c)
         o.in = r.ndim > 1 ? r.shape[1] : 1;
         return ND_OK;
     };
-    if (int rc = cq(0)) return rc;
+    auto on = [&](int li) {
+        if (!kept) return true;
+        for (int k : *kept)
+            if (k == li) return true;
+        return false;
+    };
+    if (!kept)
+        if (int rc = cq(0)) return rc;
     for (int li = 0; li < g.num_layers; ++li) {
+        if (!on(li)) continue;
         for (size_t t = 0; t < cn.taps; ++t)
             if (int rc = floats(cn.layer(li, 4 + t))) return rc;
         const size_t order[] = {0, 1, 2, 3, 4 + cn.taps, 5 + cn.taps, 6 + cn.taps, 7 + cn.taps,
@@ -283,6 +295,7 @@ int walk(Container &c)
     for (size_t k = 0; k < 3; ++k)
         if (int rc = cq(cn.phi + k)) return rc;
     for (int s = 0; s < g.n_sites; ++s) {
+        if (!on(g.sites[s])) continue;
         const size_t e = cn.engram + 4 * size_t(s);
         if (int rc = cq(e)) return rc;
         if (int rc = cq(e + 1)) return rc;
@@ -291,7 +304,175 @@ int walk(Container &c)
     }
     for (size_t k = 0; k < 2; ++k)
         if (int rc = floats(cn.perms + k)) return rc;
+    if (kept)
+        if (int rc = cq(0)) return rc;
     return floats(cn.final_norm);
+}
+
+// ---- ladder rungs (v3/ladder.rs, v3.rs:612-734) -------------------------
+// Every depth from 2 blocks up is a trained subnetwork of the full stack.  The
+// blocks a rung keeps are a bisection from both ends: the order starts with
+// the two endpoints and then repeatedly splits the widest remaining gap at its
+// midpoint, the leftmost gap winning ties (ladder_order, ladder.rs:28-61); a
+// rung of `depth` keeps the first `depth` of that order, ascending
+// (ladder_layer_indices, ladder.rs:67-74).
+std::vector<int> ladder_order(int L)
+{
+    std::vector<int> order;
+    if (L <= 0) return order;
+    if (L == 1) return {0};
+    std::vector<int> sel = {0, L - 1};
+    order = sel;
+    while (int(order.size()) < L) {
+        std::sort(sel.begin(), sel.end());
+        int bg = 0, bl = 0, br = 0;
+        for (size_t i = 0; i + 1 < sel.size(); ++i) {
+            const int gap = sel[i + 1] - sel[i];
+            if (gap <= 1) continue;
+            if (gap > bg) {  // equal gaps keep the leftmost, met first
+                bg = gap;
+                bl = sel[i];
+                br = sel[i + 1];
+            }
+        }
+        if (bg == 0) break;
+        const int mid = (bl + br) / 2;
+        sel.push_back(mid);
+        order.push_back(mid);
+    }
+    return order;
+}
+
+bool ladder_layers(int L, size_t depth, std::vector<int> &kept)
+{
+    if (depth < 2 || depth > size_t(L)) return false;
+    const std::vector<int> order = ladder_order(L);
+    kept.assign(order.begin(), order.begin() + std::ptrdiff_t(depth));
+    std::sort(kept.begin(), kept.end());
+    return true;
+}
+
+// config_at_depth (v3.rs:620-637): the kept blocks renumbered contiguously;
+// global layers and Engram sites follow their blocks.
+nd_v3_cfg config_at_depth(const nd_v3_cfg &p, const std::vector<int> &kept)
+{
+    nd_v3_cfg c = p;
+    auto rank = [&](int l) {
+        for (size_t i = 0; i < kept.size(); ++i)
+            if (kept[i] == l) return int(i);
+        return -1;
+    };
+    c.num_layers = int32_t(kept.size());
+    c.n_global = 0;
+    for (int i = 0; i < p.n_global; ++i)
+        if (rank(p.global_layers[i]) >= 0) c.global_layers[c.n_global++] = rank(p.global_layers[i]);
+    c.n_sites = 0;
+    for (int i = 0; i < p.n_sites; ++i)
+        if (rank(p.sites[i]) >= 0) c.sites[c.n_sites++] = rank(p.sites[i]);
+    return c;
+}
+
+// The records of a rung, in the rung's own canon: the kept blocks whole, the
+// per-layer mHC scalars and the phi lane rows of the kept blocks (Cactus-Quants
+// packs each row on its own, so a row cut copies packed bytes and FP16 norms
+// unchanged: CqWeight::select_rows, cq.rs:151-175), the Engram sites on kept
+// blocks, the rest as is.  Nothing is re-quantised.
+struct Rung {
+    nd_v3_cfg cfg{};
+    std::vector<nd_v3_record> out;
+    std::vector<std::vector<float>> scalars;
+    std::vector<std::vector<uint8_t>> phi;
+};
+
+int slice(const Container &c, const std::vector<int> &kept, Rung &r)
+{
+    const nd_v3_cfg &pg = c.cfg;
+    r.cfg = config_at_depth(pg, kept);
+    const Canon pc(pg), rc(r.cfg);
+    const size_t n = size_t(pg.mhc_lanes), depth = kept.size();
+    r.out.assign(rc.count, nd_v3_record{});
+    r.out[0] = c.out[0];
+    for (size_t i = 0; i < depth; ++i)
+        for (size_t slot = 0; slot < pc.per_layer; ++slot)
+            r.out[rc.layer(int(i), slot)] = c.out[pc.layer(kept[i], slot)];
+    // a_pre, a_post, a_res: one per layer; b_pre, b_post: n; b_res: n * n
+    const size_t width[6] = {1, 1, 1, n, n, n * n};
+    r.scalars.resize(6);
+    for (size_t k = 0; k < 6; ++k) {
+        const std::vector<float> &v = c.floats[pc.scalars + k];
+        std::vector<float> &o = r.scalars[k];
+        for (int l : kept) {
+            if ((size_t(l) + 1) * width[k] > v.size())
+                return nd::fail(ND_ERR_ARG, "mHC scalar %zu is too short for layer %d", k, l);
+            o.insert(o.end(), v.begin() + std::ptrdiff_t(size_t(l) * width[k]),
+                     v.begin() + std::ptrdiff_t((size_t(l) + 1) * width[k]));
+        }
+        nd_v3_record rec = c.out[pc.scalars + k];
+        rec.data = o.data();
+        rec.len = o.size() * 4;
+        rec.out = depth;
+        r.out[rc.scalars + k] = rec;
+    }
+    // phi_pre, phi_post: rows l*n .. (l+1)*n; phi_res: rows l*n*n .. (l+1)*n*n
+    const size_t rows[3] = {n, n, n * n};
+    r.phi.resize(3);
+    for (size_t k = 0; k < 3; ++k) {
+        const nd_v3_record &src = c.out[pc.phi + k];
+        if (src.group == 0 || src.group % 8 || (src.group & (src.group - 1)))
+            return nd::fail(ND_ERR_ARG, "BadGroup(%zu) at record %zu", src.group, pc.phi + k);
+        const size_t in_padded = (src.in + src.group - 1) / src.group * src.group;
+        const size_t groups = in_padded / src.group;
+        const size_t row_bytes = in_padded * (src.bits == 5 ? 2 : src.bits) / 8;
+        const size_t packed = src.out * row_bytes, norms = src.out * groups * 2;
+        if (src.len < packed + norms)
+            return nd::fail(ND_ERR_ARG, "ShortBlob { need: %zu, got: %zu } at record %zu",
+                            packed + norms, src.len, pc.phi + k);
+        const uint8_t *b = static_cast<const uint8_t *>(src.data);
+        std::vector<uint8_t> &o = r.phi[k];
+        const size_t keep = depth * rows[k];
+        o.resize(keep * (row_bytes + groups * 2));
+        size_t at = 0;
+        for (int pass = 0; pass < 2; ++pass)  // packed rows, then their norms
+            for (int l : kept)
+                for (size_t row = size_t(l) * rows[k]; row < (size_t(l) + 1) * rows[k]; ++row) {
+                    if (row >= src.out) return nd::fail(ND_ERR_ARG, "mHC lane row out of range");
+                    const size_t w = pass == 0 ? row_bytes : groups * 2;
+                    std::memcpy(o.data() + at, b + (pass == 0 ? 0 : packed) + row * w, w);
+                    at += w;
+                }
+        nd_v3_record rec = src;
+        rec.data = o.data();
+        rec.len = o.size();
+        rec.out = keep;
+        r.out[rc.phi + k] = rec;
+    }
+    for (size_t k = 0; k < 2; ++k) r.out[rc.perms + k] = c.out[pc.perms + k];
+    size_t site = 0;
+    for (int s = 0; s < pg.n_sites; ++s) {
+        if (std::find(kept.begin(), kept.end(), pg.sites[s]) == kept.end()) continue;
+        for (size_t k = 0; k < 4; ++k) r.out[rc.engram + 4 * site + k] = c.out[pc.engram + 4 * size_t(s) + k];
+        ++site;
+    }
+    r.out[rc.final_norm] = c.out[pc.final_norm];
+    return ND_OK;
+}
+
+// model_from_cact_at_depth's checks up to the slice (v3.rs:656-664): the
+// parent geometry, the ladder, then the layout of the full container.
+int read_rung(Container &c, const void *bytes, size_t len, size_t depth, std::vector<int> &kept)
+{
+    ND_REQUIRE(bytes || len == 0, "null container");
+    c.raw = static_cast<const uint8_t *>(bytes);
+    c.len = len;
+    if (int rc = parse(c)) return rc;
+    if (depth == size_t(c.cfg.num_layers)) {
+        kept.clear();
+        for (int l = 0; l < c.cfg.num_layers; ++l) kept.push_back(l);
+        return walk(c);
+    }
+    if (!ladder_layers(c.cfg.num_layers, depth, kept))
+        return nd::fail(ND_ERR_ARG, "depth is outside the ladder");
+    return walk(c, &kept);
 }
 
 int read(Container &c, const void *bytes, size_t len)
@@ -327,6 +508,49 @@ int nd_v3_model_from_cact(nd_ctx *ctx, const void *bytes, size_t len, nd_v3_mode
     if (int rc = read(c, bytes, len)) return rc;
     return nd_v3_model_create(ctx, &c.cfg, c.codebook.data(), c.codebook.size(), c.out.data(),
                               c.out.size(), out);
+}
+
+int nd_v3_ladder(size_t num_layers, size_t depth, int32_t *kept)
+{
+    nd::clear_error();
+    ND_REQUIRE(kept, "null kept");
+    ND_REQUIRE(num_layers <= 1024, "num_layers %zu too large", num_layers);
+    std::vector<int> k;
+    if (!ladder_layers(int(num_layers), depth, k)) return nd::fail(ND_ERR_ARG, "depth is outside the ladder");
+    for (size_t i = 0; i < k.size(); ++i) kept[i] = k[i];
+    return ND_OK;
+}
+
+int nd_v3_cact_config_at_depth(const void *bytes, size_t len, size_t depth, nd_v3_cfg *cfg,
+                               int32_t *kept)
+{
+    nd::clear_error();
+    ND_REQUIRE(cfg, "null cfg");
+    Container c;
+    std::vector<int> k;
+    if (int rc = read_rung(c, bytes, len, depth, k)) return rc;
+    *cfg = k.size() == size_t(c.cfg.num_layers) ? c.cfg : config_at_depth(c.cfg, k);
+    if (kept)
+        for (size_t i = 0; i < k.size(); ++i) kept[i] = k[i];
+    return ND_OK;
+}
+
+int nd_v3_model_from_cact_at_depth(nd_ctx *ctx, const void *bytes, size_t len, size_t depth,
+                                   nd_v3_model **out)
+{
+    if (int rc = nd::enter(ctx)) return rc;
+    ND_REQUIRE(out, "null output pointer");
+    *out = nullptr;
+    Container c;
+    std::vector<int> k;
+    if (int rc = read_rung(c, bytes, len, depth, k)) return rc;
+    if (k.size() == size_t(c.cfg.num_layers))
+        return nd_v3_model_create(ctx, &c.cfg, c.codebook.data(), c.codebook.size(), c.out.data(),
+                                  c.out.size(), out);
+    Rung r;
+    if (int rc = slice(c, k, r)) return rc;
+    return nd_v3_model_create(ctx, &r.cfg, c.codebook.data(), c.codebook.size(), r.out.data(),
+                              r.out.size(), out);
 }
 
 }  // extern "C"

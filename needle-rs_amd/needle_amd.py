@@ -89,6 +89,9 @@ _SIGS = [
     ("nd_v3_prefill", C.c_int, [_vp, _vp, _vp, _vp, _sz, _vp, _vp]),
     ("nd_v3_cact_config", C.c_int, [_vp, _sz, _vp, C.POINTER(_sz)]),
     ("nd_v3_model_from_cact", C.c_int, [_vp, _vp, _sz, C.POINTER(_vp)]),
+    ("nd_v3_ladder", C.c_int, [_sz, _sz, C.POINTER(C.c_int32)]),
+    ("nd_v3_cact_config_at_depth", C.c_int, [_vp, _sz, _sz, _vp, C.POINTER(C.c_int32)]),
+    ("nd_v3_model_from_cact_at_depth", C.c_int, [_vp, _vp, _sz, _sz, C.POINTER(_vp)]),
 ]
 
 
@@ -470,20 +473,48 @@ def cact_v3_config(data):
     return geom_of_cfg(cfg), n.value
 
 
+def v3_ladder(num_layers, depth):
+    """The blocks a `depth`-block rung keeps, ascending (ladder_layer_indices,
+    crates/needle-core/src/v3/ladder.rs:67-74).  Host only."""
+    kept = (C.c_int32 * max(int(depth), 1))()
+    _check(lib().nd_v3_ladder(num_layers, depth, kept))
+    return [kept[i] for i in range(depth)]
+
+
+def cact_v3_config_at_depth(data, depth):
+    """The geometry of a container's `depth`-block rung and the parent
+    blocks it keeps (config_at_depth with model_from_cact_at_depth's
+    checks, needle-infer/src/v3.rs:620-664).  Host only."""
+    buf = _container_bytes(data)
+    cfg = V3Cfg()
+    kept = (C.c_int32 * max(int(depth), 1))()
+    _check(lib().nd_v3_cact_config_at_depth(buf.ctypes.data_as(C.c_void_p), buf.size, depth,
+                                            C.byref(cfg), kept))
+    return geom_of_cfg(cfg), [kept[i] for i in range(depth)]
+
+
 class V3Model:
     """A Needle-3 model on the device, from canonical container records
     (V3Layout::derive order, crates/needle-infer/src/v3.rs:236-330), or from a
-    .cact v3 container with `from_cact` (model_from_cact, v3.rs:438-482)."""
+    .cact v3 container with `from_cact` (model_from_cact, v3.rs:438-482; with
+    `depth`, the ladder rung model_from_cact_at_depth slices, v3.rs:656-734)."""
 
     @classmethod
-    def from_cact(cls, ctx, data):
+    def from_cact(cls, ctx, data, depth=None):
         buf = _container_bytes(data)
-        geom, _ = cact_v3_config(buf)
+        if depth is None:
+            geom, _ = cact_v3_config(buf)
+        else:
+            geom, _ = cact_v3_config_at_depth(buf, depth)
         self = cls.__new__(cls)
         self.ctx, self.geom = ctx, geom
         h = C.c_void_p()
-        _check(lib().nd_v3_model_from_cact(ctx.h, buf.ctypes.data_as(C.c_void_p), buf.size,
-                                           C.byref(h)))
+        if depth is None:
+            _check(lib().nd_v3_model_from_cact(ctx.h, buf.ctypes.data_as(C.c_void_p), buf.size,
+                                               C.byref(h)))
+        else:
+            _check(lib().nd_v3_model_from_cact_at_depth(ctx.h, buf.ctypes.data_as(C.c_void_p),
+                                                        buf.size, depth, C.byref(h)))
         self.h = h
         self.rows = lib().nd_v3_logit_rows(h)
         return self

@@ -5,6 +5,7 @@ Reads JSON data files only (no reference code is imported or run):
   tests/v3_kv_quant_vectors.json  -> kv_quant_vectors.json   (upstream fake_quant KAT)
   tests/cact_vectors.json         -> cq_codebook.json        (28-float cb2|cb3|cb4)
   tests/cact_v3_vectors.json      -> v3_geometry.json, v3_cq_records.json, v3_directory.json
+  tests/v3_ladder_rungs.json      -> v3_ladder_rungs.json    (upstream ladder_config per depth)
 Run from the repo root:  python tests/golden/make_fixtures.py [/root/reference]
 """
 import json
@@ -54,6 +55,18 @@ dump("v3_directory.json", {
     "codebook_len": v3["codebook_len"],
     "records": [[r["index"], r["dtype"], r["ndim"], r["shape"], r["offset"], r["nbytes"],
                  r["group"], r["bits"]] for r in v3["records"]],
+})
+lad = json.load(open(os.path.join(REF, "tests/v3_ladder_rungs.json")))
+dump("v3_ladder_rungs.json", {
+    "provenance": "needle-rs tests/v3_ladder_rungs.json: upstream ladder_config for every "
+                  "depth of the 20-block stack (kept blocks, renumbered global layers and "
+                  "Engram sites)",
+    "parent_layers": lad["parent_layers"],
+    "ladder_order": lad["ladder_order"],
+    "parent_global": lad["parent_global"],
+    "parent_engram_sites": lad["parent_engram_sites"],
+    "rungs": [dict(depth=r["depth"], selected=r["selected"], global_layers=r["global_layers"],
+                   engram_sites=r["engram_sites"]) for r in lad["rungs"]],
 })
 print(f"wrote {len(kv['cases'])} kv cases, {len(cq)} CQ records, "
       f"{len(v3['records'])} directory records")

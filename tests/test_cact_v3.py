@@ -102,3 +102,89 @@ def test_trailing_records_are_not_read(shipped):
     fault there does not stop the model from loading."""
     geom, canon = nd.cact_v3_config(W.set_record(shipped, 575, dtype=9))
     assert canon == 573
+
+
+# ---- ladder rungs (v3/ladder.rs, v3.rs:612-734) -------------------------------
+
+LADDER = json.load(open(os.path.join(W.GOLDEN, "v3_ladder_rungs.json")))
+
+
+def _order_brute(L):
+    """The ladder order restated from its definition: both endpoints, then
+    repeatedly the midpoint of the widest gap between chosen blocks, the
+    leftmost of equal gaps first."""
+    chosen = [0, L - 1]
+    while len(chosen) < L:
+        s = sorted(chosen)
+        gaps = [(s[i + 1] - s[i], -s[i], s[i], s[i + 1]) for i in range(len(s) - 1)
+                if s[i + 1] - s[i] > 1]
+        _, _, a, b = max(gaps)
+        chosen.append((a + b) // 2)
+    return chosen
+
+
+def test_ladder_rungs_match_upstream():
+    """Every depth of the 20-block stack keeps upstream's blocks
+    (tests/v3_ladder_rungs.json, upstream ladder_config)."""
+    assert _order_brute(20) == LADDER["ladder_order"]
+    for rung in LADDER["rungs"]:
+        assert nd.v3_ladder(20, rung["depth"]) == rung["selected"], rung["depth"]
+
+
+@pytest.mark.parametrize("L", [2, 3, 4, 7, 12, 33])
+def test_ladder_nests_and_keeps_both_ends(L):
+    order = _order_brute(L)
+    prev = []
+    for depth in range(2, L + 1):
+        kept = nd.v3_ladder(L, depth)
+        assert kept == sorted(order[:depth])
+        assert kept[0] == 0 and kept[-1] == L - 1
+        assert set(prev) < set(kept)
+        prev = kept
+
+
+def test_ladder_refuses_depths_outside():
+    for bad in (0, 1, 21, 100):
+        with pytest.raises(nd.NeedleError) as e:
+            nd.v3_ladder(20, bad)
+        assert e.value.code == nd.ND_ERR_ARG and "outside the ladder" in str(e.value)
+
+
+def test_rung_geometry_of_the_shipped_container(shipped):
+    """config_at_depth on the shipped directory: kept blocks renumbered,
+    global layers and Engram sites following them, as upstream's
+    ladder_config gives for every depth."""
+    full, _ = nd.cact_v3_config(shipped)
+    for rung in LADDER["rungs"]:
+        d = rung["depth"]
+        geom, kept = nd.cact_v3_config_at_depth(shipped, d)
+        assert kept == rung["selected"]
+        assert geom["num_layers"] == d
+        assert geom["global_layers"] == rung["global_layers"], d
+        assert geom["sites"] == rung["engram_sites"], d
+        for k in ("d_model", "num_heads", "num_kv_heads", "sliding_window", "orders", "e_slots"):
+            assert geom[k] == full[k]
+    for bad in (0, 1, 21):
+        with pytest.raises(nd.NeedleError):
+            nd.cact_v3_config_at_depth(shipped, bad)
+
+
+def test_rung_reads_only_the_kept_blocks(shipped):
+    """model_from_cact_at_depth decodes the kept blocks only: a bad float
+    record in block 1 stops the full read and the 3-block rung (blocks
+    0, 9, 19) does not see it; a bad record in a kept block still stops it."""
+    per_layer = 27
+    bad1 = W.set_record(shipped, 1 + 1 * per_layer, dtype=4)  # block 1 norm_in as RAW
+    with pytest.raises(nd.NeedleError) as e:
+        nd.cact_v3_config(bad1)
+    assert "DtypeMismatch { index: 28, want: 1, got: 4 }" in str(e.value)
+    geom, kept = nd.cact_v3_config_at_depth(bad1, 3)
+    assert kept == [0, 9, 19] and geom["num_layers"] == 3
+    bad9 = W.set_record(shipped, 1 + 9 * per_layer, dtype=4)
+    with pytest.raises(nd.NeedleError) as e:
+        nd.cact_v3_config_at_depth(bad9, 3)
+    assert "DtypeMismatch { index: 244, want: 1, got: 4 }" in str(e.value)
+    # shapes are checked for every block, kept or not (V3Layout::derive)
+    with pytest.raises(nd.NeedleError) as e:
+        nd.cact_v3_config_at_depth(W.set_record(shipped, 1 + 1 * per_layer + 1, shape=[96, 768]), 3)
+    assert e.value.code == nd.ND_ERR_V3_LAYOUT and "q_proj" in str(e.value)
