@@ -329,6 +329,15 @@ int nd_v3_cact_config(const void *bytes, size_t len, nd_v3_cfg *cfg, size_t *can
  * model_from_cact (v3.rs:438-482). */
 int nd_v3_model_from_cact(nd_ctx *ctx, const void *bytes, size_t len, nd_v3_model **out);
 
+/* Key/value cache bytes a session of `seq_len` positions needs under `cfg`:
+ * per layer min(seq_len, sliding_window) positions (all of them on a global
+ * layer), each a key and a value per kv head at f32, or with kv_int8 at one
+ * byte plus one f32 scale per stored head vector.  0 (and ND_ERR_ARG in
+ * nd_last_error) for a null cfg.  Host only; what needle_v3_kv_bytes
+ * reports.  Replaces V3Config::kv_bytes_at
+ * (crates/needle-core/src/v3/config.rs:143-179). */
+size_t nd_v3_kv_bytes(const nd_v3_cfg *cfg, size_t seq_len, int kv_int8);
+
 /* ---- ladder rungs: a shallower model sliced from the full container ------ */
 
 /* The `depth` blocks a rung of a `num_layers`-block stack keeps, ascending,

@@ -510,6 +510,29 @@ int nd_v3_model_from_cact(nd_ctx *ctx, const void *bytes, size_t len, nd_v3_mode
                               c.out.size(), out);
 }
 
+size_t nd_v3_kv_bytes(const nd_v3_cfg *cfg, size_t seq_len, int kv_int8)
+{
+    nd::clear_error();
+    if (!cfg) {
+        nd::fail(ND_ERR_ARG, "cfg was null");
+        return 0;
+    }
+    // V3Config::kv_bytes / kv_bytes_at (config.rs:143-179): per position a
+    // key and a value per kv head, at 4 bytes, or at 1 byte plus an f32
+    // scale for each; a local layer holds at most its window
+    const size_t kvh = size_t(cfg->num_kv_heads);
+    const size_t per = kvh * size_t(cfg->qk_head_dim + cfg->v_head_dim);
+    const size_t per_pos = kv_int8 ? per + kvh * 8 : per * 4;
+    size_t total = 0;
+    for (int l = 0; l < cfg->num_layers; ++l) {
+        bool global = cfg->sliding_window == 0;
+        for (int g = 0; g < cfg->n_global && !global; ++g) global = cfg->global_layers[g] == l;
+        const size_t slots = global ? seq_len : std::min(seq_len, size_t(cfg->sliding_window));
+        total += slots * per_pos;
+    }
+    return total;
+}
+
 int nd_v3_ladder(size_t num_layers, size_t depth, int32_t *kept)
 {
     nd::clear_error();

@@ -89,6 +89,7 @@ _SIGS = [
     ("nd_v3_prefill", C.c_int, [_vp, _vp, _vp, _vp, _sz, _vp, _vp]),
     ("nd_v3_cact_config", C.c_int, [_vp, _sz, _vp, C.POINTER(_sz)]),
     ("nd_v3_model_from_cact", C.c_int, [_vp, _vp, _sz, C.POINTER(_vp)]),
+    ("nd_v3_kv_bytes", _sz, [_vp, _sz, C.c_int]),
     ("nd_v3_ladder", C.c_int, [_sz, _sz, C.POINTER(C.c_int32)]),
     ("nd_v3_cact_config_at_depth", C.c_int, [_vp, _sz, _sz, _vp, C.POINTER(C.c_int32)]),
     ("nd_v3_model_from_cact_at_depth", C.c_int, [_vp, _vp, _sz, _sz, C.POINTER(_vp)]),
@@ -471,6 +472,14 @@ def cact_v3_config(data):
     _check(lib().nd_v3_cact_config(buf.ctypes.data_as(C.c_void_p), buf.size, C.byref(cfg),
                                    C.byref(n)))
     return geom_of_cfg(cfg), n.value
+
+
+def v3_kv_bytes(geom, seq_len, kv_int8=True):
+    """Key/value cache bytes of one session of `seq_len` positions
+    (V3Config::kv_bytes_at, crates/needle-core/src/v3/config.rs:143-179).
+    Host only."""
+    cfg = v3_cfg(geom)
+    return lib().nd_v3_kv_bytes(C.byref(cfg), seq_len, int(bool(kv_int8)))
 
 
 def v3_ladder(num_layers, depth):

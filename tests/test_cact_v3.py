@@ -188,3 +188,38 @@ def test_rung_reads_only_the_kept_blocks(shipped):
     with pytest.raises(nd.NeedleError) as e:
         nd.cact_v3_config_at_depth(W.set_record(shipped, 1 + 1 * per_layer + 1, shape=[96, 768]), 3)
     assert e.value.code == nd.ND_ERR_V3_LAYOUT and "q_proj" in str(e.value)
+
+
+def test_kv_bytes_closed_forms_and_published_figures(shipped):
+    """V3Config::kv_bytes_at on the shipped geometry: the reference's own
+    closed forms (config.rs:255-282: 512 x 20 x 224 and
+    (16 x 1024 + 4 x 8192) x 224 at one byte per element, only the global
+    layers growing past the window) and the sizes its docs publish (42.0 /
+    11.2 MB at 8192, 8.8 / 2.3 MB at 512, docs/c-ffi.md:121-122 and
+    README.md:66; 3.5 MB for the 8-block rung and 2.6 MB for the 6-block
+    one at 512, README.md:148 and docs/v3-port-record.md:164)."""
+    geom, _ = nd.cact_v3_config(shipped)
+    per = 2 * (48 + 64)
+    assert nd.v3_kv_bytes(geom, 512, False) == 512 * 20 * per * 4
+    assert nd.v3_kv_bytes(geom, 8192, False) == (16 * 1024 + 4 * 8192) * per * 4
+    assert nd.v3_kv_bytes(geom, 8192, True) == (16 * 1024 + 4 * 8192) * (per + 2 * 8)
+    grow = nd.v3_kv_bytes(geom, 2048, False) - nd.v3_kv_bytes(geom, 1024, False)
+    assert grow == 4 * 1024 * per * 4
+    MB = float(1 << 20)
+    assert round(nd.v3_kv_bytes(geom, 8192, False) / MB, 1) == 42.0
+    assert round(nd.v3_kv_bytes(geom, 8192, True) / MB, 1) == 11.2
+    assert round(nd.v3_kv_bytes(geom, 512, False) / MB, 1) == 8.8
+    assert round(nd.v3_kv_bytes(geom, 512, True) / MB, 1) == 2.3
+    g8, _ = nd.cact_v3_config_at_depth(shipped, 8)
+    g6, _ = nd.cact_v3_config_at_depth(shipped, 6)
+    assert round(nd.v3_kv_bytes(g8, 512, False) / MB, 1) == 3.5
+    assert round(nd.v3_kv_bytes(g6, 512, False) / MB, 1) == 2.6
+    # int8: one byte plus an f32 scale per head vector -- a touch over a
+    # quarter of f32, never at or above a half (v3_kv_int8.rs:58-62)
+    a, b = nd.v3_kv_bytes(geom, 2048, False), nd.v3_kv_bytes(geom, 2048, True)
+    assert b * 3 < a < b * 5
+
+
+def test_kv_bytes_null_cfg():
+    assert nd.lib().nd_v3_kv_bytes(None, 512, 1) == 0
+    assert "null" in nd.lib().nd_last_error().decode()
