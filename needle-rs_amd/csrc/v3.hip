@@ -249,27 +249,8 @@ __global__ __launch_bounds__(kT) void k_layer_in(LayerIn a)
     const int tid = threadIdx.x, n = a.n, d = a.d, nd = n * d;
     const int G = a.phi_G, pairs = n * G;
     float *lg = a.lanes + b * size_t(nd);
-    // global operands issued up front: this thread's phi_pre group codes
-    // and norm, and its channels' norm_in / Engram key and value
-    CqGroupCodes<PP> codes;
     const bool has_pair = tid < pairs;
-    {
-        const int r = has_pair ? tid / G : 0, g = has_pair ? tid - (tid / G) * G : 0;
-        cq_group_codes128<PP>(a.phi_packed + size_t(a.phi_row0 + r) * a.phi_row_bytes +
-                                  size_t(g) * (128 / PP),
-                              codes);
-        if (has_pair) pn[tid] = a.phi_norms[size_t(a.phi_row0 + r) * G + g];
-    }
     const float *ek = a.ek ? a.ek + b * d : nullptr;
-    float nin[kCh], ekv[kCh], evv[kCh];
-#pragma unroll
-    for (int k = 0; k < kCh; ++k) {
-        const int c = tid + k * kT;
-        nin[k] = c < d ? a.norm_in[c] : 0.0f;
-        ekv[k] = ek && c < d ? ek[c] : 0.0f;
-        evv[k] = ek && c < d ? a.ev[b * d + c] : 0.0f;
-    }
-    const float bpre = tid < n ? a.b_pre[tid] : 0.0f;
     // the previous layer's lanes and block delta for this thread's channels
     constexpr int kUpLanes = 4;
     const bool up_regs = a.update && n <= kUpLanes;
@@ -282,7 +263,6 @@ __global__ __launch_bounds__(kT) void k_layer_in(LayerIn a)
 #pragma unroll
         for (int j = 0; j < kUpLanes; ++j) old[k][j] = on && j < n ? lg[size_t(j) * d + c] : 0.0f;
     }
-    if (tid < 16) lvl[tid] = a.phi_lv[a.phi_ternary ? (tid == 3 ? 0 : (tid == 1 ? 2 : 1)) : tid];
     if (a.update) {
         if (tid < n) gpp[tid] = a.gp[b * n + tid];
         if (tid < n * n) grr[tid] = a.gr[b * n * n + tid];
@@ -315,7 +295,32 @@ __global__ __launch_bounds__(kT) void k_layer_in(LayerIn a)
     // rms_unit (kernels.rs:33-41): products, then one chain
     for (int e = tid; e < nd; e += kT) nb[e] = ln[e] * ln[e];
     __syncthreads();
+    // operands needed after the chain, issued before lane 0 of wave 0 starts
+    // folding: this thread's phi_pre group codes and norm, its channels'
+    // norm_in / Engram key and value, the phi levels; values bound for LDS
+    // are stored after the fold, so no wave waits on them first
+    CqGroupCodes<PP> codes;
+    float pnv = 0.0f;
+    {
+        const int r = has_pair ? tid / G : 0, g = has_pair ? tid - (tid / G) * G : 0;
+        cq_group_codes128<PP>(a.phi_packed + size_t(a.phi_row0 + r) * a.phi_row_bytes +
+                                  size_t(g) * (128 / PP),
+                              codes);
+        if (has_pair) pnv = a.phi_norms[size_t(a.phi_row0 + r) * G + g];
+    }
+    float nin[kCh], ekv[kCh], evv[kCh];
+#pragma unroll
+    for (int k = 0; k < kCh; ++k) {
+        const int c = tid + k * kT;
+        nin[k] = c < d ? a.norm_in[c] : 0.0f;
+        ekv[k] = ek && c < d ? ek[c] : 0.0f;
+        evv[k] = ek && c < d ? a.ev[b * d + c] : 0.0f;
+    }
+    const float bpre = tid < n ? a.b_pre[tid] : 0.0f;
+    const float lvv = tid < 16 ? a.phi_lv[a.phi_ternary ? (tid == 3 ? 0 : (tid == 1 ? 2 : 1)) : tid] : 0.0f;
     if (tid == 0) tot[0] = chain_sum(nb, nd);
+    if (has_pair) pn[tid] = pnv;
+    if (tid < 16) lvl[tid] = lvv;
     __syncthreads();
     {
         // prepare_input of rms_unit(lanes): one wave per 128-group straight
@@ -597,40 +602,68 @@ struct HadaArgs {
     const float *u;   // [B][d]
     float *bx, *y;    // [B][d]
     const float *d1, *d2, *b2, *d3, *d4;  // [1024]
-    const float *w1a, *w1b, *w2a, *w2b, *w3a, *w3b;  // [32*32]
+    const float *w1a, *w1b, *w2a, *w2b, *w3a, *w3b;  // [32*32], stored transposed
     const float *cond_v;  // [d][rank]
     const float *cond_u;  // [rank][1024]
     const int32_t *p1, *p2perm;  // [1024]
     int d, rank;
 };
 
-// out[k][l] = sum_j (sum_i z[i][j] a[i][k]) b[j][l], i and j ascending, zero
-// factors skipped as kron_apply (v3/kernels.rs:41-81) skips them.
-__device__ inline void kron32(const float *z, const float *a, const float *bm, float *t, float *out)
+// out[k][l] = sum_j (sum_i z[i][l] a[i][k]) b[j][l], i and j ascending, each
+// product rounded before its add and zero factors skipped, as kron_apply
+// (v3/kernels.rs:41-81) does.  Thread (k, l) = (tid / 32, tid % 32) of 1024.
+// z, a and b are held transposed at a padded row stride (zT[l*kKS + i] =
+// z[i][l], aT[k*kKS + i] = a[i][k], bT[l*kKS + j] = b[j][l]) and t at the same
+// stride, so every operand is read four terms at a time as a float4, from
+// distinct banks; out is 32x32 row-major.  A pass whose skipping factor holds
+// no zero at all (`a_zero` false for a; for t, found at the barrier between
+// the passes) adds every product, which is the same sum.
+constexpr int kKS = 36;
+
+__device__ inline int kron_t(int e) { return (e & 31) * kKS + (e >> 5); }  // z[e / 32][e % 32]
+
+__device__ inline void kron32(const float *zT, const float *aT, const float *bT, float *t, float *out,
+                              bool a_zero)
 {
-    const int tid = threadIdx.x;  // 1024 threads: (row, col) = (tid / 32, tid % 32)
-    const int r = tid >> 5, c = tid & 31;
-    {
-        float acc = 0.0f;
-#pragma unroll 8
-        for (int i = 0; i < 32; ++i) {
-            const float aik = a[i * 32 + r];
-            const float p = z[i * 32 + c] * aik;
-            acc = aik == 0.0f ? acc : acc + p;  // a zero factor adds nothing, as skipped
+    const int tid = threadIdx.x;
+    const int k = tid >> 5, l = tid & 31;
+    float acc = 0.0f;
+#pragma unroll
+    for (int i0 = 0; i0 < 32; i0 += 4) {
+        const float4 av = *reinterpret_cast<const float4 *>(aT + k * kKS + i0);
+        const float4 zv = *reinterpret_cast<const float4 *>(zT + l * kKS + i0);
+        const float a4[4] = {av.x, av.y, av.z, av.w}, z4[4] = {zv.x, zv.y, zv.z, zv.w};
+        if (a_zero) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float p = z4[u] * a4[u];
+                acc = a4[u] == 0.0f ? acc : acc + p;
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc += z4[u] * a4[u];
         }
-        t[r * 32 + c] = acc;
     }
-    __syncthreads();
-    {
-        float acc = 0.0f;
-#pragma unroll 8
-        for (int j = 0; j < 32; ++j) {
-            const float tkj = t[r * 32 + j];
-            const float p = tkj * bm[j * 32 + c];
-            acc = tkj == 0.0f ? acc : acc + p;
+    t[k * kKS + l] = acc;
+    const bool t_zero = __syncthreads_or(acc == 0.0f);
+    float o = 0.0f;
+#pragma unroll
+    for (int j0 = 0; j0 < 32; j0 += 4) {
+        const float4 tv = *reinterpret_cast<const float4 *>(t + k * kKS + j0);
+        const float4 bv = *reinterpret_cast<const float4 *>(bT + l * kKS + j0);
+        const float t4[4] = {tv.x, tv.y, tv.z, tv.w}, b4[4] = {bv.x, bv.y, bv.z, bv.w};
+        if (t_zero) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float p = t4[u] * b4[u];
+                o = t4[u] == 0.0f ? o : o + p;
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) o += t4[u] * b4[u];
         }
-        out[r * 32 + c] = acc;
     }
+    out[k * 32 + l] = o;
     __syncthreads();
 }
 
@@ -639,17 +672,24 @@ constexpr int kCondProd = 6144;     // conditioning products held in LDS at once
 
 __global__ __launch_bounds__(1024) void k_post_hada(HadaArgs a)
 {
-    __shared__ __align__(16) float z[1024], buf[1024], t[1024], fa[1024], fb[1024], cond[1024];
+    __shared__ __align__(16) float z[32 * kKS], buf[1024], t[32 * kKS], fa[32 * kKS], fb[32 * kKS], cond[1024];
     __shared__ __align__(16) float nbs[1024], prod[kCondProd];
     __shared__ float proj[64], tot[2];
+    __shared__ unsigned zf;  // bit k: the a factor of Kronecker pass k holds a zero
     const size_t b = blockIdx.x;
     const int tid = threadIdx.x, d = a.d, r = a.rank;
-    // every global operand this thread needs, issued up front
+    // what the first chain and the step after it need, up front
     const bool ch = tid < d;
     const float pv = ch ? a.proj[b * d + tid] : 0.0f;
     const float bxv = ch ? a.bx[b * d + tid] : 0.0f;
-    const float uv = ch ? a.u[b * d + tid] : 0.0f;
     const float post_n = ch ? a.post_norm[tid] : 0.0f;
+    // post-norm of the projection, gated residual, pre-MLP norm: two chains
+    buf[tid] = pv * pv;
+    if (tid == 0) zf = 0;
+    __syncthreads();
+    if (tid == 0) tot[0] = chain_sum(buf, d);
+    // every other operand, issued while lane 0 of wave 0 folds
+    const float uv = ch ? a.u[b * d + tid] : 0.0f;
     const float pre_n = ch ? a.pre_hada[tid] : 0.0f;
     const float d1 = a.d1[tid], d2 = a.d2[tid], b2 = a.b2[tid], d3 = a.d3[tid], d4 = a.d4[tid];
     const float w1a = a.w1a[tid], w1b = a.w1b[tid], w2a = a.w2a[tid], w2b = a.w2b[tid];
@@ -662,10 +702,10 @@ __global__ __launch_bounds__(1024) void k_post_hada(HadaArgs a)
         cv[j] = regs && ch && j < r ? a.cond_v[tid * r + j] : 0.0f;
         cu[j] = regs && j < r ? a.cond_u[j * 1024 + tid] : 0.0f;
     }
-    // post-norm of the projection, gated residual, pre-MLP norm: two chains
-    buf[tid] = pv * pv;
-    __syncthreads();
-    if (tid == 0) tot[0] = chain_sum(buf, d);
+    {
+        const unsigned zb = unsigned(w1a == 0.0f) | unsigned(w2a == 0.0f) << 1 | unsigned(w3a == 0.0f) << 2;
+        if (zb) atomicOr(&zf, zb);
+    }
     __syncthreads();
     if (ch) {
         const float inv = 1.0f / sqrtf(tot[0] / float(d) + 1e-6f);
@@ -732,26 +772,26 @@ __global__ __launch_bounds__(1024) void k_post_hada(HadaArgs a)
         }
         cond[tid] = c;
     }
-    z[tid] = xv * d1;
-    fa[tid] = w1a;
-    fb[tid] = w1b;
+    z[kron_t(tid)] = xv * d1;
+    fa[(tid >> 5) * kKS + (tid & 31)] = w1a;  // w1a is stored transposed
+    fb[(tid >> 5) * kKS + (tid & 31)] = w1b;  // w1b is stored transposed
     __syncthreads();
-    kron32(z, fa, fb, t, buf);
-    z[tid] = buf[p1];
-    fa[tid] = w2a;
-    fb[tid] = w2b;
+    kron32(z, fa, fb, t, buf, zf & 1u);
+    z[kron_t(tid)] = buf[p1];
+    fa[(tid >> 5) * kKS + (tid & 31)] = w2a;  // w2a is stored transposed
+    fb[(tid >> 5) * kKS + (tid & 31)] = w2b;  // w2b is stored transposed
     __syncthreads();
     {
-        const float zz = d2 * cond[tid] * z[tid] + b2;
-        z[tid] = zz * sigmoidf_(zz);
+        const float zz = d2 * cond[tid] * z[kron_t(tid)] + b2;
+        z[kron_t(tid)] = zz * sigmoidf_(zz);
     }
     __syncthreads();
-    kron32(z, fa, fb, t, buf);
-    z[tid] = buf[p2] * d3;
-    fa[tid] = w3a;
-    fb[tid] = w3b;
+    kron32(z, fa, fb, t, buf, zf & 2u);
+    z[kron_t(tid)] = buf[p2] * d3;
+    fa[(tid >> 5) * kKS + (tid & 31)] = w3a;  // w3a is stored transposed
+    fb[(tid >> 5) * kKS + (tid & 31)] = w3b;  // w3b is stored transposed
     __syncthreads();
-    kron32(z, fa, fb, t, buf);
+    kron32(z, fa, fb, t, buf, zf & 4u);
     if (ch) {
         const float o = buf[tid] * d4;
         const float nb = nbs[tid] + o;
@@ -967,6 +1007,7 @@ struct nd_v3_model {
     nd_cq *embedding = nullptr;
     std::vector<Layer> layers;
     std::vector<float> a_pre, a_post, a_res;  // host copies, per layer
+    std::vector<std::vector<float>> staged;  // host data of in-flight uploads
     float *b_pre = nullptr, *b_post = nullptr, *b_res = nullptr;
     nd_cq *phi_pre = nullptr, *phi_post = nullptr, *phi_res = nullptr;
     int32_t *p1 = nullptr, *p2 = nullptr;
@@ -1078,6 +1119,24 @@ int upload_floats(nd_ctx *ctx, nd_v3_model *m, const nd_v3_record &r, size_t wan
                         what, want, int(r.kind), r.len);
     if (int rc = dalloc(m->mem, out, want)) return rc;
     ND_HIP(hipMemcpyAsync(*out, r.data, want * 4, hipMemcpyHostToDevice, ctx->stream));
+    return ND_OK;
+}
+
+// A 32x32 f32 record uploaded transposed (the factors of the HadamardMLP's
+// Kronecker passes, read column-wise); the host copy lives as long as the model.
+int upload_transposed32(nd_ctx *ctx, nd_v3_model *m, const nd_v3_record &r, float **out,
+                        const char *what, size_t idx)
+{
+    if (r.kind != ND_REC_F32 || r.len != 1024 * 4)
+        return nd::fail(ND_ERR_ARG, "record %zu (%s): want 1024 f32, got kind %d with %zu bytes", idx,
+                        what, int(r.kind), r.len);
+    const float *src = static_cast<const float *>(r.data);
+    m->staged.emplace_back(1024);
+    std::vector<float> &tr = m->staged.back();
+    for (int i = 0; i < 32; ++i)
+        for (int k = 0; k < 32; ++k) tr[size_t(k) * 32 + i] = src[i * 32 + k];
+    if (int rc = dalloc(m->mem, out, 1024)) return rc;
+    ND_HIP(hipMemcpyAsync(*out, tr.data(), 1024 * 4, hipMemcpyHostToDevice, ctx->stream));
     return ND_OK;
 }
 
@@ -1195,12 +1254,30 @@ int nd_v3_model_create(nd_ctx *ctx, const nd_v3_cfg *cfg, const float *codebook,
             F32(l.b2, b2, hn);
             F32(l.d3, d3, hn);
             F32(l.d4, d4, hn);
-            F32(l.w1a, w1a, 1024);
-            F32(l.w1b, w1b, 1024);
-            F32(l.w2a, w2a, 1024);
-            F32(l.w2b, w2b, 1024);
-            F32(l.w3a, w3a, 1024);
-            F32(l.w3b, w3b, 1024);
+            {
+                REC(w1a);
+                if ((rc = upload_transposed32(ctx, m, *r_w1a, &l.w1a, "w1a", i - 1))) goto fail;
+            }
+            {
+                REC(w1b);
+                if ((rc = upload_transposed32(ctx, m, *r_w1b, &l.w1b, "w1b", i - 1))) goto fail;
+            }
+            {
+                REC(w2a);
+                if ((rc = upload_transposed32(ctx, m, *r_w2a, &l.w2a, "w2a", i - 1))) goto fail;
+            }
+            {
+                REC(w2b);
+                if ((rc = upload_transposed32(ctx, m, *r_w2b, &l.w2b, "w2b", i - 1))) goto fail;
+            }
+            {
+                REC(w3a);
+                if ((rc = upload_transposed32(ctx, m, *r_w3a, &l.w3a, "w3a", i - 1))) goto fail;
+            }
+            {
+                REC(w3b);
+                if ((rc = upload_transposed32(ctx, m, *r_w3b, &l.w3b, "w3b", i - 1))) goto fail;
+            }
             {
                 if (i >= n) {
                     rc = nd::fail(ND_ERR_ARG, "records end before cond_v");
