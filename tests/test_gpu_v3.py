@@ -82,6 +82,34 @@ def test_greedy_matches_oracle_small(small):
     assert np.array_equal(got, toks.astype(np.int32))
 
 
+def test_zero_kronecker_factors_are_skipped(ctx):
+    """kron_apply skips zero factors (v3/kernels.rs:41-81): layer 0's w1a
+    gets an all-zero column (so a row of the intermediate is exactly zero
+    too, taking the second pass's skip as well) and a -0.0 entry; layer 1's
+    w2a a single zero.  Logits stay bit-identical to the oracle's."""
+    g, recs = S.build_records(S.small_geometry(4), seed=19)
+    recs = [dict(r) for r in recs]
+    for r in recs:
+        if r["name"] == "l0.w1a":
+            a = np.array(r["data"], np.float32).reshape(32, 32)
+            a[:, 3] = 0.0
+            a[5, 7] = -0.0
+            r["data"] = a
+        elif r["name"] == "l1.w2a":
+            a = np.array(r["data"], np.float32).reshape(32, 32)
+            a[9, 2] = 0.0
+            r["data"] = a
+    om, dm = O.V3Model(g, recs, S.CODEBOOK), nd.V3Model(ctx, g, recs, S.CODEBOOK)
+    prompt = S.prompt_tokens(12, 21)
+    want = _oracle_logits(om, prompt)
+    batch = nd.V3Batch(dm, 1, max_len=16)
+    lg = torch.empty(1, dm.rows, device="cuda")
+    for t, tok in enumerate(prompt):
+        batch.step([tok], logits=lg, want_next=False)
+        assert np.array_equal(_bits(lg.cpu().numpy()[0]), _bits(want[t])), t
+    batch.close()
+
+
 def test_model_rejects_a_wrong_record(ctx):
     g, recs = S.build_records(S.small_geometry(2), seed=1)
     bad = list(recs)
