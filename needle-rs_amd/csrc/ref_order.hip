@@ -15,7 +15,8 @@
 //                  element e of the group goes to lane e % 8, lanes summed
 //                  0..7, then the row total adds norm[g] * group_sum over the
 //                  groups in order.  One thread per (row, group): its codes
-//                  are decoded once per 8 elements and dotted with up to 8
+//                  are decoded a byte at a time through the reference's byte
+//                  LUT (one LDS read per byte) and dotted with up to 8
 //                  activation rows held in LDS; the group sums meet in LDS
 //                  and one thread per (row, batch row) chains them.
 //   cq_exact_serial   any other width or group: one thread per output, the
@@ -82,9 +83,9 @@ __global__ __launch_bounds__(kThreads) void cq_exact_kernel(CqExactSet set)
     // activations in LDS with each group padded by 4 floats, so that the
     // groups a wave reads at once fall in different banks
     const int gstride = a.group + 4, xstride = a.G * gstride;
-    float *lvl = sm;                        // [16] code -> level
-    float *ns = sm + 16;                    // [kThreads] this block's norms
-    float *xs = sm + 16 + kThreads;         // [BT][G][group + 4]
+    float *lut = sm;                        // [256][P] byte -> its P levels (build_lut)
+    float *ns = sm + 256 * P;               // [kThreads] this block's norms
+    float *xs = ns + kThreads;              // [BT][G][group + 4]
     float *gs = xs + BT * xstride;          // [BT][rpb * G] group sums
     const int tid = threadIdx.x;
     const int b0 = blockIdx.y * BT;
@@ -93,7 +94,13 @@ __global__ __launch_bounds__(kThreads) void cq_exact_kernel(CqExactSet set)
     const int r0 = a.row_start + tile * a.rpb;
     const int row_end = a.row_start + a.rows;
     const int nrows = row_end - r0 < a.rpb ? row_end - r0 : a.rpb;
-    if (tid < 16) lvl[tid] = a.lv[a.ternary ? ternary_index(tid) : tid];
+    // the byte LUT of cq.rs:932-964: slot k of byte b is the level of code k
+    // (bits k*W of b), so one read decodes a byte
+#pragma unroll
+    for (int k = 0; k < P; ++k) {
+        const int c = int((uint32_t(tid) >> (k * W)) & MASK);
+        lut[tid * P + k] = a.lv[a.ternary ? ternary_index(c) : c];
+    }
     if (tid < nrows * a.G) ns[tid] = a.norms[size_t(r0) * a.G + tid];
     for (int bb = 0; bb < nb; ++bb) {
         const float4 *src = reinterpret_cast<const float4 *>(a.xh + size_t(b0 + bb) * a.in_padded);
@@ -131,8 +138,23 @@ __global__ __launch_bounds__(kThreads) void cq_exact_kernel(CqExactSet set)
         auto step = [&](int i, uint32_t dw) {
             const int sh = (i * 8 * W) & 31;
             float v[8];
+            if (P == 4) {  // 2 bits: elements 8i..8i+7 are two bytes
 #pragma unroll
-            for (int k = 0; k < 8; ++k) v[k] = lvl[(dw >> (sh + k * W)) & MASK];
+                for (int q = 0; q < 2; ++q) {
+                    const float4 l4 = *reinterpret_cast<const float4 *>(lut + ((dw >> (sh + 8 * q)) & 0xffu) * 4);
+                    v[4 * q] = l4.x;
+                    v[4 * q + 1] = l4.y;
+                    v[4 * q + 2] = l4.z;
+                    v[4 * q + 3] = l4.w;
+                }
+            } else {  // 4 bits: four bytes
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float2 l2 = *reinterpret_cast<const float2 *>(lut + ((dw >> (sh + 8 * q)) & 0xffu) * 2);
+                    v[2 * q] = l2.x;
+                    v[2 * q + 1] = l2.y;
+                }
+            }
 #pragma unroll
             for (int bb = 0; bb < BT; ++bb) {
                 if (bb < nb) {
@@ -235,10 +257,10 @@ __global__ __launch_bounds__(kThreads) void cq_exact_serial_kernel(CqSerial a)
     a.y[size_t(b) * a.rows + rl] = total;
 }
 
-size_t exact_lds(int bt, size_t in_padded, size_t group, size_t pairs)
+size_t exact_lds(int bt, int per_byte, size_t in_padded, size_t group, size_t pairs)
 {
     const size_t padded = in_padded / group * (group + 4);
-    return 4 * (16 + size_t(kThreads) + size_t(bt) * padded + size_t(bt) * pairs);
+    return 4 * (256 * size_t(per_byte) + size_t(kThreads) + size_t(bt) * padded + size_t(bt) * pairs);
 }
 
 template <int P, int BT>
@@ -246,7 +268,7 @@ void launch_exact(const CqExactSet &set, hipStream_t s)
 {
     const CqExact &a = set.w[0];
     const unsigned gy = unsigned((a.batch + BT - 1) / BT);
-    const size_t lds = exact_lds(BT, a.in_padded, a.group, size_t(a.rpb) * a.G);
+    const size_t lds = exact_lds(BT, P, a.in_padded, a.group, size_t(a.rpb) * a.G);
     const dim3 grid(unsigned(set.tile0[set.n]), gy);
     if (a.group == 128)
         hipLaunchKernelGGL((cq_exact_kernel<P, BT, 128>), grid, dim3(kThreads), lds, s, set);
@@ -318,10 +340,10 @@ int nd_cq_exact_set(nd_ctx *ctx, hipStream_t stream, int n, const nd_cq *const *
         const size_t want = 2 * size_t(ctx->num_cus > 0 ? ctx->num_cus : 256);
         int bt = kMaxBt;
         while (bt > 1 &&
-               (size_t(bt) / 2 >= batch || exact_lds(bt, w0->in_padded, w0->group, pairs) > kLdsBudget ||
+               (size_t(bt) / 2 >= batch || exact_lds(bt, P, w0->in_padded, w0->group, pairs) > kLdsBudget ||
                 tiles * ((batch + bt - 1) / bt) < want))
             bt /= 2;
-        if (exact_lds(bt, w0->in_padded, w0->group, pairs) <= kLdsBudget) {
+        if (exact_lds(bt, P, w0->in_padded, w0->group, pairs) <= kLdsBudget) {
             CqExactSet set{};
             set.n = 0;
             int tiles = 0;
