@@ -1077,10 +1077,25 @@ struct nd_v3_batch {
     size_t step_bytes = 0;
     int32_t *next_host = nullptr;
     std::vector<void *> mem;
+    // With `graphs` (off unless asked for), one decode position per session
+    // replays a captured graph of the step's kernels on `gstream`: captured on
+    // the second such step (the first, eager, has sized everything the
+    // kernels touch), launched as one unit after; g_in / g_out order it after
+    // and before the caller's stream.  On ROCm 7.2 the replay of this
+    // two-branch graph of ~200 kernels is slower than enqueueing them.
+    bool graphs = false;
+    int eager_steps = 0;
+    hipGraphExec_t graph_exec = nullptr;
+    hipStream_t gstream = nullptr;
+    hipEvent_t g_in = nullptr, g_out = nullptr;
 
     ~nd_v3_batch()
     {
         (void)hipSetDevice(device);
+        if (graph_exec) {
+            (void)hipDeviceSynchronize();
+            (void)hipGraphExecDestroy(graph_exec);
+        }
         if (side) (void)hipStreamSynchronize(side);
         for (int i = 0; i < kStages; ++i)
             if (stage_pending[i]) (void)hipEventSynchronize(stage_done[i]);
@@ -1095,6 +1110,9 @@ struct nd_v3_batch {
             if (ev_gates[i]) (void)hipEventDestroy(ev_gates[i]);
         }
         if (side) (void)hipStreamDestroy(side);
+        if (g_in) (void)hipEventDestroy(g_in);
+        if (g_out) (void)hipEventDestroy(g_out);
+        if (gstream) (void)hipStreamDestroy(gstream);
     }
 };
 
@@ -1565,6 +1583,20 @@ fail:
 
 void nd_v3_batch_free(nd_v3_batch *b) { delete b; }
 
+int nd_v3_batch_set_graphs(nd_v3_batch *b, int on)
+{
+    nd::clear_error();
+    ND_REQUIRE(b, "null batch");
+    ND_HIP(hipSetDevice(b->device));
+    if (!on && b->graph_exec) {
+        ND_HIP(hipDeviceSynchronize());
+        ND_HIP(hipGraphExecDestroy(b->graph_exec));
+        b->graph_exec = nullptr;
+    }
+    b->graphs = on != 0;
+    return ND_OK;
+}
+
 int nd_v3_positions(const nd_v3_batch *b, int32_t *pos)
 {
     nd::clear_error();
@@ -1667,141 +1699,198 @@ int step_impl(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *
     b->stage_pending[stage] = true;
     b->stage_next = (stage + 1) % nd_v3_batch::kStages;
     hipStream_t st = ctx->stream;
-    int rc = ND_OK;
 #define CK(call) \
     if ((rc = (call))) return rc;
 #define LCHK(name) \
     if ((rc = nd::check_launch(name))) return rc;
 
-    // ---- Engram for this position (model.rs:162-191) -------------------------
-    for (int s = 0; s < c.n_sites; ++s) {
-        const Site &site = m->sites[s];
-        CK(nd_cq_dequantize_rows(ctx, site.tables, rows_dev, size_t(B) * nt, b->fetched));
-        CK(nd_cq_prepare_input(ctx, site.key, b->fetched, B, b->fh));
-        {
-            const nd_cq *ws[2] = {site.key, site.value};
-            const size_t r0[2] = {0, 0};
-            const size_t nr[2] = {size_t(d), size_t(d)};
-            float *ys[2] = {b->ek + size_t(s) * Rcap * d, b->ev + size_t(s) * Rcap * d};
-            CK(nd_cq_exact_set(ctx, st, 2, ws, b->fh, size_t(B), r0, nr, ys, "v3 engram key/value"));
-        }
-        const int reach = (c.e_conv_taps - 1) * c.e_conv_dilation;
-        if (C == 1) {
-            hipLaunchKernelGGL(k_engram_conv, dim3((d + 255) / 256, B), dim3(256), 0, st,
-                               b->ev + size_t(s) * Rcap * d, site.taps, b->et[s], pos_dev,
-                               c.e_conv_taps, c.e_conv_dilation, mo, reach, d);
-            LCHK("k_engram_conv");
-        } else {
-            hipLaunchKernelGGL(k_engram_conv_rows, dim3((d + 255) / 256, B), dim3(256), 0, st,
-                               b->ev + size_t(s) * Rcap * d, b->evc + size_t(s) * Rcap * d,
-                               site.taps, b->et[s], pos_dev, c.e_conv_taps, c.e_conv_dilation, mo,
-                               reach, d, C);
-            LCHK("k_engram_conv_rows");
-            hipLaunchKernelGGL(k_tails, dim3((d + 255) / 256, S), dim3(256), 0, st,
-                               b->ev + size_t(s) * Rcap * d, b->et[s], reach, C, d);
-            LCHK("k_tails");
-        }
-    }
-    float *const ev_conv = C == 1 ? b->ev : b->evc;  // [sites][Rcap][d], after the conv
-    // ---- lane stream (model.rs:194-203) --------------------------------------
-    CK(nd_cq_dequantize_rows(ctx, m->embedding, tok_dev, size_t(B), b->emb));
-    hipLaunchKernelGGL(k_embed, dim3((d + 255) / 256, B), dim3(256), 0, st, b->emb, b->lanes,
-                       m->embed_scale, nl, d);
-    LCHK("k_embed");
-
-    const float qk_scale = 1.0f / std::sqrt(float(c.qk_head_dim));
-    hipStream_t side = b->side;
-    const nd_cq *phi = m->phi_pre;
-    for (int li = 0; li < L; ++li) {
-        const Layer &l = m->layers[li];
-        const int site = site_of(c, li);
-        // previous layer's scatter up + this layer's mix down
-        if (li > 0) ND_HIP(hipStreamWaitEvent(st, b->ev_gates[(li - 1) & 1], 0));
-        LayerIn in{b->lanes, b->y, b->gp, b->gr, li > 0, b->nxh, m->pre_nx, phi->packed,
-                   phi->norms, phi->lv, phi->row_bytes, int(phi->num_groups), li * nl,
-                   int(phi->bits == 5), m->b_pre + size_t(li) * nl, m->a_pre[li], li, nl, d,
-                   site >= 0 ? b->ek + size_t(site) * Rcap * d : nullptr,
-                   site >= 0 ? ev_conv + size_t(site) * Rcap * d : nullptr, l.norm_in, b->u, b->bx,
-                   b->hh, m->pre_h};
-        if (phi->per_byte == 2)
-            hipLaunchKernelGGL(k_layer_in<2>, dim3(B), dim3(kT), 0, st, in);
-        else
-            hipLaunchKernelGGL(k_layer_in<4>, dim3(B), dim3(kT), 0, st, in);
-        LCHK("k_layer_in");
-        // side stream: this layer's scatter-up gates from the prepared lanes
-        ND_HIP(hipEventRecord(b->ev_in[li & 1], st));
-        ND_HIP(hipStreamWaitEvent(side, b->ev_in[li & 1], 0));
-        {
-            const nd_cq *ws[2] = {m->phi_post, m->phi_res};
-            const size_t r0[2] = {size_t(li) * nl, size_t(li) * nl * nl};
-            const size_t nr[2] = {size_t(nl), size_t(nl) * nl};
-            float *ys[2] = {b->hpost, b->hres};
-            CK(nd_cq_exact_set(ctx, side, 2, ws, b->nxh, size_t(B), r0, nr, ys, "v3 phi post/res"));
-        }
-        MhcGates mg{b->hpost, b->hres, m->b_post + size_t(li) * nl, m->b_res + size_t(li) * nl * nl,
-                    m->a_post[li], m->a_res[li], li, nl, b->gp, b->gr};
-        hipLaunchKernelGGL(k_mhc_gates, dim3(B), dim3(64), 0, side, mg);
-        LCHK("k_mhc_gates");
-        ND_HIP(hipEventRecord(b->ev_gates[li & 1], side));
-        // q, k, v and gate projections of the prepared h, one launch
-        {
-            const nd_cq *ws[4] = {l.q, l.k, l.v, l.gate};
-            const size_t r0[4] = {0, 0, 0, 0};
-            const size_t nr[4] = {size_t(qd), size_t(kd), size_t(vd), size_t(od)};
-            float *ys[4] = {b->q, b->k, b->v, b->gate};
-            CK(nd_cq_exact_set(ctx, st, 4, ws, b->hh, size_t(B), r0, nr, ys, "v3 qkv/gate"));
-        }
-        // conv, norm + RoPE, int8 KV append
-        {
-            const nd_kv_geom &g = b->geom[li];
-            QkvKv qk{b->q, b->k, b->v, b->qt[li], b->kt[li], b->vt[li], l.q_taps, l.k_taps,
-                     l.v_taps, l.q_norm, l.k_norm, rope_dev, pos_dev, qd, kd, vd,
-                     c.qkv_conv_taps, c.num_heads, c.num_kv_heads, c.qk_head_dim, c.v_head_dim,
-                     b->kv[li], b->kv_stride[li], nd_kv_v_offset(&g), nd_kv_ks_offset(&g),
-                     nd_kv_vs_offset(&g), g.cap, C, b->qn};
+    // every kernel of the step, on `st` and the side stream joined back into
+    // it; with `argmax`, the greedy tokens into b->next
+    auto enqueue = [&](bool argmax) -> int {
+        int rc = ND_OK;
+        // ---- Engram for this position (model.rs:162-191) -------------------------
+        for (int s = 0; s < c.n_sites; ++s) {
+            const Site &site = m->sites[s];
+            CK(nd_cq_dequantize_rows(ctx, site.tables, rows_dev, size_t(B) * nt, b->fetched));
+            CK(nd_cq_prepare_input(ctx, site.key, b->fetched, B, b->fh));
+            {
+                const nd_cq *ws[2] = {site.key, site.value};
+                const size_t r0[2] = {0, 0};
+                const size_t nr[2] = {size_t(d), size_t(d)};
+                float *ys[2] = {b->ek + size_t(s) * Rcap * d, b->ev + size_t(s) * Rcap * d};
+                CK(nd_cq_exact_set(ctx, st, 2, ws, b->fh, size_t(B), r0, nr, ys, "v3 engram key/value"));
+            }
+            const int reach = (c.e_conv_taps - 1) * c.e_conv_dilation;
             if (C == 1) {
-                hipLaunchKernelGGL(k_qkv_kv<false>, dim3(B), dim3(kT), 0, st, qk);
-                LCHK("k_qkv_kv");
+                hipLaunchKernelGGL(k_engram_conv, dim3((d + 255) / 256, B), dim3(256), 0, st,
+                                   b->ev + size_t(s) * Rcap * d, site.taps, b->et[s], pos_dev,
+                                   c.e_conv_taps, c.e_conv_dilation, mo, reach, d);
+                LCHK("k_engram_conv");
             } else {
-                hipLaunchKernelGGL(k_qkv_kv<true>, dim3(B), dim3(kT), 0, st, qk);
-                LCHK("k_qkv_kv");
-                const int tt = c.qkv_conv_taps - 1;
-                if (tt > 0) {
-                    hipLaunchKernelGGL(k_tails, dim3((qd + 255) / 256, S), dim3(256), 0, st, b->q,
-                                       b->qt[li], tt, C, qd);
-                    hipLaunchKernelGGL(k_tails, dim3((kd + 255) / 256, S), dim3(256), 0, st, b->k,
-                                       b->kt[li], tt, C, kd);
-                    hipLaunchKernelGGL(k_tails, dim3((vd + 255) / 256, S), dim3(256), 0, st, b->v,
-                                       b->vt[li], tt, C, vd);
-                    LCHK("k_tails");
-                }
+                hipLaunchKernelGGL(k_engram_conv_rows, dim3((d + 255) / 256, B), dim3(256), 0, st,
+                                   b->ev + size_t(s) * Rcap * d, b->evc + size_t(s) * Rcap * d,
+                                   site.taps, b->et[s], pos_dev, c.e_conv_taps, c.e_conv_dilation, mo,
+                                   reach, d, C);
+                LCHK("k_engram_conv_rows");
+                hipLaunchKernelGGL(k_tails, dim3((d + 255) / 256, S), dim3(256), 0, st,
+                                   b->ev + size_t(s) * Rcap * d, b->et[s], reach, C, d);
+                LCHK("k_tails");
             }
         }
-        // attention over the int8 ring (query fake-quant fused)
-        CK(nd_attend_exact_rows(ctx, &b->geom[li], b->kv[li], b->kv_stride[li], size_t(B), C,
-                                lo_dev + size_t(li) * B, hi_dev, C == 1 ? b->q : b->qn, qk_scale,
-                                1, b->attn));
-        hipLaunchKernelGGL(k_gate_prep, dim3(B), dim3(kT), 0, st, b->attn, b->gate, b->ah, od,
-                           m->pre_attn);
-        LCHK("k_gate_prep");
-        CK(project(ctx, l.out, b->ah, B, 0, d, b->proj));
-        HadaArgs ha{b->proj, l.post_norm, l.pre_hada, nd_sigmoidf(l.attn_gate), b->u, b->bx, b->y,
-                    l.d1, l.d2, l.b2, l.d3, l.d4, l.w1a, l.w1b, l.w2a, l.w2b, l.w3a, l.w3b,
-                    l.cond_v, l.cond_u, m->p1, m->p2, d, l.cond_rank};
-        hipLaunchKernelGGL(k_post_hada, dim3(B), dim3(1024), 0, st, ha);
-        LCHK("k_post_hada");
+        float *const ev_conv = C == 1 ? b->ev : b->evc;  // [sites][Rcap][d], after the conv
+        // ---- lane stream (model.rs:194-203) --------------------------------------
+        CK(nd_cq_dequantize_rows(ctx, m->embedding, tok_dev, size_t(B), b->emb));
+        hipLaunchKernelGGL(k_embed, dim3((d + 255) / 256, B), dim3(256), 0, st, b->emb, b->lanes,
+                           m->embed_scale, nl, d);
+        LCHK("k_embed");
+
+        const float qk_scale = 1.0f / std::sqrt(float(c.qk_head_dim));
+        hipStream_t side = b->side;
+        const nd_cq *phi = m->phi_pre;
+        for (int li = 0; li < L; ++li) {
+            const Layer &l = m->layers[li];
+            const int site = site_of(c, li);
+            // previous layer's scatter up + this layer's mix down
+            if (li > 0) ND_HIP(hipStreamWaitEvent(st, b->ev_gates[(li - 1) & 1], 0));
+            LayerIn in{b->lanes, b->y, b->gp, b->gr, li > 0, b->nxh, m->pre_nx, phi->packed,
+                       phi->norms, phi->lv, phi->row_bytes, int(phi->num_groups), li * nl,
+                       int(phi->bits == 5), m->b_pre + size_t(li) * nl, m->a_pre[li], li, nl, d,
+                       site >= 0 ? b->ek + size_t(site) * Rcap * d : nullptr,
+                       site >= 0 ? ev_conv + size_t(site) * Rcap * d : nullptr, l.norm_in, b->u, b->bx,
+                       b->hh, m->pre_h};
+            if (phi->per_byte == 2)
+                hipLaunchKernelGGL(k_layer_in<2>, dim3(B), dim3(kT), 0, st, in);
+            else
+                hipLaunchKernelGGL(k_layer_in<4>, dim3(B), dim3(kT), 0, st, in);
+            LCHK("k_layer_in");
+            // side stream: this layer's scatter-up gates from the prepared lanes
+            ND_HIP(hipEventRecord(b->ev_in[li & 1], st));
+            ND_HIP(hipStreamWaitEvent(side, b->ev_in[li & 1], 0));
+            {
+                const nd_cq *ws[2] = {m->phi_post, m->phi_res};
+                const size_t r0[2] = {size_t(li) * nl, size_t(li) * nl * nl};
+                const size_t nr[2] = {size_t(nl), size_t(nl) * nl};
+                float *ys[2] = {b->hpost, b->hres};
+                CK(nd_cq_exact_set(ctx, side, 2, ws, b->nxh, size_t(B), r0, nr, ys, "v3 phi post/res"));
+            }
+            MhcGates mg{b->hpost, b->hres, m->b_post + size_t(li) * nl, m->b_res + size_t(li) * nl * nl,
+                        m->a_post[li], m->a_res[li], li, nl, b->gp, b->gr};
+            hipLaunchKernelGGL(k_mhc_gates, dim3(B), dim3(64), 0, side, mg);
+            LCHK("k_mhc_gates");
+            ND_HIP(hipEventRecord(b->ev_gates[li & 1], side));
+            // q, k, v and gate projections of the prepared h, one launch
+            {
+                const nd_cq *ws[4] = {l.q, l.k, l.v, l.gate};
+                const size_t r0[4] = {0, 0, 0, 0};
+                const size_t nr[4] = {size_t(qd), size_t(kd), size_t(vd), size_t(od)};
+                float *ys[4] = {b->q, b->k, b->v, b->gate};
+                CK(nd_cq_exact_set(ctx, st, 4, ws, b->hh, size_t(B), r0, nr, ys, "v3 qkv/gate"));
+            }
+            // conv, norm + RoPE, int8 KV append
+            {
+                const nd_kv_geom &g = b->geom[li];
+                QkvKv qk{b->q, b->k, b->v, b->qt[li], b->kt[li], b->vt[li], l.q_taps, l.k_taps,
+                         l.v_taps, l.q_norm, l.k_norm, rope_dev, pos_dev, qd, kd, vd,
+                         c.qkv_conv_taps, c.num_heads, c.num_kv_heads, c.qk_head_dim, c.v_head_dim,
+                         b->kv[li], b->kv_stride[li], nd_kv_v_offset(&g), nd_kv_ks_offset(&g),
+                         nd_kv_vs_offset(&g), g.cap, C, b->qn};
+                if (C == 1) {
+                    hipLaunchKernelGGL(k_qkv_kv<false>, dim3(B), dim3(kT), 0, st, qk);
+                    LCHK("k_qkv_kv");
+                } else {
+                    hipLaunchKernelGGL(k_qkv_kv<true>, dim3(B), dim3(kT), 0, st, qk);
+                    LCHK("k_qkv_kv");
+                    const int tt = c.qkv_conv_taps - 1;
+                    if (tt > 0) {
+                        hipLaunchKernelGGL(k_tails, dim3((qd + 255) / 256, S), dim3(256), 0, st, b->q,
+                                           b->qt[li], tt, C, qd);
+                        hipLaunchKernelGGL(k_tails, dim3((kd + 255) / 256, S), dim3(256), 0, st, b->k,
+                                           b->kt[li], tt, C, kd);
+                        hipLaunchKernelGGL(k_tails, dim3((vd + 255) / 256, S), dim3(256), 0, st, b->v,
+                                           b->vt[li], tt, C, vd);
+                        LCHK("k_tails");
+                    }
+                }
+            }
+            // attention over the int8 ring (query fake-quant fused)
+            CK(nd_attend_exact_rows(ctx, &b->geom[li], b->kv[li], b->kv_stride[li], size_t(B), C,
+                                    lo_dev + size_t(li) * B, hi_dev, C == 1 ? b->q : b->qn, qk_scale,
+                                    1, b->attn));
+            hipLaunchKernelGGL(k_gate_prep, dim3(B), dim3(kT), 0, st, b->attn, b->gate, b->ah, od,
+                               m->pre_attn);
+            LCHK("k_gate_prep");
+            CK(project(ctx, l.out, b->ah, B, 0, d, b->proj));
+            HadaArgs ha{b->proj, l.post_norm, l.pre_hada, nd_sigmoidf(l.attn_gate), b->u, b->bx, b->y,
+                        l.d1, l.d2, l.b2, l.d3, l.d4, l.w1a, l.w1b, l.w2a, l.w2b, l.w3a, l.w3b,
+                        l.cond_v, l.cond_u, m->p1, m->p2, d, l.cond_rank};
+            hipLaunchKernelGGL(k_post_hada, dim3(B), dim3(1024), 0, st, ha);
+            LCHK("k_post_hada");
+        }
+        // ---- head ---------------------------------------------------------------
+        ND_HIP(hipStreamWaitEvent(st, b->ev_gates[(L - 1) & 1], 0));
+        hipLaunchKernelGGL(k_final, dim3(S), dim3(kT), 0, st, b->lanes, b->y, b->gp, b->gr,
+                           m->final_norm, b->xh, nl, d, m->pre_x, C);
+        LCHK("k_final");
+        CK(project(ctx, m->embedding, b->xh, S, 0, rows, b->logits));
+        if (argmax) {
+            hipLaunchKernelGGL(k_argmax, dim3(S), dim3(kT), 0, st, b->logits, int(rows), b->next);
+            LCHK("k_argmax");
+        }
+        return ND_OK;
+    };
+    // One position per session, graphs on: replay the captured step on the
+    // batch's own stream (a capture needs a stream of its own: the caller's
+    // may be the null stream), fenced to the caller's stream by events.  The
+    // capture is taken on the second such step; if it cannot be taken, the
+    // batch runs eagerly from then on.
+    const bool graph = C == 1 && b->graphs;
+    const bool argmax = next != nullptr || graph;
+    const hipStream_t user = st;
+    bool replayed = false;
+    if (graph && (b->graph_exec || b->eager_steps > 0)) {
+        if (!b->gstream) {
+            ND_HIP(hipStreamCreateWithFlags(&b->gstream, hipStreamNonBlocking));
+            ND_HIP(hipEventCreateWithFlags(&b->g_in, hipEventDisableTiming));
+            ND_HIP(hipEventCreateWithFlags(&b->g_out, hipEventDisableTiming));
+        }
+        ND_HIP(hipEventRecord(b->g_in, user));
+        ND_HIP(hipStreamWaitEvent(b->gstream, b->g_in, 0));
+        if (!b->graph_exec) {
+            st = b->gstream;
+            ctx->stream = b->gstream;
+            const hipError_t be = hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed);
+            const int crc = be == hipSuccess ? enqueue(true) : ND_ERR_HIP;
+            hipGraph_t g = nullptr;
+            const hipError_t ce = be == hipSuccess ? hipStreamEndCapture(st, &g) : be;
+            ctx->stream = user;
+            st = user;
+            hipGraphExec_t ex = nullptr;
+            const bool ok = crc == ND_OK && ce == hipSuccess && g &&
+                            hipGraphInstantiate(&ex, g, nullptr, nullptr, 0) == hipSuccess;
+            if (g) (void)hipGraphDestroy(g);
+            if (ok) {
+                b->graph_exec = ex;
+            } else {
+                // nothing was enqueued: this step and every later one run eagerly
+                b->graphs = false;
+                (void)hipGetLastError();
+                nd::clear_error();
+            }
+        }
+        if (b->graph_exec) {
+            ND_HIP(hipGraphLaunch(b->graph_exec, b->gstream));
+            ND_HIP(hipEventRecord(b->g_out, b->gstream));
+            ND_HIP(hipStreamWaitEvent(user, b->g_out, 0));
+            replayed = true;
+        }
     }
-    // ---- head ---------------------------------------------------------------
-    ND_HIP(hipStreamWaitEvent(st, b->ev_gates[(L - 1) & 1], 0));
-    hipLaunchKernelGGL(k_final, dim3(S), dim3(kT), 0, st, b->lanes, b->y, b->gp, b->gr,
-                       m->final_norm, b->xh, nl, d, m->pre_x, C);
-    LCHK("k_final");
-    CK(project(ctx, m->embedding, b->xh, S, 0, rows, b->logits));
+    if (!replayed) {
+        if (int rc = enqueue(argmax)) return rc;
+        if (C == 1) ++b->eager_steps;
+    }
     if (logits)
         ND_HIP(hipMemcpyAsync(logits, b->logits, size_t(S) * rows * 4, hipMemcpyDeviceToDevice, st));
     if (next) {
-        hipLaunchKernelGGL(k_argmax, dim3(S), dim3(kT), 0, st, b->logits, int(rows), b->next);
-        LCHK("k_argmax");
         ND_HIP(hipMemcpyAsync(b->next_host, b->next, size_t(S) * 4, hipMemcpyDeviceToHost, st));
         ND_HIP(hipStreamSynchronize(st));
         std::memcpy(next, b->next_host, size_t(S) * 4);

@@ -89,6 +89,7 @@ _SIGS = [
     ("nd_v3_prefill", C.c_int, [_vp, _vp, _vp, _vp, _sz, _vp, _vp]),
     ("nd_v3_cact_config", C.c_int, [_vp, _sz, _vp, C.POINTER(_sz)]),
     ("nd_v3_model_from_cact", C.c_int, [_vp, _vp, _sz, C.POINTER(_vp)]),
+    ("nd_v3_batch_set_graphs", C.c_int, [_vp, C.c_int]),
     ("nd_v3_kv_bytes", _sz, [_vp, _sz, C.c_int]),
     ("nd_v3_ladder", C.c_int, [_sz, _sz, C.POINTER(C.c_int32)]),
     ("nd_v3_cact_config_at_depth", C.c_int, [_vp, _sz, _sz, _vp, C.POINTER(C.c_int32)]),
@@ -574,6 +575,11 @@ class V3Batch:
         out = np.zeros(self.sessions, np.int32)
         _check(lib().nd_v3_positions(self.h, out.ctypes.data_as(C.c_void_p)))
         return out
+
+    def set_graphs(self, on):
+        """Single-position steps as one replayed HIP graph, or kernel by
+        kernel (the default, faster on ROCm 7.2); the results are identical."""
+        _check(lib().nd_v3_batch_set_graphs(self.h, int(bool(on))))
 
     def step(self, tokens, logits=None, want_next=True):
         """Feed tokens[i] to session i (V3Model::decode_step); returns the greedy
