@@ -36,6 +36,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "needle-rs_amd"))
 
 HBM_PEAK_GBS = 8000.0
+FP32_MFMA_TFLOPS = 157.3
 GEMV_OUT, GEMV_IN = 3072, 768
 GEMV_BYTES = GEMV_OUT * GEMV_IN + (GEMV_OUT // 64) * 256 * 4 + GEMV_IN * 4 + GEMV_OUT * 4
 GEMV_COPIES = 448
@@ -250,6 +251,21 @@ def format_a_runs(torch, nd, steps):
             for tag, exact in (("tolerance_us", False), ("exact_us", True))}
         w.close()
     out["single_call_latency"] = lat
+    # prefill GEMM (matmul_rows_prepared, fp32 MFMA): 512 prepared rows
+    # against the q projection's shape (2-bit) and the LM head's (4-bit)
+    gemm = {}
+    for name, rows, bits in (("q576x768_2bit", 576, 2), ("lm_head8192x768_4bit", 8192, 4)):
+        blob, row_bytes, ng = _cq_blob(rng, rows, inn, bits)
+        w = nd.CqWeight(ctx, blob, rows, inn, 128, bits, S.CODEBOOK)
+        M = 512
+        xh = torch.randn(M, inn, device="cuda")
+        y = torch.empty(M * rows, device="cuda")
+        ms = timed_loop(torch, lambda: w.matmul_rows_prepared(xh, M, 0, rows, y), max(20, steps), 5)
+        tf = 2.0 * M * rows * inn / (ms * 1e-3) / 1e12
+        gemm[name + "_m512"] = {"us": round(ms * 1e3, 2), "TFLOPs": round(tf, 2),
+                                "frac_fp32_mfma_peak": round(tf / FP32_MFMA_TFLOPS, 4)}
+        w.close()
+    out["prefill_gemm_fp32_mfma"] = gemm
     ctx.close()
     return out
 

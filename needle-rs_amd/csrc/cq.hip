@@ -430,6 +430,127 @@ __global__ __launch_bounds__(256) void cq_matmul_kernel(
             }
 }
 
+// The same product for the byte-aligned widths (4-bit, 2-bit, ternary), the
+// prefill path: block tile BM (batch) x 64 (rows), K steps of 32.  X is staged
+// with float4 loads; codes 8 at a time (one 16- or 32-bit load), decoded
+// through the weight's byte LUT and scaled by the group norm; the next step's
+// loads are in flight while the current step's MFMAs run.  Waves 2x2 (BM 64:
+// 32x32 each; BM 32: 16x32) or 1x4 (BM 16: 16x16).
+template <int P, int BM>
+__global__ __launch_bounds__(256) void cq_matmul_b_kernel(
+    const uint8_t *__restrict__ packed, const float *__restrict__ norms,
+    const float *__restrict__ lut_g, const float *__restrict__ xh, float *__restrict__ y,
+    int batch, int row_start, int rows, int row_bytes, int num_groups, int group, int in_padded)
+{
+    constexpr int BN = 64, BK = 32, LD = BK + 4;
+    constexpr int WGM = BM >= 32 ? 2 : 1, WGN = 4 / WGM;
+    constexpr int WM = BM / WGM, WN = BN / WGN;
+    constexpr int TA = WM / 16, TB = WN / 16;
+    constexpr int NA = (BM * BK / 4 + 255) / 256;  // float4s of X per thread per step
+    __shared__ __align__(16) float lut[256 * P];
+    __shared__ __align__(16) float As[BM][LD];
+    __shared__ __align__(16) float Bs[BN][LD];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+    const int wm = (wave % WGM) * WM, wn = (wave / WGM) * WN;
+    for (int i = t; i < 256 * P; i += 256) lut[i] = lut_g[i];
+
+    floatx4_t acc[TA][TB];
+#pragma unroll
+    for (int a = 0; a < TA; ++a)
+#pragma unroll
+        for (int b = 0; b < TB; ++b) acc[a][b] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // staging: X float4 idx = t + 256 j -> row idx / 8, cols 4 * (idx % 8);
+    // codes: row t / 4, run of 8 codes (t % 4) * 8
+    const int br = t >> 2, bk = (t & 3) * 8;
+    const bool brow = n0 + br < rows;
+    const uint8_t *crow = packed + size_t(row_start + (brow ? n0 + br : 0)) * row_bytes;
+    const float *nrow = norms + size_t(row_start + (brow ? n0 + br : 0)) * num_groups;
+    float4 xa[NA];
+    uint32_t code = 0;
+    float nrm = 0.0f;
+    auto load = [&](int k0) {
+#pragma unroll
+        for (int j = 0; j < NA; ++j) {
+            const int idx = t + 256 * j, r = idx >> 3, c = (idx & 7) * 4;
+            const bool on = idx < BM * BK / 4 && m0 + r < batch && k0 + c < in_padded;
+            xa[j] = on ? *reinterpret_cast<const float4 *>(xh + size_t(m0 + r) * in_padded + k0 + c)
+                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+        const int k = k0 + bk;
+        const bool on = brow && k < in_padded;
+        if (P == 4)
+            code = on ? uint32_t(*reinterpret_cast<const uint16_t *>(crow + k / 4)) : 0u;
+        else
+            code = on ? *reinterpret_cast<const uint32_t *>(crow + k / 2) : 0u;
+        nrm = on ? nrow[k / group] : 0.0f;
+    };
+    auto store = [&]() {
+#pragma unroll
+        for (int j = 0; j < NA; ++j) {
+            const int idx = t + 256 * j;
+            if (idx < BM * BK / 4)
+                *reinterpret_cast<float4 *>(&As[idx >> 3][(idx & 7) * 4]) = xa[j];
+        }
+        float v[8];
+        if (P == 4) {
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const float4 l4 = *reinterpret_cast<const float4 *>(lut + ((code >> (8 * q)) & 0xffu) * 4);
+                v[4 * q] = l4.x;
+                v[4 * q + 1] = l4.y;
+                v[4 * q + 2] = l4.z;
+                v[4 * q + 3] = l4.w;
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float2 l2 = *reinterpret_cast<const float2 *>(lut + ((code >> (8 * q)) & 0xffu) * 2);
+                v[2 * q] = l2.x;
+                v[2 * q + 1] = l2.y;
+            }
+        }
+        *reinterpret_cast<float4 *>(&Bs[br][bk]) = make_float4(v[0] * nrm, v[1] * nrm, v[2] * nrm, v[3] * nrm);
+        *reinterpret_cast<float4 *>(&Bs[br][bk + 4]) = make_float4(v[4] * nrm, v[5] * nrm, v[6] * nrm, v[7] * nrm);
+    };
+    __syncthreads();  // the LUT
+    load(0);
+    // MFMA 16x16x4 f32: lane l supplies A[l%16][k + l/16], B[k + l/16][l%16]
+    const int r16 = lane & 15, kq = lane >> 4;
+    for (int k0 = 0; k0 < in_padded; k0 += BK) {
+        store();
+        __syncthreads();
+        if (k0 + BK < in_padded) load(k0 + BK);
+#pragma unroll
+        for (int kk = 0; kk < BK; kk += 4) {
+            float af[TA], bf[TB];
+#pragma unroll
+            for (int a = 0; a < TA; ++a) af[a] = As[wm + a * 16 + r16][kk + kq];
+#pragma unroll
+            for (int b = 0; b < TB; ++b) bf[b] = Bs[wn + b * 16 + r16][kk + kq];
+#pragma unroll
+            for (int a = 0; a < TA; ++a)
+#pragma unroll
+                for (int b = 0; b < TB; ++b)
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[a], bf[b], acc[a][b], 0, 0, 0);
+        }
+        __syncthreads();
+    }
+    // C layout: lane l holds C[4*(l/16) + i][l%16]
+    const int col = lane & 15, rb = (lane >> 4) * 4;
+#pragma unroll
+    for (int a = 0; a < TA; ++a)
+#pragma unroll
+        for (int b = 0; b < TB; ++b)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = m0 + wm + a * 16 + rb + i;
+                const int n = n0 + wn + b * 16 + col;
+                if (m < batch && n < rows) y[size_t(m) * rows + n] = acc[a][b][i];
+            }
+}
+
 // ---------------------------------------------------------------------------
 // dequantize rows: one block per (group, requested row).
 // ---------------------------------------------------------------------------
@@ -718,6 +839,26 @@ int nd_cq_matmul_rows_prepared(nd_ctx *ctx, const nd_cq *w, const float *xh, siz
     if (rows == 0 || batch == 0) return ND_OK;
     ND_REQUIRE(xh && y, "null buffer");
     ND_REQUIRE(batch <= (size_t(1) << 22), "batch too large");
+    const bool bytes = (w->per_byte == 2 || w->per_byte == 4) && w->lut && w->in_padded % 8 == 0 &&
+                       (reinterpret_cast<uintptr_t>(xh) & 15) == 0;
+    if (bytes) {
+        // the tallest batch tile that still gives every CU a block
+        const size_t cus = size_t(ctx->num_cus > 0 ? ctx->num_cus : 256);
+        const size_t nt = (rows + 63) / 64;
+        const int bm = nt * ((batch + 63) / 64) >= cus ? 64 : nt * ((batch + 31) / 32) >= cus ? 32 : 16;
+        dim3 g2(unsigned(nt), unsigned((batch + bm - 1) / bm));
+#define ND_MMB(PP, BMM)                                                                                \
+    hipLaunchKernelGGL((cq_matmul_b_kernel<PP, BMM>), g2, dim3(256), 0, ctx->stream, w->packed, w->norms, \
+                       w->lut, xh, y, int(batch), int(row_start), int(rows), int(w->row_bytes),          \
+                       int(w->num_groups), int(w->group), int(w->in_padded))
+        if (w->per_byte == 4) {
+            if (bm == 64) ND_MMB(4, 64); else if (bm == 32) ND_MMB(4, 32); else ND_MMB(4, 16);
+        } else {
+            if (bm == 64) ND_MMB(2, 64); else if (bm == 32) ND_MMB(2, 32); else ND_MMB(2, 16);
+        }
+#undef ND_MMB
+        return nd::check_launch("cq_matmul");
+    }
     dim3 grid(unsigned((rows + kMN - 1) / kMN), unsigned((batch + kMM - 1) / kMM));
     hipLaunchKernelGGL(cq_matmul_kernel, grid, dim3(256), 0, ctx->stream, w->packed, w->norms, w->lv,
                        xh, y, int(batch), int(row_start), int(rows), int(w->row_bytes),
