@@ -190,6 +190,22 @@ def gemm_runs(torch, nd, ctx, gen, steps):
                                   "frac_bf16_mfma_dense_peak": round(tf / BF16_MFMA_PEAK_TFLOPS, 4),
                                   "flops_per_gemm": 2 * M * N * K}
         del X, W, CB, Y
+    # M = 64 (64 sessions' rows at once): each code feeds 64 rows, so the
+    # launch is bound by streaming the codes; 448 weights of 3072 x 768
+    # (1.06 GB) are read from HBM per launch
+    M, N, R = 64, 3072, 448
+    X = torch.randn(R, M, K, device="cuda", generator=gen)
+    W = torch.randint(0, 256, (R, N, K), dtype=torch.uint8, device="cuda", generator=gen)
+    CB = torch.randn(R, N // 64, 256, device="cuda", generator=gen) * 0.02
+    Y = torch.empty(R, M, N, device="cuda")
+    ms = timed_loop(torch, lambda: nd.cb8_gemm_batched(ctx, X, W, CB, Y), steps, 10)
+    nbytes = R * (N * K + N // 64 * 256 * 4 + M * K * 4 + M * N * 4)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    tf = 2.0 * M * N * K * R / (ms * 1e-3) / 1e12
+    out[f"m{M}_n{N}_k{K}"] = {"problems_per_launch": R, "us_per_launch": round(ms * 1e3, 2),
+                              "bytes_per_launch": nbytes, "GBps": round(gbs, 1),
+                              "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "TFLOPs": round(tf, 2)}
+    del X, W, CB, Y
     return out
 
 
