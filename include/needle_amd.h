@@ -146,6 +146,14 @@ int nd_cq_matmul_rows_exact(nd_ctx *ctx, const nd_cq *w, const float *xh,
                             size_t batch, size_t row_start, size_t rows,
                             float *y);
 
+/* y[r] = ((0 + x[r][0]) + x[r][1]) + ... + x[r][n-1] in fp32, each add
+ * rounded as the reference's sequential f32 sums round: the sums of squares
+ * of rms_unit and ZCRMSNorm (kernels.rs:22-24, norm.rs:25) and the softmax
+ * sum of attend_step (v3/attention.rs:361-365).  x is [rows][n], 1 <= n <=
+ * 4096.  Rows whose terms are all >= +0 and finite take an exact parallel
+ * method with the same bits; other rows are summed as the plain chain. */
+int nd_fold_rows(nd_ctx *ctx, const float *x, size_t rows, size_t n, float *y);
+
 /* out[i] = dequantized row rows[i] (in_feat floats each); rows is a device
  * int32 array of n row indices, a negative index giving a row of zeros (a
  * masked Engram fetch, v3/model.rs:172-183).  Replaces

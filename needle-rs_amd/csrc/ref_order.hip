@@ -28,6 +28,7 @@
 //                  softmax sum as one chain, and each output column as one
 //                  chain over the span.
 #include "nd_cq_internal.h"
+#include "nd_fold.h"
 #include "nd_internal.h"
 #include "nd_kv_internal.h"
 #include "nd_libm.h"
@@ -803,9 +804,43 @@ __global__ __launch_bounds__(kAttn2Threads, 4) void attn_exact2_kernel(
     if (tid < g.VD) out[(size_t(i) * g.H + h) * g.VD + tid] = acc;
 }
 
+
+// ---------------------------------------------------------------------------
+// Row sums in the reference's order: ((0 + x[0]) + x[1]) + ... per row, one
+// workgroup a row, the row staged in LDS.  Rows of terms >= +0 (sums of
+// squares, softmax sums) take the exact parallel fold of nd_fold.h; any
+// other row the plain chain, which the fold itself falls back to.
+// ---------------------------------------------------------------------------
+constexpr int kFoldRowMax = 4096;
+constexpr int kFoldThreads = 256;
+
+__global__ __launch_bounds__(kFoldThreads) void fold_rows_kernel(const float *__restrict__ x, int n,
+                                                                  float *__restrict__ y)
+{
+    __shared__ __align__(16) float buf[kFoldRowMax];
+    __shared__ NdFoldLds<kFoldThreads> fl;
+    const float *row = x + size_t(blockIdx.x) * n;
+    for (int i = threadIdx.x; i < n; i += kFoldThreads) buf[i] = row[i];
+    __syncthreads();
+    const float f = nd_fold_nonneg<kFoldThreads, kFoldRowMax / kFoldThreads>(buf, n, fl);
+    if (threadIdx.x == 0) y[blockIdx.x] = f;
+}
+
 }  // namespace
 
 extern "C" {
+
+int nd_fold_rows(nd_ctx *ctx, const float *x, size_t rows, size_t n, float *y)
+{
+    if (int rc = nd::enter(ctx)) return rc;
+    ND_REQUIRE(n >= 1 && n <= size_t(kFoldRowMax), "fold_rows: n %zu outside 1..%d", n, kFoldRowMax);
+    if (rows == 0) return ND_OK;
+    ND_REQUIRE(x && y, "fold_rows: null buffer");
+    ND_REQUIRE(rows <= 0x7fffffffu, "fold_rows: %zu rows", rows);
+    hipLaunchKernelGGL(fold_rows_kernel, dim3(unsigned(rows)), dim3(kFoldThreads), 0, ctx->stream, x,
+                       int(n), y);
+    return nd::check_launch("fold_rows");
+}
 
 int nd_cq_matvec_rows_exact(nd_ctx *ctx, const nd_cq *w, const float *xh, size_t row_start,
                             size_t rows, float *y)

@@ -26,6 +26,7 @@
 // lane sums) is one sequential chain on one thread, in the reference's
 // index order; exp and log are libm's algorithms (nd_libm.h).
 #include "nd_cq_internal.h"
+#include "nd_fold.h"
 #include "nd_internal.h"
 #include "nd_kv_internal.h"
 #include "nd_libm.h"
@@ -214,6 +215,7 @@ __global__ void k_engram_conv_rows(const float *__restrict__ raw, float *__restr
 // rows, the gated lane sum, the Engram gate and ZCRMSNorm, prepared for the
 // q/k/v/gate projections.  One workgroup per session.
 constexpr int kMaxLanesD = 4096;  // mhc_lanes * d_model
+constexpr int kFoldC = 12;        // terms a thread of the parallel rms fold (4 lanes x 768)
 constexpr int kMaxPhiPairs = 512; // mhc_lanes * (phi input groups)
 constexpr int kPadGroup = 132;    // a 128-group's stride in LDS, padded
 
@@ -245,6 +247,7 @@ __global__ __launch_bounds__(kT) void k_layer_in(LayerIn a)
     __shared__ __align__(16) float ln[kMaxLanesD], nb[kMaxLanesD];
     __shared__ __align__(16) float us[1024], bxs[1024], pa[1024], pb[1024], pc[1024];
     __shared__ float gs[kMaxPhiPairs], pn[kMaxPhiPairs], lvl[16], hp[16], gpp[16], grr[256], tot[4];
+    __shared__ NdFoldLds<kT> fl;
     const size_t b = blockIdx.x;
     const int tid = threadIdx.x, n = a.n, d = a.d, nd = n * d;
     const int G = a.phi_G, pairs = n * G;
@@ -318,7 +321,14 @@ __global__ __launch_bounds__(kT) void k_layer_in(LayerIn a)
     }
     const float bpre = tid < n ? a.b_pre[tid] : 0.0f;
     const float lvv = tid < 16 ? a.phi_lv[a.phi_ternary ? (tid == 3 ? 0 : (tid == 1 ? 2 : 1)) : tid] : 0.0f;
-    if (tid == 0) tot[0] = chain_sum(nb, nd);
+    // the rms sum of squares: the workgroup folds it in parallel with the
+    // chain's bits (nd_fold.h) when it fits kFoldC terms a thread
+    if (nd >= kNdFoldMinN && nd <= kT * kFoldC) {
+        const float f = nd_fold_nonneg<kT, kFoldC>(nb, nd, fl);
+        if (tid == 0) tot[0] = f;
+    } else if (tid == 0) {
+        tot[0] = chain_sum(nb, nd);
+    }
     if (has_pair) pn[tid] = pnv;
     if (tid < 16) lvl[tid] = lvv;
     __syncthreads();

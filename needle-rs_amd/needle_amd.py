@@ -67,6 +67,7 @@ _SIGS = [
     ("nd_cq_matvec_rows_exact", C.c_int, [_vp, _vp, _vp, _sz, _sz, _vp]),
     ("nd_cq_matmul_rows_exact", C.c_int, [_vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     ("nd_cq_dequantize_rows", C.c_int, [_vp, _vp, _vp, _sz, _vp]),
+    ("nd_fold_rows", C.c_int, [_vp, _vp, _sz, _sz, _vp]),
     ("nd_fake_quant", C.c_int, [_vp, _vp, _sz, _sz]),
     ("nd_quantize_rows", C.c_int, [_vp, _vp, _sz, _sz, _vp, _vp]),
     ("nd_kv_block_bytes", _sz, [C.POINTER(KvGeom)]),
@@ -271,6 +272,17 @@ class CqWeight:
 
 
 # ---- int8 KV ----------------------------------------------------------------
+
+def fold_rows(ctx, x, y=None):
+    """y[r] = the sequential fp32 sum of row r of x ([rows][n], n <= 4096),
+    in the reference's order (kernels.rs:22-24, v3/attention.rs:361-365)."""
+    torch = _torch()
+    rows, n = x.shape
+    if y is None:
+        y = torch.empty(rows, dtype=torch.float32, device=x.device)
+    _check(lib().nd_fold_rows(ctx.h, _ptr(x), rows, n, _ptr(y)))
+    return y
+
 
 def fake_quant(ctx, x, dim):
     """fake_quant_vec(x[r], 8) for every row of `dim`, in place."""
