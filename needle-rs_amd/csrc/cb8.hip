@@ -671,6 +671,165 @@ __global__ __launch_bounds__(512) void cb8_gemm256_kernel(const unsigned short *
             }
 }
 
+// M <= 64 (e.g. the rows of 64 sessions at once): each code feeds only 64
+// rows, so the launch streams codes and the decode, not the MFMAs, sets the
+// pace.  A 256-thread block owns 128 output columns (two codebook groups)
+// and all M rows; the codes skip LDS entirely.  Lane (r16, q) of wave w
+// loads 16 consecutive codes of rows n0 + 32w + 16t + r16 (t = 0, 1) per
+// 64-wide K step -- four lanes cover a row's 64 bytes in one load -- and
+// decodes them through a lane-replicated codebook table (entry e, replica r
+// in bank r: conflict-free gathers; both groups' bf16 in one word) straight
+// into MFMA B fragments.  X is staged in LDS 128 columns at a time, double
+// buffered.  Both operands use physical k 16q..16q+7 for the first MFMA of
+// a step and 16q+8..+15 for the second, so the K order differs from the
+// other tile shapes' (results agree to fp32 rounding, not bit for bit).
+constexpr int kRN = 128;          // output columns (N) per block: two codebook groups
+constexpr int kRC = 128;          // K per staged X chunk
+constexpr int kRXS = kRC + 8;     // padded X row in LDS (bf16)
+
+__global__ __launch_bounds__(256, 2) void cb8_gemm_m64_kernel(const unsigned short *__restrict__ Xb,
+                                                              const uint8_t *__restrict__ W,
+                                                              const float *__restrict__ cb,
+                                                              float *__restrict__ Y, int M, int N,
+                                                              int K, size_t ws, size_t cs, size_t ys,
+                                                              int tiles_n, int xcd_run)
+{
+    __shared__ __align__(16) uint32_t tab[256 * 32];
+    __shared__ __align__(16) unsigned short xs[2][64 * kRXS];
+    // the column tiles of one problem are consecutive in u and land on one
+    // XCD (workgroups are dealt to the 8 XCDs round-robin), sharing X in L2
+    const int id = blockIdx.x;
+    const int u = xcd_run ? (id % 8) * xcd_run + id / 8 : id;
+    const int z = u / tiles_n, tn = u - z * tiles_n;
+    Xb += size_t(z) * M * K;
+    W += z * ws;
+    cb += z * cs;
+    Y += z * ys;
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int r16 = lane & 15, q = lane >> 4;
+    const int n0 = tn * kRN;
+    const uint8_t *wp0 = W + size_t(n0 + 32 * w + r16) * K + 16 * q;
+    const uint8_t *wp1 = wp0 + size_t(16) * K;
+    const int nc = K / kRC;
+    // codes of chunk c: two 64-wide steps x two row groups.  Past the last
+    // chunk the load reads X instead (L2-resident, unused), so every chunk
+    // issues the same loads and the waits count them exactly.
+    uint4 cw[2][2][2];
+    auto cload = [&](int slot, int c) {
+        const bool in = c < nc;
+        const uint8_t *p0 = in ? wp0 + c * kRC : reinterpret_cast<const uint8_t *>(Xb);
+        const uint8_t *p1 = in ? wp1 + c * kRC : reinterpret_cast<const uint8_t *>(Xb);
+#pragma unroll
+        for (int kp = 0; kp < 2; ++kp) {
+            const u32x4_t c0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p0 + kp * 64));
+            const u32x4_t c1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p1 + kp * 64));
+            cw[slot][kp][0] = make_uint4(c0.x, c0.y, c0.z, c0.w);
+            cw[slot][kp][1] = make_uint4(c1.x, c1.y, c1.z, c1.w);
+        }
+    };
+    // X chunk c: 64 rows x 128 bf16, 16-byte pieces; rows past M are zero
+    uint4 xr[4];
+    auto xload = [&](int c) {
+        const int cc = c < nc ? c : nc - 1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int idx = t + 256 * i, row = idx >> 4, col = (idx & 15) * 8;
+            xr[i] = *reinterpret_cast<const uint4 *>(Xb + size_t(row < M ? row : M - 1) * K + cc * kRC + col);
+            if (row >= M) xr[i] = make_uint4(0, 0, 0, 0);
+        }
+    };
+    auto xstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int idx = t + 256 * i, row = idx >> 4, col = (idx & 15) * 8;
+            *reinterpret_cast<uint4 *>(&xs[buf][row * kRXS + col]) = xr[i];
+        }
+    };
+    cload(0, 0);
+    xload(0);
+    {
+        // the table, through a staging row in xs[1] so every write is
+        // conflict-free: word e of the staging row, then 8 x 16 bytes a thread
+        uint32_t *vals = reinterpret_cast<uint32_t *>(&xs[1][0]);
+        vals[t] = f32_to_bf16_rne(cb[size_t(n0 / 64) * 256 + t]) |
+                  (uint32_t(f32_to_bf16_rne(cb[size_t(n0 / 64 + 1) * 256 + t])) << 16);
+        __syncthreads();
+        uint4 *t4 = reinterpret_cast<uint4 *>(tab);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t v = vals[(i * 256 + t) >> 3];
+            t4[i * 256 + t] = make_uint4(v, v, v, v);
+        }
+    }
+    xstore(0);
+    __syncthreads();
+    // waves 0-1 hold rows of the first group (low halves), 2-3 the second
+    const uint32_t sel = w >= 2 ? 0x07060302u : 0x05040100u;
+    const uint32_t *tl = tab + (lane & 31);
+    floatx4_t acc[4][2];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) acc[a][b] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    auto decode = [&](const uint4 &c, bf16x8_t &f0, bf16x8_t &f1) {
+        const uint32_t d[4] = {c.x, c.y, c.z, c.w};
+        uint32_t h[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t v0 = tl[((d[k >> 1] >> (16 * (k & 1))) & 0xffu) * 32];
+            const uint32_t v1 = tl[((d[k >> 1] >> (16 * (k & 1) + 8)) & 0xffu) * 32];
+            h[k] = __builtin_amdgcn_perm(v1, v0, sel);
+        }
+        f0 = __builtin_bit_cast(bf16x8_t, make_uint4(h[0], h[1], h[2], h[3]));
+        f1 = __builtin_bit_cast(bf16x8_t, make_uint4(h[4], h[5], h[6], h[7]));
+    };
+    auto compute = [&](int buf, int slot) {
+#pragma unroll
+        for (int kp = 0; kp < 2; ++kp) {
+            bf16x8_t b[2][2];
+            decode(cw[slot][kp][0], b[0][0], b[0][1]);
+            decode(cw[slot][kp][1], b[1][0], b[1][1]);
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                const unsigned short *xa = &xs[buf][(16 * mt + r16) * kRXS + kp * 64 + 16 * q];
+                const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t *>(xa);
+                const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t *>(xa + 8);
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) {
+                    acc[mt][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b[tt][0], acc[mt][tt], 0, 0, 0);
+                    acc[mt][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b[tt][1], acc[mt][tt], 0, 0, 0);
+                }
+            }
+        }
+    };
+    // chunk c: X of chunk c + 1 and the codes of chunk c + 1 in flight while
+    // chunk c is multiplied.  The barrier only hands over LDS, so it waits
+    // for the LDS writes and leaves the code loads in flight.
+    for (int c0 = 0; c0 < nc; c0 += 2) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const int c = c0 + s;
+            if (c < nc) {
+                xload(c + 1);
+                __builtin_amdgcn_sched_barrier(0);
+                cload(s ^ 1, c + 1);
+                compute(c & 1, s);
+                if (c + 1 < nc) xstore((c + 1) & 1);
+                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            }
+        }
+    }
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = 16 * mt + 4 * q + i;
+                if (m < M) Y[size_t(m) * N + n0 + 32 * w + 16 * tt + r16] = acc[mt][tt][i];
+            }
+}
+
 constexpr int kRep = 32;
 
 int launch_gemv(nd_ctx *ctx, size_t count, const uint8_t *w, size_t w_stride, const float *cb,
@@ -755,7 +914,15 @@ int nd_cb8_gemm_batched(nd_ctx *ctx, size_t count, const float *x, size_t x_stri
     if (int rc = nd::check_launch("x_to_bf16")) return rc;
     const size_t big_tiles = (out / kPN) * ((m + kPM - 1) / kPM) * count;
     const size_t cus = size_t(ctx->num_cus > 0 ? ctx->num_cus : 256);
-    if (m >= 96 && out % kPN == 0 && big_tiles >= cus && big_tiles <= 0x7fffffff) {
+    const size_t m64_tiles = (out / kRN) * count;
+    if (m <= 64 && out % kRN == 0 && in % kRC == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0 &&
+        w_stride % 16 == 0 && m64_tiles <= 0x7fffffff) {
+        // codes streamed into registers, 128 columns a block
+        const int run = m64_tiles % 8 == 0 ? int(m64_tiles / 8) : 0;
+        hipLaunchKernelGGL(cb8_gemm_m64_kernel, dim3(unsigned(m64_tiles)), dim3(256), 0, ctx->stream, xb, w,
+                           cb, y, int(m), int(out), int(in), w_stride, cb_stride, y_stride,
+                           int(out / kRN), run);
+    } else if (m >= 96 && out % kPN == 0 && big_tiles >= cus && big_tiles <= 0x7fffffff) {
         // at least one 256x256 tile per CU: below that the 128x128 tiles fill
         // the chip better
         const int run = big_tiles % 8 == 0 ? int(big_tiles / 8) : 0;

@@ -76,10 +76,12 @@ def test_gemv_rejects_misaligned_width(ctx):
 
 @pytest.mark.parametrize("m,out,inn", [(512, 3072, 768), (512, 768, 768), (1, 64, 768),
                                        (100, 192, 768), (200, 256, 96), (130, 384, 160),
-                                       (96, 128, 32)])
+                                       (96, 128, 32), (64, 3072, 768), (50, 768, 768),
+                                       (1, 256, 128), (33, 384, 1024), (64, 128, 256)])
 def test_gemm_bf16_mfma(ctx, m, out, inn):
-    """Both tile shapes (64x64 below M = 96 or when out is not a multiple of
-    128, else 128x128), K not a multiple of the K step, ragged M."""
+    """Every tile shape: the M <= 64 streaming kernel (out and K multiples
+    of 128), 64x64 below M = 96 or when out is not a multiple of 128, else
+    128x128; K not a multiple of the K step, ragged M."""
     rng = np.random.default_rng(m + out + inn)
     w = rng.integers(0, 256, size=(out, inn), dtype=np.uint8)
     cb = rng.normal(0, 0.02, size=(out // 64, 256)).astype(np.float32)
@@ -114,10 +116,11 @@ def test_gemm_256_tiles_match_128_tiles(ctx, R, M, N, K):
         assert np.linalg.norm(got[i] - want) / np.linalg.norm(want) <= 5e-3
 
 
-def test_gemm_batched_equals_single(ctx):
-    """Problem i of one batched launch is bit-identical to its own launch."""
-    rng = np.random.default_rng(21)
-    R, M, N, K = 3, 70, 128, 96
+@pytest.mark.parametrize("R,M,N,K", [(3, 70, 128, 96), (5, 64, 384, 768), (4, 17, 256, 256)])
+def test_gemm_batched_equals_single(ctx, R, M, N, K):
+    """Problem i of one batched launch is bit-identical to its own launch
+    (the 64x64 kernel, and the M <= 64 streaming kernel)."""
+    rng = np.random.default_rng(21 + M)
     X = rng.normal(size=(R, M, K)).astype(np.float32)
     W = rng.integers(0, 256, size=(R, N, K), dtype=np.uint8)
     CB = (rng.normal(size=(R, N // 64, 256)) * 0.02).astype(np.float32)
