@@ -803,8 +803,8 @@ __global__ __launch_bounds__(256, 2) void cb8_gemm_m64_kernel(const unsigned sho
         }
     };
     // chunk c: X of chunk c + 1 and the codes of chunk c + 1 in flight while
-    // chunk c is multiplied.  The barrier only hands over LDS, so it waits
-    // for the LDS writes and leaves the code loads in flight.
+    // chunk c is multiplied.  X is issued first, so storing it waits for X
+    // only and the code loads stay in flight across the barrier.
     for (int c0 = 0; c0 < nc; c0 += 2) {
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
@@ -815,7 +815,7 @@ __global__ __launch_bounds__(256, 2) void cb8_gemm_m64_kernel(const unsigned sho
                 cload(s ^ 1, c + 1);
                 compute(c & 1, s);
                 if (c + 1 < nc) xstore((c + 1) & 1);
-                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                __syncthreads();
             }
         }
     }
