@@ -29,7 +29,8 @@
  *   or_fake_quant_vec etc.   tests/v3_kv_quant_vectors.json (upstream
  *                            fake_quant), all-zero and half-step
  *                            invariants (v3_kv_quant_parity.rs:67-92)   PINNED
- *                            (exact .5 ties of roundf: parity unpinned)
+ *                            (exact .5 ties: roundf's half-away-from-zero
+ *                            contract, tests/test_oracle_kv.py)
  *   or_ring_*                wrap/growth readback (cache.rs:578-636),
  *                            caps (:638-665), spans (:795-812), global
  *                            clamp (:699-730)                           PINNED
@@ -38,8 +39,9 @@
  *                            reader vs dequantised buffer
  *                            (v3_kv_quant_parity.rs:102-218), f64
  *                            textbook softmax attention                 PINNED
- *                            (expf last-ulp agreement with Rust libm:
- *                            parity unpinned, tolerance only)
+ *                            (expf: libm's published algorithm restated,
+ *                            within 1 ulp of the exactly rounded value and
+ *                            equal to the device copy; tests/test_oracle_libm.py)
  */
 #ifndef NEEDLE_ORACLE_H
 #define NEEDLE_ORACLE_H

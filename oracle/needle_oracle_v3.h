@@ -8,10 +8,12 @@
  * KATs (engram.rs:139-172), conv step vs the sequence conv
  * (cache.rs:814-841), RoPE as a norm-preserving rotation that is the
  * identity at position 0, mix_down's gated-lane-sum KAT (mhc.rs:168-189),
- * scatter_up's mass conservation (mhc.rs:191-238).  The whole decode step's
- * logits at random init are parity unpinned against the reference (no
- * reference forward can run here); they are checked for decode == decode
- * self-consistency and used as the GPU engine's checker.
+ * scatter_up's mass conservation (mhc.rs:191-238).  The whole decode step
+ * with an f32 KV cache agrees with the reference's numpy transcription of
+ * the forward (tools/needle3_reference.py) on a seeded random-init container
+ * to float rounding, greedy tokens identical (tests/test_forward_reference.py);
+ * the int8 path adds the quantiser, pinned by its own fixture.  The oracle
+ * is test infrastructure: the GPU engine's checker.
  */
 #ifndef NEEDLE_ORACLE_V3_H
 #define NEEDLE_ORACLE_V3_H

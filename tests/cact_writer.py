@@ -142,6 +142,9 @@ def pack_synth(geom, records, codebook):
             continue
         arr = np.asarray(r["data"], np.float32)
         shape = list(arr.shape) if arr.ndim else [1]
+        if r["name"] == "b_res":  # stored [L][n][n], as the shipped container has it
+            n = int(round(np.sqrt(arr.shape[1])))
+            shape = [arr.shape[0], n, n]
         if "perm" in r["name"]:
             data = arr.astype("<f4").tobytes()
             tensors.append((FP32, shape, 0, 0, data, len(data)))

@@ -41,6 +41,21 @@ def test_quantize_rows_golden_bit_exact(ctx):
         assert np.all(np.abs(host(fq) - np.array(case["out"], np.float32)) <= tol)
 
 
+def test_quantize_ties_round_away_from_zero(ctx):
+    """Exact .5 products round away from zero on the device as in the oracle
+    (libm's roundf): rows with absmax 127 have scale and inverse 1."""
+    from test_oracle_kv import TIE_CODES, TIE_ROW
+    x = np.stack([TIE_ROW, -TIE_ROW, TIE_ROW[::-1].copy()]).astype(np.float32)
+    qi, qs = nd.quantize_rows(ctx, dev(x), TIE_ROW.size)
+    oi, os_ = O.quantize_rows(x, TIE_ROW.size)
+    assert np.array_equal(host(qi), oi)
+    assert host(qi)[: TIE_ROW.size].tolist() == TIE_CODES
+    assert np.array_equal(host(qs).view(np.uint32), os_.view(np.uint32))
+    fq = dev(x.copy())
+    nd.fake_quant(ctx, fq, TIE_ROW.size)
+    assert np.array_equal(host(fq).reshape(-1), np.concatenate([O.fake_quant_vec(r) for r in x]))
+
+
 @pytest.mark.parametrize("dim", [48, 64, 16, 256, 100])
 def test_quantize_rows_random_bit_exact(ctx, dim):
     rng = np.random.default_rng(dim)

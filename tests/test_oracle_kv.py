@@ -81,6 +81,25 @@ def test_quantizer_closed_form():
 
 # ---- v3/cache.rs ring -------------------------------------------------------
 
+TIE_ROW = np.array([127.0, 2.5, -3.5, 0.5, -0.5, 126.5, -126.5, 1.5, -2.5, 3.0,
+                    0.0, 0.0, 0.0, 0.0, 0.0, 0.0], np.float32)
+TIE_CODES = [127, 3, -4, 1, -1, 127, -127, 2, -3, 3, 0, 0, 0, 0, 0, 0]
+
+
+def test_roundf_ties_round_away_from_zero():
+    """A product x * (1 / scale) on exactly k + 0.5 rounds away from zero:
+    the contract of libm's roundf, which the reference's quantiser calls
+    (math.rs:39-41; cache.rs:98-104), and which no fixture of the reference
+    holds.  A row whose absmax is 127 has scale 127 / 127 = 1 and inverse 1
+    exactly, so its codes are the rounded values themselves."""
+    ints, scales = O.quantize_rows(TIE_ROW, TIE_ROW.size)
+    assert scales[0] == np.float32(1.0)
+    assert ints.tolist() == TIE_CODES
+    # the row does tell the tie rules apart: half-to-even differs
+    assert np.rint(TIE_ROW).astype(int).tolist() != TIE_CODES
+    assert np.array_equal(O.fake_quant_vec(TIE_ROW), np.array(TIE_CODES, np.float32))
+
+
 def test_int8_ring_wraps_and_grows():
     """cache.rs:578-636 with the toy geometry (1 kv head, qk 4, window 4)."""
     r = O.Ring(True, 1, 4, 4, hint=2, window=4, max_seq_len=64)
