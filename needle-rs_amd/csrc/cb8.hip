@@ -531,7 +531,7 @@ __global__ __launch_bounds__(256) void cb8_gemm128_kernel(const unsigned short *
 constexpr int kPM = 256, kPN = 256, kPK = 64;
 constexpr int kPWM = 64, kPWN = 128;  // wave tile: waves 4 (M) x 2 (N)
 
-__global__ __launch_bounds__(512) void cb8_gemm256_kernel(const unsigned short *__restrict__ Xb,
+__global__ __launch_bounds__(512) void cb8_gemm256_kernel(const float *__restrict__ Xf, size_t xs,
                                                           const uint8_t *__restrict__ W,
                                                           const float *__restrict__ cb,
                                                           float *__restrict__ Y, int M, int N,
@@ -549,7 +549,7 @@ __global__ __launch_bounds__(512) void cb8_gemm256_kernel(const unsigned short *
     const int z = u / (tiles_n * tiles_m);
     const int m0 = (u % tiles_m) * kPM;
     const int n0 = ((u / tiles_m) % tiles_n) * kPN;
-    Xb += z * size_t(M) * K;
+    Xf += z * xs;  // X stays fp32 in HBM; it is rounded to bf16 as it is staged
     W += z * ws;
     cb += z * cs;
     Y += z * ys;
@@ -570,15 +570,15 @@ __global__ __launch_bounds__(512) void cb8_gemm256_kernel(const unsigned short *
     const int r8 = t >> 3;       // staged row within a 64-row slab
     const int c8 = (t & 7) * 8;  // staged columns c8..c8+7 of the K step
     bool mok[J];
-    const unsigned short *xp[J];
+    const float *xp[J];
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         const int m = m0 + r8 + 64 * j;
         mok[j] = m < M;
-        xp[j] = Xb + size_t(m < M ? m : M - 1) * K + c8;
+        xp[j] = Xf + size_t(m < M ? m : M - 1) * K + c8;
     }
     const uint8_t *wp = W + size_t(n0 + r8) * K + c8;  // N is a multiple of 256 here
-    uint4 xa[J];
+    float4 xa[J][2];
     uint2 wc[J];
     bool on = true;
     auto load = [&](int k0) {
@@ -587,7 +587,10 @@ __global__ __launch_bounds__(512) void cb8_gemm256_kernel(const unsigned short *
         // and the run 32 columns back is in range
         const int kc = on ? k0 : k0 - 32;
 #pragma unroll
-        for (int j = 0; j < J; ++j) xa[j] = *reinterpret_cast<const uint4 *>(xp[j] + kc);
+        for (int j = 0; j < J; ++j) {
+            xa[j][0] = *reinterpret_cast<const float4 *>(xp[j] + kc);
+            xa[j][1] = *reinterpret_cast<const float4 *>(xp[j] + kc + 4);
+        }
 #pragma unroll
         for (int j = 0; j < J; ++j) wc[j] = *reinterpret_cast<const uint2 *>(wp + size_t(64 * j) * K + kc);
     };
@@ -595,7 +598,7 @@ __global__ __launch_bounds__(512) void cb8_gemm256_kernel(const unsigned short *
 #pragma unroll
         for (int j = 0; j < J; ++j)
             *reinterpret_cast<uint4 *>(&As[buf][r8 + 64 * j][c8]) =
-                on && mok[j] ? xa[j] : make_uint4(0, 0, 0, 0);
+                on && mok[j] ? pack_bf16x8(xa[j][0], xa[j][1]) : make_uint4(0, 0, 0, 0);
 #pragma unroll
         for (int j = 0; j < J; ++j) {
             const uint32_t d[2] = {wc[j].x, wc[j].y};
@@ -904,30 +907,37 @@ int nd_cb8_gemm_batched(nd_ctx *ctx, size_t count, const float *x, size_t x_stri
     ND_REQUIRE((reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(w) & 7) == 0 &&
                    x_stride % 4 == 0 && w_stride % 8 == 0,
                "x must be 16-byte and w 8-byte aligned, problem by problem");
-    // X to bf16 once per call, into the context workspace
-    const size_t mk = m * in;
-    void *wsp = nullptr;
-    if (int rc = nd::workspace(ctx, count * mk * sizeof(unsigned short), &wsp)) return rc;
-    unsigned short *xb = static_cast<unsigned short *>(wsp);
-    hipLaunchKernelGGL(x_to_bf16_kernel, dim3(unsigned((mk + 2048 * kXRuns - 1) / (2048 * kXRuns)), unsigned(count)),
-                       dim3(256), 0, ctx->stream, x, x_stride, xb, mk);
-    if (int rc = nd::check_launch("x_to_bf16")) return rc;
     const size_t big_tiles = (out / kPN) * ((m + kPM - 1) / kPM) * count;
     const size_t cus = size_t(ctx->num_cus > 0 ? ctx->num_cus : 256);
     const size_t m64_tiles = (out / kRN) * count;
-    if (m <= 64 && out % kRN == 0 && in % kRC == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0 &&
-        w_stride % 16 == 0 && m64_tiles <= 0x7fffffff) {
+    const bool use_m64 = m <= 64 && out % kRN == 0 && in % kRC == 0 &&
+                         (reinterpret_cast<uintptr_t>(w) & 15) == 0 && w_stride % 16 == 0 &&
+                         m64_tiles <= 0x7fffffff;
+    const bool use_256 = !use_m64 && m >= 96 && out % kPN == 0 && big_tiles >= cus && big_tiles <= 0x7fffffff;
+    // X to bf16 once per call, into the context workspace, for the kernels
+    // that stage bf16 X; the 256x256 kernel rounds fp32 X as it stages it
+    const size_t mk = m * in;
+    unsigned short *xb = nullptr;
+    if (!use_256) {
+        void *wsp = nullptr;
+        if (int rc = nd::workspace(ctx, count * mk * sizeof(unsigned short), &wsp)) return rc;
+        xb = static_cast<unsigned short *>(wsp);
+        hipLaunchKernelGGL(x_to_bf16_kernel, dim3(unsigned((mk + 2048 * kXRuns - 1) / (2048 * kXRuns)), unsigned(count)),
+                           dim3(256), 0, ctx->stream, x, x_stride, xb, mk);
+        if (int rc = nd::check_launch("x_to_bf16")) return rc;
+    }
+    if (use_m64) {
         // codes streamed into registers, 128 columns a block
         const int run = m64_tiles % 8 == 0 ? int(m64_tiles / 8) : 0;
         hipLaunchKernelGGL(cb8_gemm_m64_kernel, dim3(unsigned(m64_tiles)), dim3(256), 0, ctx->stream, xb, w,
                            cb, y, int(m), int(out), int(in), w_stride, cb_stride, y_stride,
                            int(out / kRN), run);
-    } else if (m >= 96 && out % kPN == 0 && big_tiles >= cus && big_tiles <= 0x7fffffff) {
+    } else if (use_256) {
         // at least one 256x256 tile per CU: below that the 128x128 tiles fill
         // the chip better
         const int run = big_tiles % 8 == 0 ? int(big_tiles / 8) : 0;
-        hipLaunchKernelGGL(cb8_gemm256_kernel, dim3(unsigned(big_tiles)), dim3(512), 0, ctx->stream, xb,
-                           w, cb, y, int(m), int(out), int(in), w_stride, cb_stride, y_stride,
+        hipLaunchKernelGGL(cb8_gemm256_kernel, dim3(unsigned(big_tiles)), dim3(512), 0, ctx->stream, x,
+                           x_stride, w, cb, y, int(m), int(out), int(in), w_stride, cb_stride, y_stride,
                            int(out / kPN), int((m + kPM - 1) / kPM), run);
     } else if (m >= 96 && out % kBN == 0) {
         dim3 grid(static_cast<unsigned>(out / kBN), static_cast<unsigned>((m + kBM - 1) / kBM),
