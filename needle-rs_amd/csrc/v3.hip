@@ -935,36 +935,75 @@ __global__ __launch_bounds__(kT) void k_final(float *__restrict__ lanes, const f
 }
 
 // ---- greedy argmax, first maximum wins (v3_engine.rs:410-420) -----------------
+// Greedy token: the first index of the largest logit (v3_engine.rs:410-420:
+// a strict `>` scan, so NaN never wins and a tie keeps the lower index).
+// Each thread scans its indices in increasing order with all its loads in
+// flight first; the partial (value, index) pairs then combine by "larger
+// value, or equal value and lower index", which is the scan's own order.
+__device__ inline void argmax_take(float &best, int &bi, float v, int i)
+{
+    if (v > best || (v == best && i < bi)) {
+        best = v;
+        bi = i;
+    }
+}
+
 __global__ __launch_bounds__(kT) void k_argmax(const float *__restrict__ logits, int rows,
                                               int32_t *__restrict__ next)
 {
-    __shared__ float sv[kT];
-    __shared__ int si[kT];
+    __shared__ float sv[kT / 64];
+    __shared__ int si[kT / 64];
     const size_t b = blockIdx.x;
+    const float *row = logits + b * rows;
     float best = -INFINITY;
     int bi = 0;
-    for (int i = threadIdx.x; i < rows; i += kT) {
-        const float v = logits[b * rows + i];
-        if (v > best) {
-            best = v;
-            bi = i;
-        }
-    }
-    sv[threadIdx.x] = best;
-    si[threadIdx.x] = bi;
-    __syncthreads();
-    for (int s = kT / 2; s > 0; s >>= 1) {
-        if (threadIdx.x < s) {
-            const float ov = sv[threadIdx.x + s];
-            const int oi = si[threadIdx.x + s];
-            if (ov > sv[threadIdx.x] || (ov == sv[threadIdx.x] && oi < si[threadIdx.x])) {
-                sv[threadIdx.x] = ov;
-                si[threadIdx.x] = oi;
+    if ((rows & 3) == 0 && (reinterpret_cast<uintptr_t>(row) & 15) == 0) {
+        constexpr int U = 8;
+        const float4 *r4 = reinterpret_cast<const float4 *>(row);
+        const int n4 = rows / 4;
+        for (int base = threadIdx.x; base < n4; base += kT * U) {
+            float4 q[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int i4 = base + u * kT;
+                q[u] = r4[i4 < n4 ? i4 : n4 - 1];
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int i4 = base + u * kT;
+                if (i4 < n4) {
+                    if (q[u].x > best) { best = q[u].x; bi = 4 * i4; }
+                    if (q[u].y > best) { best = q[u].y; bi = 4 * i4 + 1; }
+                    if (q[u].z > best) { best = q[u].z; bi = 4 * i4 + 2; }
+                    if (q[u].w > best) { best = q[u].w; bi = 4 * i4 + 3; }
+                }
             }
         }
-        __syncthreads();
+    } else {
+        for (int i = threadIdx.x; i < rows; i += kT) {
+            const float v = row[i];
+            if (v > best) {
+                best = v;
+                bi = i;
+            }
+        }
     }
-    if (threadIdx.x == 0) next[b] = si[0];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(best, off, 64);
+        const int oi = __shfl_xor(bi, off, 64);
+        argmax_take(best, bi, ov, oi);
+    }
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        sv[w] = best;
+        si[w] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < kT / 64; ++k) argmax_take(best, bi, sv[k], si[k]);
+        next[b] = bi;
+    }
 }
 
 // ---------------------------------------------------------------------------
