@@ -323,6 +323,33 @@ def attention_ctx_runs(torch, nd, ctx, gen, steps):
     return out
 
 
+def exact_attention_runs(torch, nd, ctx, gen):
+    """One session's reference-order decode attention (nd_attend_step_i8_exact,
+    the forward's attention) over spans of 384..4096 positions, at the
+    forward's head geometry (12 q / 2 kv heads, qk 48, vd 64): microseconds
+    per call.  Spans of 2048 and more sum the softmax with the parallel fold."""
+    H, KVH, QK, VD = 12, 2, 48, 64
+    out = {}
+    for span in (384, 1024, 2048, 4096):
+        g = nd.kv_geom(H, KVH, QK, VD, span)
+        nb = nd.kv_block_bytes(g)
+        off = nd.kv_offsets(g)
+        blk = torch.empty(nb, dtype=torch.uint8, device="cuda")
+        blk[:off["ks"]].copy_(torch.randint(-127, 128, (off["ks"],), dtype=torch.int8, device="cuda",
+                                            generator=gen).view(torch.uint8))
+        scales = torch.rand(2 * KVH * span, device="cuda", generator=gen) * 0.03 + 1e-3
+        blk[off["ks"]:off["ks"] + 8 * KVH * span].copy_(scales.view(torch.uint8))
+        q = torch.randn(1, H * QK, device="cuda", generator=gen)
+        lo = torch.zeros(1, dtype=torch.int32, device="cuda")
+        hi = torch.full((1,), span - 1, dtype=torch.int32, device="cuda")
+        o = torch.empty(1, H * VD, device="cuda")
+        ms = timed_loop(torch, lambda: nd.attend_step_i8(ctx, g, blk, nb, lo, hi, q, quant_query=True,
+                                                         out=o, exact=True), 200, 20)
+        out[f"span{span}_us"] = round(ms * 1e3, 2)
+        del blk, scales, q, o
+    return out
+
+
 def forward_runs(torch, nd, ctx, sessions, ctx_len, cpu_tokens=8):
     """The Needle-3 forward on the device: batch 1 (128-token prompt, 256
     greedy steps) and `sessions` sessions prefilled with `ctx_len` tokens
@@ -536,6 +563,7 @@ def main():
 
     if not args.no_secondary and args.only in (None, "attn"):
         result.setdefault("secondary", {}).update(attention_ctx_runs(torch, nd, ctx, gen, args.steps))
+        result["secondary"]["exact_attention_one_session"] = exact_attention_runs(torch, nd, ctx, gen)
 
     if not args.no_secondary and args.only is None:
         result.setdefault("secondary", {})["prefill_gemm_bf16"] = gemm_runs(torch, nd, ctx, gen, 50)

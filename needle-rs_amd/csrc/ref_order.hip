@@ -524,6 +524,14 @@ constexpr int kProdBuf = 64 * 52;  // products per buffer: VD x (T + 4) <= 64 x 
 constexpr int kPrefetch = 8;
 constexpr int kAttn2MaxCap = 8192;  // scores 32 KB + two product buffers 26 KB
 constexpr int kScoreBatch = 4;      // positions per thread whose K rows load together
+// Spans of 2048..4096 positions sum by the parallel fold.  Measured per
+// workgroup against the chain (12 q / 2 kv heads, qk 48, vd 64): span 4096
+// 53.6 -> 45.9 us, 2048 29.0 -> 26.8 us, but 1024 16.4 -> 17.3 us and 384
+// 10.2 -> 12.8 us, where the fold's barrier rounds cost more than the chain.
+constexpr int kAttnFoldMin = 2048;
+constexpr int kAttnFoldC = 16;
+static_assert(sizeof(NdFoldLds<kAttn2Threads>) <= 2 * kProdBuf * sizeof(float),
+              "the fold's LDS lives in the product buffers");
 
 // One (q, key) score chain per position, QC = qk / 16 pieces of 16 codes
 // (0: any qk, read piece by piece).  With QC set, a thread loads the K rows
@@ -732,8 +740,15 @@ __global__ __launch_bounds__(kAttn2Threads, 4) void attn_exact2_kernel(
     };
 #pragma unroll
     for (int j = 0; j < kPrefetch; ++j) load(j, vb[j], vsb[j]);
-    if (tid == 0) {
-        // the softmax sum: one chain in position order
+    // The softmax sum, with the bits of one chain in position order.  The
+    // exps are >= +0, so a span long enough to pay for it takes the exact
+    // parallel fold, its LDS in the product buffers (first written after the
+    // barrier below); a shorter or longer one is the chain itself.
+    if (span >= kAttnFoldMin && span <= NT * kAttnFoldC) {
+        const float s = nd_fold_nonneg<NT, kAttnFoldC>(sc, span,
+                                                        *reinterpret_cast<NdFoldLds<NT> *>(prod));
+        if (tid == 0) total = s;
+    } else if (tid == 0) {
         __builtin_amdgcn_s_setprio(2);
         const float s = lds_chain(0.0f, sc, span);
         total = s;

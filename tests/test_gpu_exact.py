@@ -127,6 +127,20 @@ def test_attend_exact_ring_window(ctx, lo, hi):
     assert _same_bits(out, _oracle(g, host(blk), q, lo, hi))
 
 
+@pytest.mark.parametrize("span", [2047, 2048, 2049, 3333, 4096, 4097])
+def test_attend_exact_softmax_sum_paths(ctx, span):
+    """Spans of 2048..4096 positions take the parallel fold for the softmax
+    sum, the others the chain; both give the chain's bits."""
+    H, KVH, QK, VD, cap = 12, 2, 48, 64, 4200
+    rng = np.random.default_rng(span)
+    g, blk, nb = _fill(ctx, rng, H, KVH, QK, VD, cap, cap, scale=2.0)
+    q = (rng.normal(size=H * QK) * 3).astype(np.float32)
+    lo, hi = cap - span - 7, cap - 8
+    out = host(nd.attend_step_i8(ctx, g, blk, nb, dev(np.array([lo], np.int32)),
+                                 dev(np.array([hi], np.int32)), dev(q)[None], exact=True))[0]
+    assert _same_bits(out, _oracle(g, host(blk), q, lo, hi))
+
+
 def test_attend_exact_batched_sessions(ctx):
     H, KVH, QK, VD, cap, count = 12, 2, 48, 64, 2048, 6
     rng = np.random.default_rng(11)
