@@ -315,6 +315,13 @@ int nd_v3_positions(const nd_v3_batch *b, int32_t *pos);
 int nd_v3_step(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *tokens,
                int32_t *next, float *logits);
 
+/* out[r] = the greedy token of row r of x ([count][n] fp32): the index of
+ * its first maximum under a strict `>` scan from -inf, so a tie keeps the
+ * lower index, NaN never wins and a row of -inf or NaN gives 0.  Replaces
+ * the engine's argmax (needle-infer/src/v3_engine.rs:410-420); the same
+ * kernel picks nd_v3_step's `next`. */
+int nd_argmax_rows(nd_ctx *ctx, const float *x, size_t count, size_t n, int32_t *out);
+
 /* `count` consecutive positions for every session in one pass over the
  * layers: tokens (host) is [sessions][count], session-major.  Replaces the
  * reference's chunked prefill (V3Model::prefill -> forward_impl_pooled,

@@ -1654,6 +1654,17 @@ int nd_v3_positions(const nd_v3_batch *b, int32_t *pos)
     return ND_OK;
 }
 
+int nd_argmax_rows(nd_ctx *ctx, const float *x, size_t count, size_t n, int32_t *out)
+{
+    if (int rc = nd::enter(ctx)) return rc;
+    if (count == 0) return ND_OK;
+    ND_REQUIRE(x && out, "argmax_rows: null buffer");
+    ND_REQUIRE(n >= 1 && n <= 0x7fffffffu, "argmax_rows: row length %zu outside 1..2^31-1", n);
+    ND_REQUIRE(count <= 0x7fffffffu, "argmax_rows: %zu rows", count);
+    hipLaunchKernelGGL(k_argmax, dim3(unsigned(count)), dim3(kT), 0, ctx->stream, x, int(n), out);
+    return nd::check_launch("argmax_rows");
+}
+
 }  // extern "C"
 
 namespace {

@@ -86,6 +86,7 @@ _SIGS = [
     ("nd_v3_batch_free", None, [_vp]),
     ("nd_v3_positions", C.c_int, [_vp, _vp]),
     ("nd_v3_step", C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp]),
+    ("nd_argmax_rows", C.c_int, [_vp, _vp, _sz, _sz, _vp]),
     ("nd_v3_batch_create_chunked", C.c_int, [_vp, _vp, _sz, _sz, _sz, _sz, C.POINTER(_vp)]),
     ("nd_v3_prefill", C.c_int, [_vp, _vp, _vp, _vp, _sz, _vp, _vp]),
     ("nd_v3_cact_config", C.c_int, [_vp, _sz, _vp, C.POINTER(_sz)]),
@@ -134,6 +135,27 @@ def _ptr(t):
     return C.c_void_p(t.data_ptr()) if t is not None else C.c_void_p(0)
 
 
+def _arg(t, dtype, name, numel=0, rows=False):
+    """The device pointer of tensor `t` once it is a device tensor of `dtype`
+    holding at least `numel` elements, contiguous (with rows=True: each
+    slice t[i] contiguous, for the strided batched calls).  The library
+    reads exactly the bytes its sizes imply, so a wrong dtype or layout
+    would read past the buffer or in the wrong order: raise instead."""
+    if not t.is_cuda:
+        raise ValueError(f"{name}: a device tensor is required")
+    if t.dtype != dtype:
+        raise ValueError(f"{name}: dtype {t.dtype}, expected {dtype}")
+    ok = (t.dim() == 0 or all(t[i].is_contiguous() for i in range(min(t.shape[0], 1)))) \
+        if rows else t.is_contiguous()
+    if rows and t.dim() > 1:
+        ok = ok and t.stride(0) >= t[0].numel()
+    if not ok:
+        raise ValueError(f"{name}: layout {tuple(t.shape)} strides {t.stride()} is not contiguous")
+    if t.numel() < numel:
+        raise ValueError(f"{name}: {t.numel()} elements, at least {numel} needed")
+    return C.c_void_p(t.data_ptr())
+
+
 def _torch():
     import torch
     if not torch.cuda.is_available():
@@ -172,15 +194,22 @@ def cb8_gemv(ctx, w, cb, x, y=None):
     out, inn = w.shape
     if y is None:
         y = torch.empty(out, dtype=torch.float32, device=w.device)
-    _check(lib().nd_cb8_gemv(ctx.h, _ptr(w), _ptr(cb), _ptr(x), _ptr(y), out, inn))
+    f32 = torch.float32
+    _check(lib().nd_cb8_gemv(ctx.h, _arg(w, torch.uint8, "w"),
+                             _arg(cb, f32, "cb", (out + 63) // 64 * 256), _arg(x, f32, "x", inn),
+                             _arg(y, f32, "y", out), out, inn))
     return y
 
 
 def cb8_gemv_batched(ctx, w, cb, x, y):
     """w [count, out, in] u8, cb [count, out/64, 256], x [count, in], y [count, out]."""
+    torch = _torch()
     count, out, inn = w.shape
-    _check(lib().nd_cb8_gemv_batched(ctx.h, count, _ptr(w), w.stride(0), _ptr(cb), cb.stride(0),
-                                     _ptr(x), x.stride(0), _ptr(y), y.stride(0), out, inn))
+    f32 = torch.float32
+    _check(lib().nd_cb8_gemv_batched(
+        ctx.h, count, _arg(w, torch.uint8, "w", rows=True), w.stride(0),
+        _arg(cb, f32, "cb", rows=True), cb.stride(0), _arg(x, f32, "x", rows=True), x.stride(0),
+        _arg(y, f32, "y", rows=True), y.stride(0), out, inn))
     return y
 
 
@@ -190,17 +219,24 @@ def cb8_gemm(ctx, x, w, cb, y=None):
     out = w.shape[0]
     if y is None:
         y = torch.empty(m, out, dtype=torch.float32, device=x.device)
-    _check(lib().nd_cb8_gemm(ctx.h, _ptr(x), _ptr(w), _ptr(cb), _ptr(y), m, out, inn))
+    f32 = torch.float32
+    _check(lib().nd_cb8_gemm(ctx.h, _arg(x, f32, "x"), _arg(w, torch.uint8, "w", out * inn),
+                             _arg(cb, f32, "cb", (out + 63) // 64 * 256), _arg(y, f32, "y", m * out),
+                             m, out, inn))
     return y
 
 
 def cb8_gemm_batched(ctx, x, w, cb, y):
     """x [count][m][in] f32, w [count][out][in] u8, cb [count][out/64][256],
     y [count][m][out]: one launch."""
+    torch = _torch()
     count, m, inn = x.shape
     out = w.shape[1]
-    _check(lib().nd_cb8_gemm_batched(ctx.h, count, _ptr(x), x.stride(0), _ptr(w), w.stride(0),
-                                     _ptr(cb), cb.stride(0), _ptr(y), y.stride(0), m, out, inn))
+    f32 = torch.float32
+    _check(lib().nd_cb8_gemm_batched(
+        ctx.h, count, _arg(x, f32, "x", rows=True), x.stride(0),
+        _arg(w, torch.uint8, "w", rows=True), w.stride(0), _arg(cb, f32, "cb", rows=True),
+        cb.stride(0), _arg(y, f32, "y", rows=True), y.stride(0), m, out, inn))
     return y
 
 
@@ -235,7 +271,9 @@ class CqWeight:
         x2 = x.reshape(-1, self.in_feat)
         if xh is None:
             xh = torch.empty(x2.shape[0], self.in_padded, dtype=torch.float32, device=x.device)
-        _check(lib().nd_cq_prepare_input(self.ctx.h, self.h, _ptr(x2), x2.shape[0], _ptr(xh)))
+        n = x2.shape[0]
+        _check(lib().nd_cq_prepare_input(self.ctx.h, self.h, _arg(x2, torch.float32, "x"), n,
+                                         _arg(xh, torch.float32, "xh", n * self.in_padded)))
         return xh
 
     def matvec_rows_prepared(self, xh, row_start, rows, y=None, exact=False):
@@ -244,7 +282,8 @@ class CqWeight:
         if y is None:
             y = torch.empty(rows, dtype=torch.float32, device=xh.device)
         fn = lib().nd_cq_matvec_rows_exact if exact else lib().nd_cq_matvec_rows_prepared
-        _check(fn(self.ctx.h, self.h, _ptr(xh), row_start, rows, _ptr(y)))
+        _check(fn(self.ctx.h, self.h, _arg(xh, torch.float32, "xh", self.in_padded), row_start,
+                  rows, _arg(y, torch.float32, "y", rows)))
         return y
 
     def matvec_prepared(self, xh, y=None):
@@ -259,7 +298,8 @@ class CqWeight:
         if y is None:
             y = torch.empty(batch * rows, dtype=torch.float32, device=xh.device)
         fn = lib().nd_cq_matmul_rows_exact if exact else lib().nd_cq_matmul_rows_prepared
-        _check(fn(self.ctx.h, self.h, _ptr(xh), batch, row_start, rows, _ptr(y)))
+        _check(fn(self.ctx.h, self.h, _arg(xh, torch.float32, "xh", batch * self.in_padded),
+                  batch, row_start, rows, _arg(y, torch.float32, "y", batch * rows)))
         return y
 
     def dequantize_rows(self, rows_i32, out=None):
@@ -267,7 +307,8 @@ class CqWeight:
         n = rows_i32.numel()
         if out is None:
             out = torch.empty(n, self.in_feat, dtype=torch.float32, device=rows_i32.device)
-        _check(lib().nd_cq_dequantize_rows(self.ctx.h, self.h, _ptr(rows_i32), n, _ptr(out)))
+        _check(lib().nd_cq_dequantize_rows(self.ctx.h, self.h, _arg(rows_i32, torch.int32, "rows"),
+                                           n, _arg(out, torch.float32, "out", n * self.in_feat)))
         return out
 
 
@@ -280,13 +321,27 @@ def fold_rows(ctx, x, y=None):
     rows, n = x.shape
     if y is None:
         y = torch.empty(rows, dtype=torch.float32, device=x.device)
-    _check(lib().nd_fold_rows(ctx.h, _ptr(x), rows, n, _ptr(y)))
+    _check(lib().nd_fold_rows(ctx.h, _arg(x, torch.float32, "x"), rows, n,
+                              _arg(y, torch.float32, "y", rows)))
     return y
+
+
+def argmax_rows(ctx, x, out=None):
+    """The greedy token of each row of x ([count][n] fp32): the first maximum
+    (needle-infer/src/v3_engine.rs:410-420)."""
+    torch = _torch()
+    count, n = x.shape
+    if out is None:
+        out = torch.empty(count, dtype=torch.int32, device=x.device)
+    _check(lib().nd_argmax_rows(ctx.h, _arg(x, torch.float32, "x"), count, n,
+                                _arg(out, torch.int32, "out", count)))
+    return out
 
 
 def fake_quant(ctx, x, dim):
     """fake_quant_vec(x[r], 8) for every row of `dim`, in place."""
-    _check(lib().nd_fake_quant(ctx.h, _ptr(x), x.numel() // dim, dim))
+    torch = _torch()
+    _check(lib().nd_fake_quant(ctx.h, _arg(x, torch.float32, "x"), x.numel() // dim, dim))
     return x
 
 
@@ -295,7 +350,8 @@ def quantize_rows(ctx, x, head_dim):
     rows = x.numel() // head_dim
     ints = torch.empty(rows * head_dim, dtype=torch.int8, device=x.device)
     scales = torch.empty(rows, dtype=torch.float32, device=x.device)
-    _check(lib().nd_quantize_rows(ctx.h, _ptr(x), rows, head_dim, _ptr(ints), _ptr(scales)))
+    _check(lib().nd_quantize_rows(ctx.h, _arg(x, torch.float32, "x"), rows, head_dim, _ptr(ints),
+                                  _ptr(scales)))
     return ints, scales
 
 
@@ -321,8 +377,14 @@ def kv_alloc(g, count=1, device=0):
 
 
 def kv_write(ctx, g, kv, kv_stride, pos_i32, k, v):
-    _check(lib().nd_kv_write(ctx.h, C.byref(g), _ptr(kv), kv_stride, pos_i32.numel(), _ptr(pos_i32),
-                             _ptr(k), _ptr(v)))
+    torch = _torch()
+    n = pos_i32.numel()
+    blocks = kv_block_bytes(g) + (n - 1) * kv_stride if n else 0
+    _check(lib().nd_kv_write(
+        ctx.h, C.byref(g), _arg(kv, torch.uint8, "kv", blocks), kv_stride, n,
+        _arg(pos_i32, torch.int32, "pos"),
+        _arg(k, torch.float32, "k", n * g.num_kv_heads * g.qk_head_dim),
+        _arg(v, torch.float32, "v", n * g.num_kv_heads * g.v_head_dim)))
 
 
 def attend_step_i8(ctx, g, kv, kv_stride, lo_i32, hi_i32, q, scale=None, quant_query=False,
@@ -335,8 +397,12 @@ def attend_step_i8(ctx, g, kv, kv_stride, lo_i32, hi_i32, q, scale=None, quant_q
     if out is None:
         out = torch.empty(count, g.num_heads * g.v_head_dim, dtype=torch.float32, device=q.device)
     fn = lib().nd_attend_step_i8_exact if exact else lib().nd_attend_step_i8
-    _check(fn(ctx.h, C.byref(g), _ptr(kv), kv_stride, count, _ptr(lo_i32), _ptr(hi_i32), _ptr(q),
-              scale, int(bool(quant_query)), _ptr(out)))
+    blocks = kv_block_bytes(g) + (count - 1) * kv_stride if count else 0
+    i32, f32 = torch.int32, torch.float32
+    _check(fn(ctx.h, C.byref(g), _arg(kv, torch.uint8, "kv", blocks), kv_stride, count,
+              _arg(lo_i32, i32, "lo"), _arg(hi_i32, i32, "hi", count),
+              _arg(q, f32, "q", count * g.num_heads * g.qk_head_dim), scale,
+              int(bool(quant_query)), _arg(out, f32, "out", count * g.num_heads * g.v_head_dim)))
     return out
 
 
@@ -593,6 +659,12 @@ class V3Batch:
         kernel (the default, faster on ROCm 7.2); the results are identical."""
         _check(lib().nd_v3_batch_set_graphs(self.h, int(bool(on))))
 
+    def _logits_arg(self, logits):
+        if logits is None:
+            return None
+        torch = _torch()
+        return _arg(logits, torch.float32, "logits", self.sessions * self.model.rows)
+
     def step(self, tokens, logits=None, want_next=True):
         """Feed tokens[i] to session i (V3Model::decode_step); returns the greedy
         next tokens, and fills `logits` ([sessions][rows] device tensor) if given."""
@@ -601,7 +673,7 @@ class V3Batch:
         _check(lib().nd_v3_step(self.model.ctx.h, self.model.h, self.h,
                                 tok.ctypes.data_as(C.c_void_p),
                                 nxt.ctypes.data_as(C.c_void_p) if want_next else None,
-                                _ptr(logits) if logits is not None else None))
+                                self._logits_arg(logits)))
         return nxt
 
     def prefill(self, tokens, logits=None, want_next=True):
@@ -612,7 +684,7 @@ class V3Batch:
         _check(lib().nd_v3_prefill(self.model.ctx.h, self.model.h, self.h,
                                    tok.ctypes.data_as(C.c_void_p), tok.shape[1],
                                    nxt.ctypes.data_as(C.c_void_p) if want_next else None,
-                                   _ptr(logits) if logits is not None else None))
+                                   self._logits_arg(logits)))
         return nxt
 
     def generate(self, prompts, steps):

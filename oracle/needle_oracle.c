@@ -163,6 +163,453 @@ float or_logf(float x)
     return s * (hfsq + r) + dk * LN2_LO - hfsq + f + dk * LN2_HI;
 }
 
+/*
+ * math.rs:13-36 route sin, cos and powf through libm 0.2.16 as well; the
+ * RoPE table (model.rs:378-413) is their only caller on the path.  Their
+ * single-precision versions are msun's e_powf.c, s_sinf.c / s_cosf.c with
+ * the k_sinf.c / k_cosf.c kernels and the e_rem_pio2f.c / k_rem_pio2.c
+ * reductions, restated here from those published sources.
+ */
+static double double_of(uint64_t u)
+{
+    double d;
+    memcpy(&d, &u, 8);
+    return d;
+}
+
+/* k_sinf.c: sin on [-pi/4, pi/4], |sin(x)/x - s(x)| < 2^-37.5 */
+static float kern_sin(double x)
+{
+    const double S1 = double_of(0xBFC5555554CBAC77ull), S2 = double_of(0x3F811110896EFBB2ull);
+    const double S3 = double_of(0xBF2A00F9E2CAE774ull), S4 = double_of(0x3EC6CD878C3B46A7ull);
+    double z = x * x, w = z * z, r = S3 + z * S4, s = z * x;
+    return (float)((x + s * (S1 + z * S2)) + s * w * r);
+}
+
+/* k_cosf.c: cos on [-pi/4, pi/4], |cos(x) - c(x)| < 2^-34.1 */
+static float kern_cos(double x)
+{
+    const double C0 = double_of(0xBFDFFFFFFD0C5E81ull), C1 = double_of(0x3FA55553E1053A42ull);
+    const double C2 = double_of(0xBF56C087E80F1E27ull), C3 = double_of(0x3EF99342E0EE5069ull);
+    double z = x * x, w = z * z, r = C2 + z * C3;
+    return (float)(((1.0 + z * C0) + w * C1) + (w * z) * r);
+}
+
+/* k_rem_pio2.c for one input chunk (nx = 1) at prec 0 (jk = jp = 3):
+ * x = t * 2^e0 with t an integer below 2^24; returns n mod 8, *y the
+ * remainder x - n*pi/2. */
+static int rem_pio2_big(double t, int e0, double *y)
+{
+    /* 2/pi, 24 bits per entry */
+    static const int32_t TWO_OVER_PI[24] = {
+        0xA2F983, 0x6E4E44, 0x1529FC, 0x2757D1, 0xF534DD, 0xC0DB62,
+        0x95993C, 0x439041, 0xFE5163, 0xABDEBB, 0xC561B7, 0x246E3A,
+        0x424DD2, 0xE00649, 0x2EEA09, 0xD1921C, 0xFE1DEB, 0x1CB129,
+        0xA73EE8, 0x8235F5, 0x2EBB44, 0x84E99C, 0x7026B4, 0x5F7E41};
+    /* pi/2, 24 bits per entry */
+    static const uint64_t PIO2_BITS[8] = {
+        0x3FF921FB40000000ull, 0x3E74442D00000000ull, 0x3CF8469880000000ull,
+        0x3B78CC5160000000ull, 0x39F01B8380000000ull, 0x387A252040000000ull,
+        0x36E3822280000000ull, 0x3569F31D00000000ull};
+    const double T24 = 16777216.0, TM24 = 1.0 / 16777216.0;
+    const int JK = 3;
+    double f[20], q[20], fq[20], z, w;
+    int32_t iq[20];
+    int jv = (e0 - 3) / 24, q0, jz, n, ih, i, j, k;
+    if (jv < 0)
+        jv = 0;
+    q0 = e0 - 24 * (jv + 1);
+    for (i = 0; i <= JK; i++) {
+        j = jv + i;
+        f[i] = j < 0 ? 0.0 : (double)TWO_OVER_PI[j];
+        q[i] = 0.0 + t * f[i];
+    }
+    jz = JK;
+recompute:
+    z = q[jz];
+    for (i = 0, j = jz; j > 0; i++, j--) {
+        w = (double)(int32_t)(TM24 * z);
+        iq[i] = (int32_t)(z - T24 * w);
+        z = q[j - 1] + w;
+    }
+    z = ldexp(z, q0);
+    z -= 8.0 * floor(z * 0.125);
+    n = (int32_t)z;
+    z -= (double)n;
+    ih = 0;
+    if (q0 > 0) {
+        i = iq[jz - 1] >> (24 - q0);
+        n += i;
+        iq[jz - 1] -= i << (24 - q0);
+        ih = iq[jz - 1] >> (23 - q0);
+    } else if (q0 == 0) {
+        ih = iq[jz - 1] >> 23;
+    } else if (z >= 0.5) {
+        ih = 2;
+    }
+    if (ih > 0) {
+        int carry = 0;
+        n += 1;
+        for (i = 0; i < jz; i++) {
+            j = iq[i];
+            if (carry == 0) {
+                if (j != 0) {
+                    carry = 1;
+                    iq[i] = 0x1000000 - j;
+                }
+            } else {
+                iq[i] = 0xffffff - j;
+            }
+        }
+        if (q0 == 1)
+            iq[jz - 1] &= 0x7fffff;
+        if (q0 == 2)
+            iq[jz - 1] &= 0x3fffff;
+        if (ih == 2) {
+            z = 1.0 - z;
+            if (carry)
+                z -= ldexp(1.0, q0);
+        }
+    }
+    if (z == 0.0) {
+        j = 0;
+        for (i = jz - 1; i >= JK; i--)
+            j |= iq[i];
+        if (j == 0) {
+            for (k = 1; iq[JK - k] == 0; k++)
+                ;
+            for (i = jz + 1; i <= jz + k; i++) {
+                f[i] = (double)TWO_OVER_PI[jv + i];
+                q[i] = 0.0 + t * f[i];
+            }
+            jz += k;
+            goto recompute;
+        }
+    }
+    if (z == 0.0) {
+        jz--;
+        q0 -= 24;
+        while (iq[jz] == 0) {
+            jz--;
+            q0 -= 24;
+        }
+    } else {
+        z = ldexp(z, -q0);
+        if (z >= T24) {
+            w = (double)(int32_t)(TM24 * z);
+            iq[jz] = (int32_t)(z - T24 * w);
+            jz++;
+            q0 += 24;
+            iq[jz] = (int32_t)w;
+        } else {
+            iq[jz] = (int32_t)z;
+        }
+    }
+    w = ldexp(1.0, q0);
+    for (i = jz; i >= 0; i--) {
+        q[i] = w * (double)iq[i];
+        w *= TM24;
+    }
+    for (i = jz; i >= 0; i--) {
+        w = 0.0;
+        for (k = 0; k <= JK && k <= jz - i; k++)
+            w += double_of(PIO2_BITS[k]) * q[i + k];
+        fq[jz - i] = w;
+    }
+    w = 0.0;
+    for (i = jz; i >= 0; i--)
+        w += fq[i];
+    *y = ih == 0 ? w : -w;
+    return n & 7;
+}
+
+/* e_rem_pio2f.c: n and x - n*pi/2 in double. */
+static int rem_pio2f(float x, double *y)
+{
+    const double TOINT = double_of(0x4338000000000000ull);   /* 1.5 * 2^52 */
+    const double INV_PIO2 = double_of(0x3FE45F306DC9C883ull);
+    const double PIO2_1 = double_of(0x3FF921FB50000000ull);  /* 25 bits */
+    const double PIO2_1T = double_of(0x3E5110B4611A6263ull); /* the rest */
+    uint32_t u = bits_of(x), ax = u & 0x7fffffffu;
+    if (ax < 0x4dc90fdbu) {
+        double fn = (double)x * INV_PIO2 + TOINT;
+        fn = fn - TOINT;
+        *y = (double)x - fn * PIO2_1 - fn * PIO2_1T;
+        return (int)fn;
+    }
+    if (ax >= 0x7f800000u) {
+        *y = (double)x - (double)x;
+        return 0;
+    }
+    int e0 = (int)(ax >> 23) - 150;
+    double r;
+    int n = rem_pio2_big((double)float_of(ax - ((uint32_t)e0 << 23)), e0, &r);
+    if (u >> 31) {
+        *y = -r;
+        return -n;
+    }
+    *y = r;
+    return n;
+}
+
+/* s_sinf.c */
+float or_sinf(float x)
+{
+    const double P1 = double_of(0x3FF921FB54442D18ull), P2 = double_of(0x400921FB54442D18ull);
+    const double P3 = double_of(0x4012D97C7F3321D2ull), P4 = double_of(0x401921FB54442D18ull);
+    uint32_t u = bits_of(x), ax = u & 0x7fffffffu;
+    int neg = (int)(u >> 31);
+    double d = (double)x, y;
+    if (ax <= 0x3f490fdau)
+        return ax < 0x39800000u ? x : kern_sin(d);
+    if (ax <= 0x407b53d1u) {
+        if (ax <= 0x4016cbe3u)
+            return neg ? -kern_cos(d + P1) : kern_cos(d - P1);
+        return kern_sin(neg ? -(d + P2) : -(d - P2));
+    }
+    if (ax <= 0x40e231d5u) {
+        if (ax <= 0x40afeddfu)
+            return neg ? kern_cos(d + P3) : -kern_cos(d - P3);
+        return kern_sin(neg ? d + P4 : d - P4);
+    }
+    if (ax >= 0x7f800000u)
+        return x - x;
+    int n = rem_pio2f(x, &y) & 3;
+    if (n == 0)
+        return kern_sin(y);
+    if (n == 1)
+        return kern_cos(y);
+    if (n == 2)
+        return kern_sin(-y);
+    return -kern_cos(y);
+}
+
+/* s_cosf.c */
+float or_cosf(float x)
+{
+    const double P1 = double_of(0x3FF921FB54442D18ull), P2 = double_of(0x400921FB54442D18ull);
+    const double P3 = double_of(0x4012D97C7F3321D2ull), P4 = double_of(0x401921FB54442D18ull);
+    uint32_t u = bits_of(x), ax = u & 0x7fffffffu;
+    int neg = (int)(u >> 31);
+    double d = (double)x, y;
+    if (ax <= 0x3f490fdau)
+        return ax < 0x39800000u ? 1.0f : kern_cos(d);
+    if (ax <= 0x407b53d1u) {
+        if (ax > 0x4016cbe3u)
+            return -kern_cos(neg ? d + P2 : d - P2);
+        return neg ? kern_sin(d + P1) : kern_sin(P1 - d);
+    }
+    if (ax <= 0x40e231d5u) {
+        if (ax > 0x40afeddfu)
+            return kern_cos(neg ? d + P4 : d - P4);
+        return neg ? kern_sin(-d - P3) : kern_sin(d - P3);
+    }
+    if (ax >= 0x7f800000u)
+        return x - x;
+    int n = rem_pio2f(x, &y) & 3;
+    if (n == 0)
+        return kern_cos(y);
+    if (n == 1)
+        return kern_sin(-y);
+    if (n == 2)
+        return -kern_cos(y);
+    return kern_sin(y);
+}
+
+/* Keep the high 20 bits of a float (the 12-bit-mantissa split). */
+static float hi20(float v) { return float_of(bits_of(v) & 0xfffff000u); }
+
+/* e_powf.c */
+float or_powf(float x, float y)
+{
+    const float BP[2] = {1.0f, 1.5f};
+    const float DP_H[2] = {0.0f, float_of(0x3f15c000u)};
+    const float DP_L[2] = {0.0f, float_of(0x35d1cfdcu)};
+    const float L1 = float_of(0x3f19999au), L2 = float_of(0x3edb6db7u);
+    const float L3 = float_of(0x3eaaaaabu), L4 = float_of(0x3e8ba305u);
+    const float L5 = float_of(0x3e6c3255u), L6 = float_of(0x3e53f142u);
+    const float P1 = float_of(0x3e2aaaabu), P2 = float_of(0xbb360b61u);
+    const float P3 = float_of(0x388ab355u), P4 = float_of(0xb5ddea0eu);
+    const float P5 = float_of(0x3331bb4cu);
+    const float LG2 = float_of(0x3f317218u), LG2_H = float_of(0x3f317200u);
+    const float LG2_L = float_of(0x35bfbe8cu);
+    const float OVT = float_of(0x3338aa3cu);
+    const float CP = float_of(0x3f76384fu), CP_H = float_of(0x3f764000u);
+    const float CP_L = float_of(0xb8f623c6u);
+    const float IVLN2 = float_of(0x3fb8aa3bu), IVLN2_H = float_of(0x3fb8aa00u);
+    const float IVLN2_L = float_of(0x36eca570u);
+    const float BIG = float_of(0x7149f2cau), SMALL = float_of(0x0da24260u); /* 1e30, 1e-30 */
+    int32_t hx = (int32_t)bits_of(x), hy = (int32_t)bits_of(y);
+    int32_t ix = hx & 0x7fffffff, iy = hy & 0x7fffffff;
+    int32_t yisint = 0, n, j, k, i;
+    float ax, sn, t1, t2, z, p_h, p_l, t, u, v, w, r;
+
+    if (iy == 0 || hx == 0x3f800000)
+        return 1.0f;
+    if (ix > 0x7f800000 || iy > 0x7f800000)
+        return x + y;
+    if (hx < 0) {
+        if (iy >= 0x4b800000) {
+            yisint = 2;
+        } else if (iy >= 0x3f800000) {
+            k = (iy >> 23) - 127;
+            j = iy >> (23 - k);
+            if ((j << (23 - k)) == iy)
+                yisint = 2 - (j & 1);
+        }
+    }
+    if (iy == 0x7f800000) {
+        if (ix == 0x3f800000)
+            return 1.0f;
+        if (ix > 0x3f800000)
+            return hy >= 0 ? y : 0.0f;
+        return hy >= 0 ? 0.0f : -y;
+    }
+    if (iy == 0x3f800000)
+        return hy >= 0 ? x : 1.0f / x;
+    if (hy == 0x40000000)
+        return x * x;
+    if (hy == 0x3f000000 && hx >= 0)
+        return sqrtf(x);
+    ax = fabsf(x);
+    if (ix == 0x7f800000 || ix == 0 || ix == 0x3f800000) {
+        z = hy < 0 ? 1.0f / ax : ax;
+        if (hx < 0) {
+            if (((ix - 0x3f800000) | yisint) == 0)
+                z = (z - z) / (z - z);
+            else if (yisint == 1)
+                z = -z;
+        }
+        return z;
+    }
+    sn = 1.0f;
+    if (hx < 0) {
+        if (yisint == 0)
+            return (x - x) / (x - x);
+        if (yisint == 1)
+            sn = -1.0f;
+    }
+    if (iy > 0x4d000000) {
+        /* |y| > 2^27: overflow or underflow unless |1 - x| <= 2^-20 */
+        if (ix < 0x3f7ffff8)
+            return hy < 0 ? sn * BIG * BIG : sn * SMALL * SMALL;
+        if (ix > 0x3f800007)
+            return hy > 0 ? sn * BIG * BIG : sn * SMALL * SMALL;
+        t = ax - 1.0f;
+        w = (t * t) * (0.5f - t * (float_of(0x3eaaaaabu) - t * 0.25f));
+        u = IVLN2_H * t;
+        v = t * IVLN2_L - w * IVLN2;
+        t1 = hi20(u + v);
+        t2 = v - (t1 - u);
+    } else {
+        float s, s_h, s_l, s2, t_h, t_l, z_h, z_l;
+        n = 0;
+        if (ix < 0x00800000) {
+            ax *= float_of(0x4b800000u);
+            n -= 24;
+            ix = (int32_t)bits_of(ax);
+        }
+        n += (ix >> 23) - 127;
+        j = ix & 0x007fffff;
+        ix = j | 0x3f800000;
+        if (j <= 0x1cc471) {
+            k = 0;
+        } else if (j < 0x5db3d7) {
+            k = 1;
+        } else {
+            k = 0;
+            n += 1;
+            ix -= 0x00800000;
+        }
+        ax = float_of((uint32_t)ix);
+        u = ax - BP[k];
+        v = 1.0f / (ax + BP[k]);
+        s = u * v;
+        s_h = hi20(s);
+        t_h = float_of((uint32_t)((((ix >> 1) & 0xfffff000) | 0x20000000) + 0x00400000 + (k << 21)));
+        t_l = ax - (t_h - BP[k]);
+        s_l = v * ((u - s_h * t_h) - s_h * t_l);
+        s2 = s * s;
+        r = s2 * s2 * (L1 + s2 * (L2 + s2 * (L3 + s2 * (L4 + s2 * (L5 + s2 * L6)))));
+        r += s_l * (s_h + s);
+        s2 = s_h * s_h;
+        t_h = hi20(3.0f + s2 + r);
+        t_l = r - ((t_h - 3.0f) - s2);
+        u = s_h * t_h;
+        v = s_l * t_h + t_l * s;
+        p_h = hi20(u + v);
+        p_l = v - (p_h - u);
+        z_h = CP_H * p_h;
+        z_l = CP_L * p_h + p_l * CP + DP_L[k];
+        t = (float)n;
+        t1 = hi20(((z_h + z_l) + DP_H[k]) + t);
+        t2 = z_l - (((t1 - t) - DP_H[k]) - z_h);
+    }
+    {
+        float y1 = hi20(y);
+        p_l = (y - y1) * t1 + y * t2;
+        p_h = y1 * t1;
+    }
+    z = p_l + p_h;
+    j = (int32_t)bits_of(z);
+    if (j > 0x43000000)
+        return sn * BIG * BIG;
+    if (j == 0x43000000) {
+        if (p_l + OVT > z - p_h)
+            return sn * BIG * BIG;
+    } else if ((j & 0x7fffffff) > 0x43160000) {
+        return sn * SMALL * SMALL;
+    } else if (bits_of(z) == 0xc3160000u) {
+        if (p_l <= z - p_h)
+            return sn * SMALL * SMALL;
+    }
+    i = j & 0x7fffffff;
+    k = (i >> 23) - 127;
+    n = 0;
+    if (i > 0x3f000000) {
+        n = j + (0x00800000 >> (k + 1));
+        k = ((n & 0x7fffffff) >> 23) - 127;
+        t = float_of((uint32_t)(n & ~(0x007fffff >> k)));
+        n = ((n & 0x007fffff) | 0x00800000) >> (23 - k);
+        if (j < 0)
+            n = -n;
+        p_h -= t;
+    }
+    t = float_of(bits_of(p_l + p_h) & 0xffff8000u);
+    u = t * LG2_H;
+    v = (p_l - (t - p_h)) * LG2 + t * LG2_L;
+    z = u + v;
+    w = v - (z - u);
+    t = z * z;
+    t1 = z - t * (P1 + t * (P2 + t * (P3 + t * (P4 + t * P5))));
+    r = (z * t1) / (t1 - 2.0f) - (w + z * w);
+    z = 1.0f - (r - z);
+    j = (int32_t)(bits_of(z) + ((uint32_t)n << 23));
+    if ((j >> 23) <= 0)
+        z = scale_pow2(z, n);
+    else
+        z = float_of((uint32_t)j);
+    return sn * z;
+}
+
+void or_sinf_n(const float *x, size_t n, float *y)
+{
+    for (size_t i = 0; i < n; i++)
+        y[i] = or_sinf(x[i]);
+}
+
+void or_cosf_n(const float *x, size_t n, float *y)
+{
+    for (size_t i = 0; i < n; i++)
+        y[i] = or_cosf(x[i]);
+}
+
+void or_powf_n(const float *x, const float *e, size_t n, float *y)
+{
+    for (size_t i = 0; i < n; i++)
+        y[i] = or_powf(x[i], e[i]);
+}
+
 void or_expf_n(const float *x, size_t n, float *y)
 {
     for (size_t i = 0; i < n; i++)
@@ -381,9 +828,35 @@ static float dot_group(size_t P, const float *lut, const uint8_t *gbytes,
     return acc;
 }
 
+/* ------------------------------------------------------------------------ */
+/* Threads.  The reference splits a call across its rayon pool only past     */
+/* fixed size rules (cq.rs:301-323, 446-472, 474-581; constants :815-823);   */
+/* each row's (or batch row's) arithmetic is unchanged, so every split is    */
+/* bit-identical to the serial loop.  OR_SPLIT_REFERENCE applies those rules */
+/* (the CPU baseline); OR_SPLIT_ALL also splits every smaller row loop and    */
+/* attention's heads, for a faster checker with the same bits.               */
+/* ------------------------------------------------------------------------ */
+
+#define MIN_PAR_ROWS 64   /* cq.rs:815 */
+#define MIN_PAR_BATCH 8   /* cq.rs:819 */
+#define PAR_MIN_MACS ((size_t)1 << 20) /* cq.rs:823 */
+
+static int or_threads = 1;
+static int or_split = OR_SPLIT_REFERENCE;
+
+void or_set_threads(int threads, int split)
+{
+    or_threads = threads > 0 ? threads : 1;
+    or_split = split;
+}
+
+int or_get_threads(void) { return or_threads; }
+
+static size_t div_ceil(size_t a, size_t b) { return (a + b - 1) / b; }
+
 /* cq.rs:721-735 (LUT widths) and cq.rs:738-757 (3-bit generic). */
-void or_cq_matvec_rows_prepared(const or_cq *w, const float *xh,
-                                size_t row_start, size_t rows, float *y)
+static void matvec_rows_serial(const or_cq *w, const float *xh,
+                               size_t row_start, size_t rows, float *y)
 {
     for (size_t yi = 0; yi < rows; yi++) {
         size_t o = row_start + yi;
@@ -411,6 +884,35 @@ void or_cq_matvec_rows_prepared(const or_cq *w, const float *xh,
             }
         }
         y[yi] = total;
+    }
+}
+
+/* cq.rs:301-323: rows split into bands of max(ceil(rows/threads), 64) when
+ * should_parallelise (rows >= 128 and rows*in_padded >= 2^20, :474-484). */
+void or_cq_matvec_rows_prepared(const or_cq *w, const float *xh,
+                                size_t row_start, size_t rows, float *y)
+{
+    int split;
+    size_t chunk;
+    if (or_split == OR_SPLIT_ALL) {
+        split = rows >= 2 && rows * w->in_padded >= 4096;
+        chunk = div_ceil(rows, (size_t)or_threads);
+    } else {
+        split = rows >= 2 * MIN_PAR_ROWS && rows * w->in_padded >= PAR_MIN_MACS;
+        chunk = div_ceil(rows, (size_t)or_threads);
+        if (chunk < MIN_PAR_ROWS)
+            chunk = MIN_PAR_ROWS;
+    }
+    if (or_threads <= 1 || !split) {
+        matvec_rows_serial(w, xh, row_start, rows, y);
+        return;
+    }
+    long bands = (long)div_ceil(rows, chunk);
+#pragma omp parallel for num_threads(or_threads) schedule(static, 1)
+    for (long b = 0; b < bands; b++) {
+        size_t r0 = (size_t)b * chunk;
+        size_t n = rows - r0 < chunk ? rows - r0 : chunk;
+        matvec_rows_serial(w, xh, row_start + r0, n, y + r0);
     }
 }
 
@@ -492,9 +994,10 @@ static float group_dot_serial(const float *u, const float *x, size_t n)
 }
 
 /* cq.rs:632-679: decode each group once (norm 1.0), dot with every batch
- * row in the matvec's lane order, acc[b] += norm * s; batch-major output. */
-void or_cq_matmul_rows_prepared(const or_cq *w, const float *xh, size_t batch,
-                                size_t row_start, size_t rows, float *y)
+ * row in the matvec's lane order, acc[b] += norm * s; batch-major output
+ * with row stride `ystride` (the caller's `rows`). */
+static void matmul_rows_serial(const or_cq *w, const float *xh, size_t batch,
+                               size_t row_start, size_t rows, float *y, size_t ystride)
 {
     size_t stride = w->in_padded;
     float ug[OR_MAX_GROUP];
@@ -517,9 +1020,47 @@ void or_cq_matmul_rows_prepared(const or_cq *w, const float *xh, size_t batch,
             }
         }
         for (size_t b = 0; b < batch; b++)
-            y[b * rows + r] = acc[b];
+            y[b * ystride + r] = acc[b];
     }
     free(acc);
+}
+
+/* cq.rs:446-472: past 2^20 multiply-adds, row bands of
+ * max(ceil(rows/threads), 64) when rows >= 128 (:494-544), else batch bands
+ * of max(ceil(batch/threads), 8) when batch >= 16 (:552-581). */
+void or_cq_matmul_rows_prepared(const or_cq *w, const float *xh, size_t batch,
+                                size_t row_start, size_t rows, float *y)
+{
+    size_t work = rows * batch * w->in_padded;
+    int all = or_split == OR_SPLIT_ALL;
+    int big = all ? work >= 4096 : work >= PAR_MIN_MACS;
+    if (or_threads > 1 && big && rows >= (all ? 2 : 2 * MIN_PAR_ROWS)) {
+        size_t chunk = div_ceil(rows, (size_t)or_threads);
+        if (!all && chunk < MIN_PAR_ROWS)
+            chunk = MIN_PAR_ROWS;
+        long bands = (long)div_ceil(rows, chunk);
+#pragma omp parallel for num_threads(or_threads) schedule(static, 1)
+        for (long b = 0; b < bands; b++) {
+            size_t r0 = (size_t)b * chunk;
+            size_t n = rows - r0 < chunk ? rows - r0 : chunk;
+            matmul_rows_serial(w, xh, batch, row_start + r0, n, y + r0, rows);
+        }
+        return;
+    }
+    if (or_threads > 1 && big && batch >= (all ? 2 : 2 * MIN_PAR_BATCH)) {
+        size_t band = div_ceil(batch, (size_t)or_threads);
+        if (!all && band < MIN_PAR_BATCH)
+            band = MIN_PAR_BATCH;
+        long bands = (long)div_ceil(batch, band);
+#pragma omp parallel for num_threads(or_threads) schedule(static, 1)
+        for (long b = 0; b < bands; b++) {
+            size_t b0 = (size_t)b * band;
+            size_t n = batch - b0 < band ? batch - b0 : band;
+            matmul_rows_serial(w, xh + b0 * w->in_padded, n, row_start, rows, y + b0 * rows, rows);
+        }
+        return;
+    }
+    matmul_rows_serial(w, xh, batch, row_start, rows, y, rows);
 }
 
 /* cq.rs:763-779: u = levels * norm, FWHT per group, truncate to in_feat. */
@@ -788,9 +1329,13 @@ static void attend_step_impl(const float *q, const float *kf, const float *vf,
     float scale = 1.0f / sqrtf((float)d->qk_head_dim);
     size_t repeat = d->num_heads / d->num_kv_heads;
     size_t span = hi - lo + 1;
-    float *scores = malloc(span * sizeof(float));
     size_t QK = d->qk_head_dim, VD = d->v_head_dim, H = d->num_kv_heads;
-    for (size_t h = 0; h < d->num_heads; h++) {
+    /* Heads are independent; the checker's split runs them on threads. */
+    int par = or_threads > 1 && or_split == OR_SPLIT_ALL && span * d->num_heads >= 4096;
+#pragma omp parallel for num_threads(or_threads) schedule(static, 1) if (par)
+    for (long hh = 0; hh < (long)d->num_heads; hh++) {
+        size_t h = (size_t)hh;
+        float *scores = malloc(span * sizeof(float));
         size_t kvh = h / repeat;
         const float *qv = q + h * QK;
         float max = -INFINITY;
@@ -825,8 +1370,8 @@ static void attend_step_impl(const float *q, const float *kf, const float *vf,
                     o[j] += w * vf[vo + j];
             }
         }
+        free(scores);
     }
-    free(scores);
 }
 
 void or_attend_step_f32(const float *q, const float *k, const float *v,

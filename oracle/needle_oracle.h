@@ -60,6 +60,15 @@ float or_expf(float x);
 float or_logf(float x);
 void or_expf_n(const float *x, size_t n, float *y);
 void or_logf_n(const float *x, size_t n, float *y);
+/* libm 0.2.16 sinf / cosf / powf (msun s_sinf.c, s_cosf.c, k_sinf.c,
+ * k_cosf.c, e_rem_pio2f.c, k_rem_pio2.c, e_powf.c), math.rs:13-36: the RoPE
+ * table's functions (v3/model.rs:378-413). */
+float or_sinf(float x);
+float or_cosf(float x);
+float or_powf(float x, float y);
+void or_sinf_n(const float *x, size_t n, float *y);
+void or_cosf_n(const float *x, size_t n, float *y);
+void or_powf_n(const float *x, const float *e, size_t n, float *y);
 
 /* ---- hadamard.rs ------------------------------------------------------ */
 void or_fwht(float *x, size_t n);
@@ -121,6 +130,15 @@ void or_cb8_gemv_f64(const uint8_t *w, const float *cb, const float *x,
                      double *y, size_t out, size_t in);
 void or_cb8_gemm(const float *x, const uint8_t *w, const float *cb, float *y,
                  size_t m, size_t out, size_t in);
+/* Threads for the reference's rayon splits (cq.rs:301-323, 446-581):
+ * OR_SPLIT_REFERENCE applies its size rules (the CPU baseline);
+ * OR_SPLIT_ALL splits every independent row loop and attention's heads too
+ * (a faster checker, the same bits).  One thread (the default) is serial. */
+#define OR_SPLIT_REFERENCE 0
+#define OR_SPLIT_ALL 1
+void or_set_threads(int threads, int split);
+int or_get_threads(void);
+
 void or_cb8_gemv_omp(const uint8_t *w, const float *cb, const float *x,
                      float *y, size_t out, size_t in);
 

@@ -63,6 +63,9 @@ def lib():
         L.or_f16_to_f32.restype = C.c_float
         L.or_expf_n.argtypes = [_f32p, _sz, _f32p]
         L.or_logf_n.argtypes = [_f32p, _sz, _f32p]
+        L.or_sinf_n.argtypes = [_f32p, _sz, _f32p]
+        L.or_cosf_n.argtypes = [_f32p, _sz, _f32p]
+        L.or_powf_n.argtypes = [_f32p, _f32p, _sz, _f32p]
         L.or_fwht.argtypes = [_f32p, _sz]
         L.or_fwht_normalized.argtypes = [_f32p, _sz]
         L.or_packed_row_bytes.argtypes = [_sz, C.c_uint8]
@@ -82,6 +85,9 @@ def lib():
         L.or_cq_dequantize_row.argtypes = [C.POINTER(_Cq), _sz, _f32p]
         L.or_cb8_gemv.argtypes = [_u8p, _f32p, _f32p, _f32p, _sz, _sz]
         L.or_cb8_gemv_omp.argtypes = [_u8p, _f32p, _f32p, _f32p, _sz, _sz]
+        L.or_set_threads.argtypes = [C.c_int, C.c_int]
+        L.or_set_threads.restype = None
+        L.or_get_threads.restype = C.c_int
         L.or_cb8_gemv_f64.argtypes = [_u8p, _f32p, _f32p, _f64p, _sz, _sz]
         L.or_cb8_gemm.argtypes = [_f32p, _u8p, _f32p, _f32p, _sz, _sz, _sz]
         L.or_fake_quant_vec.argtypes = [_f32p, _sz, C.c_uint32]
@@ -129,6 +135,31 @@ def logf(x):
     x = _f32(x).ravel()
     y = np.empty_like(x)
     lib().or_logf_n(x, x.size, y)
+    return y
+
+
+def sinf(x):
+    """libm's sinf (math.rs:23-26), elementwise."""
+    x = _f32(x).ravel()
+    y = np.empty_like(x)
+    lib().or_sinf_n(x, x.size, y)
+    return y
+
+
+def cosf(x):
+    """libm's cosf (math.rs:28-31), elementwise."""
+    x = _f32(x).ravel()
+    y = np.empty_like(x)
+    lib().or_cosf_n(x, x.size, y)
+    return y
+
+
+def powf(x, e):
+    """libm's powf (math.rs:43-46), elementwise over broadcast x and e."""
+    x, e = np.broadcast_arrays(_f32(x), _f32(e))
+    x, e = _f32(x).ravel(), _f32(e).ravel()
+    y = np.empty_like(x)
+    lib().or_powf_n(x, e, x.size, y)
     return y
 
 
@@ -251,6 +282,20 @@ def cb8_gemv(w, cb, x):
     y = np.zeros(out, np.float32)
     lib().or_cb8_gemv(w, _f32(cb), _f32(x), y, out, inn)
     return y
+
+
+SPLIT_REFERENCE, SPLIT_ALL = 0, 1
+
+
+def set_threads(threads, split=SPLIT_REFERENCE):
+    """Threads for the reference's rayon splits (cq.rs:301-323, 446-581).
+    SPLIT_REFERENCE keeps its size rules; SPLIT_ALL also splits the smaller
+    row loops and attention's heads (the same bits, a faster checker)."""
+    lib().or_set_threads(int(threads), int(split))
+
+
+def get_threads():
+    return lib().or_get_threads()
 
 
 def cb8_gemv_omp(w, cb, x, y):
@@ -519,6 +564,12 @@ def v3_generate(model, prompt, steps, int8=True, hint=None):
     margins = np.zeros(steps, np.float32)
     _v3_lib().or_v3_generate(model._p, cache._p, prompt, len(prompt), steps, toks, margins)
     return toks, margins
+
+
+def argmax(x):
+    """The engine's greedy pick (v3_engine.rs:410-420): first maximum under
+    a strict `>` scan from -inf."""
+    return int(_v3_lib().or_argmax(_f32(x).reshape(-1), np.asarray(x).size))
 
 
 def sinkhorn(m):

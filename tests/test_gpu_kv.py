@@ -93,6 +93,55 @@ def test_write_kv_ring_matches_oracle(ctx):
     assert np.array_equal(ks.reshape(-1), st["k_scale"]) and np.array_equal(vs.reshape(-1), st["v_scale"])
 
 
+@pytest.mark.parametrize("ctxlen,batch", [(2048, 1), (2048, 64), (512, 3)])
+def test_write_kv_config3_bytes(ctx, ctxlen, batch):
+    """Config 3's append at 12 kv heads x 64: positions 0..ctx-1 written
+    `batch` positions per call, as a decode loop appends them; every slot's
+    K and V codes and scales equal the oracle's quantize_rows of that
+    position's rows (cache.rs:113-122, 346-379), byte for byte, and the
+    untouched bytes of the block stay zero.  A second pass over the ring
+    (positions ctx..ctx+batch-1, slots 0..batch-1) overwrites only its slots."""
+    H = KVH = 12
+    QK = VD = 64
+    rng = np.random.default_rng(ctxlen + batch)
+    g = nd.kv_geom(H, KVH, QK, VD, ctxlen)
+    blk, nb = nd.kv_alloc(g)
+    mags = 10.0 ** rng.uniform(-3, 3, size=(ctxlen + batch, 1))
+    k = (rng.normal(size=(ctxlen + batch, KVH * QK)) * mags).astype(np.float32)
+    v = rng.normal(size=(ctxlen + batch, KVH * VD)).astype(np.float32)
+    k[5] = 0.0  # an all-zero row keeps scale 1
+    kd, vd_ = dev(k), dev(v)
+    for p0 in range(0, ctxlen, batch):
+        p1 = min(ctxlen, p0 + batch)
+        pos = torch.arange(p0, p1, dtype=torch.int32, device="cuda")
+        nd.kv_write(ctx, g, blk, 0, pos, kd[p0:p1], vd_[p0:p1])
+    raw = host(blk)
+    kk, kks, vv, vvs = nd.kv_unpack(g, raw)
+    kq, ks = O.quantize_rows(k[:ctxlen], QK)
+    vq, vs = O.quantize_rows(v[:ctxlen], VD)
+    assert np.array_equal(kk.reshape(-1), kq) and np.array_equal(vv.reshape(-1), vq)
+    assert np.array_equal(kks.reshape(-1).view(np.uint32), ks.view(np.uint32))
+    assert np.array_equal(vvs.reshape(-1).view(np.uint32), vs.view(np.uint32))
+    off = nd.kv_offsets(g)
+    used = [(0, KVH * ctxlen * QK), (off["v"], off["v"] + KVH * ctxlen * VD),
+            (off["ks"], off["ks"] + 4 * KVH * ctxlen), (off["vs"], off["vs"] + 4 * KVH * ctxlen)]
+    mask = np.ones(raw.size, bool)
+    for a, b in used:
+        mask[a:b] = False
+    assert not raw[mask].any(), "bytes outside the K/V/scale runs were written"
+    # the ring wraps: the next positions land in slots 0..batch-1 only
+    pos = torch.arange(ctxlen, ctxlen + batch, dtype=torch.int32, device="cuda")
+    nd.kv_write(ctx, g, blk, 0, pos, kd[ctxlen:], vd_[ctxlen:])
+    kk2, kks2, vv2, vvs2 = nd.kv_unpack(g, host(blk))
+    kq2, ks2 = O.quantize_rows(k[ctxlen:], QK)
+    vq2, vs2 = O.quantize_rows(v[ctxlen:], VD)
+    assert np.array_equal(kk2[:batch].reshape(-1), kq2) and np.array_equal(vv2[:batch].reshape(-1), vq2)
+    assert np.array_equal(kks2[:batch].reshape(-1).view(np.uint32), ks2.view(np.uint32))
+    assert np.array_equal(vvs2[:batch].reshape(-1).view(np.uint32), vs2.view(np.uint32))
+    assert np.array_equal(kk2[batch:], kk[batch:]) and np.array_equal(vv2[batch:], vv[batch:])
+    assert np.array_equal(kks2[batch:], kks[batch:]) and np.array_equal(vvs2[batch:], vvs[batch:])
+
+
 def _fill(ctx, rng, H, KVH, QK, VD, cap, npos, count=1):
     """`count` blocks, positions 0..npos-1 written (ring-wrapped at cap)."""
     g = nd.kv_geom(H, KVH, QK, VD, cap)
