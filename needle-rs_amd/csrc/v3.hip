@@ -1063,6 +1063,8 @@ struct nd_v3_model {
     std::vector<Site> sites;
     float *final_norm = nullptr;
     float embed_scale = 1.0f;
+    // RoPE frequencies 1 / theta^(2j / qk), libm's powf (model.rs:378-386)
+    std::vector<float> rope_freq;
     // prepared-input geometry of the projections each fused kernel feeds
     Prep pre_nx{}, pre_h{}, pre_attn{}, pre_x{};
     std::vector<void *> mem;  // every device float/int buffer
@@ -1261,6 +1263,8 @@ int nd_v3_model_create(nd_ctx *ctx, const nd_v3_cfg *cfg, const float *codebook,
     nd_v3_model *m = new (std::nothrow) nd_v3_model;
     if (!m) return nd::fail(ND_ERR_NOMEM, "host allocation failed");
     m->cfg = c;
+    for (int j = 0; j < c.qk_head_dim / 2; ++j)
+        m->rope_freq.push_back(1.0f / nd_powf(c.rope_theta, float(2 * j) / float(c.qk_head_dim)));
     m->device = ctx->device;
     const size_t d = c.d_model, L = c.num_layers, nl = c.mhc_lanes;
     const size_t qd = size_t(c.num_heads) * c.qk_head_dim, kd = size_t(c.num_kv_heads) * c.qk_head_dim;
@@ -1726,12 +1730,11 @@ int step_impl(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *
                 const bool valid = pos + 1 >= c.orders[oi];
                 h_rows[size_t(i) * nt + table] = valid ? int32_t(uint32_t(table) * uint32_t(c.e_slots) + slot) : -1;
             }
-        // model.rs:378-394 RoPE angles for this position
+        // model.rs:378-394 RoPE angles for this position, libm's cosf/sinf
         for (int j = 0; j < half; ++j) {
-            const float freq = 1.0f / std::pow(c.rope_theta, float(2 * j) / float(c.qk_head_dim));
-            const float angle = float(pos) * freq;
-            h_rope[size_t(i) * 2 * half + j] = std::cos(angle);
-            h_rope[size_t(i) * 2 * half + half + j] = std::sin(angle);
+            const float angle = float(pos) * m->rope_freq[j];
+            h_rope[size_t(i) * 2 * half + j] = nd_cosf(angle);
+            h_rope[size_t(i) * 2 * half + half + j] = nd_sinf(angle);
         }
         // cache.rs:291-331 ensure + span per layer
         for (int li = 0; li < L; ++li) {

@@ -554,15 +554,16 @@ void or_v3_norm_and_rope(float *buf, const float *scale, const float *cs, const 
     }
 }
 
-/* model.rs:378-394 */
+/* model.rs:378-394, with math.rs's libm powf / cos / sin (or_powf, or_cosf,
+ * or_sinf: the msun algorithms libm 0.2.16 carries). */
 void or_v3_rope_at(const or_v3_cfg *c, size_t pos, float *cs, float *sn)
 {
     size_t half = c->qk_head_dim / 2;
     for (size_t i = 0; i < half; i++) {
-        float freq = 1.0f / powf(c->rope_theta, (float)(2 * i) / (float)c->qk_head_dim);
+        float freq = 1.0f / or_powf(c->rope_theta, (float)(2 * i) / (float)c->qk_head_dim);
         float angle = (float)pos * freq;
-        cs[i] = cosf(angle);
-        sn[i] = sinf(angle);
+        cs[i] = or_cosf(angle);
+        sn[i] = or_sinf(angle);
     }
 }
 
