@@ -222,6 +222,26 @@ int nd_attend_step_i8(nd_ctx *ctx, const nd_kv_geom *g, const void *kv,
                       const int32_t *hi, const float *q, float scale,
                       int quant_query, float *out);
 
+/*
+ * nd_attend_step_i8 without any allocation, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  No reference counterpart.
+ * The same kernels and the same results, bit for bit; the split-K
+ * partials live in a fixed 4 MiB device array per GPU (held until the
+ * process ends) instead of the context workspace.  A call whose partials
+ * need more -- count * num_heads * splits * (v_head_dim + 2) floats above
+ * 1048576 -- fails with ND_ERR_ARG.  The span is split only while
+ * count * num_kv_heads < 4 * CUs, so the partials stay below
+ * 8 * CUs * (num_heads / num_kv_heads) * (v_head_dim + 2) floats: on a
+ * 256-CU MI355X only 8 query heads per kv head can exceed the array.
+ * Every call on a GPU shares that GPU's array: calls that overlap on one
+ * GPU (two streams, or two threads) race.
+ */
+int nd_attend_step_i8_noalloc(nd_ctx *ctx, const nd_kv_geom *g, const void *kv,
+                              size_t kv_stride, size_t count, const int32_t *lo,
+                              const int32_t *hi, const float *q, float scale,
+                              int quant_query, float *out);
+
 /* As nd_attend_step_i8, bit-identical to attend_step over the int8 view
  * (attention.rs:327-377): each score is one dot chain over the head dim,
  * scaled by the key scale and then `scale`; the softmax sum and every

@@ -94,6 +94,10 @@ static int ctx_create(int device, bool own, void *stream, nd_ctx **out)
         return nd::hip_fail(e, "hipGetDeviceProperties");
     }
     c->num_cus = prop.multiProcessorCount;
+    if (int rc = nd::noalloc_setup(device)) {
+        delete c;
+        return rc;
+    }
     if (!own) {
         c->stream = static_cast<hipStream_t>(stream);
     } else {

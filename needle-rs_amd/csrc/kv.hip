@@ -16,6 +16,40 @@
 #include "nd_kv_internal.h"
 
 #include <cmath>
+#include <mutex>
+
+// Split-K partials of nd_attend_step_i8_noalloc: one fixed device array per
+// GPU (every device the library runs on holds its copy until the process
+// ends).  Host code never passes `scratch` itself to a kernel: its name is a
+// host-side stand-in, and the device address comes from hipGetSymbolAddress
+// once per device (nd::noalloc_setup, called when a context is created).
+static constexpr size_t kNoAllocScratchFloats = size_t(1) << 20;  // 4 MiB
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float *g_scratch[kMaxDevices] = {};
+}  // namespace
+
+namespace nd {
+
+int noalloc_setup(int device)
+{
+    if (device < 0 || device >= kMaxDevices)
+        return fail(ND_ERR_ARG, "device %d beyond the %d the no-allocation scratch covers", device,
+                    kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch[device]) return ND_OK;
+    void *p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (!p) return fail(ND_ERR_HIP, "hipGetSymbolAddress(scratch) gave a null address");
+    g_scratch[device] = static_cast<float *>(p);
+    return ND_OK;
+}
+
+}  // namespace nd
 
 namespace {
 
@@ -474,9 +508,15 @@ int nd_kv_write(nd_ctx *ctx, const nd_kv_geom *g, void *kv, size_t kv_stride, si
     return nd::check_launch("kv_write");
 }
 
-int nd_attend_step_i8(nd_ctx *ctx, const nd_kv_geom *g, const void *kv, size_t kv_stride,
-                      size_t count, const int32_t *lo, const int32_t *hi, const float *q,
-                      float scale, int quant_query, float *out)
+}  // extern "C"
+
+namespace {
+
+// nd_attend_step_i8 with its split-K partials either in the context's
+// growable workspace (fixed == nullptr) or in `fixed`, `fixed_floats` long.
+int attend_i8(nd_ctx *ctx, const nd_kv_geom *g, const void *kv, size_t kv_stride, size_t count,
+              const int32_t *lo, const int32_t *hi, const float *q, float scale, int quant_query,
+              float *out, float *fixed, size_t fixed_floats)
 {
     if (int rc = nd::enter(ctx)) return rc;
     if (int rc = check_geom(g)) return rc;
@@ -503,7 +543,15 @@ int nd_attend_step_i8(nd_ctx *ctx, const nd_kv_geom *g, const void *kv, size_t k
         void *wsp = nullptr;
         const size_t n_o = count * size_t(g->num_heads) * splits * g->v_head_dim;
         const size_t n_ml = count * size_t(g->num_heads) * splits * 2;
-        if (int rc = nd::workspace(ctx, (n_o + n_ml) * sizeof(float), &wsp)) return rc;
+        if (fixed) {
+            ND_REQUIRE(n_o + n_ml <= fixed_floats,
+                       "split-K partials need %zu floats (%zu queries x %d heads x %zu splits x "
+                       "(%d + 2)); the no-allocation scratch holds %zu",
+                       n_o + n_ml, count, g->num_heads, splits, g->v_head_dim, fixed_floats);
+            wsp = fixed;
+        } else if (int rc = nd::workspace(ctx, (n_o + n_ml) * sizeof(float), &wsp)) {
+            return rc;
+        }
         po = static_cast<float *>(wsp);
         pml = po + n_o;
     }
@@ -517,6 +565,31 @@ int nd_attend_step_i8(nd_ctx *ctx, const nd_kv_geom *g, const void *kv, size_t k
         return nd::check_launch("attn_combine");
     }
     return ND_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int nd_attend_step_i8(nd_ctx *ctx, const nd_kv_geom *g, const void *kv, size_t kv_stride,
+                      size_t count, const int32_t *lo, const int32_t *hi, const float *q,
+                      float scale, int quant_query, float *out)
+{
+    return attend_i8(ctx, g, kv, kv_stride, count, lo, hi, q, scale, quant_query, out, nullptr, 0);
+}
+
+int nd_attend_step_i8_noalloc(nd_ctx *ctx, const nd_kv_geom *g, const void *kv, size_t kv_stride,
+                              size_t count, const int32_t *lo, const int32_t *hi, const float *q,
+                              float scale, int quant_query, float *out)
+{
+    if (!ctx) return nd::fail(ND_ERR_ARG, "null context");
+    float *p = ctx->device >= 0 && ctx->device < kMaxDevices ? g_scratch[ctx->device] : nullptr;
+    if (!p) return nd::fail(ND_ERR_HIP, "no-allocation scratch of device %d was not set up",
+                            ctx->device);
+    // Every partial the merge reads is written by the same call first, so
+    // the array's previous contents never matter and nothing is cleared.
+    return attend_i8(ctx, g, kv, kv_stride, count, lo, hi, q, scale, quant_query, out, p,
+                     kNoAllocScratchFloats);
 }
 
 }  // extern "C"

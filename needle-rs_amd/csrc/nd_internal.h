@@ -37,6 +37,10 @@ int enter(nd_ctx *ctx);
 // Ensures the context workspace holds at least `bytes`.
 int workspace(nd_ctx *ctx, size_t bytes, void **out);
 
+// Looks up, once per device and with that device current, the device
+// address of the no-allocation entry point's scratch array.
+int noalloc_setup(int device);
+
 // Checks the launch that was just enqueued.
 int check_launch(const char *kernel);
 

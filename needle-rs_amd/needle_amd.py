@@ -79,6 +79,8 @@ _SIGS = [
                                     C.c_float, C.c_int, _vp]),
     ("nd_attend_step_i8_exact", C.c_int, [_vp, C.POINTER(KvGeom), _vp, _sz, _sz, _vp, _vp, _vp,
                                           C.c_float, C.c_int, _vp]),
+    ("nd_attend_step_i8_noalloc", C.c_int, [_vp, C.POINTER(KvGeom), _vp, _sz, _sz, _vp, _vp, _vp,
+                                            C.c_float, C.c_int, _vp]),
     ("nd_v3_model_create", C.c_int, [_vp, _vp, _vp, _sz, _vp, _sz, C.POINTER(_vp)]),
     ("nd_v3_model_free", None, [_vp]),
     ("nd_v3_logit_rows", _sz, [_vp]),
@@ -388,8 +390,10 @@ def kv_write(ctx, g, kv, kv_stride, pos_i32, k, v):
 
 
 def attend_step_i8(ctx, g, kv, kv_stride, lo_i32, hi_i32, q, scale=None, quant_query=False,
-                   out=None, exact=False):
-    """exact=True: nd_attend_step_i8_exact, bit-identical to attend_step."""
+                   out=None, exact=False, noalloc=False):
+    """exact=True: nd_attend_step_i8_exact, bit-identical to attend_step.
+    noalloc=True: nd_attend_step_i8_noalloc (no device allocation; split-K
+    partials in the library's fixed per-GPU array)."""
     torch = _torch()
     count = lo_i32.numel()
     if scale is None:
@@ -397,6 +401,10 @@ def attend_step_i8(ctx, g, kv, kv_stride, lo_i32, hi_i32, q, scale=None, quant_q
     if out is None:
         out = torch.empty(count, g.num_heads * g.v_head_dim, dtype=torch.float32, device=q.device)
     fn = lib().nd_attend_step_i8_exact if exact else lib().nd_attend_step_i8
+    if noalloc:
+        if exact:
+            raise ValueError("the no-allocation entry point is the tolerance-order kernel")
+        fn = lib().nd_attend_step_i8_noalloc
     blocks = kv_block_bytes(g) + (count - 1) * kv_stride if count else 0
     i32, f32 = torch.int32, torch.float32
     _check(fn(ctx.h, C.byref(g), _arg(kv, torch.uint8, "kv", blocks), kv_stride, count,
