@@ -14,14 +14,15 @@ Also reported ("secondary"):
   - the Cactus-Quants (Format A) decode GEMV, tolerance and reference order,
     streaming and at the shipped shapes;
   - the Format B prefill GEMM on bf16 MFMA;
-  - the Needle-3 forward (shipped geometry, random init, int8 KV cache),
-    bit-identical to the CPU oracle: one session with a 128-token prompt and
-    256 greedy tokens, and 64 sessions each prefilled with 2048 tokens then
-    128 greedy tokens in lockstep ("decode tok/s @ ctx2048 int8 KV").
+  - the Needle-3 forward (shipped geometry, random init, int8 KV cache):
+    one session with a 128-token prompt and 256 greedy tokens, and 64
+    sessions each prefilled with 2048 tokens then 128 greedy tokens in
+    lockstep ("decode tok/s @ ctx2048 int8 KV"), whose tokens are then
+    checked (untimed) against batch-1 device runs and the oracle.
 
-cpu_baseline: the oracle's Format-B GEMV (the closed form, fp32, row-parallel
-with OpenMP like the reference's rayon row bands) on the host cores, on a
-bounded sample of the same workload.
+cpu_baseline: the oracle (the reference's CPU arithmetic restated in C) on
+the host cores, 1 thread and all threads, on bounded samples of configs
+1-5; the headline value is config 1's GEMV at all threads.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 """
@@ -69,6 +70,8 @@ def parse():
     p.add_argument("--no-forward", action="store_true", help="skip the Needle-3 forward runs")
     p.add_argument("--forward-sessions", type=int, default=64)
     p.add_argument("--forward-ctx", type=int, default=2048)
+    p.add_argument("--no-check", action="store_true",
+                   help="skip the untimed token check of the multi-session forward")
     p.add_argument("--only", choices=["gemv", "attn", "forward", "gemm", "cqa"], default=None,
                    help="run one workload only, without the batch-1 latency probes "
                         "(for per-kernel profiles)")
@@ -139,32 +142,156 @@ def timed_loop(torch, fn, steps, warmup, min_warm_s=None):
     return start.elapsed_time(end) / steps  # ms
 
 
-def cpu_baseline(seconds=12.0):
-    """Oracle Format-B GEMV on the host: 64 distinct copies (151 MB), looped
-    until `seconds` have elapsed, OpenMP over the rows."""
+def _threads_all():
+    """Host threads this process may use: its CPU affinity, capped by
+    OMP_NUM_THREADS when that is set (the OpenMP default the oracle uses)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return max(1, n)
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def _time_for(fn, seconds, min_calls=1):
+    calls, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        calls += 1
+        el = time.perf_counter() - t0
+        if el >= seconds and calls >= min_calls:
+            return calls, el
+
+
+def cpu_baseline(sec=2.5):
+    """The reference's CPU path, as the oracle restates it, on the host cores
+    of this run: 1 thread and all threads, each on a bounded sample of the
+    same workloads the GPU lines run.  Threads split the work as the
+    reference's rayon pool would (row bands past cq.rs's size rules; one
+    session per thread for independent sessions, as a server runs one
+    V3Cache per session)."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
+    import v3_synth as S
+    T = _threads_all()
     rng = np.random.default_rng(1)
+    out = {}
+
+    # config 1: the codebook GEMV, 64 distinct copies (151 MB)
     copies = 64
     W = rng.integers(0, 256, size=(copies, GEMV_OUT, GEMV_IN), dtype=np.uint8)
     CB = rng.normal(0, 0.02, size=(copies, GEMV_OUT // 64, 256)).astype(np.float32)
     X = rng.normal(size=(copies, GEMV_IN)).astype(np.float32)
     y = np.zeros(GEMV_OUT, np.float32)
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    O.cb8_gemv_omp(W[0], CB[0], X[0], y)  # warm
-    calls, t0 = 0, time.perf_counter()
-    while True:
-        i = calls % copies
-        O.cb8_gemv_omp(W[i], CB[i], X[i], y)
-        calls += 1
-        el = time.perf_counter() - t0
-        if el >= seconds and calls >= copies:
-            break
-    return {"value": round(calls * GEMV_BYTES / el / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "kind": "port",
-            "sample": f"{calls} GEMVs of 3072x768 u8 over 64 distinct weight copies in "
-                      f"{el:.1f} s (oracle or_cb8_gemv_omp, {threads} OpenMP threads)"}
+    it = [0]
+
+    def gemv(par):
+        i = it[0] % copies
+        it[0] += 1
+        if par:
+            O.cb8_gemv_omp(W[i], CB[i], X[i], y)
+        else:
+            O.lib().or_cb8_gemv(W[i], CB[i], X[i], y, GEMV_OUT, GEMV_IN)
+    gemv(True)
+    n1, e1 = _time_for(lambda: gemv(False), sec, copies // 8)
+    nT, eT = _time_for(lambda: gemv(True), 2 * sec, copies)
+    g1, gT = n1 * GEMV_BYTES / e1 / 1e9, nT * GEMV_BYTES / eT / 1e9
+    del W, CB, X
+    out["config1_gemv_GBps"] = {"1_thread": round(g1, 3), "all_threads": round(gT, 3),
+                                "sample": f"{n1} and {nT} GEMVs of 3072x768 over 64 copies"}
+
+    # config 2: the Format B GEMM, M 512 x K 768, N 3072 and 768
+    gemm = {}
+    for N in (3072, 768):
+        x = rng.normal(size=(512, 768)).astype(np.float32)
+        w = rng.integers(0, 256, size=(N, 768), dtype=np.uint8)
+        cb = rng.normal(0, 0.02, size=(N // 64, 256)).astype(np.float32)
+        yy = np.zeros((512, N), np.float32)
+        flops = 2.0 * 512 * 768 * N
+        a, ea = _time_for(lambda: O.cb8_gemm_omp(x, w, cb, 1, yy), sec / 2)
+        b, eb = _time_for(lambda: O.cb8_gemm_omp(x, w, cb, T, yy), sec / 2)
+        gemm[f"m512_n{N}_k768_GFLOPs"] = {"1_thread": round(a * flops / ea / 1e9, 2),
+                                          "all_threads": round(b * flops / eb / 1e9, 2)}
+    out["config2_gemm"] = gemm
+
+    # config 3: int8-KV decode attention at ctx 2048, 12 heads x 64 (MHA),
+    # over 64 sessions' own caches (214 MB)
+    H, D, ctxn, ns = ATT_H, ATT_D, ATT_CTX, 64
+    kq = rng.integers(-127, 128, size=(ns, ctxn * H * D), dtype=np.int8)
+    vq = rng.integers(-127, 128, size=(ns, ctxn * H * D), dtype=np.int8)
+    ks = (rng.random((ns, ctxn * H)) * 0.03 + 1e-3).astype(np.float32)
+    vs = (rng.random((ns, ctxn * H)) * 0.03 + 1e-3).astype(np.float32)
+    q = rng.normal(size=(ns, H * D)).astype(np.float32)
+    o = np.zeros((ns, H * D), np.float32)
+
+    def att(threads, n):
+        O.attend_step_i8_sessions(q[:n], kq[:n], ks[:n], vq[:n], vs[:n], ctxn, 0, ctxn - 1,
+                                  H, H, D, D, threads, o[:n])
+    a, ea = _time_for(lambda: att(1, 8), sec / 2)
+    b, eb = _time_for(lambda: att(T, ns), sec / 2)
+    out["config3_attention_ctx2048_GBps"] = {
+        "1_thread": round(a * 8 * ATT_BYTES / ea / 1e9, 3),
+        "all_threads": round(b * ns * ATT_BYTES / eb / 1e9, 3),
+        "sample": f"{a} x 8 and {b} x {ns} session decodes (one session per thread)"}
+    del kq, vq, ks, vs
+
+    # config 4: one session's decode step on the shipped geometry after a
+    # 128-token prompt (the reference's split rules: only the LM head splits)
+    g, recs = S.build_records(None, seed=0)
+    om = O.V3Model(g, recs, S.CODEBOOK)
+    prompt = S.prompt_tokens(128, 4)
+    cache = om.new_cache(128 + 64, True)
+    O.set_threads(T, O.SPLIT_ALL)  # prefill the prompt quickly (same bits)
+    lg = None
+    for t in prompt:
+        lg = cache.decode_step(int(t))
+    res4, done = {}, 0
+    for name, th in (("1_thread", 1), ("all_threads", T)):
+        O.set_threads(th, O.SPLIT_REFERENCE)
+
+        def dec():
+            nonlocal lg
+            lg = cache.decode_step(int(np.argmax(lg)))
+        n, e = _time_for(dec, sec / 2, 4)
+        done += n
+        res4[name] = round(e / n * 1e3, 2)
+    O.set_threads(1, O.SPLIT_REFERENCE)
+    out["config4_decode_ms_per_token"] = dict(res4, sample=f"{done} greedy steps at positions "
+                                              f"128..{128 + done} after a 128-token prompt")
+
+    # config 5: 64 sessions at ctx 2048, one session per thread; the caches
+    # are put at position 2048 with seeded contents (the per-step work of a
+    # prefilled session, without prefilling 131k positions on the CPU)
+    ns = 64
+    caches = [om.new_cache(2048 + 128, True) for _ in range(ns)]
+    for i, c in enumerate(caches):
+        c.fill_synthetic(2048, 1000 + i)
+    toks = np.array(S.prompt_tokens(ns, 9), np.uint32)
+    a, ea = _time_for(lambda: O.v3_decode_sessions(om, caches[:4], toks[:4], 1), sec / 2)
+    b, eb = _time_for(lambda: O.v3_decode_sessions(om, caches, toks, T), sec / 2)
+    out["config5_sessions64_ctx2048_tok_per_s"] = {
+        "1_thread": round(a * 4 / ea, 2), "all_threads": round(b * ns / eb, 2),
+        "sample": f"{a} x 4 and {b} x {ns} session steps at positions 2048+ (synthetic cache "
+                  "contents at the real spans)"}
+    del caches
+    return {"value": round(gT, 3), "unit": "GB/s", "cores": T, "kind": "port",
+            "sample": f"config 1: {nT} GEMVs of 3072x768 u8 over 64 distinct weight copies in "
+                      f"{eT:.1f} s (oracle or_cb8_gemv_omp, {T} OpenMP threads)",
+            "value_1_thread": round(g1, 3), "nproc": os.cpu_count(), "cpu_model": _cpu_model(),
+            "configs": out}
 
 
 BF16_MFMA_PEAK_TFLOPS = 2500.0
@@ -350,20 +477,26 @@ def exact_attention_runs(torch, nd, ctx, gen):
     return out
 
 
-def forward_runs(torch, nd, ctx, sessions, ctx_len, cpu_tokens=8):
+def forward_runs(torch, nd, ctx, sessions, ctx_len, check=True):
     """The Needle-3 forward on the device: batch 1 (128-token prompt, 256
     greedy steps) and `sessions` sessions prefilled with `ctx_len` tokens
     then 128 greedy steps.  Wall-clock over host-driven steps, each greedy
-    step ending with its tokens back on the host."""
+    step ending with its tokens back on the host.  Then, untimed, the
+    multi-session tokens are checked: sessions 0 and sessions-1 against
+    batch-1 device runs and against the oracle's decode_step over every
+    position."""
     import numpy as np
     import v3_synth as S
     g, recs = S.build_records(None, seed=0)
     model = nd.V3Model(ctx, g, recs, S.CODEBOOK)
     out = {}
 
-    def run(B, prompt_len, steps, chunk):
+    def run(B, prompt_len, steps, chunk, prompts=None):
         batch = nd.V3Batch(model, B, max_len=prompt_len + steps, max_chunk=chunk)
-        prompts = np.stack([S.prompt_tokens(prompt_len, 100 + i) for i in range(B)]).astype(np.int32)
+        if prompts is None:
+            prompts = np.stack([S.prompt_tokens(prompt_len, 100 + i) for i in range(B)])
+        prompts = np.ascontiguousarray(prompts, np.int32)
+        toks = []
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         nxt = None
@@ -374,15 +507,16 @@ def forward_runs(torch, nd, ctx, sessions, ctx_len, cpu_tokens=8):
         t_pre = time.perf_counter() - t0
         t0 = time.perf_counter()
         for _ in range(steps):
+            toks.append(nxt)
             nxt = batch.step(nxt)
         t_dec = time.perf_counter() - t0
         batch.close()
-        return t_pre, t_dec
+        return t_pre, t_dec, np.stack(toks, axis=1)
 
     # warm, untimed: code objects, and about half a second of steps so the
     # clocks have left their idle state before the timed decode
     run(1, 16, 240, 16)
-    t_pre, t_dec = run(1, 128, 256, 128)
+    t_pre, t_dec, _ = run(1, 128, 256, 128)
     out["batch1_prompt128_greedy256"] = {
         "workload": "shipped Needle-3 geometry (20 layers, d 768, 12 q / 2 kv heads, vocab "
                     "8192), random init, Cactus-Quants weights, int8 KV; one session, "
@@ -392,32 +526,55 @@ def forward_runs(torch, nd, ctx, sessions, ctx_len, cpu_tokens=8):
         "decode_ms_per_token": round(t_dec / 256 * 1e3, 3),
         "decode_tok_per_s": round(256 / t_dec, 1),
     }
-    t_pre, t_dec = run(sessions, ctx_len, 128, 32)
-    out[f"sessions{sessions}_ctx{ctx_len}_greedy128"] = {
+    steps = 128
+    t_pre, t_dec, toks = run(sessions, ctx_len, steps, 32)
+    key = f"sessions{sessions}_ctx{ctx_len}_greedy{steps}"
+    out[key] = {
         "workload": f"{sessions} sessions of the same model in lockstep, each prefilled with "
-                    f"{ctx_len} uniform prompt tokens (32 positions per pass), then 128 greedy "
+                    f"{ctx_len} uniform prompt tokens (32 positions per pass), then {steps} greedy "
                     "steps; projections batched over sessions, attention per session",
-        "decode_tok_per_s": round(sessions * 128 / t_dec, 1),
-        "decode_ms_per_step": round(t_dec / 128 * 1e3, 3),
+        "decode_tok_per_s": round(sessions * steps / t_dec, 1),
+        "decode_ms_per_step": round(t_dec / steps * 1e3, 3),
         "prefill_tok_per_s": round(sessions * ctx_len / t_pre, 1),
     }
-    # the oracle's decode step on one host core, for scale
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import oracle as O
-    om = O.V3Model(g, recs, S.CODEBOOK)
-    cache = om.new_cache(64, True)
-    toks = S.prompt_tokens(cpu_tokens, 7)
-    cache.decode_step(toks[0])
-    t0 = time.perf_counter()
-    for t in toks[1:]:
-        cache.decode_step(t)
-    out["cpu_oracle_decode_ms_per_token"] = round((time.perf_counter() - t0) / (cpu_tokens - 1) * 1e3, 2)
-    out["cpu_oracle_note"] = ("the oracle's scalar decode step (1 host core, reference float "
-                              "order) on the same model; the reference publishes 8.72 ms/token "
-                              "for its own multi-threaded NEON build on an M5 Max")
-    out["bit_identical_to_oracle"] = "yes (tests/test_gpu_v3.py)"
+    if check:
+        out[key]["check"] = forward_check(model, g, recs, toks, ctx_len, steps, run)
     model.close()
     return out
+
+
+def forward_check(model, g, recs, toks, ctx_len, steps, run):
+    """The timed multi-session run's greedy tokens for sessions 0 and B-1:
+    equal to a batch-1 device run of the session, and to the oracle's
+    decode_step over all ctx_len + steps positions (two host threads, the
+    oracle splitting rows and heads across the rest, which keeps its bits)."""
+    import threading
+    import numpy as np
+    import v3_synth as S
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    B = toks.shape[0]
+    picks = sorted({0, B - 1})
+    t0 = time.perf_counter()
+    om = O.V3Model(g, recs, S.CODEBOOK)
+    O.set_threads(max(1, _threads_all() // len(picks)), O.SPLIT_ALL)
+    want = {}
+
+    def oracle(i):
+        want[i] = O.v3_generate(om, S.prompt_tokens(ctx_len, 100 + i), steps,
+                                hint=ctx_len + steps)[0].astype(np.int32)
+    th = [threading.Thread(target=oracle, args=(i,)) for i in picks]
+    for t in th:
+        t.start()
+    batch1 = {i: run(1, ctx_len, steps, 32, S.prompt_tokens(ctx_len, 100 + i)[None])[2][0]
+              for i in picks}
+    for t in th:
+        t.join()
+    O.set_threads(1, O.SPLIT_REFERENCE)
+    return {"sessions": picks, "tokens_per_session": steps,
+            "equal_to_batch1_device_run": all(np.array_equal(batch1[i], toks[i]) for i in picks),
+            "equal_to_oracle": all(np.array_equal(want[i], toks[i]) for i in picks),
+            "seconds": round(time.perf_counter() - t0, 1)}
 
 
 def main():
@@ -451,7 +608,7 @@ def main():
         return
     if args.only == "forward":
         out = {"secondary": {"needle3_forward": forward_runs(
-            torch, nd, ctx, args.forward_sessions, args.forward_ctx)}}
+            torch, nd, ctx, args.forward_sessions, args.forward_ctx, not args.no_check)}}
         ctx.close()
         print(json.dumps(out))
         return
@@ -573,7 +730,7 @@ def main():
 
     if not args.no_secondary and not args.no_forward and args.only is None:
         result.setdefault("secondary", {})["needle3_forward"] = forward_runs(
-            torch, nd, ctx, args.forward_sessions, args.forward_ctx)
+            torch, nd, ctx, args.forward_sessions, args.forward_ctx, not args.no_check)
 
     if args.calibrate_copy:
         # A plain device copy of exactly 1 GiB: the byte counters' reference.

@@ -1115,6 +1115,27 @@ void or_cb8_gemv_omp(const uint8_t *w, const float *cb, const float *x,
     }
 }
 
+/* The closed-form GEMM with output rows split across threads in bands,
+ * as the reference's matmul_rows_par splits its row bands (cq.rs:494-544);
+ * each output keeps or_cb8_gemm's k-order sum, so the bits are the same. */
+void or_cb8_gemm_omp(const float *x, const uint8_t *w, const float *cb, float *y,
+                     size_t m, size_t out, size_t in, int threads)
+{
+    long n = (long)out;
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+    for (long o = 0; o < n; o++) {
+        const float *c = cb + ((size_t)o / 64) * 256;
+        const uint8_t *row = w + (size_t)o * in;
+        for (size_t i = 0; i < m; i++) {
+            const float *xi = x + i * in;
+            float acc = 0.0f;
+            for (size_t k = 0; k < in; k++)
+                acc += c[row[k]] * xi[k];
+            y[i * out + (size_t)o] = acc;
+        }
+    }
+}
+
 void or_cb8_gemv_f64(const uint8_t *w, const float *cb, const float *x,
                      double *y, size_t out, size_t in)
 {
@@ -1372,6 +1393,29 @@ static void attend_step_impl(const float *q, const float *kf, const float *vf,
         }
         free(scores);
     }
+}
+
+/* `count` independent sessions' attend_step over their own int8 caches
+ * (session i's at k + i*slots*kvh*qk and likewise), sessions split across
+ * threads as a server runs one V3Cache per session on its pool
+ * (v3_engine.rs:547-560); each session's arithmetic is attend_step's. */
+void or_attend_step_i8_sessions(size_t count, const float *q, const int8_t *k,
+                                const float *k_scale, const int8_t *v,
+                                const float *v_scale, size_t slots, size_t lo, size_t hi,
+                                const or_attn_dims *d, float *out, int threads)
+{
+    size_t H = d->num_kv_heads, qn = d->num_heads * d->qk_head_dim;
+    size_t on = d->num_heads * d->v_head_dim;
+    int saved = or_threads;
+    or_threads = 1; /* one session per thread; its heads stay serial */
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(dynamic, 1)
+    for (long i = 0; i < (long)count; i++) {
+        size_t s = (size_t)i;
+        attend_step_impl(q + s * qn, NULL, NULL, k + s * slots * H * d->qk_head_dim,
+                         k_scale + s * slots * H, v + s * slots * H * d->v_head_dim,
+                         v_scale + s * slots * H, slots, lo, hi, d, out + s * on);
+    }
+    or_threads = saved;
 }
 
 void or_attend_step_f32(const float *q, const float *k, const float *v,

@@ -141,6 +141,8 @@ int or_get_threads(void);
 
 void or_cb8_gemv_omp(const uint8_t *w, const float *cb, const float *x,
                      float *y, size_t out, size_t in);
+void or_cb8_gemm_omp(const float *x, const uint8_t *w, const float *cb, float *y,
+                     size_t m, size_t out, size_t in, int threads);
 
 /* ---- v3/cache.rs ------------------------------------------------------ */
 void or_fake_quant_vec(float *x, size_t n, uint32_t bits);
@@ -176,6 +178,10 @@ void or_attend_step_f32(const float *q, const float *k, const float *v,
 void or_attend_step_i8(const float *q, const int8_t *k, const float *k_scale,
                        const int8_t *v, const float *v_scale, size_t slots,
                        size_t lo, size_t hi, const or_attn_dims *d, float *out);
+void or_attend_step_i8_sessions(size_t count, const float *q, const int8_t *k,
+                                const float *k_scale, const int8_t *v,
+                                const float *v_scale, size_t slots, size_t lo, size_t hi,
+                                const or_attn_dims *d, float *out, int threads);
 void or_attend_f32(const float *q, const float *k, const float *v,
                    const or_attn_dims *d, size_t window, float *out);
 void or_attend_i8(const float *q, const int8_t *k, const float *k_scale,

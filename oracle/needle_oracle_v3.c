@@ -752,6 +752,76 @@ void or_v3_decode_step(const or_v3_model *m, or_v3_cache *cache, uint32_t token,
     free(mlp_out); free(y);
 }
 
+/* One decode step for each of `n` sessions (V3Model::decode_step per
+ * session, v3/model.rs:150-375), sessions split across `threads` as a
+ * server runs one V3Cache per session on its pool (v3_engine.rs:547-560);
+ * each session's step runs serially.  logits: [n][logit rows]. */
+void or_v3_decode_sessions(const or_v3_model *m, or_v3_cache **caches, const uint32_t *tokens,
+                           size_t n, float *logits, int threads)
+{
+    size_t rows = m->cfg.out_vocab ? m->cfg.out_vocab : m->cfg.vocab_size;
+    int saved = or_get_threads();
+    or_set_threads(1, OR_SPLIT_REFERENCE);
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(dynamic, 1)
+    for (long i = 0; i < (long)n; i++)
+        or_v3_decode_step(m, caches[i], tokens[i], logits + (size_t)i * rows);
+    or_set_threads(saved, OR_SPLIT_REFERENCE);
+}
+
+static uint64_t splitmix64(uint64_t *s)
+{
+    uint64_t z = (*s += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+/* For timing only: put a fresh int8 cache, made with a hint of at least
+ * `pos` + the steps to be timed (so its rings need not grow), at position
+ * `pos` as if `pos` tokens had been decoded -- every slot's codes and
+ * scales, the conv and Engram tails and the token history filled from a
+ * seeded generator -- so that a decode step's work (spans, reads) is that
+ * of a session at `pos` without prefilling it. */
+void or_v3_cache_fill_synthetic(or_v3_cache *k, size_t pos, uint64_t seed)
+{
+    const or_v3_cfg *c = &k->cfg;
+    uint64_t st = seed;
+    for (size_t li = 0; li < c->num_layers; li++) {
+        or_ring *r = k->rings[li];
+        size_t kn = r->slots * r->num_kv_heads * r->qk_head_dim;
+        size_t vn = r->slots * r->num_kv_heads * r->v_head_dim;
+        for (size_t i = 0; i < kn; i++)
+            r->kq[i] = (int8_t)((int)(splitmix64(&st) % 255) - 127);
+        for (size_t i = 0; i < vn; i++)
+            r->vq[i] = (int8_t)((int)(splitmix64(&st) % 255) - 127);
+        for (size_t i = 0; i < r->slots * r->num_kv_heads; i++) {
+            r->k_scale[i] = 0.01f + (float)(splitmix64(&st) % 1000) * 1e-5f;
+            r->v_scale[i] = 0.01f + (float)(splitmix64(&st) % 1000) * 1e-5f;
+        }
+    }
+    size_t qd = c->num_heads * c->qk_head_dim, kd = c->num_kv_heads * c->qk_head_dim;
+    size_t vd = c->num_kv_heads * c->v_head_dim, tt = c->qkv_conv_taps ? c->qkv_conv_taps - 1 : 0;
+    for (size_t li = 0; li < c->num_layers; li++) {
+        for (size_t i = 0; i < tt * qd; i++)
+            k->q_tail[li][i] = (float)(splitmix64(&st) % 2001) * 1e-3f - 1.0f;
+        for (size_t i = 0; i < tt * kd; i++)
+            k->k_tail[li][i] = (float)(splitmix64(&st) % 2001) * 1e-3f - 1.0f;
+        for (size_t i = 0; i < tt * vd; i++)
+            k->v_tail[li][i] = (float)(splitmix64(&st) % 2001) * 1e-3f - 1.0f;
+    }
+    size_t reach = (c->e_conv_taps ? c->e_conv_taps - 1 : 0) * c->e_conv_dilation;
+    for (size_t s = 0; s < c->n_sites; s++)
+        for (size_t i = 0; i < reach * c->d_model; i++)
+            k->engram_tail[s][i] = (float)(splitmix64(&st) % 2001) * 1e-3f - 1.0f;
+    size_t keep = max_order(c);
+    if (keep > OR_V3_MAX_HIST)
+        keep = OR_V3_MAX_HIST;
+    k->n_tokens = pos < keep ? pos : keep;
+    for (size_t i = 0; i < k->n_tokens; i++)
+        k->tokens[i] = 3 + (uint32_t)(splitmix64(&st) % (c->vocab_size - 3));
+    k->pos = pos;
+}
+
 /* v3_engine.rs:410-420: strict '>' so the first maximum wins. */
 uint32_t or_argmax(const float *x, size_t n)
 {

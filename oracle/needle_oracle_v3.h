@@ -98,6 +98,9 @@ void or_v3_decode_step(const or_v3_model *m, or_v3_cache *cache, uint32_t token,
 void or_v3_generate(const or_v3_model *m, or_v3_cache *cache, const uint32_t *prompt,
                     size_t n_prompt, size_t steps, uint32_t *out_tokens, float *out_margin);
 uint32_t or_argmax(const float *x, size_t n);
+void or_v3_decode_sessions(const or_v3_model *m, or_v3_cache **caches, const uint32_t *tokens,
+                           size_t n, float *logits, int threads);
+void or_v3_cache_fill_synthetic(or_v3_cache *k, size_t pos, uint64_t seed);
 
 void or_sinkhorn(float *m, size_t n);
 void or_hada_blocks(size_t n, size_t *ba, size_t *bb);

@@ -90,6 +90,9 @@ def lib():
         L.or_get_threads.restype = C.c_int
         L.or_cb8_gemv_f64.argtypes = [_u8p, _f32p, _f32p, _f64p, _sz, _sz]
         L.or_cb8_gemm.argtypes = [_f32p, _u8p, _f32p, _f32p, _sz, _sz, _sz]
+        L.or_cb8_gemm_omp.argtypes = [_f32p, _u8p, _f32p, _f32p, _sz, _sz, _sz, C.c_int]
+        L.or_attend_step_i8_sessions.argtypes = [_sz, _f32p, _i8p, _f32p, _i8p, _f32p, _sz, _sz,
+                                                 _sz, C.POINTER(_AttnDims), _f32p, C.c_int]
         L.or_fake_quant_vec.argtypes = [_f32p, _sz, C.c_uint32]
         L.or_quant_into.argtypes = [_f32p, _sz, _i8p]
         L.or_quant_into.restype = C.c_float
@@ -321,6 +324,18 @@ def cb8_gemm(x, w, cb):
     return y
 
 
+def cb8_gemm_omp(x, w, cb, threads, y=None):
+    """cb8_gemm with output-row bands on `threads` threads (the same bits)."""
+    x = _f32(x)
+    w = np.ascontiguousarray(w, np.uint8)
+    m = x.shape[0]
+    out, inn = w.shape
+    if y is None:
+        y = np.zeros((m, out), np.float32)
+    lib().or_cb8_gemm_omp(x, w, _f32(cb), y, m, out, inn, int(threads))
+    return y
+
+
 # ---- v3/cache.rs ------------------------------------------------------------
 
 def fake_quant_vec(x, bits=8):
@@ -419,6 +434,19 @@ def attend_step_i8(q, k, ks, v, vs, slots, lo, hi, nh, nkv, qk, vd):
     return out
 
 
+def attend_step_i8_sessions(q, k, ks, v, vs, slots, lo, hi, nh, nkv, qk, vd, threads, out=None):
+    """attend_step for each session i over its own cache (k[i], ks[i], v[i],
+    vs[i], each `slots` positions), sessions split across `threads`."""
+    count = q.shape[0]
+    if out is None:
+        out = np.zeros((count, nh * vd), np.float32)
+    d = _dims(1, nh, nkv, qk, vd)
+    lib().or_attend_step_i8_sessions(count, _f32(q), np.ascontiguousarray(k, np.int8), _f32(ks),
+                                     np.ascontiguousarray(v, np.int8), _f32(vs), slots, lo, hi,
+                                     C.byref(d), out, int(threads))
+    return out
+
+
 def attend_f32(q, k, v, seq, nh, nkv, qk, vd, window=0):
     out = np.zeros(seq * nh * vd, np.float32)
     d = _dims(seq, nh, nkv, qk, vd)
@@ -491,6 +519,9 @@ def _v3_lib():
                                      _sz, _sz, np.ctypeslib.ndpointer(np.uint32), _f32p]
         L.or_argmax.argtypes = [_f32p, _sz]
         L.or_argmax.restype = C.c_uint32
+        L.or_v3_decode_sessions.argtypes = [C.c_void_p, C.POINTER(C.c_void_p),
+                                            np.ctypeslib.ndpointer(np.uint32), _sz, _f32p, C.c_int]
+        L.or_v3_cache_fill_synthetic.argtypes = [C.c_void_p, _sz, C.c_uint64]
         L.or_sinkhorn.argtypes = [_f32p, _sz]
         L.or_kron_apply.argtypes = [_f32p, _f32p, _f32p, _sz, _sz, _f32p]
         L.or_engram_indices.argtypes = [np.ctypeslib.ndpointer(np.uint32), _sz,
@@ -554,6 +585,23 @@ class V3Cache:
         out = np.zeros(self.model.rows, np.float32)
         _v3_lib().or_v3_decode_step(self.model._p, self._p, int(token), out)
         return out
+
+    def fill_synthetic(self, pos, seed):
+        """For timing only: this fresh cache (hint >= pos + the steps to be
+        timed) put at position `pos` with seeded contents, as if `pos`
+        tokens had been decoded."""
+        _v3_lib().or_v3_cache_fill_synthetic(self._p, int(pos), int(seed))
+
+
+def v3_decode_sessions(model, caches, tokens, threads):
+    """One decode_step per session, sessions split across `threads`;
+    returns the logits [sessions][rows]."""
+    n = len(caches)
+    arr = (C.c_void_p * n)(*[c._p for c in caches])
+    tok = np.ascontiguousarray(tokens, np.uint32)
+    out = np.zeros((n, model.rows), np.float32)
+    _v3_lib().or_v3_decode_sessions(model._p, arr, tok, n, out, int(threads))
+    return out
 
 
 def v3_generate(model, prompt, steps, int8=True, hint=None):

@@ -103,3 +103,48 @@ def test_decode_steps_keep_bits_under_every_split():
         runs.append(np.stack([cache.decode_step(t) for t in prompt]))
     for r in runs[1:]:
         assert np.array_equal(_bits(r), _bits(runs[0]))
+
+
+def test_session_splits_keep_bits():
+    """The CPU baseline's session-parallel helpers give each session's own
+    serial result: decode steps of three sessions at once, attention over
+    four sessions' caches, and the row-band Format B GEMM."""
+    import v3_synth as S
+    g, recs = S.build_records(S.small_geometry(2), seed=8)
+    om = O.V3Model(g, recs, S.CODEBOOK)
+    prompts = [S.prompt_tokens(6, 40 + i) for i in range(3)]
+    serial = []
+    for p in prompts:
+        c = om.new_cache(8, True)
+        serial.append(np.stack([c.decode_step(t) for t in p]))
+    caches = [om.new_cache(8, True) for _ in prompts]
+    par = np.stack([O.v3_decode_sessions(om, caches, [p[t] for p in prompts], 3)
+                    for t in range(6)], axis=1)
+    assert np.array_equal(_bits(par), _bits(np.stack(serial)))
+
+    rng = np.random.default_rng(12)
+    H, KVH, QK, VD, slots, n = 12, 12, 64, 64, 300, 4
+    k = rng.integers(-127, 128, size=(n, slots * KVH * QK)).astype(np.int8)
+    v = rng.integers(-127, 128, size=(n, slots * KVH * VD)).astype(np.int8)
+    ks = (rng.random((n, slots * KVH)) * 0.05 + 1e-3).astype(np.float32)
+    vs = (rng.random((n, slots * KVH)) * 0.05 + 1e-3).astype(np.float32)
+    q = rng.normal(size=(n, H * QK)).astype(np.float32)
+    got = O.attend_step_i8_sessions(q, k, ks, v, vs, slots, 0, slots - 1, H, KVH, QK, VD, 3)
+    for i in range(n):
+        want = O.attend_step_i8(q[i], k[i], ks[i], v[i], vs[i], slots, 0, slots - 1, H, KVH, QK, VD)
+        assert np.array_equal(_bits(got[i]), _bits(want))
+
+    w = rng.integers(0, 256, size=(192, 96), dtype=np.uint8)
+    cb = rng.normal(0, 0.02, size=(3, 256)).astype(np.float32)
+    x = rng.normal(size=(5, 96)).astype(np.float32)
+    assert np.array_equal(_bits(O.cb8_gemm_omp(x, w, cb, 4)), _bits(O.cb8_gemm(x, w, cb)))
+
+
+def test_synthetic_cache_runs_a_decode_step():
+    import v3_synth as S
+    g, recs = S.build_records(S.small_geometry(2), seed=8)
+    om = O.V3Model(g, recs, S.CODEBOOK)
+    c = om.new_cache(80, True)
+    c.fill_synthetic(70, 3)
+    lg = c.decode_step(5)
+    assert np.isfinite(lg).all()
