@@ -82,7 +82,6 @@ ND_LIBM_FN float nd_scalbnf(float x, int n)
 
 ND_LIBM_FN float nd_expf(float x)
 {
-    const float half[2] = {0.5f, -0.5f};
     const float ln2_hi = 6.9314575195e-01f;  // 0x3f317200
     const float ln2_lo = 1.4286067653e-06f;  // 0x35bfbe8e
     const float inv_ln2 = 1.4426950216e+00f; // 0x3fb8aa3b
@@ -100,7 +99,7 @@ ND_LIBM_FN float nd_expf(float x)
     float hi, lo;
     if (hx > 0x3eb17218u) {        // |x| > ln2 / 2
         if (hx > 0x3f851592u)      // |x| > 1.5 ln2
-            k = (int)(inv_ln2 * x + half[sign]);
+            k = (int)(inv_ln2 * x + (sign ? -0.5f : 0.5f));  // a select, not a table in memory
         else
             k = 1 - sign - sign;
         const float kf = (float)k;
@@ -163,9 +162,7 @@ ND_LIBM_FN float nd_sigmoidf(float x) { return 1.0f / (1.0f + nd_expf(-x)); }
 
 ND_LIBM_FN float nd_powf(float x, float y)
 {
-    const float bp[2] = {1.0f, 1.5f};
-    const float dp_h[2] = {0.0f, 5.84960938e-01f};  // 0x3f15c000
-    const float dp_l[2] = {0.0f, 1.56322085e-06f};  // 0x35d1cfdc
+    const float bp1 = 1.5f, dp_h1 = 5.84960938e-01f, dp_l1 = 1.56322085e-06f;  // 0x3f15c000, 0x35d1cfdc
     const float two24 = 16777216.0f;
     const float huge = 1.0e30f, tiny = 1.0e-30f;
     // (3/2) (log(x) - 2s - 2/3 s^3) series
@@ -259,13 +256,14 @@ ND_LIBM_FN float nd_powf(float x, float y)
         }
         ax = nd_u2f((uint32_t)ix);
         // s = s_h + s_l = (x - 1)/(x + 1) or (x - 1.5)/(x + 1.5)
-        float u = ax - bp[k];
-        float v = 1.0f / (ax + bp[k]);
+        const float bpk = k ? bp1 : 1.0f, dphk = k ? dp_h1 : 0.0f, dplk = k ? dp_l1 : 0.0f;
+        float u = ax - bpk;
+        float v = 1.0f / (ax + bpk);
         const float s = u * v;
         const float s_h = nd_u2f(nd_f2u(s) & 0xfffff000u);
         float t_h = nd_u2f((uint32_t)((((ix >> 1) & 0xfffff000) | 0x20000000) + 0x00400000 +
                                       (k << 21)));
-        float t_l = ax - (t_h - bp[k]);
+        float t_l = ax - (t_h - bpk);
         const float s_l = v * ((u - s_h * t_h) - s_h * t_l);
         // log(ax)
         float s2 = s * s;
@@ -280,11 +278,11 @@ ND_LIBM_FN float nd_powf(float x, float y)
         const float p_h = nd_u2f(nd_f2u(u + v) & 0xfffff000u);
         const float p_l = v - (p_h - u);
         const float z_h = cp_h * p_h;
-        const float z_l = cp_l * p_h + p_l * cp + dp_l[k];
+        const float z_l = cp_l * p_h + p_l * cp + dplk;
         // log2(ax) = n + dp_h + z_h + z_l
         const float t = (float)n;
-        t1 = nd_u2f(nd_f2u(((z_h + z_l) + dp_h[k]) + t) & 0xfffff000u);
-        t2 = z_l - (((t1 - t) - dp_h[k]) - z_h);
+        t1 = nd_u2f(nd_f2u(((z_h + z_l) + dphk) + t) & 0xfffff000u);
+        t2 = z_l - (((t1 - t) - dphk) - z_h);
     }
 
     // (y1 + y2)(t1 + t2)

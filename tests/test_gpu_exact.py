@@ -205,3 +205,36 @@ def test_attend_exact_cap_8192(ctx):
         out = host(nd.attend_step_i8(ctx, g, blk, nb, dev(np.array([lo], np.int32)),
                                      dev(np.array([hi], np.int32)), dev(q)[None], exact=True))[0]
         assert _same_bits(out, _oracle(g, host(blk), q, lo, hi))
+
+
+@pytest.mark.parametrize("H,KVH,QK", [(12, 2, 48), (12, 12, 64), (8, 4, 48), (12, 4, 64),
+                                      (16, 4, 48), (16, 2, 64)])
+@pytest.mark.parametrize("cap", [300, 2176, 10000])
+def test_attend_exact_grouped_heads(ctx, H, KVH, QK, cap):
+    """1, 2, 3, 4, 6 and 8 query heads per kv head (v_head_dim 64, qk 48 or
+    64) at caps on both sides of the split-role kernel's 8192 limit; spans
+    of 1 position up to the whole ring, across the ring's wrap, three
+    sessions with different spans in one call; bit for bit against
+    attend_step."""
+    VD, count = 64, 3
+    rng = np.random.default_rng(cap * 7 + H * 3 + KVH + QK)
+    npos = cap + 300  # the ring wraps: positions 300.. overwrite the first slots
+    g, blk, nb = _fill(ctx, rng, H, KVH, QK, VD, cap, npos, count, scale=2.0)
+    top = npos - 1
+    spans = [(top, top), (top - 255, top), (top - 256, top), (top - 511, top),
+             (top - 512, top), (top - cap + 1, top), (top - cap + 1, top - 1),
+             (top - (cap * 2) // 3, top - 5)]
+    spans = [(lo, hi) for lo, hi in spans if hi - lo < cap and lo >= npos - cap]
+    blocks = None
+    for lo_v, hi_v in spans:
+        q = (rng.normal(size=(count, H * QK)) * 3).astype(np.float32)
+        lo = np.array([lo_v, lo_v + 1 if lo_v < hi_v else lo_v, hi_v], np.int32)
+        hi = np.array([hi_v, hi_v, hi_v], np.int32)
+        out = host(nd.attend_step_i8(ctx, g, blk, nb, dev(lo), dev(hi), dev(q), quant_query=True,
+                                     exact=True))
+        if blocks is None:
+            blocks = host(blk)
+        for i in range(count):
+            want = _oracle(g, blocks[i * nb:(i + 1) * nb], O.quant_rows(q[i], 1, H, QK),
+                           int(lo[i]), int(hi[i]))
+            assert _same_bits(out[i], want), (lo_v, hi_v, i)
