@@ -10,16 +10,23 @@
 // of weight k from row_start[k], batch-major ([batch][rows[k]]).
 // Bit-identical to CqWeight::matvec_rows_prepared / matmul_rows_prepared
 // per weight.
+// half_inv != 0: xh holds each 128-group with butterfly stages 1..32 done
+// (the gated attention epilogue's output); the load applies the last stage
+// and the 1/sqrt(128) scale (half_inv), so the dots see prepare_input's bits.
 int nd_cq_exact_set(nd_ctx *ctx, hipStream_t stream, int n, const nd_cq *const *w, const float *xh,
                     size_t batch, const size_t *row_start, const size_t *rows, float *const *y,
-                    const char *what);
+                    const char *what, float half_inv = 0.0f);
 
 // nd_attend_step_i8_exact with query row i reading the KV block of
 // kv + (i / rows_per_block) * kv_stride: several positions of one session
-// in one call.
+// in one call.  With `gate` ([count][num_heads * 64], v_head_dim 64) each
+// output column becomes attn * sigmoid(gate) with butterfly stages 1..32
+// of its 128-wide group applied: the input nd_cq_exact_set finishes with
+// half_inv (v3/model.rs:309-313, hadamard.rs:24-55).
 int nd_attend_exact_rows(nd_ctx *ctx, const nd_kv_geom *g, const void *kv, size_t kv_stride,
                          size_t count, int rows_per_block, const int32_t *lo, const int32_t *hi,
-                         const float *q, float scale, int quant_query, float *out);
+                         const float *q, float scale, int quant_query, float *out,
+                         const float *gate = nullptr);
 
 // One 128-wide group of a Cactus-Quants row dotted with a prepared
 // activation group in the reference's order (cq.rs:838-873): element e into

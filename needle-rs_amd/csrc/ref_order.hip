@@ -53,6 +53,10 @@ struct CqExact {
     float *y;
     size_t row_bytes;
     int in_padded, group, G, row_start, rows, batch, rpb, ternary;
+    // 0: xh is prepared.  Otherwise xh holds each 128-group with butterfly
+    // stages h = 1..32 done; the load finishes the transform: stage h = 64
+    // and the scale by half_inv (1/sqrt(128)), as fwht_normalized would.
+    float half_inv;
 };
 
 // Up to kMaxSet weights with the same input, width and group in one launch:
@@ -107,7 +111,15 @@ __global__ __launch_bounds__(kThreads) void cq_exact_kernel(CqExactSet set)
         const float4 *src = reinterpret_cast<const float4 *>(a.xh + size_t(b0 + bb) * a.in_padded);
         for (int e = tid; e < a.in_padded / 4; e += kThreads) {
             const int g = (4 * e) / a.group, k = 4 * e - g * a.group;
-            *reinterpret_cast<float4 *>(xs + bb * xstride + g * gstride + k) = src[e];
+            float4 v = src[e];
+            if (a.half_inv != 0.0f) {
+                // the last butterfly stage: lower half a + b, upper half a - b
+                const float4 o = src[e + (k < 64 ? 16 : -16)];
+                const float s = a.half_inv;
+                v = k < 64 ? make_float4((v.x + o.x) * s, (v.y + o.y) * s, (v.z + o.z) * s, (v.w + o.w) * s)
+                           : make_float4((o.x - v.x) * s, (o.y - v.y) * s, (o.z - v.z) * s, (o.w - v.w) * s);
+            }
+            *reinterpret_cast<float4 *>(xs + bb * xstride + g * gstride + k) = v;
         }
     }
     // this thread's (row, group) and its codes
@@ -307,7 +319,7 @@ int cq_serial(hipStream_t stream, const nd_cq *w, const float *xh, size_t batch,
 // rows[k] rows of weight k from row_start[k], batch-major.
 int nd_cq_exact_set(nd_ctx *ctx, hipStream_t stream, int n, const nd_cq *const *w, const float *xh,
                     size_t batch, const size_t *row_start, const size_t *rows, float *const *y,
-                    const char *what)
+                    const char *what, float half_inv)
 {
     if (int rc = nd::enter(ctx)) return rc;
     ND_REQUIRE(n >= 1 && n <= kMaxSet && w && xh && row_start && rows && y, "%s: bad arguments",
@@ -344,6 +356,8 @@ int nd_cq_exact_set(nd_ctx *ctx, hipStream_t stream, int n, const nd_cq *const *
                (size_t(bt) / 2 >= batch || exact_lds(bt, P, w0->in_padded, w0->group, pairs) > kLdsBudget ||
                 tiles * ((batch + bt - 1) / bt) < want))
             bt /= 2;
+        ND_REQUIRE(half_inv == 0.0f || w0->group == 128,
+                   "%s: a half-transformed input needs 128-wide groups", what);
         if (exact_lds(bt, P, w0->in_padded, w0->group, pairs) <= kLdsBudget) {
             CqExactSet set{};
             set.n = 0;
@@ -353,7 +367,7 @@ int nd_cq_exact_set(nd_ctx *ctx, hipStream_t stream, int n, const nd_cq *const *
                 set.w[set.n] = CqExact{w[k]->packed, w[k]->norms, w[k]->lv, xh, y[k], w[k]->row_bytes,
                                        int(w[k]->in_padded), int(w[k]->group), int(G),
                                        int(row_start[k]), int(rows[k]), int(batch), rpb,
-                                       int(w[k]->bits == kTernary)};
+                                       int(w[k]->bits == kTernary), half_inv};
                 set.tile0[set.n++] = tiles;
                 tiles += int((rows[k] + rpb - 1) / rpb);
             }
@@ -366,6 +380,7 @@ int nd_cq_exact_set(nd_ctx *ctx, hipStream_t stream, int n, const nd_cq *const *
             return nd::check_launch(what);
         }
     }
+    ND_REQUIRE(half_inv == 0.0f, "%s: a half-transformed input needs the 128-group kernel", what);
     for (int k = 0; k < n; ++k)
         if (rows[k])
             if (int rc = cq_serial(stream, w[k], xh, batch, row_start[k], rows[k], y[k], what))
@@ -380,13 +395,33 @@ namespace {
 // ---------------------------------------------------------------------------
 __device__ inline float i8_lane(uint32_t dw, int b) { return float(int32_t(dw << (24 - 8 * b)) >> 24); }
 
+// Output column `lane` (0..63, all 64 lanes of the wave) of one head, with
+// `gate` set: attn * sigmoid(gate) (v3/model.rs:309-312), then butterfly
+// stages h = 1..32 of the normalised FWHT prepare_input applies to the
+// out projection's 128-wide groups (hadamard.rs:24-42): with a 64-wide head
+// each half of a group is one head, and those stages pair columns within
+// it.  The last stage (h = 64, across the two heads) and the 1/sqrt(128)
+// scale are left to the projection's activation load.
+__device__ inline float gate_half_fwht(float v, const float *gate, int lane)
+{
+    if (!gate) return v;
+    v = v * nd_sigmoidf(gate[lane]);
+#pragma unroll
+    for (int h = 1; h < 64; h <<= 1) {
+        const float p = __shfl_xor(v, h, 64);
+        v = (lane & h) ? p - v : v + p;
+    }
+    return v;
+}
+
 __global__ __launch_bounds__(kThreads) void attn_exact_kernel(ndkv::Geom g,
                                                              const uint8_t *__restrict__ kv,
                                                              size_t stride, int rows_per_block,
                                                              const int32_t *__restrict__ lo,
                                                              const int32_t *__restrict__ hi,
                                                              const float *__restrict__ q, float scale,
-                                                             int quant_query, float *__restrict__ out)
+                                                             int quant_query, float *__restrict__ out,
+                                                             const float *__restrict__ gate)
 {
     extern __shared__ __align__(16) float sc[];  // [span] scores, then weights
     __shared__ float qs[ndkv::kMaxDim];
@@ -506,7 +541,9 @@ __global__ __launch_bounds__(kThreads) void attn_exact_kernel(ndkv::Geom g,
             for (; t < cn; ++t) acc += w[t] * float(col[t * g.VD]);
         }
     }
-    if (tid < g.VD) out[(i * g.H + h) * size_t(g.VD) + tid] = acc;
+    if (tid < g.VD)
+        out[(i * g.H + h) * size_t(g.VD) + tid] =
+            gate_half_fwht(acc, gate ? gate + (i * g.H + h) * size_t(g.VD) : nullptr, tid);
 }
 
 // The same arithmetic, with the value pass split between roles.  Of the 256
@@ -652,7 +689,7 @@ template <int CW, int QC>
 __global__ __launch_bounds__(kAttn2Threads, 4) void attn_exact2_kernel(
     ndkv::Geom g, const uint8_t *__restrict__ kv, size_t stride, const int32_t *__restrict__ lo,
     const int32_t *__restrict__ hi, const float *__restrict__ q, float scale, int quant_query,
-    float *__restrict__ out, int groups, int rows_per_block)
+    float *__restrict__ out, int groups, int rows_per_block, const float *__restrict__ gate)
 {
     constexpr int NT = kAttn2Threads;
     extern __shared__ __align__(16) float sm[];
@@ -816,7 +853,9 @@ __global__ __launch_bounds__(kAttn2Threads, 4) void attn_exact2_kernel(
             __syncthreads();
         }
     }
-    if (tid < g.VD) out[(size_t(i) * g.H + h) * g.VD + tid] = acc;
+    if (tid < g.VD)
+        out[(size_t(i) * g.H + h) * g.VD + tid] =
+            gate_half_fwht(acc, gate ? gate + (size_t(i) * g.H + h) * g.VD : nullptr, tid);
 }
 
 
@@ -875,17 +914,21 @@ int nd_attend_step_i8_exact(nd_ctx *ctx, const nd_kv_geom *g, const void *kv, si
                             size_t count, const int32_t *lo, const int32_t *hi, const float *q,
                             float scale, int quant_query, float *out)
 {
-    return nd_attend_exact_rows(ctx, g, kv, kv_stride, count, 1, lo, hi, q, scale, quant_query, out);
+    return nd_attend_exact_rows(ctx, g, kv, kv_stride, count, 1, lo, hi, q, scale, quant_query, out,
+                                nullptr);
 }
 
 }  // extern "C"
 
 int nd_attend_exact_rows(nd_ctx *ctx, const nd_kv_geom *g, const void *kv, size_t kv_stride,
                          size_t count, int rows_per_block, const int32_t *lo, const int32_t *hi,
-                         const float *q, float scale, int quant_query, float *out)
+                         const float *q, float scale, int quant_query, float *out,
+                         const float *gate)
 {
     if (int rc = nd::enter(ctx)) return rc;
     ND_REQUIRE(rows_per_block >= 1, "rows_per_block %d", rows_per_block);
+    ND_REQUIRE(!gate || g->v_head_dim == 64, "the gated epilogue needs v_head_dim 64, not %d",
+               g->v_head_dim);
     if (int rc = ndkv::check_geom(g)) return rc;
     if (count == 0) return ND_OK;
     ND_REQUIRE(kv && lo && hi && q && out, "null buffer");
@@ -906,7 +949,7 @@ int nd_attend_exact_rows(nd_ctx *ctx, const nd_kv_geom *g, const void *kv, size_
     hipLaunchKernelGGL((attn_exact2_kernel<CW, QC>), dim3(unsigned(blocks)),                   \
                        dim3(kAttn2Threads), lds, ctx->stream, ndkv::make_geom(g),               \
                        static_cast<const uint8_t *>(kv), kv_stride, lo, hi, q, scale, quant_query, \
-                       out, int(groups), rows_per_block)
+                       out, int(groups), rows_per_block, gate)
 #define ND_ATTN2_QC(CW)                    \
     switch (qc) {                          \
     case 1: ND_ATTN2(CW, 1); break;        \
@@ -928,6 +971,6 @@ int nd_attend_exact_rows(nd_ctx *ctx, const nd_kv_geom *g, const void *kv, size_
     const size_t lds = size_t((g->cap + 3) & ~3) * 4 + kVChunk;
     hipLaunchKernelGGL(attn_exact_kernel, grid, dim3(kThreads), lds, ctx->stream,
                        ndkv::make_geom(g), static_cast<const uint8_t *>(kv), kv_stride,
-                       rows_per_block, lo, hi, q, scale, quant_query, out);
+                       rows_per_block, lo, hi, q, scale, quant_query, out, gate);
     return nd::check_launch("attn_exact");
 }

@@ -1808,6 +1808,8 @@ int step_impl(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *
         LCHK("k_embed");
 
         const float qk_scale = 1.0f / std::sqrt(float(c.qk_head_dim));
+        const bool gate_fused = c.v_head_dim == 64 && m->pre_attn.group == 128 &&
+                                m->pre_attn.in_padded == od && m->layers[0].out->per_byte != 0;
         hipStream_t side = b->side;
         const nd_cq *phi = m->phi_pre;
         for (int li = 0; li < L; ++li) {
@@ -1875,14 +1877,26 @@ int step_impl(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *
                     }
                 }
             }
-            // attention over the int8 ring (query fake-quant fused)
-            CK(nd_attend_exact_rows(ctx, &b->geom[li], b->kv[li], b->kv_stride[li], size_t(B), C,
-                                    lo_dev + size_t(li) * B, hi_dev, C == 1 ? b->q : b->qn, qk_scale,
-                                    1, b->attn));
-            hipLaunchKernelGGL(k_gate_prep, dim3(B), dim3(kT), 0, st, b->attn, b->gate, b->ah, od,
-                               m->pre_attn);
-            LCHK("k_gate_prep");
-            CK(project(ctx, l.out, b->ah, B, 0, d, b->proj));
+            // attention over the int8 ring (query fake-quant fused); with
+            // 64-wide heads and 128-wide groups its epilogue also applies
+            // the sigmoid gate and the butterfly stages inside each head,
+            // and out_proj's load finishes prepare_input
+            if (gate_fused) {
+                CK(nd_attend_exact_rows(ctx, &b->geom[li], b->kv[li], b->kv_stride[li], size_t(B), C,
+                                        lo_dev + size_t(li) * B, hi_dev, C == 1 ? b->q : b->qn,
+                                        qk_scale, 1, b->attn, b->gate));
+                const size_t r0 = 0, nr = size_t(d);
+                CK(nd_cq_exact_set(ctx, st, 1, &l.out, b->attn, size_t(B), &r0, &nr, &b->proj,
+                                   "v3 out projection", m->pre_attn.inv));
+            } else {
+                CK(nd_attend_exact_rows(ctx, &b->geom[li], b->kv[li], b->kv_stride[li], size_t(B), C,
+                                        lo_dev + size_t(li) * B, hi_dev, C == 1 ? b->q : b->qn,
+                                        qk_scale, 1, b->attn));
+                hipLaunchKernelGGL(k_gate_prep, dim3(B), dim3(kT), 0, st, b->attn, b->gate, b->ah, od,
+                                   m->pre_attn);
+                LCHK("k_gate_prep");
+                CK(project(ctx, l.out, b->ah, B, 0, d, b->proj));
+            }
             HadaArgs ha{b->proj, l.post_norm, l.pre_hada, nd_sigmoidf(l.attn_gate), b->u, b->bx, b->y,
                         l.d1, l.d2, l.b2, l.d3, l.d4, l.w1a, l.w1b, l.w2a, l.w2b, l.w3a, l.w3b,
                         l.cond_v, l.cond_u, m->p1, m->p2, d, l.cond_rank};
