@@ -637,25 +637,26 @@ __global__ __launch_bounds__(512) void cb8_gemm256_kernel(const float *__restric
     load(0);
     __syncthreads();  // codebooks in LDS
     store(0);
-    if (nk > 1) load(kPK);
+    load(nk > 1 ? kPK : 0);
     __syncthreads();
     const bool first = wave < 4;
     for (int i = 0; i < nk; ++i) {
         const int cur = i & 1;
         const int halves = (K - i * kPK < kPK ? K - i * kPK : kPK) / 32;
         // step i+1 into the other buffer (read last in step i-1, before the
-        // barrier that ended it); step i+2's loads go out behind it
+        // barrier that ended it); step i+2's loads go out behind it.  Every
+        // step stores and loads -- the last ones repeat the final step into a
+        // buffer nothing reads -- so no load sits behind a branch and the
+        // waits count the loads in flight exactly (a load behind a branch
+        // makes the compiler wait for it at the join)
+        const int kl = (i + 2 < nk ? i + 2 : nk - 1) * kPK;
         if (first) {
             multiply(cur, halves);
-            if (i + 1 < nk) {
-                store(cur ^ 1);
-                if (i + 2 < nk) load((i + 2) * kPK);
-            }
+            store(cur ^ 1);
+            load(kl);
         } else {
-            if (i + 1 < nk) {
-                store(cur ^ 1);
-                if (i + 2 < nk) load((i + 2) * kPK);
-            }
+            store(cur ^ 1);
+            load(kl);
             multiply(cur, halves);
         }
         __syncthreads();

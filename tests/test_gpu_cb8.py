@@ -94,12 +94,14 @@ def test_gemm_bf16_mfma(ctx, m, out, inn):
     assert np.linalg.norm(Y - ref) / np.linalg.norm(ref) <= 5e-3
 
 
-@pytest.mark.parametrize("R,M,N,K", [(11, 512, 3072, 768), (43, 300, 768, 800)])
+@pytest.mark.parametrize("R,M,N,K", [(11, 512, 3072, 768), (43, 300, 768, 768),
+                                     (43, 300, 768, 800)])
 def test_gemm_256_tiles_match_128_tiles(ctx, R, M, N, K):
-    """A batched launch with at least one 256x256 tile per CU runs the 256
-    kernel; each problem alone has too few tiles and runs the 128x128 one.
-    The K order per output is the same, so the two agree bit for bit (ragged
-    M, K with a final half step); two problems also against the oracle."""
+    """A batched launch with at least one 256x256 tile per CU runs the
+    256x256 kernel; each problem alone has too few tiles and runs the
+    128x128 one.  Per output both sum K in the same order, so they agree
+    bit for bit, with K in whole 64-wide steps and with a final half step
+    (K 800).  Ragged M; two problems also against the oracle."""
     rng = np.random.default_rng(R * 1000 + K)
     X = rng.normal(size=(R, M, K)).astype(np.float32)
     W = rng.integers(0, 256, size=(R, N, K), dtype=np.uint8)
@@ -114,6 +116,36 @@ def test_gemm_256_tiles_match_128_tiles(ctx, R, M, N, K):
         want = O.cb8_gemm(X[i], W[i], CB[i])
         assert np.max(np.abs(got[i] - want)) <= 2e-2 * np.max(np.abs(want))
         assert np.linalg.norm(got[i] - want) / np.linalg.norm(want) <= 5e-3
+
+
+def test_gemm_256_edges(ctx):
+    """The 256x256 kernel on its edges: ragged M (300 = 256 + 44 rows),
+    16 problems of N 4096 (512 tiles, 64 codebook groups each), codebooks
+    holding +-0, a subnormal and a bf16 rounding tie; outputs against the
+    f64 closed form (bf16 operands, fp32 sums)."""
+    R, M, N, K = 16, 300, 4096, 768
+    rng = np.random.default_rng(77)
+    X = rng.normal(size=(R, M, K)).astype(np.float32)
+    W = rng.integers(0, 256, size=(R, N, K), dtype=np.uint8)
+    CB = (rng.normal(size=(R, N // 64, 256)) * 0.02).astype(np.float32)
+    CB[:, :, 0] = 0.0
+    CB[:, :, 1] = -0.0
+    CB[:, :, 2] = np.float32(1e-40)
+    CB[:, :, 3] = np.float32(1.0 + 2.0 ** -8)  # a bf16 tie: rounds to even
+    Y = torch.empty(R, M, N, device="cuda")
+    nd.cb8_gemm_batched(ctx, dev(X), dev(W), dev(CB), Y)
+    got = host(Y)
+
+    def bf16(a):
+        u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+        u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16 << 16
+        return u.astype(np.uint32).view(np.float32)
+    rows = np.arange(N)
+    for i in (0, 7, R - 1):
+        deq = CB[i][rows // 64][rows[:, None], W[i].astype(np.int64)]  # (N, K)
+        ref = bf16(X[i]).astype(np.float64) @ bf16(deq).astype(np.float64).T
+        err = np.max(np.abs(got[i] - ref)) / np.max(np.abs(ref))
+        assert err <= 1e-5, (i, err)
 
 
 @pytest.mark.parametrize("R,M,N,K", [(3, 70, 128, 96), (5, 64, 384, 768), (4, 17, 256, 256)])
