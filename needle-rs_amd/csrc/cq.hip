@@ -290,6 +290,125 @@ __global__ __launch_bounds__(kThreads) void cq_gemv_stream_kernel(
     }
 }
 
+// Batch-1 GEMV on 2-bit (and ternary) rows of 16 * ND code dwords, ND <= 3
+// (in <= 768), by product lookup.  Each workgroup first builds, from the
+// prepared activation, T(p, e) = lvl(e & 3) * xh[2p] + lvl(e >> 2) * xh[2p+1]
+// for every nibble position p of a row and nibble value e, so a code nibble
+// costs one 4-byte LDS gather and one add: half the LDS bytes of the level
+// table (a 16-byte read per code byte) and half its VALU work.
+// Lane j of a 16-lane row group owns code dwords j * ND .. j * ND + ND - 1,
+// nibble positions 8 * ND * j + 8 i + s (dword i, nibble s).  Four shifted
+// copies of a dword put nibbles 2q and 2q + 1 at bits 7-10 and 11-14 of copy
+// q, so a gather address is one and-or with the lane's base; the table keeps
+// the even nibbles' entries at e << 7 (subtable k = 4i + q at k << 11) and
+// the odd ones' at 32 KiB + (e << 11) (subtable k at k << 7), the subtable
+// offset riding in the instruction.  Every entry is a 32-dword block indexed
+// [row group & 1][j]: the two row groups of a half-wave read disjoint banks,
+// so a gather does not conflict whatever codes the lanes hold.  Two
+// 1024-thread workgroups share a CU; each streams a contiguous run of 64-row
+// tiles with the codes and norms of the next D tiles in flight (rows past the
+// end reread the last row and store nothing, so every load is unconditional).
+// The 16 partial sums of a row meet through DPP row rotations.
+constexpr int kNibThreads = 1024;
+constexpr int kNibRows = kNibThreads / kLanesPerRow;  // 64 rows per tile
+
+__device__ inline float row16_sum(float v)
+{
+    // rotations within a 16-lane DPP row: 8, 4, 2, 1 (row_ror:n = 0x120 + n)
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x124, 0xf, 0xf, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x122, 0xf, 0xf, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x121, 0xf, 0xf, false));
+    return v;
+}
+
+template <int ND, int D>
+__global__ __launch_bounds__(kNibThreads, 2) void cq_gemv_nib_kernel(
+    const uint8_t *__restrict__ packed, const float *__restrict__ norms,
+    const float *__restrict__ lut, const float *__restrict__ xh, float *__restrict__ y,
+    int row_start, int rows, int row_bytes, int num_groups, int group, int tiles_per_block)
+{
+    constexpr int NI = 8 * ND;  // nibble positions per lane
+    __shared__ float tab[16384];  // 64 KiB
+    const int t = threadIdx.x;
+    const int j = t & (kLanesPerRow - 1);
+    const int rg = t / kLanesPerRow;  // row of the tile
+    // lut[4c] is the level of code c (byte value c, first crumb), ternary
+    // crumb map included
+    for (int f = t; f < 16 * NI * kLanesPerRow; f += kNibThreads) {
+        const int fj = f % kLanesPerRow, n = (f / kLanesPerRow) % NI, e = f / (kLanesPerRow * NI);
+        const int p = fj * NI + n;
+        const float v = lut[(e & 3) * 4] * xh[2 * p] + lut[(e >> 2) * 4] * xh[2 * p + 1];
+        const int i = n / 8, sn = n % 8, k = 4 * i + sn / 2;
+        const int at = (sn & 1) ? 0x8000 | (e << 11) | (k << 7) : (k << 11) | (e << 7);
+        tab[at / 4 + fj] = v;
+        tab[at / 4 + 16 + fj] = v;
+    }
+    // the lane's ND * 16 elements span groups g0 and g0 + 1 at most
+    const int g0 = (j * ND * 16) / group;
+    bool second[ND];
+#pragma unroll
+    for (int i = 0; i < ND; ++i) second[i] = ((j * ND + i) * 16) / group != g0;
+    const int g1 = g0 + 1 < num_groups ? g0 + 1 : g0;
+    __syncthreads();
+
+    const uint32_t lb = uint32_t(((rg & 1) * kLanesPerRow + j) * 4);
+    const char *tb = reinterpret_cast<const char *>(tab);
+    // the launch's rows through buffer resources: 32-bit offsets (the caller
+    // keeps rows * row_bytes and rows * num_groups * 4 below 2^31)
+    const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(packed + size_t(row_start) * row_bytes), (short)0, rows * row_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rn = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(norms + size_t(row_start) * num_groups), (short)0, rows * num_groups * 4, 0x00020000);
+    const int ntiles = (rows + kNibRows - 1) / kNibRows;
+    const int tile0 = blockIdx.x * tiles_per_block;
+    const int tile1 = tile0 + tiles_per_block < ntiles ? tile0 + tiles_per_block : ntiles;
+    uint32_t cb[D][ND];
+    float nb[D][2];
+    auto load = [&](int tile, uint32_t (&c)[ND], float (&nr)[2]) {
+        int r = tile * kNibRows + rg;
+        r = r < rows ? r : rows - 1;
+        // rows < 2^24 here, so 24-bit multiplies give the offsets; codes are
+        // read once: nontemporal (aux bit 1)
+        const int co = int(__umul24(uint32_t(r), uint32_t(row_bytes))) + j * (4 * ND);
+#pragma unroll
+        for (int i = 0; i < ND; ++i) c[i] = __builtin_amdgcn_raw_buffer_load_b32(rc, co + 4 * i, 0, 2);
+        const int no = int(__umul24(uint32_t(r), uint32_t(num_groups * 4)));
+        nr[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rn, no + 4 * g0, 0, 0));
+        nr[1] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rn, no + 4 * g1, 0, 0));
+    };
+#pragma unroll
+    for (int k = 0; k < D; ++k) load(tile0 + k, cb[k], nb[k]);
+    for (int tile = tile0; tile < tile1; tile += D) {
+#pragma unroll
+        for (int k = 0; k < D; ++k) {
+            const int tt = tile + k;
+            if (tt < tile1) {
+                float total = 0.0f;
+#pragma unroll
+                for (int i = 0; i < ND; ++i) {
+                    const uint32_t dw = cb[k][i];
+                    const uint32_t cq[4] = {dw << 7, dw >> 1, dw >> 9, dw >> 17};
+                    float dot = 0.0f;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int kk = 4 * i + q;
+                        const float lo = *reinterpret_cast<const float *>(tb + ((cq[q] & 0x780u) | lb) + (kk << 11));
+                        const float hi =
+                            *reinterpret_cast<const float *>(tb + ((cq[q] & 0x7800u) | lb) + (0x8000 | (kk << 7)));
+                        dot = q == 0 ? lo + hi : dot + lo + hi;
+                    }
+                    total += (second[i] ? nb[k][1] : nb[k][0]) * dot;
+                }
+                total = row16_sum(total);
+                const int r = tt * kNibRows + rg;
+                if (j == 0 && r < rows) y[r] = total;
+            }
+            load(tt + D, cb[k], nb[k]);
+        }
+    }
+}
+
 // Reads code k of a row with the bit reader of cq.rs:914-925 (any width).
 __device__ inline uint32_t read_code(const uint8_t *row, int k, int w, int row_bytes)
 {
@@ -761,6 +880,27 @@ int nd_cq_matvec_rows_prepared(nd_ctx *ctx, const nd_cq *w, const float *xh, siz
     // dwords at 2 bits, 96 at 4 bits); other rows take the per-dword kernel
     const bool stream = w->per_byte != 0 && w->row_bytes % 64 == 0 && row_dwords / 16 >= 1 &&
                         row_dwords / 16 <= 6 && size_t(E) * (row_dwords / 16) <= w->group;
+    if (stream && w->per_byte == 4 && row_dwords <= 16 * 3 && rows < (size_t(1) << 24) &&
+        rows * w->row_bytes < (size_t(1) << 31) && rows * w->num_groups * 4 < (size_t(1) << 31)) {
+        // 2-bit / ternary, in <= 768: product lookup, two 1024-thread
+        // workgroups per CU
+        const size_t tiles = (rows + kNibRows - 1) / kNibRows;
+        const size_t slots = 2 * size_t(ctx->num_cus > 0 ? ctx->num_cus : 256);
+        const int tpb = int(tiles > slots ? (tiles + slots - 1) / slots : 1);
+        dim3 grid(unsigned((tiles + tpb - 1) / tpb));
+        const int args_rb = int(w->row_bytes), ng = int(w->num_groups), gr = int(w->group);
+#define ND_CQN(NDV)                                                                              \
+    hipLaunchKernelGGL((cq_gemv_nib_kernel<NDV, 8>), grid, dim3(kNibThreads), 0, ctx->stream,     \
+                       w->packed, w->norms, w->lut, xh, y, int(row_start), int(rows), args_rb, ng, \
+                       gr, tpb)
+        switch (row_dwords / 16) {
+        case 1: ND_CQN(1); break;
+        case 2: ND_CQN(2); break;
+        default: ND_CQN(3); break;
+        }
+#undef ND_CQN
+        return nd::check_launch("cq_gemv_nib");
+    }
     if (stream) {
         const size_t tiles = (rows + kRowsPerPass - 1) / kRowsPerPass;
         const size_t slots = 4 * size_t(ctx->num_cus > 0 ? ctx->num_cus : 256);
