@@ -201,7 +201,9 @@ size_t nd_kv_vs_offset(const nd_kv_geom *g);
  * head and store them, with their scales, at slot pos[i] % cap of the block
  * at kv + i*kv_stride bytes (kv_stride 0: every row into one block, e.g. a
  * prompt).  pos: device int32[count].  Replaces V3Cache::write_kv
- * (cache.rs:346-379) -> quant_into (cache.rs:98-104); bit-exact. */
+ * (cache.rs:346-379) -> quant_into (cache.rs:98-104); bit-exact.  The rows
+ * of one call are written in parallel: two rows for one block must not map
+ * to one slot (the reference's sequential writes would keep the later). */
 int nd_kv_write(nd_ctx *ctx, const nd_kv_geom *g, void *kv, size_t kv_stride,
                 size_t count, const int32_t *pos, const float *k,
                 const float *v);
@@ -252,6 +254,39 @@ int nd_attend_step_i8_exact(nd_ctx *ctx, const nd_kv_geom *g, const void *kv,
                             size_t kv_stride, size_t count, const int32_t *lo,
                             const int32_t *hi, const float *q, float scale,
                             int quant_query, float *out);
+
+/* ---- f32 KV cache (KvPrecision::F32, v3/cache.rs:177-238, 355-362) ------- */
+
+/*
+ * An f32 KV block of the same geometry: the layer's keys and values stored
+ * as written, head-major like the int8 block,
+ *   k  f32 [num_kv_heads][cap][qk_head_dim]     at offset 0
+ *   v  f32 [num_kv_heads][cap][v_head_dim]      at nd_kv_f32_v_offset()
+ * each part 256-byte aligned.  Logical position p lives at slot p % cap.
+ */
+size_t nd_kv_f32_block_bytes(const nd_kv_geom *g);
+size_t nd_kv_f32_v_offset(const nd_kv_geom *g);
+
+/* For i < count: store k[i] ([num_kv_heads][qk] f32) and v[i] unchanged at
+ * slot pos[i] % cap of the f32 block at kv + i*kv_stride bytes (kv_stride
+ * 0: every row into one block).  pos: device int32[count].  Replaces
+ * V3Cache::write_kv with KvPrecision::F32 (cache.rs:346-362).  As for
+ * nd_kv_write, two rows of one call must not map to one slot of a block. */
+int nd_kv_write_f32(nd_ctx *ctx, const nd_kv_geom *g, void *kv, size_t kv_stride,
+                    size_t count, const int32_t *pos, const float *k,
+                    const float *v);
+
+/* As nd_attend_step_i8_exact over the f32 block: bit-identical to
+ * attend_step over KvStore::F32 (F32View, attention.rs:166-189, 327-377):
+ * each score is one dot chain q . k over the head dim, then times `scale`;
+ * the weights are exp(s - max) * (1 / sum), each output column one chain
+ * of w * v over the span.  The query is used as given (the reference
+ * fake-quantises it for the int8 cache only, v3/model.rs:289-293).
+ * Requires v_head_dim <= 128 and cap <= 8192. */
+int nd_attend_step_f32_exact(nd_ctx *ctx, const nd_kv_geom *g, const void *kv,
+                             size_t kv_stride, size_t count, const int32_t *lo,
+                             const int32_t *hi, const float *q, float scale,
+                             float *out);
 
 /* ---- Needle-3 forward on the device (v3/model.rs, v3/cache.rs) ----------- */
 
@@ -306,6 +341,16 @@ int nd_v3_batch_create(nd_ctx *ctx, const nd_v3_model *m, size_t sessions, size_
 int nd_v3_batch_create_chunked(nd_ctx *ctx, const nd_v3_model *m, size_t sessions,
                                size_t max_len, size_t hint, size_t max_chunk,
                                nd_v3_batch **out);
+/* As nd_v3_batch_create_chunked with the sessions' KV precision chosen:
+ * kv_int8 != 0 is KvPrecision::Int8 (the batch the other constructors
+ * make), kv_int8 == 0 KvPrecision::F32 -- the default of needle_v3_run and
+ * needle_v3_generate(kv_int8 = false) (crates/needle-c/src/v3.rs:219-250):
+ * keys and values cached as f32 (nd_kv_write_f32) and read through the f32
+ * view (nd_attend_step_f32_exact), the query not fake-quantised.  Steps
+ * stay bit-identical to V3Model::decode_step / prefill with that cache. */
+int nd_v3_batch_create_ex(nd_ctx *ctx, const nd_v3_model *m, size_t sessions,
+                          size_t max_len, size_t hint, size_t max_chunk, int kv_int8,
+                          nd_v3_batch **out);
 void nd_v3_batch_free(nd_v3_batch *b);
 /* Whether this batch's single-position steps (nd_v3_step) run as one
  * captured HIP graph -- off by default: the step's kernels are captured on

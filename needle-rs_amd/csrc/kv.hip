@@ -112,6 +112,28 @@ __global__ __launch_bounds__(128) void kv_write_kernel(Geom g, uint8_t *__restri
     if ((threadIdx.x & 63) == 0) *sc = scale;
 }
 
+// write_kv with KvPrecision::F32 (cache.rs:359-362): block (i, h) copies kv
+// head h's K and V of row i into slot pos[i] % cap of the f32 block.
+__global__ __launch_bounds__(64) void kv_write_f32_kernel(Geom g, uint8_t *__restrict__ kv,
+                                                          size_t kv_stride,
+                                                          const int32_t *__restrict__ pos,
+                                                          const float *__restrict__ k,
+                                                          const float *__restrict__ v)
+{
+    const size_t i = blockIdx.x;
+    const int h = blockIdx.y;
+    const int p = pos[i];
+    if (p < 0) return;
+    const int slot = p % g.cap;
+    uint8_t *blk = kv + i * kv_stride;
+    const float *ks = k + (i * size_t(g.KVH) + h) * g.QK;
+    const float *vs = v + (i * size_t(g.KVH) + h) * g.VD;
+    float *kd = reinterpret_cast<float *>(blk) + (size_t(h) * g.cap + slot) * g.QK;
+    float *vd = reinterpret_cast<float *>(blk + g.v_off) + (size_t(h) * g.cap + slot) * g.VD;
+    for (int e = threadIdx.x; e < g.QK; e += 64) kd[e] = ks[e];
+    for (int e = threadIdx.x; e < g.VD; e += 64) vd[e] = vs[e];
+}
+
 // ---------------------------------------------------------------------------
 // Decode attention over the int8 ring, flash-decoding style.
 //
@@ -467,6 +489,32 @@ size_t nd_kv_vs_offset(const nd_kv_geom *g)
 size_t nd_kv_block_bytes(const nd_kv_geom *g)
 {
     return nd_kv_vs_offset(g) + nd::align_up(size_t(g->num_kv_heads) * g->cap * 4, 256);
+}
+
+size_t nd_kv_f32_v_offset(const nd_kv_geom *g)
+{
+    return nd::align_up(size_t(g->num_kv_heads) * g->cap * g->qk_head_dim * 4, 256);
+}
+
+size_t nd_kv_f32_block_bytes(const nd_kv_geom *g)
+{
+    return nd_kv_f32_v_offset(g) + nd::align_up(size_t(g->num_kv_heads) * g->cap * g->v_head_dim * 4, 256);
+}
+
+int nd_kv_write_f32(nd_ctx *ctx, const nd_kv_geom *g, void *kv, size_t kv_stride, size_t count,
+                    const int32_t *pos, const float *k, const float *v)
+{
+    if (int rc = nd::enter(ctx)) return rc;
+    if (int rc = check_geom(g)) return rc;
+    if (count == 0) return ND_OK;
+    ND_REQUIRE(kv && pos && k && v, "null buffer");
+    ND_REQUIRE(count <= 0x7fffffff, "count too large");
+    Geom kg = make_geom(g);
+    kg.v_off = nd_kv_f32_v_offset(g);
+    dim3 grid(unsigned(count), unsigned(g->num_kv_heads));
+    hipLaunchKernelGGL(kv_write_f32_kernel, grid, dim3(64), 0, ctx->stream, kg,
+                       static_cast<uint8_t *>(kv), kv_stride, pos, k, v);
+    return nd::check_launch("kv_write_f32");
 }
 
 int nd_fake_quant(nd_ctx *ctx, float *x, size_t rows, size_t dim)

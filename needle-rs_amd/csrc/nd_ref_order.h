@@ -22,11 +22,13 @@ int nd_cq_exact_set(nd_ctx *ctx, hipStream_t stream, int n, const nd_cq *const *
 // in one call.  With `gate` ([count][num_heads * 64], v_head_dim 64) each
 // output column becomes attn * sigmoid(gate) with butterfly stages 1..32
 // of its 128-wide group applied: the input nd_cq_exact_set finishes with
-// half_inv (v3/model.rs:309-313, hadamard.rs:24-55).
+// half_inv (v3/model.rs:309-313, hadamard.rs:24-55).  kv_f32: the blocks
+// are f32 KV blocks (nd_kv_f32_block_bytes) read through the f32 view, as
+// nd_attend_step_f32_exact.
 int nd_attend_exact_rows(nd_ctx *ctx, const nd_kv_geom *g, const void *kv, size_t kv_stride,
                          size_t count, int rows_per_block, const int32_t *lo, const int32_t *hi,
                          const float *q, float scale, int quant_query, float *out,
-                         const float *gate = nullptr);
+                         const float *gate = nullptr, int kv_f32 = 0);
 
 // One 128-wide group of a Cactus-Quants row dotted with a prepared
 // activation group in the reference's order (cq.rs:838-873): element e into

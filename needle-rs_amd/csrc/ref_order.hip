@@ -646,6 +646,86 @@ __device__ __forceinline__ float attn_scores(const ndkv::Geom &g, const float *q
     return mx;
 }
 
+// The same over the f32 view (F32View::dot, attention.rs:171-178): each
+// score is its own qk-long chain of q[e] * k[e], then times 1/sqrt(qk); no
+// key scale.  QC > 0: two positions' K rows load together and their chains
+// run interleaved.
+template <int QC, int NT>
+__device__ __forceinline__ float attn_scores_f32(const ndkv::Geom &g, const float *qs,
+                                                 const float *kb, int base, int span, float scale,
+                                                 float *sc)
+{
+    constexpr int kB = QC >= 4 ? 1 : 2;  // K rows in registers: at most 96 floats
+    const int tid = threadIdx.x;
+    float mx = -INFINITY;
+    if constexpr (QC > 0) {
+        for (int t0 = tid; t0 < span; t0 += NT * kB) {
+            float4 kw[kB][4 * QC];
+#pragma unroll
+            for (int u = 0; u < kB; ++u) {
+                const int t = t0 + u * NT;
+                int slot = base + (t < span ? t : 0);
+                if (slot >= g.cap) slot -= g.cap;
+                const float4 *kr = reinterpret_cast<const float4 *>(kb + size_t(slot) * (16 * QC));
+#pragma unroll
+                for (int c = 0; c < 4 * QC; ++c) kw[u][c] = kr[c];
+            }
+            float acc[kB];
+#pragma unroll
+            for (int u = 0; u < kB; ++u) acc[u] = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 4 * QC; ++c) {
+#pragma unroll
+                for (int u = 0; u < kB; ++u) {
+                    acc[u] += qs[4 * c] * kw[u][c].x;
+                    acc[u] += qs[4 * c + 1] * kw[u][c].y;
+                    acc[u] += qs[4 * c + 2] * kw[u][c].z;
+                    acc[u] += qs[4 * c + 3] * kw[u][c].w;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kB; ++u) {
+                const int t = t0 + u * NT;
+                if (t < span) {
+                    const float s = acc[u] * scale;
+                    sc[t] = s;
+                    if (s > mx) mx = s;
+                }
+            }
+        }
+    } else {
+        for (int t = tid; t < span; t += NT) {
+            int slot = base + t;
+            if (slot >= g.cap) slot -= g.cap;
+            const float4 *kr = reinterpret_cast<const float4 *>(kb + size_t(slot) * g.QK);
+            float acc = 0.0f;
+            for (int c = 0; c < g.QK / 4; ++c) {
+                const float4 w = kr[c];
+                acc += qs[4 * c] * w.x;
+                acc += qs[4 * c + 1] * w.y;
+                acc += qs[4 * c + 2] * w.z;
+                acc += qs[4 * c + 3] * w.w;
+            }
+            const float s = acc * scale;
+            sc[t] = s;
+            if (s > mx) mx = s;
+        }
+    }
+    return mx;
+}
+
+// One value item of the producers: 16 columns of one position, int8 codes
+// and the position's scale, or f32 values.
+template <bool KF>
+struct AttnVItem {
+    uint4 v;
+    float s;
+};
+template <>
+struct AttnVItem<true> {
+    float4 v[4];
+};
+
 // acc += v[0]; acc += v[1]; ... acc += v[n-1] in index order, v 16-byte
 // aligned LDS with at least 32 readable floats past v[n-1].  Terms go in
 // groups of 32, read into two register sets in turn, so that a group's
@@ -685,7 +765,9 @@ __device__ inline float lds_chain(float acc, const float *v, int n)
     return acc;
 }
 
-template <int CW, int QC>
+// KF: the cache is the f32 view (F32View, attention.rs:166-189): f32 K/V
+// rows at the f32 block's offsets, no scales, weights e * inv.
+template <int CW, int QC, bool KF>
 __global__ __launch_bounds__(kAttn2Threads, 4) void attn_exact2_kernel(
     ndkv::Geom g, const uint8_t *__restrict__ kv, size_t stride, const int32_t *__restrict__ lo,
     const int32_t *__restrict__ hi, const float *__restrict__ q, float scale, int quant_query,
@@ -724,10 +806,16 @@ __global__ __launch_bounds__(kAttn2Threads, 4) void attn_exact2_kernel(
         }
     }
     __syncthreads();
-    const int8_t *kb = reinterpret_cast<const int8_t *>(blk) + size_t(kvh) * g.cap * g.QK;
-    const float *ks = reinterpret_cast<const float *>(blk + g.ks_off) + size_t(kvh) * g.cap;
     const int base = p0 % g.cap;
-    float mx = attn_scores<QC, NT>(g, qs, kb, ks, base, span, scale, sc);
+    float mx;
+    if constexpr (KF) {
+        const float *kb = reinterpret_cast<const float *>(blk) + size_t(kvh) * g.cap * g.QK;
+        mx = attn_scores_f32<QC, NT>(g, qs, kb, base, span, scale, sc);
+    } else {
+        const int8_t *kb = reinterpret_cast<const int8_t *>(blk) + size_t(kvh) * g.cap * g.QK;
+        const float *ks = reinterpret_cast<const float *>(blk + g.ks_off) + size_t(kvh) * g.cap;
+        mx = attn_scores<QC, NT>(g, qs, kb, ks, base, span, scale, sc);
+    }
     mx = ndkv::wave_max(mx);
     if ((tid & 63) == 0) red[tid >> 6] = mx;
     __syncthreads();
@@ -760,23 +848,34 @@ __global__ __launch_bounds__(kAttn2Threads, 4) void attn_exact2_kernel(
     const int pt = tid - 64 * CW;
     const int pc = pt / T, tl = pt - (pt / T) * T;
     const bool has_item = producer && pc < pieces;
-    const int8_t *vbase = reinterpret_cast<const int8_t *>(blk + g.v_off) + size_t(kvh) * g.cap * g.VD;
-    const float *vs = reinterpret_cast<const float *>(blk + g.vs_off) + size_t(kvh) * g.cap;
-    uint4 vb[kPrefetch];
-    float vsb[kPrefetch];
+    // chunks of V loads in flight: f32 items are four times the registers
+    constexpr int PF = KF ? 2 : kPrefetch;
+    AttnVItem<KF> vb[PF];
     // Every load is issued unconditionally (a position past the span reads
     // position 0 and is never used), so the compiler can count the loads in
     // flight and wait for the oldest one only.
-    auto load = [&](int k, uint4 &v, float &f) {
+    auto load = [&](int k, AttnVItem<KF> &it) {
         int t = k * T + tl;
         t = has_item && t < span ? t : 0;
         int slot = base + t;
         if (slot >= g.cap) slot -= g.cap;
-        v = *reinterpret_cast<const uint4 *>(vbase + size_t(slot) * g.VD + pc * 16);
-        f = vs[slot];
+        if constexpr (KF) {
+            // V is the f32 block's last part: a thread without an item reads
+            // piece 0, so no read passes the row
+            const float4 *src = reinterpret_cast<const float4 *>(
+                reinterpret_cast<const float *>(blk + g.v_off) +
+                (size_t(kvh) * g.cap + slot) * g.VD + (has_item ? pc : 0) * 16);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) it.v[u] = src[u];
+        } else {
+            const int8_t *vbase = reinterpret_cast<const int8_t *>(blk + g.v_off) + size_t(kvh) * g.cap * g.VD;
+            const float *vs = reinterpret_cast<const float *>(blk + g.vs_off) + size_t(kvh) * g.cap;
+            it.v = *reinterpret_cast<const uint4 *>(vbase + size_t(slot) * g.VD + pc * 16);
+            it.s = vs[slot];
+        }
     };
 #pragma unroll
-    for (int j = 0; j < kPrefetch; ++j) load(j, vb[j], vsb[j]);
+    for (int j = 0; j < PF; ++j) load(j, vb[j]);
     // The softmax sum, with the bits of one chain in position order.  The
     // exps are >= +0, so a span long enough to pay for it takes the exact
     // parallel fold, its LDS in the product buffers (first written after the
@@ -796,32 +895,45 @@ __global__ __launch_bounds__(kAttn2Threads, 4) void attn_exact2_kernel(
     float acc = 0.0f;
     // Step k: producers fill chunk k, consumers add chunk k - 1.  Each role
     // runs its own loop; the roles are whole waves and both pass the same
-    // number of barriers (a multiple of kPrefetch, the last few empty).
-    const int steps = (nch + 1 + kPrefetch - 1) / kPrefetch * kPrefetch;
+    // number of barriers (a multiple of PF, the last few empty).
+    const int steps = (nch + 1 + PF - 1) / PF * PF;
     if (producer) {
         // this item's exp for the step after the current one, read ahead
         float e_next = sc[tl < span ? tl : 0];
-        for (int k0 = 0; k0 < steps; k0 += kPrefetch) {
+        for (int k0 = 0; k0 < steps; k0 += PF) {
 #pragma unroll
-            for (int j = 0; j < kPrefetch; ++j) {
+            for (int j = 0; j < PF; ++j) {
                 const int k = k0 + j;
                 const int t = k * T + tl;
                 const float e = e_next;
                 const int tn = t + T;
                 e_next = sc[tn < span ? tn : 0];
                 if (has_item && k < nch && t < span) {
-                    const float w = e * inv * vsb[j];
-                    const uint32_t dws[4] = {vb[j].x, vb[j].y, vb[j].z, vb[j].w};
                     float p[16];
+                    if constexpr (KF) {
+                        // F32View::accum: w = e * inv, then w * v
+                        const float w = e * inv;
 #pragma unroll
-                    for (int d = 0; d < 4; ++d)
+                        for (int u = 0; u < 4; ++u) {
+                            p[4 * u] = w * vb[j].v[u].x;
+                            p[4 * u + 1] = w * vb[j].v[u].y;
+                            p[4 * u + 2] = w * vb[j].v[u].z;
+                            p[4 * u + 3] = w * vb[j].v[u].w;
+                        }
+                    } else {
+                        // Int8View::accum: w = (e * inv) * v_scale, then w * code
+                        const float w = e * inv * vb[j].s;
+                        const uint32_t dws[4] = {vb[j].v.x, vb[j].v.y, vb[j].v.z, vb[j].v.w};
 #pragma unroll
-                        for (int b = 0; b < 4; ++b) p[d * 4 + b] = w * i8_lane(dws[d], b);
+                        for (int d = 0; d < 4; ++d)
+#pragma unroll
+                            for (int b = 0; b < 4; ++b) p[d * 4 + b] = w * i8_lane(dws[d], b);
+                    }
                     float *dst = prod + (k & 1) * kProdBuf + (pc * 16) * TS + tl;
 #pragma unroll
                     for (int u = 0; u < 16; ++u) dst[u * TS] = p[u];
                 }
-                load(k + kPrefetch, vb[j], vsb[j]);
+                load(k + PF, vb[j]);
                 __syncthreads();
             }
         }
@@ -918,18 +1030,30 @@ int nd_attend_step_i8_exact(nd_ctx *ctx, const nd_kv_geom *g, const void *kv, si
                                 nullptr);
 }
 
+int nd_attend_step_f32_exact(nd_ctx *ctx, const nd_kv_geom *g, const void *kv, size_t kv_stride,
+                             size_t count, const int32_t *lo, const int32_t *hi, const float *q,
+                             float scale, float *out)
+{
+    return nd_attend_exact_rows(ctx, g, kv, kv_stride, count, 1, lo, hi, q, scale, 0, out, nullptr,
+                                1);
+}
+
 }  // extern "C"
 
 int nd_attend_exact_rows(nd_ctx *ctx, const nd_kv_geom *g, const void *kv, size_t kv_stride,
                          size_t count, int rows_per_block, const int32_t *lo, const int32_t *hi,
                          const float *q, float scale, int quant_query, float *out,
-                         const float *gate)
+                         const float *gate, int kv_f32)
 {
     if (int rc = nd::enter(ctx)) return rc;
     ND_REQUIRE(rows_per_block >= 1, "rows_per_block %d", rows_per_block);
     ND_REQUIRE(!gate || g->v_head_dim == 64, "the gated epilogue needs v_head_dim 64, not %d",
                g->v_head_dim);
     if (int rc = ndkv::check_geom(g)) return rc;
+    ND_REQUIRE(!kv_f32 || !quant_query, "the f32 view takes the query as it is");
+    ND_REQUIRE(!kv_f32 || (g->v_head_dim <= 128 && g->cap <= kAttn2MaxCap),
+               "the f32 view needs v_head_dim <= 128 and cap <= %d (v %d, cap %d)", kAttn2MaxCap,
+               g->v_head_dim, g->cap);
     if (count == 0) return ND_OK;
     ND_REQUIRE(kv && lo && hi && q && out, "null buffer");
     ND_REQUIRE(count <= 65535, "count %zu above 65535", count);
@@ -945,11 +1069,19 @@ int nd_attend_exact_rows(nd_ctx *ctx, const nd_kv_geom *g, const void *kv, size_
         const size_t lds = size_t((g->cap + 3) & ~3) * 4 + 2 * kProdBuf * sizeof(float);
         const int cw = g->v_head_dim <= 64 ? 1 : 2;
         const int qc = g->qk_head_dim <= 64 ? g->qk_head_dim / 16 : 0;
-#define ND_ATTN2(CW, QC)                                                                       \
-    hipLaunchKernelGGL((attn_exact2_kernel<CW, QC>), dim3(unsigned(blocks)),                   \
-                       dim3(kAttn2Threads), lds, ctx->stream, ndkv::make_geom(g),               \
-                       static_cast<const uint8_t *>(kv), kv_stride, lo, hi, q, scale, quant_query, \
-                       out, int(groups), rows_per_block, gate)
+        ndkv::Geom kg = ndkv::make_geom(g);
+        if (kv_f32) kg.v_off = nd_kv_f32_v_offset(g);
+#define ND_ATTN2(CW, QC)                                                                          \
+    if (kv_f32)                                                                                   \
+        hipLaunchKernelGGL((attn_exact2_kernel<CW, QC, true>), dim3(unsigned(blocks)),            \
+                           dim3(kAttn2Threads), lds, ctx->stream, kg,                             \
+                           static_cast<const uint8_t *>(kv), kv_stride, lo, hi, q, scale, 0, out, \
+                           int(groups), rows_per_block, gate);                                    \
+    else                                                                                          \
+        hipLaunchKernelGGL((attn_exact2_kernel<CW, QC, false>), dim3(unsigned(blocks)),           \
+                           dim3(kAttn2Threads), lds, ctx->stream, kg,                             \
+                           static_cast<const uint8_t *>(kv), kv_stride, lo, hi, q, scale,         \
+                           quant_query, out, int(groups), rows_per_block, gate)
 #define ND_ATTN2_QC(CW)                    \
     switch (qc) {                          \
     case 1: ND_ATTN2(CW, 1); break;        \

@@ -502,7 +502,9 @@ __global__ void k_tails(const float *__restrict__ rows, float *__restrict__ tail
 constexpr int kMaxQkDims = 2048;  // (num_heads + num_kv_heads) * qk_head_dim
 constexpr int kMaxVDims = 1024;   // num_kv_heads * v_head_dim
 
-template <bool CHUNK>
+// KF: the session's cache is f32 (write_kv with KvPrecision::F32,
+// cache.rs:359-362): k and v are stored as they are.
+template <bool CHUNK, bool KF>
 __global__ __launch_bounds__(kT) void k_qkv_kv(QkvKv a)
 {
     __shared__ __align__(16) float qk[kMaxQkDims], sq[kMaxQkDims], vl[kMaxVDims];
@@ -572,6 +574,17 @@ __global__ __launch_bounds__(kT) void k_qkv_kv(QkvKv a)
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     uint8_t *blk = a.kv + sess * a.kv_stride;
     const int slot = p % a.cap;
+    if constexpr (KF) {
+        for (int vec = wave; vec < 2 * a.KVH; vec += kT / 64) {
+            const bool isv = vec >= a.KVH;
+            const int h = isv ? vec - a.KVH : vec;
+            const int dim = isv ? a.VD : hd;
+            const float *src = isv ? vl + h * a.VD : sq + (a.H + h) * hd;
+            float *dst = reinterpret_cast<float *>(blk + (isv ? a.v_off : 0)) + (size_t(h) * a.cap + slot) * dim;
+            for (int e = lane; e < dim; e += 64) dst[e] = src[e];
+        }
+        return;
+    }
     for (int vec = wave; vec < 2 * a.KVH; vec += kT / 64) {
         const bool isv = vec >= a.KVH;
         const int h = isv ? vec - a.KVH : vec;
@@ -1090,6 +1103,8 @@ struct nd_v3_batch {
     // positions one step may take per session (prefill), and the rows the
     // per-row buffers hold: B * chunk
     int chunk = 1, R = 0;
+    // KvPrecision::F32: f32 KV blocks, the query not fake-quantised
+    bool kv_f32 = false;
     std::vector<SessionHost> s;
     std::vector<uint8_t *> kv;        // per layer: B blocks
     std::vector<size_t> kv_stride;    // per layer
@@ -1482,6 +1497,12 @@ int nd_v3_batch_create(nd_ctx *ctx, const nd_v3_model *m, size_t sessions, size_
 int nd_v3_batch_create_chunked(nd_ctx *ctx, const nd_v3_model *m, size_t sessions, size_t max_len,
                                size_t hint, size_t max_chunk, nd_v3_batch **out)
 {
+    return nd_v3_batch_create_ex(ctx, m, sessions, max_len, hint, max_chunk, 1, out);
+}
+
+int nd_v3_batch_create_ex(nd_ctx *ctx, const nd_v3_model *m, size_t sessions, size_t max_len,
+                          size_t hint, size_t max_chunk, int kv_int8, nd_v3_batch **out)
+{
     if (int rc = nd::enter(ctx)) return rc;
     ND_REQUIRE(m && out, "null argument");
     *out = nullptr;
@@ -1498,6 +1519,7 @@ int nd_v3_batch_create_chunked(nd_ctx *ctx, const nd_v3_model *m, size_t session
     b->max_len = int(max_len);
     b->chunk = int(max_chunk);
     b->R = int(sessions * max_chunk);
+    b->kv_f32 = kv_int8 == 0;
     const int B = b->R, L = c.num_layers, nl = c.mhc_lanes, d = c.d_model;
     const int S = b->B;  // sessions: per-session state
     const int qd = c.num_heads * c.qk_head_dim, kd = c.num_kv_heads * c.qk_head_dim;
@@ -1528,10 +1550,15 @@ int nd_v3_batch_create_chunked(nd_ctx *ctx, const nd_v3_model *m, size_t session
         // while a row of the step still reads it
         const long wide = long(ref_cap) + long(b->chunk) - 1;
         const int dev_cap = int(wide < b->max_len ? wide : b->max_len);
+        if (b->kv_f32 && dev_cap > 8192) {
+            rc = nd::fail(ND_ERR_ARG, "layer %d: an f32 KV ring of %d positions (the f32 view "
+                          "attends over at most 8192)", li, dev_cap);
+            goto fail;
+        }
         for (auto &sh : b->s) sh.slots[li] = int(hnt < size_t(ref_cap) ? hnt : size_t(ref_cap));
         nd_kv_geom g{c.num_heads, c.num_kv_heads, c.qk_head_dim, c.v_head_dim, dev_cap};
         b->geom[li] = g;
-        b->kv_stride[li] = nd_kv_block_bytes(&g);
+        b->kv_stride[li] = b->kv_f32 ? nd_kv_f32_block_bytes(&g) : nd_kv_block_bytes(&g);
         if ((rc = dalloc(b->mem, &b->kv[li], b->kv_stride[li] * S))) goto fail;
         {
             hipError_t e = hipMemsetAsync(b->kv[li], 0, b->kv_stride[li] * S, ctx->stream);
@@ -1808,6 +1835,7 @@ int step_impl(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *
         LCHK("k_embed");
 
         const float qk_scale = 1.0f / std::sqrt(float(c.qk_head_dim));
+        const int kf = b->kv_f32 ? 1 : 0;
         const bool gate_fused = c.v_head_dim == 64 && m->pre_attn.group == 128 &&
                                 m->pre_attn.in_padded == od && m->layers[0].out->per_byte != 0;
         hipStream_t side = b->side;
@@ -1859,11 +1887,18 @@ int step_impl(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *
                          c.qkv_conv_taps, c.num_heads, c.num_kv_heads, c.qk_head_dim, c.v_head_dim,
                          b->kv[li], b->kv_stride[li], nd_kv_v_offset(&g), nd_kv_ks_offset(&g),
                          nd_kv_vs_offset(&g), g.cap, C, b->qn};
+                if (kf) qk.v_off = nd_kv_f32_v_offset(&g);
                 if (C == 1) {
-                    hipLaunchKernelGGL(k_qkv_kv<false>, dim3(B), dim3(kT), 0, st, qk);
+                    if (kf)
+                        hipLaunchKernelGGL((k_qkv_kv<false, true>), dim3(B), dim3(kT), 0, st, qk);
+                    else
+                        hipLaunchKernelGGL((k_qkv_kv<false, false>), dim3(B), dim3(kT), 0, st, qk);
                     LCHK("k_qkv_kv");
                 } else {
-                    hipLaunchKernelGGL(k_qkv_kv<true>, dim3(B), dim3(kT), 0, st, qk);
+                    if (kf)
+                        hipLaunchKernelGGL((k_qkv_kv<true, true>), dim3(B), dim3(kT), 0, st, qk);
+                    else
+                        hipLaunchKernelGGL((k_qkv_kv<true, false>), dim3(B), dim3(kT), 0, st, qk);
                     LCHK("k_qkv_kv");
                     const int tt = c.qkv_conv_taps - 1;
                     if (tt > 0) {
@@ -1884,14 +1919,14 @@ int step_impl(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *
             if (gate_fused) {
                 CK(nd_attend_exact_rows(ctx, &b->geom[li], b->kv[li], b->kv_stride[li], size_t(B), C,
                                         lo_dev + size_t(li) * B, hi_dev, C == 1 ? b->q : b->qn,
-                                        qk_scale, 1, b->attn, b->gate));
+                                        qk_scale, kf ? 0 : 1, b->attn, b->gate, kf));
                 const size_t r0 = 0, nr = size_t(d);
                 CK(nd_cq_exact_set(ctx, st, 1, &l.out, b->attn, size_t(B), &r0, &nr, &b->proj,
                                    "v3 out projection", m->pre_attn.inv));
             } else {
                 CK(nd_attend_exact_rows(ctx, &b->geom[li], b->kv[li], b->kv_stride[li], size_t(B), C,
                                         lo_dev + size_t(li) * B, hi_dev, C == 1 ? b->q : b->qn,
-                                        qk_scale, 1, b->attn));
+                                        qk_scale, kf ? 0 : 1, b->attn, nullptr, kf));
                 hipLaunchKernelGGL(k_gate_prep, dim3(B), dim3(kT), 0, st, b->attn, b->gate, b->ah, od,
                                    m->pre_attn);
                 LCHK("k_gate_prep");

@@ -98,6 +98,12 @@ _SIGS = [
     ("nd_v3_ladder", C.c_int, [_sz, _sz, C.POINTER(C.c_int32)]),
     ("nd_v3_cact_config_at_depth", C.c_int, [_vp, _sz, _sz, _vp, C.POINTER(C.c_int32)]),
     ("nd_v3_model_from_cact_at_depth", C.c_int, [_vp, _vp, _sz, _sz, C.POINTER(_vp)]),
+    ("nd_kv_f32_block_bytes", _sz, [C.POINTER(KvGeom)]),
+    ("nd_kv_f32_v_offset", _sz, [C.POINTER(KvGeom)]),
+    ("nd_kv_write_f32", C.c_int, [_vp, C.POINTER(KvGeom), _vp, _sz, _sz, _vp, _vp, _vp]),
+    ("nd_attend_step_f32_exact", C.c_int, [_vp, C.POINTER(KvGeom), _vp, _sz, _sz, _vp, _vp, _vp,
+                                           C.c_float, _vp]),
+    ("nd_v3_batch_create_ex", C.c_int, [_vp, _vp, _sz, _sz, _sz, _sz, C.c_int, C.POINTER(_vp)]),
 ]
 
 
@@ -414,6 +420,61 @@ def attend_step_i8(ctx, g, kv, kv_stride, lo_i32, hi_i32, q, scale=None, quant_q
     return out
 
 
+# ---- f32 KV (KvPrecision::F32) ----------------------------------------------
+
+def kv_f32_block_bytes(g):
+    return lib().nd_kv_f32_block_bytes(C.byref(g))
+
+
+def kv_alloc_f32(g, count=1, device=0):
+    """`count` zeroed f32 KV blocks, one after another (stride = block bytes)."""
+    torch = _torch()
+    nb = kv_f32_block_bytes(g)
+    return torch.zeros(count * nb, dtype=torch.uint8, device=device), nb
+
+
+def kv_write_f32(ctx, g, kv, kv_stride, pos_i32, k, v):
+    """V3Cache::write_kv with KvPrecision::F32 (cache.rs:359-362)."""
+    torch = _torch()
+    n = pos_i32.numel()
+    blocks = kv_f32_block_bytes(g) + (n - 1) * kv_stride if n else 0
+    _check(lib().nd_kv_write_f32(
+        ctx.h, C.byref(g), _arg(kv, torch.uint8, "kv", blocks), kv_stride, n,
+        _arg(pos_i32, torch.int32, "pos"),
+        _arg(k, torch.float32, "k", n * g.num_kv_heads * g.qk_head_dim),
+        _arg(v, torch.float32, "v", n * g.num_kv_heads * g.v_head_dim)))
+
+
+def attend_step_f32(ctx, g, kv, kv_stride, lo_i32, hi_i32, q, scale=None, out=None):
+    """attend_step over KvStore::F32 (attention.rs:166-189, 327-377),
+    bit-identical (nd_attend_step_f32_exact)."""
+    torch = _torch()
+    count = lo_i32.numel()
+    if scale is None:
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(g.qk_head_dim)))
+    if out is None:
+        out = torch.empty(count, g.num_heads * g.v_head_dim, dtype=torch.float32, device=q.device)
+    blocks = kv_f32_block_bytes(g) + (count - 1) * kv_stride if count else 0
+    i32, f32 = torch.int32, torch.float32
+    _check(lib().nd_attend_step_f32_exact(
+        ctx.h, C.byref(g), _arg(kv, torch.uint8, "kv", blocks), kv_stride, count,
+        _arg(lo_i32, i32, "lo"), _arg(hi_i32, i32, "hi", count),
+        _arg(q, f32, "q", count * g.num_heads * g.qk_head_dim), scale,
+        _arg(out, f32, "out", count * g.num_heads * g.v_head_dim)))
+    return out
+
+
+def kv_unpack_f32(g, block_u8):
+    """One f32 device block (CPU uint8 numpy array) as the reference's
+    slot-major views: k [cap][kvh][qk] f32, v [cap][kvh][vd]."""
+    H, cap, qk, vd = g.num_kv_heads, g.cap, g.qk_head_dim, g.v_head_dim
+    vo = lib().nd_kv_f32_v_offset(C.byref(g))
+    b = np.asarray(block_u8)
+    k = b[:4 * H * cap * qk].view(np.float32).reshape(H, cap, qk).transpose(1, 0, 2)
+    v = b[vo:vo + 4 * H * cap * vd].view(np.float32).reshape(H, cap, vd).transpose(1, 0, 2)
+    return np.ascontiguousarray(k), np.ascontiguousarray(v)
+
+
 def kv_unpack(g, block_u8):
     """Split one device block (as a CPU uint8 numpy array) into the
     reference's slot-major views: k [cap][kvh][qk] i8, v, ks [cap][kvh], vs."""
@@ -639,15 +700,19 @@ class V3Model:
 
 
 class V3Batch:
-    """`sessions` int8-KV decode sessions stepped in lockstep on the device;
-    with max_chunk > 1 a prompt is prefilled up to max_chunk positions per
-    pass (the reference's chunked prefill, bit-identical to stepping)."""
+    """`sessions` decode sessions stepped in lockstep on the device, with
+    int8 KV caches (kv_int8=True, KvPrecision::Int8) or f32 ones
+    (KvPrecision::F32, needle_v3_generate's default); with max_chunk > 1 a
+    prompt is prefilled up to max_chunk positions per pass (the reference's
+    chunked prefill, bit-identical to stepping)."""
 
-    def __init__(self, model, sessions, max_len, hint=None, max_chunk=1):
+    def __init__(self, model, sessions, max_len, hint=None, max_chunk=1, kv_int8=True):
         self.model, self.sessions, self.max_chunk = model, sessions, max_chunk
+        self.kv_int8 = bool(kv_int8)
         h = C.c_void_p()
-        _check(lib().nd_v3_batch_create_chunked(model.ctx.h, model.h, sessions, max_len,
-                                                hint or max_len, max_chunk, C.byref(h)))
+        _check(lib().nd_v3_batch_create_ex(model.ctx.h, model.h, sessions, max_len,
+                                           hint or max_len, max_chunk, int(self.kv_int8),
+                                           C.byref(h)))
         self.h = h
 
     def close(self):

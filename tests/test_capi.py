@@ -39,6 +39,20 @@ def test_kv_block_layout_v3_and_mha():
         assert off_v % 256 == 0
 
 
+def test_kv_f32_block_layout():
+    """f32 blocks: k [kvh][cap][qk] then v [kvh][cap][vd], 256-aligned; per
+    position per layer kv_heads*(qk+v)*4 bytes, as kv_bytes_at counts an f32
+    cache (config.rs:162-179)."""
+    g = nd.kv_geom(12, 2, 48, 64, 1000)
+    v_off = (2 * 1000 * 48 * 4 + 255) // 256 * 256
+    assert nd.lib().nd_kv_f32_v_offset(g) == v_off
+    assert nd.kv_f32_block_bytes(g) == v_off + (2 * 1000 * 64 * 4 + 255) // 256 * 256
+    g = nd.kv_geom(12, 2, 48, 64, 1024)
+    assert nd.kv_f32_block_bytes(g) // 1024 == 2 * (48 + 64) * 4
+    g = nd.kv_geom(4, 2, 48, 64, 17)
+    assert nd.lib().nd_kv_f32_v_offset(g) % 256 == 0 and nd.kv_f32_block_bytes(g) % 256 == 0
+
+
 def test_ctx_create_reports_error_without_gpu():
     import torch
     if torch.cuda.is_available():
