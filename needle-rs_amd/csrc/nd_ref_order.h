@@ -4,7 +4,7 @@
 
 #include "nd_cq_internal.h"
 
-// n (<= 4) Cactus-Quants weights applied to the same prepared input xh
+// n (<= 12) Cactus-Quants weights applied to the same prepared input xh
 // ([batch][in_padded]) in one launch on `stream` when they share width,
 // group and input size (else one launch each); y[k] receives rows[k] rows
 // of weight k from row_start[k], batch-major ([batch][rows[k]]).
@@ -16,6 +16,14 @@
 int nd_cq_exact_set(nd_ctx *ctx, hipStream_t stream, int n, const nd_cq *const *w, const float *xh,
                     size_t batch, const size_t *row_start, const size_t *rows, float *const *y,
                     const char *what, float half_inv = 0.0f);
+
+// As nd_cq_exact_set with an input of its own per weight (xhs[k],
+// [batch][in_padded]), up to 12 weights: e.g. every Engram site's key and
+// value projections in one launch.
+int nd_cq_exact_multi(nd_ctx *ctx, hipStream_t stream, int n, const nd_cq *const *w,
+                      const float *const *xhs, size_t batch, const size_t *row_start,
+                      const size_t *rows, float *const *y, const char *what,
+                      float half_inv = 0.0f);
 
 // nd_attend_step_i8_exact with query row i reading the KV block of
 // kv + (i / rows_per_block) * kv_stride: several positions of one session

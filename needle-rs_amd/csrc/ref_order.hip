@@ -61,7 +61,7 @@ struct CqExact {
 
 // Up to kMaxSet weights with the same input, width and group in one launch:
 // blocks [tile0[k], tile0[k + 1]) work on weight k.
-constexpr int kMaxSet = 4;
+constexpr int kMaxSet = 12;
 struct CqExactSet {
     CqExact w[kMaxSet];
     int tile0[kMaxSet + 1];
@@ -321,14 +321,25 @@ int nd_cq_exact_set(nd_ctx *ctx, hipStream_t stream, int n, const nd_cq *const *
                     size_t batch, const size_t *row_start, const size_t *rows, float *const *y,
                     const char *what, float half_inv)
 {
+    ND_REQUIRE(n >= 1 && n <= kMaxSet, "%s: %d weights in one set", what, n);
+    const float *xhs[kMaxSet];
+    for (int k = 0; k < n; ++k) xhs[k] = xh;
+    return nd_cq_exact_multi(ctx, stream, n, w, xhs, batch, row_start, rows, y, what, half_inv);
+}
+
+int nd_cq_exact_multi(nd_ctx *ctx, hipStream_t stream, int n, const nd_cq *const *w,
+                      const float *const *xhs, size_t batch, const size_t *row_start,
+                      const size_t *rows, float *const *y, const char *what, float half_inv)
+{
     if (int rc = nd::enter(ctx)) return rc;
-    ND_REQUIRE(n >= 1 && n <= kMaxSet && w && xh && row_start && rows && y, "%s: bad arguments",
+    ND_REQUIRE(n >= 1 && n <= kMaxSet && w && xhs && row_start && rows && y, "%s: bad arguments",
                what);
     if (batch == 0) return ND_OK;
     const nd_cq *w0 = w[0];
-    bool same = true;
+    bool same = true, aligned = true;
     for (int k = 0; k < n; ++k) {
-        ND_REQUIRE(w[k] && y[k], "%s: null weight or output", what);
+        ND_REQUIRE(w[k] && y[k] && xhs[k], "%s: null weight, input or output", what);
+        aligned = aligned && (reinterpret_cast<uintptr_t>(xhs[k]) & 15) == 0;
         ND_REQUIRE(row_start[k] <= w[k]->out_feat && rows[k] <= w[k]->out_feat - row_start[k],
                    "%s: rows %zu..%zu outside %zu", what, row_start[k], row_start[k] + rows[k],
                    w[k]->out_feat);
@@ -341,8 +352,7 @@ int nd_cq_exact_set(nd_ctx *ctx, hipStream_t stream, int n, const nd_cq *const *
     const size_t G = w0->num_groups;
     const int P = int(w0->per_byte);
     const bool fast = same && (P == 2 || P == 4) && w0->group % 8 == 0 && (w0->group / P) % 4 == 0 &&
-                      G <= kThreads && w0->row_bytes % 4 == 0 &&
-                      (reinterpret_cast<uintptr_t>(xh) & 15) == 0;
+                      G <= kThreads && w0->row_bytes % 4 == 0 && aligned;
     if (fast) {
         const int rpb = int(kThreads / G);
         const size_t pairs = size_t(rpb) * G;
@@ -364,7 +374,7 @@ int nd_cq_exact_set(nd_ctx *ctx, hipStream_t stream, int n, const nd_cq *const *
             int tiles = 0;
             for (int k = 0; k < n; ++k) {
                 if (rows[k] == 0) continue;
-                set.w[set.n] = CqExact{w[k]->packed, w[k]->norms, w[k]->lv, xh, y[k], w[k]->row_bytes,
+                set.w[set.n] = CqExact{w[k]->packed, w[k]->norms, w[k]->lv, xhs[k], y[k], w[k]->row_bytes,
                                        int(w[k]->in_padded), int(w[k]->group), int(G),
                                        int(row_start[k]), int(rows[k]), int(batch), rpb,
                                        int(w[k]->bits == kTernary), half_inv};
@@ -383,7 +393,7 @@ int nd_cq_exact_set(nd_ctx *ctx, hipStream_t stream, int n, const nd_cq *const *
     ND_REQUIRE(half_inv == 0.0f, "%s: a half-transformed input needs the 128-group kernel", what);
     for (int k = 0; k < n; ++k)
         if (rows[k])
-            if (int rc = cq_serial(stream, w[k], xh, batch, row_start[k], rows[k], y[k], what))
+            if (int rc = cq_serial(stream, w[k], xhs[k], batch, row_start[k], rows[k], y[k], what))
                 return rc;
     return ND_OK;
 }

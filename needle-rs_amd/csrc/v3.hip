@@ -161,16 +161,26 @@ __device__ inline void scatter_up(float *lg, float *ln, const float *gp, const f
     }
 }
 
-// ---- Engram value conv step (cache.rs:445-482) -------------------------------
-__global__ void k_engram_conv(float *__restrict__ ev, const float *__restrict__ taps,
-                              float *__restrict__ tail, const int32_t *__restrict__ pos, int taps_n,
-                              int dil, int max_order, int reach, int d)
+// ---- Engram value conv step (cache.rs:445-482), every site at once ----------
+// (blockIdx.z: the site; its values at ev + z * site_stride)
+constexpr int kMaxSitesLaunch = 8;
+struct EngramConv {
+    float *ev;
+    size_t site_stride;
+    const float *taps[kMaxSitesLaunch];
+    float *tail[kMaxSitesLaunch];
+};
+
+__global__ void k_engram_conv(EngramConv a, const int32_t *__restrict__ pos, int taps_n, int dil,
+                              int max_order, int reach, int d)
 {
     const size_t b = blockIdx.y;
     const int c = blockIdx.x * blockDim.x + threadIdx.x;
     if (c >= d) return;
+    float *__restrict__ ev = a.ev + blockIdx.z * a.site_stride;
+    const float *__restrict__ taps = a.taps[blockIdx.z];
     const int p = pos[b];
-    float *tb = tail + b * size_t(reach) * d;
+    float *tb = a.tail[blockIdx.z] + b * size_t(reach) * d;
     const float raw = ev[b * d + c];
     float acc = 0.0f;
     for (int j = 0; j < taps_n; ++j) {
@@ -208,6 +218,56 @@ __global__ void k_engram_conv_rows(const float *__restrict__ raw, float *__restr
         acc += taps[j * d + c] * val;
     }
     out[b * d + c] = acc;
+}
+
+// ---- Engram fetch, every site at once (engram.rs:67-104, model.rs:162-191):
+// one wave per (site, row, table) takes the hashed table row through
+// dequantize_row (cq.rs:763-779: level * norm, then the normalised FWHT of
+// its one 128-wide group) and then through the key projection's
+// prepare_input (hadamard.rs:24-55: the FWHT of that same group of the
+// concatenated input), into the site's prepared key input.  A masked row
+// (an n-gram with too little history) is zeros throughout.
+struct EngramFetch {
+    const uint8_t *packed[kMaxSitesLaunch];
+    const float *norms[kMaxSitesLaunch];
+    const float *lv[kMaxSitesLaunch];
+    float *fh[kMaxSitesLaunch];  // [B][nt * 128] per site
+    const int32_t *rows;         // [B][nt] table rows, -1 masked
+    int out_feat, row_bytes, w, ternary, count, sites;  // count = B * nt
+    float inv_t, inv_k;
+};
+
+__device__ inline uint32_t fetch_code(const uint8_t *row, int k, int w, int row_bytes)
+{
+    const int bit = k * w, byte = bit >> 3, shift = bit & 7;
+    const uint32_t lo = row[byte];
+    const uint32_t hi = (shift + w > 8 && byte + 1 < row_bytes) ? row[byte + 1] : 0u;
+    return ((lo | (hi << 8)) >> shift) & ((1u << w) - 1u);
+}
+
+__global__ __launch_bounds__(256) void k_engram_fetch(EngramFetch a)
+{
+    const int wave = int(blockIdx.x) * 4 + int(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (wave >= a.sites * a.count) return;  // the whole wave leaves
+    const int s = wave / a.count, i = wave - s * a.count;
+    int o = a.rows[i];
+    float x0 = 0.0f, x1 = 0.0f;
+    if (o >= 0) {
+        o = o >= a.out_feat ? a.out_feat - 1 : o;
+        const uint8_t *row = a.packed[s] + size_t(o) * a.row_bytes;
+        const float norm = a.norms[s][o];
+        const uint32_t c0 = fetch_code(row, lane, a.w, a.row_bytes);
+        const uint32_t c1 = fetch_code(row, 64 + lane, a.w, a.row_bytes);
+        const float *lv = a.lv[s];
+        x0 = lv[a.ternary ? (c0 == 3 ? 0 : (c0 == 1 ? 2 : 1)) : int(c0)] * norm;
+        x1 = lv[a.ternary ? (c1 == 3 ? 0 : (c1 == 1 ? 2 : 1)) : int(c1)] * norm;
+        fwht128_wave(x0, x1, a.inv_t);
+        fwht128_wave(x0, x1, a.inv_k);
+    }
+    float *dst = a.fh[s] + size_t(i) * 128;
+    dst[lane] = x0;
+    dst[64 + lane] = x1;
 }
 
 // ---- layer input: the previous layer's scatter up, then this layer's mix
@@ -434,7 +494,7 @@ struct QkvKv {
     float *qt, *kt, *vt;                    // tails [B][taps-1][dim]
     const float *q_taps, *k_taps, *v_taps;  // [taps][dim]
     const float *q_norm, *k_norm;           // [hd]
-    const float *rope;                      // [R][2][hd/2]: cos then sin
+    const float *rope;                      // [max_seq_len][2][hd/2]: cos then sin
     const int32_t *pos;                     // [R]
     int qd, kd, vd, taps, H, KVH, hd, VD;
     uint8_t *kv;                            // session s's block at kv + s * kv_stride
@@ -550,7 +610,7 @@ __global__ __launch_bounds__(kT) void k_qkv_kv(QkvKv a)
     if (threadIdx.x < heads)
         rms[threadIdx.x] = sqrtf(chain_sum(sq + threadIdx.x * hd, hd) / float(hd) + 1e-6f);
     __syncthreads();
-    const float *cs = a.rope + b * 2 * half, *sn = cs + half;
+    const float *cs = a.rope + size_t(p) * 2 * half, *sn = cs + half;
     for (int e = threadIdx.x; e < heads * half; e += kT) {
         const int hh = e / half, i = e - hh * half;
         const float *sc = hh < a.H ? a.q_norm : a.k_norm;
@@ -1078,6 +1138,9 @@ struct nd_v3_model {
     float embed_scale = 1.0f;
     // RoPE frequencies 1 / theta^(2j / qk), libm's powf (model.rs:378-386)
     std::vector<float> rope_freq;
+    // [max_seq_len][qk]: cos then sin of pos * freq[j], libm's cosf/sinf
+    // (model.rs:387-394), for every position a session can reach
+    float *rope_tab = nullptr;
     // prepared-input geometry of the projections each fused kernel feeds
     Prep pre_nx{}, pre_h{}, pre_attn{}, pre_x{};
     std::vector<void *> mem;  // every device float/int buffer
@@ -1123,6 +1186,7 @@ struct nd_v3_batch {
     // several positions per step: the normed q ([R][qd]) and the Engram
     // conv ([sites][R][d]) go here, the projections' rows stay as they are
     float *qn = nullptr, *evc = nullptr;
+    size_t fh_width = 0;  // floats per row of a site's prepared key input
     int32_t *next = nullptr;
     // The scatter-up gates of a layer depend only on its input lanes: they
     // run on `side` while the layer's attention and MLP run on the caller's
@@ -1281,6 +1345,28 @@ int nd_v3_model_create(nd_ctx *ctx, const nd_v3_cfg *cfg, const float *codebook,
     for (int j = 0; j < c.qk_head_dim / 2; ++j)
         m->rope_freq.push_back(1.0f / nd_powf(c.rope_theta, float(2 * j) / float(c.qk_head_dim)));
     m->device = ctx->device;
+    {
+        const int half = c.qk_head_dim / 2;
+        m->staged.emplace_back(size_t(c.max_seq_len) * c.qk_head_dim);
+        std::vector<float> &tab = m->staged.back();
+        for (int pos = 0; pos < c.max_seq_len; ++pos)
+            for (int j = 0; j < half; ++j) {
+                const float angle = float(pos) * m->rope_freq[j];
+                tab[size_t(pos) * c.qk_head_dim + j] = nd_cosf(angle);
+                tab[size_t(pos) * c.qk_head_dim + half + j] = nd_sinf(angle);
+            }
+        int rc0 = dalloc(m->mem, &m->rope_tab, tab.size());
+        if (rc0) {
+            delete m;
+            return rc0;
+        }
+        hipError_t e = hipMemcpyAsync(m->rope_tab, tab.data(), tab.size() * 4, hipMemcpyHostToDevice,
+                                      ctx->stream);
+        if (e != hipSuccess) {
+            delete m;
+            return nd::hip_fail(e, "hipMemcpyAsync (RoPE table)");
+        }
+    }
     const size_t d = c.d_model, L = c.num_layers, nl = c.mhc_lanes;
     const size_t qd = size_t(c.num_heads) * c.qk_head_dim, kd = size_t(c.num_kv_heads) * c.qk_head_dim;
     const size_t vd = size_t(c.num_kv_heads) * c.v_head_dim, od = size_t(c.num_heads) * c.v_head_dim;
@@ -1605,7 +1691,12 @@ int nd_v3_batch_create_ex(nd_ctx *ctx, const nd_v3_model *m, size_t sessions, si
     A(hres, size_t(B) * nl * nl);
     A(emb, size_t(B) * d);
     A(fetched, size_t(B) * nt * c.e_sub_dim);
-    A(fh, size_t(B) * nt * c.e_sub_dim);
+    // one prepared key input per site: [sites][B][fh_width]
+    b->fh_width = size_t(nt) * c.e_sub_dim;
+    for (int s = 0; s < c.n_sites; ++s)
+        if (m->sites[s].key->in_padded > b->fh_width) b->fh_width = m->sites[s].key->in_padded;
+    b->fh_width = (b->fh_width + 3) & ~size_t(3);
+    A(fh, size_t(c.n_sites > 0 ? c.n_sites : 1) * B * b->fh_width);
     A(ek, size_t(c.n_sites > 0 ? c.n_sites : 1) * B * d);
     A(ev, size_t(c.n_sites > 0 ? c.n_sites : 1) * B * d);
     A(xh, size_t(S) * m->pre_x.in_padded);
@@ -1621,8 +1712,11 @@ int nd_v3_batch_create_ex(nd_ctx *ctx, const nd_v3_model *m, size_t sessions, si
     {
         hipError_t e = hipStreamCreateWithFlags(&b->side, hipStreamNonBlocking);
         for (int i = 0; i < 2 && e == hipSuccess; ++i) {
-            e = hipEventCreateWithFlags(&b->ev_in[i], hipEventDisableTiming);
-            if (e == hipSuccess) e = hipEventCreateWithFlags(&b->ev_gates[i], hipEventDisableTiming);
+            // these only order the two streams on this GPU: no system-scope
+            // fence (with one, each record cost ~12 us of idle GPU per layer)
+            const unsigned fl = hipEventDisableTiming | hipEventDisableSystemFence;
+            e = hipEventCreateWithFlags(&b->ev_in[i], fl);
+            if (e == hipSuccess) e = hipEventCreateWithFlags(&b->ev_gates[i], fl);
         }
         if (e != hipSuccess) {
             rc = nd::hip_fail(e, "stream/event creation");
@@ -1630,15 +1724,18 @@ int nd_v3_batch_create_ex(nd_ctx *ctx, const nd_v3_model *m, size_t sessions, si
         }
     }
     {
-        // step inputs: tokens, pos, lo[L][B], hi[B], engram rows [B][nt], rope [B][qk]
+        // step inputs: tokens, pos, hi[B], lo[L][B], engram rows [B][nt]
         const size_t ints = size_t(B) * (3 + L + nt);
-        const size_t floats = size_t(B) * c.qk_head_dim;
-        b->step_bytes = ints * 4 + floats * 4;
+        b->step_bytes = ints * 4;
         if ((rc = dalloc(b->mem, reinterpret_cast<uint8_t **>(&b->step_dev), b->step_bytes))) goto fail;
         hipError_t e = hipSuccess;
         for (int i = 0; i < nd_v3_batch::kStages && e == hipSuccess; ++i) {
             e = hipHostMalloc(&b->stage_host[i], b->step_bytes, hipHostMallocDefault);
-            if (e == hipSuccess) e = hipEventCreateWithFlags(&b->stage_done[i], hipEventDisableTiming);
+            // the host waits on it before rewriting the buffer the copy read;
+            // no device data is read through it, so no system-scope fence
+            if (e == hipSuccess)
+                e = hipEventCreateWithFlags(&b->stage_done[i],
+                                            hipEventDisableTiming | hipEventDisableSystemFence);
         }
         if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void **>(&b->next_host), size_t(S) * 4, hipHostMallocDefault);
         if (e != hipSuccess) {
@@ -1715,7 +1812,7 @@ int step_impl(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *
     const int L = c.num_layers, nl = c.mhc_lanes, d = c.d_model;
     const int qd = c.num_heads * c.qk_head_dim, kd = c.num_kv_heads * c.qk_head_dim;
     const int vd = c.num_kv_heads * c.v_head_dim, od = c.num_heads * c.v_head_dim;
-    const int nt = c.n_orders * c.e_heads, half = c.qk_head_dim / 2;
+    const int nt = c.n_orders * c.e_heads;
     const int mo = max_order(c);
     const size_t rows = nd_v3_logit_rows(m);
     for (int i = 0; i < S; ++i)
@@ -1728,7 +1825,6 @@ int step_impl(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *
     int32_t *si = static_cast<int32_t *>(b->stage_host[stage]);
     int32_t *h_tok = si, *h_pos = si + B, *h_hi = si + 2 * B, *h_lo = si + 3 * B;
     int32_t *h_rows = si + 3 * B + size_t(L) * B;
-    float *h_rope = reinterpret_cast<float *>(si + size_t(B) * (3 + L + nt));
     for (int row = 0; row < B; ++row) {
         const int i = row;  // buffer row: session row / C, position pos + row % C
         SessionHost &sh = b->s[row / C];
@@ -1757,12 +1853,6 @@ int step_impl(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *
                 const bool valid = pos + 1 >= c.orders[oi];
                 h_rows[size_t(i) * nt + table] = valid ? int32_t(uint32_t(table) * uint32_t(c.e_slots) + slot) : -1;
             }
-        // model.rs:378-394 RoPE angles for this position, libm's cosf/sinf
-        for (int j = 0; j < half; ++j) {
-            const float angle = float(pos) * m->rope_freq[j];
-            h_rope[size_t(i) * 2 * half + j] = nd_cosf(angle);
-            h_rope[size_t(i) * 2 * half + half + j] = nd_sinf(angle);
-        }
         // cache.rs:291-331 ensure + span per layer
         for (int li = 0; li < L; ++li) {
             const int cap = b->cap[li];
@@ -1778,13 +1868,12 @@ int step_impl(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *
         }
     }
     // this step's rows only: the buffer is sized for a full pass of max_chunk
-    const size_t used = size_t(B) * (3 + L + nt) * 4 + size_t(B) * c.qk_head_dim * 4;
+    const size_t used = size_t(B) * (3 + L + nt) * 4;
     ND_HIP(hipMemcpyAsync(b->step_dev, b->stage_host[stage], used, hipMemcpyHostToDevice,
                           ctx->stream));
     int32_t *tok_dev = static_cast<int32_t *>(b->step_dev);
     int32_t *pos_dev = tok_dev + B, *hi_dev = tok_dev + 2 * B, *lo_dev = tok_dev + 3 * B;
     int32_t *rows_dev = tok_dev + 3 * B + size_t(L) * B;
-    float *rope_dev = reinterpret_cast<float *>(tok_dev + size_t(B) * (3 + L + nt));
     ND_HIP(hipEventRecord(b->stage_done[stage], ctx->stream));
     b->stage_pending[stage] = true;
     b->stage_next = (stage + 1) % nd_v3_batch::kStages;
@@ -1799,24 +1888,89 @@ int step_impl(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *
     auto enqueue = [&](bool argmax) -> int {
         int rc = ND_OK;
         // ---- Engram for this position (model.rs:162-191) -------------------------
-        for (int s = 0; s < c.n_sites; ++s) {
-            const Site &site = m->sites[s];
-            CK(nd_cq_dequantize_rows(ctx, site.tables, rows_dev, size_t(B) * nt, b->fetched));
-            CK(nd_cq_prepare_input(ctx, site.key, b->fetched, B, b->fh));
-            {
-                const nd_cq *ws[2] = {site.key, site.value};
-                const size_t r0[2] = {0, 0};
-                const size_t nr[2] = {size_t(d), size_t(d)};
-                float *ys[2] = {b->ek + size_t(s) * Rcap * d, b->ev + size_t(s) * Rcap * d};
-                CK(nd_cq_exact_set(ctx, st, 2, ws, b->fh, size_t(B), r0, nr, ys, "v3 engram key/value"));
+        // the prepared key inputs of every site: one fused fetch when every
+        // table row is one 128-wide group feeding the key's 128-groups
+        const size_t fstride = size_t(B) * b->fh_width;
+        bool fused = c.n_sites > 0;
+        for (int s = 0; s < c.n_sites && fused; ++s) {
+            const nd_cq *t = m->sites[s].tables, *k = m->sites[s].key, *t0 = m->sites[0].tables;
+            fused = t->group == 128 && t->in_feat == 128 && t->num_groups == 1 && k->group == 128 &&
+                    k->in_feat == size_t(nt) * 128 && k->in_padded == size_t(nt) * 128 &&
+                    t->out_feat == t0->out_feat && t->row_bytes == t0->row_bytes &&
+                    t->bits == t0->bits && t->per_byte != 0 && t->inv_sqrt_group == t0->inv_sqrt_group &&
+                    k->inv_sqrt_group == m->sites[0].key->inv_sqrt_group;
+        }
+        if (fused) {
+            for (int s0 = 0; s0 < c.n_sites; s0 += kMaxSitesLaunch) {
+                const int ns = c.n_sites - s0 < kMaxSitesLaunch ? c.n_sites - s0 : kMaxSitesLaunch;
+                const nd_cq *t0 = m->sites[s0].tables;
+                EngramFetch ef{};
+                for (int j = 0; j < ns; ++j) {
+                    const nd_cq *t = m->sites[s0 + j].tables;
+                    ef.packed[j] = t->packed;
+                    ef.norms[j] = t->norms;
+                    ef.lv[j] = t->lv;
+                    ef.fh[j] = b->fh + size_t(s0 + j) * fstride;
+                }
+                ef.rows = rows_dev;
+                ef.out_feat = int(t0->out_feat);
+                ef.row_bytes = int(t0->row_bytes);
+                ef.w = t0->bits == 5 ? 2 : int(t0->bits);
+                ef.ternary = t0->bits == 5;
+                ef.count = B * nt;
+                ef.sites = ns;
+                ef.inv_t = t0->inv_sqrt_group;
+                ef.inv_k = m->sites[s0].key->inv_sqrt_group;
+                const int waves = ns * B * nt;
+                hipLaunchKernelGGL(k_engram_fetch, dim3((waves + 3) / 4), dim3(256), 0, st, ef);
+                LCHK("k_engram_fetch");
             }
-            const int reach = (c.e_conv_taps - 1) * c.e_conv_dilation;
-            if (C == 1) {
-                hipLaunchKernelGGL(k_engram_conv, dim3((d + 255) / 256, B), dim3(256), 0, st,
-                                   b->ev + size_t(s) * Rcap * d, site.taps, b->et[s], pos_dev,
-                                   c.e_conv_taps, c.e_conv_dilation, mo, reach, d);
+        } else {
+            for (int s = 0; s < c.n_sites; ++s) {
+                const Site &site = m->sites[s];
+                CK(nd_cq_dequantize_rows(ctx, site.tables, rows_dev, size_t(B) * nt, b->fetched));
+                CK(nd_cq_prepare_input(ctx, site.key, b->fetched, B, b->fh + size_t(s) * fstride));
+            }
+        }
+        // every site's key and value projections, six sites a launch
+        for (int s0 = 0; s0 < c.n_sites; s0 += 6) {
+            const int ns = c.n_sites - s0 < 6 ? c.n_sites - s0 : 6;
+            const nd_cq *ws[12];
+            const float *xs[12];
+            size_t r0[12], nr[12];
+            float *ys[12];
+            for (int j = 0; j < ns; ++j) {
+                const Site &site = m->sites[s0 + j];
+                const float *fh = b->fh + size_t(s0 + j) * fstride;
+                ws[2 * j] = site.key;
+                ws[2 * j + 1] = site.value;
+                xs[2 * j] = xs[2 * j + 1] = fh;
+                r0[2 * j] = r0[2 * j + 1] = 0;
+                nr[2 * j] = nr[2 * j + 1] = size_t(d);
+                ys[2 * j] = b->ek + size_t(s0 + j) * Rcap * d;
+                ys[2 * j + 1] = b->ev + size_t(s0 + j) * Rcap * d;
+            }
+            CK(nd_cq_exact_multi(ctx, st, 2 * ns, ws, xs, size_t(B), r0, nr, ys, "v3 engram key/value"));
+        }
+        const int reach = (c.e_conv_taps - 1) * c.e_conv_dilation;
+        if (C == 1) {
+            for (int s0 = 0; s0 < c.n_sites; s0 += kMaxSitesLaunch) {
+                const int ns = c.n_sites - s0 < kMaxSitesLaunch ? c.n_sites - s0 : kMaxSitesLaunch;
+                EngramConv ec{};
+                ec.ev = b->ev + size_t(s0) * Rcap * d;
+                ec.site_stride = size_t(Rcap) * d;
+                for (int j = 0; j < ns; ++j) {
+                    ec.taps[j] = m->sites[s0 + j].taps;
+                    ec.tail[j] = b->et[s0 + j];
+                }
+                hipLaunchKernelGGL(k_engram_conv, dim3((d + 255) / 256, B, ns), dim3(256), 0, st, ec,
+                                   pos_dev, c.e_conv_taps, c.e_conv_dilation, mo, reach, d);
                 LCHK("k_engram_conv");
-            } else {
+            }
+        }
+        for (int s = 0; s < c.n_sites && C > 1; ++s) {
+            const Site &site = m->sites[s];
+            {
                 hipLaunchKernelGGL(k_engram_conv_rows, dim3((d + 255) / 256, B), dim3(256), 0, st,
                                    b->ev + size_t(s) * Rcap * d, b->evc + size_t(s) * Rcap * d,
                                    site.taps, b->et[s], pos_dev, c.e_conv_taps, c.e_conv_dilation, mo,
@@ -1883,7 +2037,7 @@ int step_impl(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *
             {
                 const nd_kv_geom &g = b->geom[li];
                 QkvKv qk{b->q, b->k, b->v, b->qt[li], b->kt[li], b->vt[li], l.q_taps, l.k_taps,
-                         l.v_taps, l.q_norm, l.k_norm, rope_dev, pos_dev, qd, kd, vd,
+                         l.v_taps, l.q_norm, l.k_norm, m->rope_tab, pos_dev, qd, kd, vd,
                          c.qkv_conv_taps, c.num_heads, c.num_kv_heads, c.qk_head_dim, c.v_head_dim,
                          b->kv[li], b->kv_stride[li], nd_kv_v_offset(&g), nd_kv_ks_offset(&g),
                          nd_kv_vs_offset(&g), g.cap, C, b->qn};
