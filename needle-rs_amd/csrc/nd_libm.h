@@ -80,6 +80,13 @@ ND_LIBM_FN float nd_scalbnf(float x, int n)
     return x * nd_u2f((uint32_t)(0x7f + n) << 23);
 }
 
+// e_expf.c as one straight line: every path's result is computed and the
+// input's class selects it, so lanes of a wave whose inputs take different
+// msun paths do not serialise.  The arithmetic of each path is msun's: the
+// specials (NaN, overflow, underflow) return what msun returns; with k = 0
+// the reduction computes hi = x - 0 = x and lo = +0, the values msun's
+// middle path sets; |x| <= 2^-14 gives 1 + x.  The main path runs on 0 in
+// place of a special input, so every conversion in it stays in range.
 ND_LIBM_FN float nd_expf(float x)
 {
     const float ln2_hi = 6.9314575195e-01f;  // 0x3f317200
@@ -87,38 +94,43 @@ ND_LIBM_FN float nd_expf(float x)
     const float inv_ln2 = 1.4426950216e+00f; // 0x3fb8aa3b
     const float p1 = 1.6666625440e-1f;
     const float p2 = -2.7667332906e-3f;
-    uint32_t hx = nd_f2u(x);
-    const int sign = (int)(hx >> 31);
-    hx &= 0x7fffffffu;
-    if (hx >= 0x42aeac50u) {       // |x| >= 87.33655 or NaN
-        if (hx > 0x7f800000u) return x;  // NaN
-        if (hx >= 0x42b17218u && !sign) return x * nd_u2f(0x7f000000u);  // overflow
-        if (sign && hx >= 0x42cff1b5u) return 0.0f;  // x <= -103.972084: underflow
-    }
-    int k;
-    float hi, lo;
-    if (hx > 0x3eb17218u) {        // |x| > ln2 / 2
-        if (hx > 0x3f851592u)      // |x| > 1.5 ln2
-            k = (int)(inv_ln2 * x + (sign ? -0.5f : 0.5f));  // a select, not a table in memory
-        else
-            k = 1 - sign - sign;
-        const float kf = (float)k;
-        hi = x - kf * ln2_hi;
-        lo = kf * ln2_lo;
-        x = hi - lo;
-    } else if (hx > 0x39000000u) { // |x| > 2^-14
-        k = 0;
-        hi = x;
-        lo = 0.0f;
-    } else {
-        return 1.0f + x;
-    }
-    const float xx = x * x;
-    const float c = x - xx * (p1 + xx * p2);
-    const float y = 1.0f + (x * c / (2.0f - c) - lo + hi);
-    return k == 0 ? y : nd_scalbnf(y, k);
+    const uint32_t bx = nd_f2u(x);
+    const int sign = (int)(bx >> 31);
+    const uint32_t ax = bx & 0x7fffffffu;
+    const int nan = ax > 0x7f800000u;
+    const int over = !sign && ax >= 0x42b17218u;  // x >= 88.7228 (and +inf)
+    const int under = sign && ax >= 0x42cff1b5u;  // x <= -103.972084 (and -inf)
+    const int special = nan | over | under;
+    const float xs = special ? 0.0f : x;
+    const uint32_t hx = special ? 0u : ax;
+    // k: round(x / ln2) past 1.5 ln2 (the +-1/2 a select, not a table in
+    // memory), +-1 past ln2 / 2, else 0
+    const int kr = (int)(inv_ln2 * xs + (sign ? -0.5f : 0.5f));
+    const int k = hx > 0x3eb17218u ? (hx > 0x3f851592u ? kr : 1 - sign - sign) : 0;
+    const float kf = (float)k;
+    const float hi = xs - kf * ln2_hi;
+    const float lo = kf * ln2_lo;
+    const float xr = hi - lo;
+    const float xx = xr * xr;
+    const float c = xr - xx * (p1 + xx * p2);
+    const float y = 1.0f + (xr * c / (2.0f - c) - lo + hi);
+    // scalbnf(y, k) for the k this range gives (-150..128): one over- or
+    // underflow step at most, then the power of two
+    const float ys = k > 127 ? y * nd_u2f(0x7f000000u)
+                             : (k < -126 ? y * (nd_u2f(0x00800000u) * nd_u2f(0x4b800000u)) : y);
+    const int ks = k > 127 ? k - 127 : (k < -126 ? k + 126 - 24 : k);
+    float r = k == 0 ? y : ys * nd_u2f((uint32_t)(0x7f + ks) << 23);
+    r = hx > 0x39000000u ? r : 1.0f + xs;  // |x| <= 2^-14
+    r = under ? 0.0f : r;
+    r = over ? x * nd_u2f(0x7f000000u) : r;
+    return nan ? x : r;
 }
 
+// e_logf.c as one straight line: subnormals are scaled up by 2^25 (k -25)
+// before the main path, which runs on 1 in place of zero, negative,
+// infinite or NaN input; the input's class selects msun's result: -inf for
+// +-0, a NaN for a negative input ((x - x) times infinity, the invalid
+// operation msun's (x - x) / 0 is), x for +inf and NaN, an exact 0 for 1.
 ND_LIBM_FN float nd_logf(float x)
 {
     const float ln2_hi = 6.9313812256e-01f;  // 0x3f317180
@@ -127,24 +139,20 @@ ND_LIBM_FN float nd_logf(float x)
     const float lg2 = 0.40000972152f;
     const float lg3 = 0.28498786688f;
     const float lg4 = 0.24279078841f;
-    uint32_t ix = nd_f2u(x);
-    int k = 0;
-    if (ix < 0x00800000u || (ix >> 31)) {  // x < 2^-126, or negative
-        if ((ix << 1) == 0) return -1.0f / (x * x);  // log(+-0) = -inf
-        if (ix >> 31) return (x - x) / 0.0f;          // log(negative) = NaN
-        k -= 25;                                      // subnormal: scale up
-        x *= nd_u2f(0x4c000000u);
-        ix = nd_f2u(x);
-    } else if (ix >= 0x7f800000u) {
-        return x;
-    } else if (ix == 0x3f800000u) {
-        return 0.0f;
-    }
+    const uint32_t bx = nd_f2u(x);
+    const int zero = (bx << 1) == 0;
+    const int neg = (bx >> 31) && !zero;
+    const int upper = !(bx >> 31) && bx >= 0x7f800000u;  // +inf, NaN
+    const int sub = bx < 0x00800000u && !zero;
+    const int one = bx == 0x3f800000u;
+    const float xs = (zero | neg | upper) ? 1.0f : (sub ? x * nd_u2f(0x4c000000u) : x);
+    uint32_t ix = nd_f2u(xs);
+    int k = sub ? -25 : 0;
     ix += 0x3f800000u - 0x3f3504f3u;
     k += (int)(ix >> 23) - 0x7f;
     ix = (ix & 0x007fffffu) + 0x3f3504f3u;
-    x = nd_u2f(ix);
-    const float f = x - 1.0f;
+    const float xm = nd_u2f(ix);
+    const float f = xm - 1.0f;
     const float s = f / (2.0f + f);
     const float z = s * s;
     const float w = z * z;
@@ -153,7 +161,11 @@ ND_LIBM_FN float nd_logf(float x)
     const float r = t2 + t1;
     const float hfsq = 0.5f * f * f;
     const float dk = (float)k;
-    return s * (hfsq + r) + dk * ln2_lo - hfsq + f + dk * ln2_hi;
+    float v = s * (hfsq + r) + dk * ln2_lo - hfsq + f + dk * ln2_hi;
+    v = one ? 0.0f : v;
+    v = upper ? x : v;
+    v = neg ? (x - x) * nd_u2f(0x7f800000u) : v;
+    return zero ? nd_u2f(0xff800000u) : v;
 }
 
 ND_LIBM_FN float nd_sigmoidf(float x) { return 1.0f / (1.0f + nd_expf(-x)); }

@@ -276,7 +276,8 @@ __global__ __launch_bounds__(256) void k_engram_fetch(EngramFetch a)
 // q/k/v/gate projections.  One workgroup per session.
 constexpr int kMaxLanesD = 4096;  // mhc_lanes * d_model
 constexpr int kFoldC = 12;        // terms a thread of the parallel rms fold (4 lanes x 768)
-constexpr int kMaxPhiPairs = 512; // mhc_lanes * (phi input groups)
+constexpr int kMaxPhiPairs = 768; // (phi rows of a layer) * (phi input groups)
+constexpr int kPhiPerThread = 3;  // phi (row, group) pairs a thread holds codes for
 constexpr int kPadGroup = 132;    // a 128-group's stride in LDS, padded
 
 struct LayerIn {
@@ -293,6 +294,14 @@ struct LayerIn {
     const float *b_pre;       // [n] this layer's slice
     float a_pre;
     int layer, n, d;
+    // with `gates`, this layer's phi_post and phi_res rows too (the raw
+    // scatter-up gates, into graw [B][n + n*n]): same width, group and input
+    int gates;
+    const uint8_t *post_packed, *res_packed;
+    const float *post_norms, *res_norms, *post_lv, *res_lv;
+    size_t post_row_bytes, res_row_bytes;
+    int post_row0, res_row0, post_ternary, res_ternary;
+    float *graw;
     const float *ek, *ev;     // [B][d] this layer's Engram site, or null
     const float *norm_in;     // [d]
     float *u, *bx;            // [B][d]
@@ -306,13 +315,13 @@ __global__ __launch_bounds__(kT) void k_layer_in(LayerIn a)
     constexpr int kCh = 1024 / kT;  // model-dim channels per thread
     __shared__ __align__(16) float ln[kMaxLanesD], nb[kMaxLanesD];
     __shared__ __align__(16) float us[1024], bxs[1024], pa[1024], pb[1024], pc[1024];
-    __shared__ float gs[kMaxPhiPairs], pn[kMaxPhiPairs], lvl[16], hp[16], gpp[16], grr[256], tot[4];
+    __shared__ float gs[kMaxPhiPairs], pn[kMaxPhiPairs], lvl[48], hp[16], gpp[16], grr[256], tot[4];
     __shared__ NdFoldLds<kT> fl;
     const size_t b = blockIdx.x;
     const int tid = threadIdx.x, n = a.n, d = a.d, nd = n * d;
-    const int G = a.phi_G, pairs = n * G;
+    // phi rows: phi_pre's n, then (gates) phi_post's n and phi_res's n * n
+    const int G = a.phi_G, prows = a.gates ? 2 * n + n * n : n, pairs = prows * G;
     float *lg = a.lanes + b * size_t(nd);
-    const bool has_pair = tid < pairs;
     const float *ek = a.ek ? a.ek + b * d : nullptr;
     // the previous layer's lanes and block delta for this thread's channels
     constexpr int kUpLanes = 4;
@@ -362,14 +371,34 @@ __global__ __launch_bounds__(kT) void k_layer_in(LayerIn a)
     // folding: this thread's phi_pre group codes and norm, its channels'
     // norm_in / Engram key and value, the phi levels; values bound for LDS
     // are stored after the fold, so no wave waits on them first
-    CqGroupCodes<PP> codes;
-    float pnv = 0.0f;
-    {
-        const int r = has_pair ? tid / G : 0, g = has_pair ? tid - (tid / G) * G : 0;
-        cq_group_codes128<PP>(a.phi_packed + size_t(a.phi_row0 + r) * a.phi_row_bytes +
-                                  size_t(g) * (128 / PP),
-                              codes);
-        if (has_pair) pnv = a.phi_norms[size_t(a.phi_row0 + r) * G + g];
+    // pair t = (row t / G, group t % G); row r of phi_pre, phi_post or phi_res
+    auto phi_row = [&](int r, const float *&norms, int &wsel) -> const uint8_t * {
+        if (r < n) {
+            norms = a.phi_norms + size_t(a.phi_row0 + r) * G;
+            wsel = 0;
+            return a.phi_packed + size_t(a.phi_row0 + r) * a.phi_row_bytes;
+        }
+        if (r < 2 * n) {
+            norms = a.post_norms + size_t(a.post_row0 + r - n) * G;
+            wsel = 1;
+            return a.post_packed + size_t(a.post_row0 + r - n) * a.post_row_bytes;
+        }
+        norms = a.res_norms + size_t(a.res_row0 + r - 2 * n) * G;
+        wsel = 2;
+        return a.res_packed + size_t(a.res_row0 + r - 2 * n) * a.res_row_bytes;
+    };
+    CqGroupCodes<PP> codes[kPhiPerThread];
+    float pnv[kPhiPerThread];
+    int wsel[kPhiPerThread];
+#pragma unroll
+    for (int k = 0; k < kPhiPerThread; ++k) {
+        const int t = tid + k * kT;
+        const bool has = t < pairs;
+        const int r = has ? t / G : 0, g = has ? t - (t / G) * G : 0;
+        const float *nr;
+        const uint8_t *row = phi_row(r, nr, wsel[k]);
+        if (k == 0 || has) cq_group_codes128<PP>(row + size_t(g) * (128 / PP), codes[k]);
+        pnv[k] = has ? nr[g] : 0.0f;
     }
     float nin[kCh], ekv[kCh], evv[kCh];
 #pragma unroll
@@ -380,7 +409,13 @@ __global__ __launch_bounds__(kT) void k_layer_in(LayerIn a)
         evv[k] = ek && c < d ? a.ev[b * d + c] : 0.0f;
     }
     const float bpre = tid < n ? a.b_pre[tid] : 0.0f;
-    const float lvv = tid < 16 ? a.phi_lv[a.phi_ternary ? (tid == 3 ? 0 : (tid == 1 ? 2 : 1)) : tid] : 0.0f;
+    float lvv = 0.0f;
+    if (tid < 48) {
+        const int k = tid & 15, w = tid >> 4;
+        const float *lv = w == 0 ? a.phi_lv : (w == 1 ? a.post_lv : a.res_lv);
+        const int tern = w == 0 ? a.phi_ternary : (w == 1 ? a.post_ternary : a.res_ternary);
+        if (w == 0 || a.gates) lvv = lv[tern ? (k == 3 ? 0 : (k == 1 ? 2 : 1)) : k];
+    }
     // the rms sum of squares: the workgroup folds it in parallel with the
     // chain's bits (nd_fold.h) when it fits kFoldC terms a thread
     if (nd >= kNdFoldMinN && nd <= kT * kFoldC) {
@@ -389,8 +424,10 @@ __global__ __launch_bounds__(kT) void k_layer_in(LayerIn a)
     } else if (tid == 0) {
         tot[0] = chain_sum(nb, nd);
     }
-    if (has_pair) pn[tid] = pnv;
-    if (tid < 16) lvl[tid] = lvv;
+#pragma unroll
+    for (int k = 0; k < kPhiPerThread; ++k)
+        if (tid + k * kT < pairs) pn[tid + k * kT] = pnv[k];
+    if (tid < 48) lvl[tid] = lvv;
     __syncthreads();
     {
         // prepare_input of rms_unit(lanes): one wave per 128-group straight
@@ -411,23 +448,22 @@ __global__ __launch_bounds__(kT) void k_layer_in(LayerIn a)
         }
     }
     __syncthreads();
-    // phi_pre rows of this layer (matvec_rows_prepared, reference order)
-    if (has_pair) gs[tid] = cq_group_dot128<PP>(codes, lvl, nb + (tid % G) * kPadGroup);
-    for (int t = tid + kT; t < pairs; t += kT) {  // more pairs than threads
-        const int r = t / G, g = t - r * G;
-        CqGroupCodes<PP> more;
-        cq_group_codes128<PP>(a.phi_packed + size_t(a.phi_row0 + r) * a.phi_row_bytes +
-                                  size_t(g) * (128 / PP),
-                              more);
-        gs[t] = cq_group_dot128<PP>(more, lvl, nb + g * kPadGroup);
-        pn[t] = a.phi_norms[size_t(a.phi_row0 + r) * G + g];
+    // this layer's phi rows (matvec_rows_prepared, reference order)
+#pragma unroll
+    for (int k = 0; k < kPhiPerThread; ++k) {
+        const int t = tid + k * kT;
+        if (t < pairs) gs[t] = cq_group_dot128<PP>(codes[k], lvl + 16 * wsel[k], nb + (t % G) * kPadGroup);
     }
     __syncthreads();
-    if (tid < n) {
+    if (tid < prows) {
         float total = 0.0f;
         for (int g = 0; g < G; ++g) total += pn[tid * G + g] * gs[tid * G + g];
-        const float off = tid == a.layer % n ? 4.0f : -4.0f;
-        hp[tid] = sigmoidf_(a.a_pre * total + bpre + off);
+        if (tid < n) {
+            const float off = tid == a.layer % n ? 4.0f : -4.0f;
+            hp[tid] = sigmoidf_(a.a_pre * total + bpre + off);
+        } else {
+            a.graw[b * (prows - n) + (tid - n)] = total;  // nx . phi_post, nx . phi_res
+        }
     }
     __syncthreads();
     // gated lane sum, Engram gate (engram.rs:111-132), ZCRMSNorm (norm.rs:23-30)
@@ -482,6 +518,225 @@ __global__ __launch_bounds__(kT) void k_layer_in(LayerIn a)
     for (int c = d + tid; c < a.ph.in_padded; c += kT) pa[c] = 0.0f;
     __syncthreads();
     prepare_lds(pa, a.hh + b * a.ph.in_padded, a.ph.in_padded, a.ph.group, a.ph.inv, false);
+}
+
+// ---- the scatter-up gates of a layer (mhc.rs:111-152), on the side stream:
+// H_post = 2 sigmoid(a_post . raw + b_post + off), H_res = Sinkhorn(a_res .
+// raw + b_res).  They depend only on the layer's input lanes.
+struct MhcGates {
+    const float *hpost_raw;    // [B][n]
+    const float *hres_raw;     // [B][n*n]
+    const float *b_post;       // [n]
+    const float *b_res;        // [n*n]
+    float a_post, a_res;
+    int layer, n;
+    float *gp, *gr;            // [B][n], [B][n*n]
+};
+
+__device__ inline float lse_row(const float *x, int n)
+{
+    float mx = -INFINITY;
+    for (int i = 0; i < n; ++i) mx = fmaxf(mx, x[i]);
+    if (!(mx == mx) || mx == INFINITY || mx == -INFINITY) return mx;
+    float s = 0.0f;
+    for (int i = 0; i < n; ++i) s += nd_expf(x[i] - mx);
+    return mx + nd_logf(s);
+}
+
+// kernels.rs:48-74 on an n x n matrix (n * n <= 64) held one entry per lane
+// of one wave: every row (then column) logsumexp is the reference's loop --
+// max, sequential sum of exps, max + log.  Each lane exponentiates its own
+// entry; the lanes of a row (column) then fold the row's exps in index
+// order from shuffles, all rows at once.
+__device__ inline float sinkhorn_wave(float m, int n)
+{
+    const int lane = threadIdx.x & 63;
+    const int i = lane / n, j = lane - (lane / n) * n;
+    const int rb = i * n;  // first lane of this row
+    for (int it = 0; it < 20; ++it) {
+        {
+            float mx = -INFINITY;
+            for (int k = 0; k < n; ++k) mx = fmaxf(mx, __shfl(m, rb + k, 64));
+            const float e = nd_expf(m - mx);
+            float s = 0.0f;
+            for (int k = 0; k < n; ++k) s += __shfl(e, rb + k, 64);
+            const bool finite = mx == mx && mx != INFINITY && mx != -INFINITY;
+            m -= finite ? mx + nd_logf(s) : mx;
+        }
+        {
+            float mx = -INFINITY;
+            for (int k = 0; k < n; ++k) mx = fmaxf(mx, __shfl(m, k * n + j, 64));
+            const float e = nd_expf(m - mx);
+            float s = 0.0f;
+            for (int k = 0; k < n; ++k) s += __shfl(e, k * n + j, 64);
+            m -= mx + nd_logf(s);
+        }
+    }
+    return nd_expf(m);
+}
+
+// One iteration of sinkhorn_wave (rows, then columns).
+__device__ inline float sinkhorn_iter_wave(float m, int n)
+{
+    const int lane = threadIdx.x & 63;
+    const int i = lane / n, j = lane - (lane / n) * n;
+    const int rb = i * n;
+    {
+        float mx = -INFINITY;
+        for (int k = 0; k < n; ++k) mx = fmaxf(mx, __shfl(m, rb + k, 64));
+        const float e = nd_expf(m - mx);
+        float s = 0.0f;
+        for (int k = 0; k < n; ++k) s += __shfl(e, rb + k, 64);
+        const bool finite = mx == mx && mx != INFINITY && mx != -INFINITY;
+        m -= finite ? mx + nd_logf(s) : mx;
+    }
+    {
+        float mx = -INFINITY;
+        for (int k = 0; k < n; ++k) mx = fmaxf(mx, __shfl(m, k * n + j, 64));
+        const float e = nd_expf(m - mx);
+        float s = 0.0f;
+        for (int k = 0; k < n; ++k) s += __shfl(e, k * n + j, 64);
+        m -= mx + nd_logf(s);
+    }
+    return m;
+}
+
+__global__ __launch_bounds__(64) void k_mhc_gates(MhcGates a)
+{
+    __shared__ float hr[256];
+    const size_t b = blockIdx.x;
+    const int n = a.n, tid = threadIdx.x;
+    if (tid < n) {
+        const float off = tid == a.layer % n ? 0.0f : -4.0f;
+        a.gp[b * n + tid] = 2.0f * sigmoidf_(a.a_post * a.hpost_raw[b * n + tid] + a.b_post[tid] + off);
+    }
+    if (n * n <= 64) {
+        const bool on = tid < n * n;
+        float m = on ? a.a_res * a.hres_raw[b * n * n + tid] + a.b_res[tid] : 0.0f;
+        m = sinkhorn_wave(m, n);
+        if (on) a.gr[b * n * n + tid] = m;
+        return;
+    }
+    if (tid == 0) {
+        for (int x = 0; x < n * n; ++x) hr[x] = a.a_res * a.hres_raw[b * n * n + x] + a.b_res[x];
+        for (int it = 0; it < 20; ++it) {
+            for (int i = 0; i < n; ++i) {
+                const float lse = lse_row(hr + i * n, n);
+                for (int j = 0; j < n; ++j) hr[i * n + j] -= lse;
+            }
+            for (int j = 0; j < n; ++j) {
+                float mx = -INFINITY;
+                for (int i = 0; i < n; ++i) mx = fmaxf(mx, hr[i * n + j]);
+                float s = 0.0f;
+                for (int i = 0; i < n; ++i) s += nd_expf(hr[i * n + j] - mx);
+                const float lse = mx + nd_logf(s);
+                for (int i = 0; i < n; ++i) hr[i * n + j] -= lse;
+            }
+        }
+        for (int x = 0; x < n * n; ++x) a.gr[b * n * n + x] = nd_expf(hr[x]);
+    }
+}
+
+// The same Sinkhorn for n = 4 without a trip through LDS: lane 4i + j of
+// lanes 0..15 holds m[i][j], so a row is a quad and its entries reach every
+// lane of the quad by DPP quad broadcasts (in index order, as the loops
+// read them).  The column pass runs as a row pass of the transpose, which
+// DPP row shifts build: lane 4a + b takes lane 4b + a, 3(b - a) lanes away.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                                  0xf, 0xf, false));
+}
+
+constexpr int quad_bcast(int k) { return k | (k << 2) | (k << 4) | (k << 6); }
+
+// m minus the logsumexp of its quad's four entries (kernels.rs:76-85 for a
+// row; with `row` false the column pass's form, which has no finite check)
+__device__ __forceinline__ float lse_quad(float m, bool row)
+{
+    float mx = -INFINITY;
+    mx = fmaxf(mx, dpp_f<quad_bcast(0)>(m));
+    mx = fmaxf(mx, dpp_f<quad_bcast(1)>(m));
+    mx = fmaxf(mx, dpp_f<quad_bcast(2)>(m));
+    mx = fmaxf(mx, dpp_f<quad_bcast(3)>(m));
+    const float e = nd_expf(m - mx);
+    float s = 0.0f;
+    s += dpp_f<quad_bcast(0)>(e);
+    s += dpp_f<quad_bcast(1)>(e);
+    s += dpp_f<quad_bcast(2)>(e);
+    s += dpp_f<quad_bcast(3)>(e);
+    const bool finite = mx == mx && mx != INFINITY && mx != -INFINITY;
+    return m - (row && !finite ? mx : mx + nd_logf(s));
+}
+
+// lane 4a + b <- lane 4b + a within each 16-lane row (row_shl:n reads lane
+// l + n, row_shr:n lane l - n)
+__device__ __forceinline__ float transpose4x4(float m)
+{
+    const int l = threadIdx.x & 15, d = (l & 3) - (l >> 2);
+    const float u3 = dpp_f<0x103>(m), u6 = dpp_f<0x106>(m), u9 = dpp_f<0x109>(m);
+    const float d3 = dpp_f<0x113>(m), d6 = dpp_f<0x116>(m), d9 = dpp_f<0x119>(m);
+    return d == 0 ? m : d == 1 ? u3 : d == 2 ? u6 : d == 3 ? u9 : d == -1 ? d3 : d == -2 ? d6 : d9;
+}
+
+// ---- the scatter-up gates inside the layer's own launches.  k_layer_in
+// leaves the raw gates nx . phi_post and nx . phi_res in graw (its phi
+// rows); phase 0, a second workgroup per row of k_qkv_kv's launch, forms
+// H_post (mhc.rs:126-128) and runs the first `split` Sinkhorn iterations of
+// H_res (mhc.rs:129-138, kernels.rs:46-74); phase 1, a second workgroup per
+// row of k_post_hada's, runs the rest and the final exp.  The 16 Sinkhorn
+// values pass between the phases through `state`.  So the gates need no
+// stream of their own and lengthen no launch of the layer's chain.
+constexpr int kSinkhornIters = 20;   // SINKHORN_ITERS (kernels.rs)
+// iterations in phase 0: about 1.1 us each, so 6 fit k_qkv_kv's time and
+// the other 14 k_post_hada's
+constexpr int kGateSplit = 6;
+struct MhcIn {
+    int on;                     // this launch runs a gate phase
+    const float *graw;          // [B][n + n*n] from k_layer_in
+    int n, layer, split;
+    const float *b_post, *b_res;  // this layer's slices
+    float a_post, a_res;
+    float *gp, *gr;             // [B][n], [B][n*n]
+    float *state;               // [B][64]: lane values of the Sinkhorn wave between phases
+};
+
+__device__ inline float sinkhorn_iters(float m, int n, int it0, int it1)
+{
+    for (int it = it0; it < it1; ++it) {
+        if (n == 4) {
+            m = lse_quad(m, true);
+            m = transpose4x4(lse_quad(transpose4x4(m), false));
+        } else {
+            m = sinkhorn_iter_wave(m, n);
+        }
+    }
+    return m;
+}
+
+// Phase 0: one wave's work (the block's other waves leave).
+__device__ void mhc_gates_phase0(const MhcIn &a, size_t b)
+{
+    const int tid = threadIdx.x, n = a.n, rows = n + n * n;
+    if (tid >= 64) return;
+    const float *raw = a.graw + b * rows;
+    if (tid < n) {
+        const float off = tid == a.layer % n ? 0.0f : -4.0f;
+        a.gp[b * n + tid] = 2.0f * sigmoidf_(a.a_post * raw[tid] + a.b_post[tid] + off);
+    }
+    float m = tid < n * n ? a.a_res * raw[n + tid] + a.b_res[tid] : 0.0f;
+    a.state[b * 64 + tid] = sinkhorn_iters(m, n, 0, a.split);
+}
+
+// Phase 1: one wave's work (the block's other waves leave).
+__device__ void mhc_gates_phase1(const MhcIn &a, size_t b)
+{
+    const int tid = threadIdx.x, n = a.n;
+    if (tid >= 64) return;
+    float m = a.state[b * 64 + tid];
+    m = nd_expf(sinkhorn_iters(m, n, a.split, kSinkhornIters));
+    if (tid < n * n) a.gr[b * n * n + tid] = m;
 }
 
 // ---- after the projections: causal conv step over q/k/v with the retained
@@ -564,11 +819,17 @@ constexpr int kMaxVDims = 1024;   // num_kv_heads * v_head_dim
 
 // KF: the session's cache is f32 (write_kv with KvPrecision::F32,
 // cache.rs:359-362): k and v are stored as they are.
+// With mhc.on (single positions), a second workgroup per row runs phase 0
+// of the layer's scatter-up gates in the same launch.
 template <bool CHUNK, bool KF>
-__global__ __launch_bounds__(kT) void k_qkv_kv(QkvKv a)
+__global__ __launch_bounds__(kT) void k_qkv_kv(QkvKv a, MhcIn mhc)
 {
     __shared__ __align__(16) float qk[kMaxQkDims], sq[kMaxQkDims], vl[kMaxVDims];
     __shared__ float rms[64];
+    if (blockIdx.y == 1) {
+        mhc_gates_phase0(mhc, blockIdx.x);
+        return;
+    }
     const size_t b = blockIdx.x;
     const size_t sess = CHUNK ? b / a.C : b;
     const int r = CHUNK ? int(b % a.C) : 0;
@@ -677,7 +938,8 @@ __global__ __launch_bounds__(kT) void k_gate_prep(const float *__restrict__ attn
 // ---- post-norm, gated residual, pre-MLP norm (model.rs:313-321), then the
 // HadamardMLP (v3/kernels.rs:119-180, hada_n = 1024 = 32 x 32), the
 // residual and the block delta y = bx - u.  One 1024-thread workgroup per
-// session.
+// session; with the gates on (mhc.on), a second one per session computes
+// the layer's scatter-up gates.
 struct HadaArgs {
     const float *proj;  // [B][d] out_proj output
     const float *post_norm, *pre_hada;  // [d]
@@ -753,12 +1015,17 @@ __device__ inline void kron32(const float *zT, const float *aT, const float *bT,
 constexpr int kMaxCondRegs = 8;     // cond_v / cond_u values a thread preloads
 constexpr int kCondProd = 6144;     // conditioning products held in LDS at once
 
-__global__ __launch_bounds__(1024) void k_post_hada(HadaArgs a)
+
+__global__ __launch_bounds__(1024) void k_post_hada(HadaArgs a, MhcIn mhc)
 {
     __shared__ __align__(16) float z[32 * kKS], buf[1024], t[32 * kKS], fa[32 * kKS], fb[32 * kKS], cond[1024];
     __shared__ __align__(16) float nbs[1024], prod[kCondProd];
     __shared__ float proj[64], tot[2];
     __shared__ unsigned zf;  // bit k: the a factor of Kronecker pass k holds a zero
+    if (blockIdx.y == 1) {
+        mhc_gates_phase1(mhc, blockIdx.x);
+        return;
+    }
     const size_t b = blockIdx.x;
     const int tid = threadIdx.x, d = a.d, r = a.rank;
     // what the first chain and the step after it need, up front
@@ -880,97 +1147,6 @@ __global__ __launch_bounds__(1024) void k_post_hada(HadaArgs a)
         const float nb = nbs[tid] + o;
         a.bx[b * d + tid] = nb;
         a.y[b * d + tid] = nb - uv;
-    }
-}
-
-// ---- the scatter-up gates of a layer (mhc.rs:111-152), on the side stream:
-// H_post = 2 sigmoid(a_post . raw + b_post + off), H_res = Sinkhorn(a_res .
-// raw + b_res).  They depend only on the layer's input lanes.
-struct MhcGates {
-    const float *hpost_raw;    // [B][n]
-    const float *hres_raw;     // [B][n*n]
-    const float *b_post;       // [n]
-    const float *b_res;        // [n*n]
-    float a_post, a_res;
-    int layer, n;
-    float *gp, *gr;            // [B][n], [B][n*n]
-};
-
-__device__ inline float lse_row(const float *x, int n)
-{
-    float mx = -INFINITY;
-    for (int i = 0; i < n; ++i) mx = fmaxf(mx, x[i]);
-    if (!(mx == mx) || mx == INFINITY || mx == -INFINITY) return mx;
-    float s = 0.0f;
-    for (int i = 0; i < n; ++i) s += nd_expf(x[i] - mx);
-    return mx + nd_logf(s);
-}
-
-// kernels.rs:48-74 on an n x n matrix (n * n <= 64) held one entry per lane
-// of one wave: every row (then column) logsumexp is the reference's loop --
-// max, sequential sum of exps, max + log.  Each lane exponentiates its own
-// entry; the lanes of a row (column) then fold the row's exps in index
-// order from shuffles, all rows at once.
-__device__ inline float sinkhorn_wave(float m, int n)
-{
-    const int lane = threadIdx.x & 63;
-    const int i = lane / n, j = lane - (lane / n) * n;
-    const int rb = i * n;  // first lane of this row
-    for (int it = 0; it < 20; ++it) {
-        {
-            float mx = -INFINITY;
-            for (int k = 0; k < n; ++k) mx = fmaxf(mx, __shfl(m, rb + k, 64));
-            const float e = nd_expf(m - mx);
-            float s = 0.0f;
-            for (int k = 0; k < n; ++k) s += __shfl(e, rb + k, 64);
-            const bool finite = mx == mx && mx != INFINITY && mx != -INFINITY;
-            m -= finite ? mx + nd_logf(s) : mx;
-        }
-        {
-            float mx = -INFINITY;
-            for (int k = 0; k < n; ++k) mx = fmaxf(mx, __shfl(m, k * n + j, 64));
-            const float e = nd_expf(m - mx);
-            float s = 0.0f;
-            for (int k = 0; k < n; ++k) s += __shfl(e, k * n + j, 64);
-            m -= mx + nd_logf(s);
-        }
-    }
-    return nd_expf(m);
-}
-
-__global__ __launch_bounds__(64) void k_mhc_gates(MhcGates a)
-{
-    __shared__ float hr[256];
-    const size_t b = blockIdx.x;
-    const int n = a.n, tid = threadIdx.x;
-    if (tid < n) {
-        const float off = tid == a.layer % n ? 0.0f : -4.0f;
-        a.gp[b * n + tid] = 2.0f * sigmoidf_(a.a_post * a.hpost_raw[b * n + tid] + a.b_post[tid] + off);
-    }
-    if (n * n <= 64) {
-        const bool on = tid < n * n;
-        float m = on ? a.a_res * a.hres_raw[b * n * n + tid] + a.b_res[tid] : 0.0f;
-        m = sinkhorn_wave(m, n);
-        if (on) a.gr[b * n * n + tid] = m;
-        return;
-    }
-    if (tid == 0) {
-        for (int x = 0; x < n * n; ++x) hr[x] = a.a_res * a.hres_raw[b * n * n + x] + a.b_res[x];
-        for (int it = 0; it < 20; ++it) {
-            for (int i = 0; i < n; ++i) {
-                const float lse = lse_row(hr + i * n, n);
-                for (int j = 0; j < n; ++j) hr[i * n + j] -= lse;
-            }
-            for (int j = 0; j < n; ++j) {
-                float mx = -INFINITY;
-                for (int i = 0; i < n; ++i) mx = fmaxf(mx, hr[i * n + j]);
-                float s = 0.0f;
-                for (int i = 0; i < n; ++i) s += nd_expf(hr[i * n + j] - mx);
-                const float lse = mx + nd_logf(s);
-                for (int i = 0; i < n; ++i) hr[i * n + j] -= lse;
-            }
-        }
-        for (int x = 0; x < n * n; ++x) a.gr[b * n * n + x] = nd_expf(hr[x]);
     }
 }
 
@@ -1183,6 +1359,8 @@ struct nd_v3_batch {
           *hpost = nullptr, *hres = nullptr, *emb = nullptr, *fetched = nullptr, *fh = nullptr,
           *ek = nullptr, *ev = nullptr, *xh = nullptr, *logits = nullptr;
     float *gp = nullptr, *gr = nullptr;  // scatter-up gates of the latest layer
+    float *gstate = nullptr;             // [R][64] Sinkhorn state between the gate phases
+    float *graw = nullptr;               // [R][n + n*n] raw gates from k_layer_in
     // several positions per step: the normed q ([R][qd]) and the Engram
     // conv ([sites][R][d]) go here, the projections' rows stay as they are
     float *qn = nullptr, *evc = nullptr;
@@ -1703,6 +1881,8 @@ int nd_v3_batch_create_ex(nd_ctx *ctx, const nd_v3_model *m, size_t sessions, si
     A(logits, size_t(S) * rows);
     A(gp, size_t(B) * nl);
     A(gr, size_t(B) * nl * nl);
+    A(gstate, size_t(B) * 64);
+    A(graw, size_t(B) * (nl + nl * nl));
     A(next, size_t(S));
     if (b->chunk > 1) {
         A(qn, size_t(B) * qd);
@@ -1994,14 +2174,29 @@ int step_impl(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *
                                 m->pre_attn.in_padded == od && m->layers[0].out->per_byte != 0;
         hipStream_t side = b->side;
         const nd_cq *phi = m->phi_pre;
+        // The scatter-up gates ride in k_post_hada's launch (a second
+        // workgroup per row) when the phi weights fit its gate block; else
+        // they run on the side stream, joined by events.
+        const nd_cq *fpo = m->phi_post, *fre = m->phi_res;
+        const bool gates_in = (phi->per_byte == 2 || phi->per_byte == 4) && phi->group == 128 &&
+                              fpo->per_byte == phi->per_byte && fre->per_byte == phi->per_byte &&
+                              fpo->group == 128 && fre->group == 128 &&
+                              fpo->in_padded == phi->in_padded && fre->in_padded == phi->in_padded &&
+                              size_t(2 * nl + nl * nl) * phi->num_groups <= size_t(kMaxPhiPairs) &&
+                              size_t(2 * nl + nl * nl) * phi->num_groups <= size_t(kPhiPerThread * kT) &&
+                              nl * nl <= 64 && fpo->row_bytes % 16 == 0 && fre->row_bytes % 16 == 0 &&
+                              C == 1;
         for (int li = 0; li < L; ++li) {
             const Layer &l = m->layers[li];
             const int site = site_of(c, li);
             // previous layer's scatter up + this layer's mix down
-            if (li > 0) ND_HIP(hipStreamWaitEvent(st, b->ev_gates[(li - 1) & 1], 0));
+            if (li > 0 && !gates_in) ND_HIP(hipStreamWaitEvent(st, b->ev_gates[(li - 1) & 1], 0));
             LayerIn in{b->lanes, b->y, b->gp, b->gr, li > 0, b->nxh, m->pre_nx, phi->packed,
                        phi->norms, phi->lv, phi->row_bytes, int(phi->num_groups), li * nl,
                        int(phi->bits == 5), m->b_pre + size_t(li) * nl, m->a_pre[li], li, nl, d,
+                       gates_in ? 1 : 0, fpo->packed, fre->packed, fpo->norms, fre->norms, fpo->lv, fre->lv,
+                       fpo->row_bytes, fre->row_bytes, li * nl, li * nl * nl, int(fpo->bits == 5),
+                       int(fre->bits == 5), b->graw,
                        site >= 0 ? b->ek + size_t(site) * Rcap * d : nullptr,
                        site >= 0 ? ev_conv + size_t(site) * Rcap * d : nullptr, l.norm_in, b->u, b->bx,
                        b->hh, m->pre_h};
@@ -2010,21 +2205,24 @@ int step_impl(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *
             else
                 hipLaunchKernelGGL(k_layer_in<4>, dim3(B), dim3(kT), 0, st, in);
             LCHK("k_layer_in");
-            // side stream: this layer's scatter-up gates from the prepared lanes
-            ND_HIP(hipEventRecord(b->ev_in[li & 1], st));
-            ND_HIP(hipStreamWaitEvent(side, b->ev_in[li & 1], 0));
-            {
-                const nd_cq *ws[2] = {m->phi_post, m->phi_res};
-                const size_t r0[2] = {size_t(li) * nl, size_t(li) * nl * nl};
-                const size_t nr[2] = {size_t(nl), size_t(nl) * nl};
-                float *ys[2] = {b->hpost, b->hres};
-                CK(nd_cq_exact_set(ctx, side, 2, ws, b->nxh, size_t(B), r0, nr, ys, "v3 phi post/res"));
+            if (!gates_in) {
+                // side stream: this layer's scatter-up gates from the prepared lanes
+                ND_HIP(hipEventRecord(b->ev_in[li & 1], st));
+                ND_HIP(hipStreamWaitEvent(side, b->ev_in[li & 1], 0));
+                {
+                    const nd_cq *ws[2] = {m->phi_post, m->phi_res};
+                    const size_t r0[2] = {size_t(li) * nl, size_t(li) * nl * nl};
+                    const size_t nr[2] = {size_t(nl), size_t(nl) * nl};
+                    float *ys[2] = {b->hpost, b->hres};
+                    CK(nd_cq_exact_set(ctx, side, 2, ws, b->nxh, size_t(B), r0, nr, ys, "v3 phi post/res"));
+                }
+                MhcGates mg{b->hpost, b->hres, m->b_post + size_t(li) * nl,
+                            m->b_res + size_t(li) * nl * nl, m->a_post[li], m->a_res[li], li, nl,
+                            b->gp, b->gr};
+                hipLaunchKernelGGL(k_mhc_gates, dim3(B), dim3(64), 0, side, mg);
+                LCHK("k_mhc_gates");
+                ND_HIP(hipEventRecord(b->ev_gates[li & 1], side));
             }
-            MhcGates mg{b->hpost, b->hres, m->b_post + size_t(li) * nl, m->b_res + size_t(li) * nl * nl,
-                        m->a_post[li], m->a_res[li], li, nl, b->gp, b->gr};
-            hipLaunchKernelGGL(k_mhc_gates, dim3(B), dim3(64), 0, side, mg);
-            LCHK("k_mhc_gates");
-            ND_HIP(hipEventRecord(b->ev_gates[li & 1], side));
             // q, k, v and gate projections of the prepared h, one launch
             {
                 const nd_cq *ws[4] = {l.q, l.k, l.v, l.gate};
@@ -2033,6 +2231,23 @@ int step_impl(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *
                 float *ys[4] = {b->q, b->k, b->v, b->gate};
                 CK(nd_cq_exact_set(ctx, st, 4, ws, b->hh, size_t(B), r0, nr, ys, "v3 qkv/gate"));
             }
+            // this layer's scatter-up gates, when they ride in the layer's launches
+            MhcIn mi{};
+            if (gates_in) {
+                mi.on = 1;
+                mi.graw = b->graw;
+                mi.n = nl;
+                mi.layer = li;
+                mi.split = kGateSplit;
+                mi.b_post = m->b_post + size_t(li) * nl;
+                mi.b_res = m->b_res + size_t(li) * nl * nl;
+                mi.a_post = m->a_post[li];
+                mi.a_res = m->a_res[li];
+                mi.gp = b->gp;
+                mi.gr = b->gr;
+                mi.state = b->gstate;
+            }
+            const unsigned gy = gates_in ? 2u : 1u;
             // conv, norm + RoPE, int8 KV append
             {
                 const nd_kv_geom &g = b->geom[li];
@@ -2042,17 +2257,19 @@ int step_impl(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *
                          b->kv[li], b->kv_stride[li], nd_kv_v_offset(&g), nd_kv_ks_offset(&g),
                          nd_kv_vs_offset(&g), g.cap, C, b->qn};
                 if (kf) qk.v_off = nd_kv_f32_v_offset(&g);
+                const dim3 qg(unsigned(B), gy);
                 if (C == 1) {
                     if (kf)
-                        hipLaunchKernelGGL((k_qkv_kv<false, true>), dim3(B), dim3(kT), 0, st, qk);
+                        hipLaunchKernelGGL((k_qkv_kv<false, true>), qg, dim3(kT), 0, st, qk, mi);
                     else
-                        hipLaunchKernelGGL((k_qkv_kv<false, false>), dim3(B), dim3(kT), 0, st, qk);
+                        hipLaunchKernelGGL((k_qkv_kv<false, false>), qg, dim3(kT), 0, st, qk, mi);
                     LCHK("k_qkv_kv");
                 } else {
+                    // prefill passes run the gates on the side stream
                     if (kf)
-                        hipLaunchKernelGGL((k_qkv_kv<true, true>), dim3(B), dim3(kT), 0, st, qk);
+                        hipLaunchKernelGGL((k_qkv_kv<true, true>), dim3(B), dim3(kT), 0, st, qk, mi);
                     else
-                        hipLaunchKernelGGL((k_qkv_kv<true, false>), dim3(B), dim3(kT), 0, st, qk);
+                        hipLaunchKernelGGL((k_qkv_kv<true, false>), dim3(B), dim3(kT), 0, st, qk, mi);
                     LCHK("k_qkv_kv");
                     const int tt = c.qkv_conv_taps - 1;
                     if (tt > 0) {
@@ -2089,11 +2306,11 @@ int step_impl(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *
             HadaArgs ha{b->proj, l.post_norm, l.pre_hada, nd_sigmoidf(l.attn_gate), b->u, b->bx, b->y,
                         l.d1, l.d2, l.b2, l.d3, l.d4, l.w1a, l.w1b, l.w2a, l.w2b, l.w3a, l.w3b,
                         l.cond_v, l.cond_u, m->p1, m->p2, d, l.cond_rank};
-            hipLaunchKernelGGL(k_post_hada, dim3(B), dim3(1024), 0, st, ha);
+            hipLaunchKernelGGL(k_post_hada, dim3(unsigned(B), gy), dim3(1024), 0, st, ha, mi);
             LCHK("k_post_hada");
         }
         // ---- head ---------------------------------------------------------------
-        ND_HIP(hipStreamWaitEvent(st, b->ev_gates[(L - 1) & 1], 0));
+        if (!gates_in) ND_HIP(hipStreamWaitEvent(st, b->ev_gates[(L - 1) & 1], 0));
         hipLaunchKernelGGL(k_final, dim3(S), dim3(kT), 0, st, b->lanes, b->y, b->gp, b->gr,
                            m->final_norm, b->xh, nl, d, m->pre_x, C);
         LCHK("k_final");
