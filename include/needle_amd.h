@@ -255,6 +255,15 @@ int nd_attend_step_i8_exact(nd_ctx *ctx, const nd_kv_geom *g, const void *kv,
                             const int32_t *hi, const float *q, float scale,
                             int quant_query, float *out);
 
+/* ---- libm on the device (crates/needle-core/src/math.rs:3-46) ------------- */
+
+/* y[i] = f(x[i]) for i < n (device buffers), f the device copy of the
+ * reference's libm 0.2.16 wrapper that the device path uses: fn 0 expf
+ * (math::exp), 1 logf (math::ln), 2 the sigmoid 1 / (1 + expf(-x))
+ * (ops::sigmoid).  The same bits as the reference's functions for every
+ * input (the msun algorithms, restated); used to check the device copies. */
+int nd_libm_map(nd_ctx *ctx, int fn, const float *x, size_t n, float *y);
+
 /* ---- f32 KV cache (KvPrecision::F32, v3/cache.rs:177-238, 355-362) ------- */
 
 /*

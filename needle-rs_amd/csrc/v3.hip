@@ -1183,6 +1183,17 @@ __global__ __launch_bounds__(kT) void k_final(float *__restrict__ lanes, const f
     prepare_lds(sq, xh + b * pp.in_padded, pp.in_padded, pp.group, pp.inv, false);
 }
 
+// ---- the device copies of the reference's libm wrappers (math.rs:3-46), one
+// value a thread: expf, logf, and the sigmoid built on expf (ops.rs)
+__global__ __launch_bounds__(256) void k_libm_map(int fn, const float *__restrict__ x, size_t n,
+                                                  float *__restrict__ y)
+{
+    const size_t i = size_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float v = x[i];
+    y[i] = fn == 0 ? nd_expf(v) : (fn == 1 ? nd_logf(v) : nd_sigmoidf(v));
+}
+
 // ---- greedy argmax, first maximum wins (v3_engine.rs:410-420) -----------------
 // Greedy token: the first index of the largest logit (v3_engine.rs:410-420:
 // a strict `>` scan, so NaN never wins and a tie keeps the lower index).
@@ -1960,6 +1971,18 @@ int nd_v3_positions(const nd_v3_batch *b, int32_t *pos)
     ND_REQUIRE(b && pos, "null argument");
     for (int i = 0; i < b->B; ++i) pos[i] = b->s[i].pos;
     return ND_OK;
+}
+
+int nd_libm_map(nd_ctx *ctx, int fn, const float *x, size_t n, float *y)
+{
+    if (int rc = nd::enter(ctx)) return rc;
+    ND_REQUIRE(fn >= 0 && fn <= 2, "libm function %d (0 expf, 1 logf, 2 sigmoid)", fn);
+    if (n == 0) return ND_OK;
+    ND_REQUIRE(x && y, "null buffer");
+    const size_t blocks = (n + 255) / 256;
+    ND_REQUIRE(blocks <= 0x7fffffffu, "n %zu too large", n);
+    hipLaunchKernelGGL(k_libm_map, dim3(unsigned(blocks)), dim3(256), 0, ctx->stream, fn, x, n, y);
+    return nd::check_launch("k_libm_map");
 }
 
 int nd_argmax_rows(nd_ctx *ctx, const float *x, size_t count, size_t n, int32_t *out)

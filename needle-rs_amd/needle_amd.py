@@ -104,6 +104,7 @@ _SIGS = [
     ("nd_attend_step_f32_exact", C.c_int, [_vp, C.POINTER(KvGeom), _vp, _sz, _sz, _vp, _vp, _vp,
                                            C.c_float, _vp]),
     ("nd_v3_batch_create_ex", C.c_int, [_vp, _vp, _sz, _sz, _sz, _sz, C.c_int, C.POINTER(_vp)]),
+    ("nd_libm_map", C.c_int, [_vp, C.c_int, _vp, _sz, _vp]),
 ]
 
 
@@ -344,6 +345,21 @@ def argmax_rows(ctx, x, out=None):
     _check(lib().nd_argmax_rows(ctx.h, _arg(x, torch.float32, "x"), count, n,
                                 _arg(out, torch.int32, "out", count)))
     return out
+
+
+LIBM = {"expf": 0, "logf": 1, "sigmoid": 2}
+
+
+def libm_map(ctx, fn, x, y=None):
+    """The device copy of the reference's libm wrapper `fn` ("expf", "logf",
+    "sigmoid"; math.rs:3-46) applied to every element of x (fp32)."""
+    torch = _torch()
+    if y is None:
+        y = torch.empty_like(x)
+    n = x.numel()
+    _check(lib().nd_libm_map(ctx.h, LIBM[fn], _arg(x, torch.float32, "x"), n,
+                             _arg(y, torch.float32, "y", n)))
+    return y
 
 
 def fake_quant(ctx, x, dim):
