@@ -97,6 +97,36 @@ __device__ inline void fwht128_wave(float &x0, float &x1, float inv)
     x1 = (a - b) * inv;
 }
 
+// fwht128_wave over NG groups at once (one pair of registers per group),
+// each stage applied to every group before the next, so the shuffles of
+// different groups overlap; the same operations as fwht128_wave per group.
+template <int NG>
+__device__ inline void fwht128_wave_n(float (&x0)[NG], float (&x1)[NG], float inv)
+{
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int h = 1; h < 64; h <<= 1) {
+        float p0[NG], p1[NG];
+#pragma unroll
+        for (int q = 0; q < NG; ++q) {
+            p0[q] = __shfl_xor(x0[q], h, 64);
+            p1[q] = __shfl_xor(x1[q], h, 64);
+        }
+        const bool hi = (lane & h) != 0;
+#pragma unroll
+        for (int q = 0; q < NG; ++q) {
+            x0[q] = hi ? p0[q] - x0[q] : x0[q] + p0[q];
+            x1[q] = hi ? p1[q] - x1[q] : x1[q] + p1[q];
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < NG; ++q) {
+        const float a = x0[q], b = x1[q];
+        x0[q] = (a + b) * inv;
+        x1[q] = (a - b) * inv;
+    }
+}
+
 // prepare_input of `buf` (LDS, pp.in_padded floats, written and synchronised)
 // into `out` (global, and back into buf when `keep`): one wave per 128-group
 // when the group is 128, else the block-wide butterfly.  Every thread of the
@@ -437,14 +467,26 @@ __global__ __launch_bounds__(kT) void k_layer_in(LayerIn a)
         const float inv = 1.0f / sqrtf(tot[0] / float(nd) + 1e-6f);
         const int wave = tid >> 6, lane = tid & 63;
         float *xo = a.nxh + b * a.pnx.in_padded;
-        for (int g = wave; g < G; g += kT / 64) {
-            const int e0 = g * 128 + lane, e1 = e0 + 64;
-            float x0 = e0 < nd ? ln[e0] * inv : 0.0f, x1 = e1 < nd ? ln[e1] * inv : 0.0f;
-            fwht128_wave(x0, x1, a.pnx.inv);
-            xo[e0] = x0;
-            xo[e1] = x1;
-            nb[g * kPadGroup + lane] = x0;
-            nb[g * kPadGroup + 64 + lane] = x1;
+        // three groups a wave at a time, their shuffles overlapped
+        constexpr int NG = 3;
+        for (int g0 = wave; g0 < G; g0 += NG * (kT / 64)) {
+            float x0[NG], x1[NG];
+#pragma unroll
+            for (int q = 0; q < NG; ++q) {
+                const int e0 = (g0 + q * (kT / 64)) * 128 + lane, e1 = e0 + 64;
+                x0[q] = e0 < nd ? ln[e0] * inv : 0.0f;
+                x1[q] = e1 < nd ? ln[e1] * inv : 0.0f;
+            }
+            fwht128_wave_n<NG>(x0, x1, a.pnx.inv);
+#pragma unroll
+            for (int q = 0; q < NG; ++q) {
+                const int g = g0 + q * (kT / 64);
+                if (g >= G) break;
+                xo[g * 128 + lane] = x0[q];
+                xo[g * 128 + 64 + lane] = x1[q];
+                nb[g * kPadGroup + lane] = x0[q];
+                nb[g * kPadGroup + 64 + lane] = x1[q];
+            }
         }
     }
     __syncthreads();
