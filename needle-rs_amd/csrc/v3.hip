@@ -2045,21 +2045,52 @@ namespace {
 // C consecutive positions for every session (C = 1: one decode step).  Row
 // i * C + j of every per-row buffer is position pos + j of session i; the
 // layers run once over all rows; only each session's last row is scored.
-int step_impl(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *tokens, int C,
-              int32_t *next, float *logits)
+// One step (or prefill pass) of one batch, in pieces: begin() does the host
+// bookkeeping and the upload of the step's inputs; enqueue(phase) queues the
+// Engram and embedding prologue (phase -1), layer `phase` (0..L-1) or the
+// head (L) on the batch's stream; finish() the copies out.  A batch split
+// into session groups runs one StepRun per group and interleaves their
+// phases, so the groups' kernels overlap on the GPU.
+struct StepRun {
+    nd_ctx *ctx;
+    const nd_v3_model *m;
+    nd_v3_batch *b;
+    int C;
+    int S = 0, B = 0, Rcap = 0, L = 0, nl = 0, d = 0, qd = 0, kd = 0, vd = 0, od = 0, nt = 0, mo = 0;
+    size_t rows = 0;
+    int32_t *tok_dev = nullptr, *pos_dev = nullptr, *hi_dev = nullptr, *lo_dev = nullptr,
+            *rows_dev = nullptr;
+    hipStream_t st = nullptr;
+    float qk_scale = 1.0f;
+    int kf = 0;
+    bool gate_fused = false, gates_in = false;
+    const nd_cq *phi = nullptr, *fpo = nullptr, *fre = nullptr;
+    float *ev_conv = nullptr;  // [sites][Rcap][d], after the conv
+
+    int begin(const int32_t *tokens);
+    int enqueue(int phase, bool argmax);
+};
+
+int StepRun::begin(const int32_t *tokens)
 {
     if (int rc = nd::enter(ctx)) return rc;
     ND_REQUIRE(m && b && tokens, "null argument");
     ND_REQUIRE(C >= 1 && C <= b->chunk, "%d positions per step; the batch takes at most %d", C,
                b->chunk);
     const nd_v3_cfg &c = m->cfg;
-    const int S = b->B, B = S * C, Rcap = b->R;
-    const int L = c.num_layers, nl = c.mhc_lanes, d = c.d_model;
-    const int qd = c.num_heads * c.qk_head_dim, kd = c.num_kv_heads * c.qk_head_dim;
-    const int vd = c.num_kv_heads * c.v_head_dim, od = c.num_heads * c.v_head_dim;
-    const int nt = c.n_orders * c.e_heads;
-    const int mo = max_order(c);
-    const size_t rows = nd_v3_logit_rows(m);
+    S = b->B;
+    B = S * C;
+    Rcap = b->R;
+    L = c.num_layers;
+    nl = c.mhc_lanes;
+    d = c.d_model;
+    qd = c.num_heads * c.qk_head_dim;
+    kd = c.num_kv_heads * c.qk_head_dim;
+    vd = c.num_kv_heads * c.v_head_dim;
+    od = c.num_heads * c.v_head_dim;
+    nt = c.n_orders * c.e_heads;
+    mo = max_order(c);
+    rows = nd_v3_logit_rows(m);
     for (int i = 0; i < S; ++i)
         ND_REQUIRE(b->s[i].pos + C <= b->max_len, "session %d is full (%d positions)", i, b->max_len);
 
@@ -2116,22 +2147,49 @@ int step_impl(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *
     const size_t used = size_t(B) * (3 + L + nt) * 4;
     ND_HIP(hipMemcpyAsync(b->step_dev, b->stage_host[stage], used, hipMemcpyHostToDevice,
                           ctx->stream));
-    int32_t *tok_dev = static_cast<int32_t *>(b->step_dev);
-    int32_t *pos_dev = tok_dev + B, *hi_dev = tok_dev + 2 * B, *lo_dev = tok_dev + 3 * B;
-    int32_t *rows_dev = tok_dev + 3 * B + size_t(L) * B;
+    tok_dev = static_cast<int32_t *>(b->step_dev);
+    pos_dev = tok_dev + B;
+    hi_dev = tok_dev + 2 * B;
+    lo_dev = tok_dev + 3 * B;
+    rows_dev = tok_dev + 3 * B + size_t(L) * B;
     ND_HIP(hipEventRecord(b->stage_done[stage], ctx->stream));
     b->stage_pending[stage] = true;
     b->stage_next = (stage + 1) % nd_v3_batch::kStages;
-    hipStream_t st = ctx->stream;
+    st = ctx->stream;
+    qk_scale = 1.0f / std::sqrt(float(c.qk_head_dim));
+    kf = b->kv_f32 ? 1 : 0;
+    gate_fused = c.v_head_dim == 64 && m->pre_attn.group == 128 &&
+                 m->pre_attn.in_padded == od && m->layers[0].out->per_byte != 0;
+    phi = m->phi_pre;
+    // The scatter-up gates ride in the layer's launches (k_layer_in's phi
+    // rows, second workgroups of k_qkv_kv and k_post_hada) for single
+    // positions when the phi weights fit; else (and for prefill passes)
+    // they run on the side stream, joined by events.
+    fpo = m->phi_post;
+    fre = m->phi_res;
+    gates_in = (phi->per_byte == 2 || phi->per_byte == 4) && phi->group == 128 &&
+                  fpo->per_byte == phi->per_byte && fre->per_byte == phi->per_byte &&
+                  fpo->group == 128 && fre->group == 128 &&
+                  fpo->in_padded == phi->in_padded && fre->in_padded == phi->in_padded &&
+                  size_t(2 * nl + nl * nl) * phi->num_groups <= size_t(kMaxPhiPairs) &&
+                  size_t(2 * nl + nl * nl) * phi->num_groups <= size_t(kPhiPerThread * kT) &&
+                  nl * nl <= 64 && fpo->row_bytes % 16 == 0 && fre->row_bytes % 16 == 0 &&
+                  C == 1;
+    ev_conv = C == 1 ? b->ev : b->evc;
+    return ND_OK;
+}
+
 #define CK(call) \
     if ((rc = (call))) return rc;
 #define LCHK(name) \
     if ((rc = nd::check_launch(name))) return rc;
 
-    // every kernel of the step, on `st` and the side stream joined back into
-    // it; with `argmax`, the greedy tokens into b->next
-    auto enqueue = [&](bool argmax) -> int {
-        int rc = ND_OK;
+int StepRun::enqueue(int phase, bool argmax)
+{
+    const nd_v3_cfg &c = m->cfg;
+    hipStream_t side = b->side;
+    int rc = ND_OK;
+    if (phase < 0) {
         // ---- Engram for this position (model.rs:162-191) -------------------------
         // the prepared key inputs of every site: one fused fetch when every
         // table row is one 128-wide group feeding the key's 128-groups
@@ -2226,164 +2284,165 @@ int step_impl(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *
                 LCHK("k_tails");
             }
         }
-        float *const ev_conv = C == 1 ? b->ev : b->evc;  // [sites][Rcap][d], after the conv
         // ---- lane stream (model.rs:194-203) --------------------------------------
         CK(nd_cq_dequantize_rows(ctx, m->embedding, tok_dev, size_t(B), b->emb));
         hipLaunchKernelGGL(k_embed, dim3((d + 255) / 256, B), dim3(256), 0, st, b->emb, b->lanes,
                            m->embed_scale, nl, d);
         LCHK("k_embed");
 
-        const float qk_scale = 1.0f / std::sqrt(float(c.qk_head_dim));
-        const int kf = b->kv_f32 ? 1 : 0;
-        const bool gate_fused = c.v_head_dim == 64 && m->pre_attn.group == 128 &&
-                                m->pre_attn.in_padded == od && m->layers[0].out->per_byte != 0;
-        hipStream_t side = b->side;
-        const nd_cq *phi = m->phi_pre;
-        // The scatter-up gates ride in k_post_hada's launch (a second
-        // workgroup per row) when the phi weights fit its gate block; else
-        // they run on the side stream, joined by events.
-        const nd_cq *fpo = m->phi_post, *fre = m->phi_res;
-        const bool gates_in = (phi->per_byte == 2 || phi->per_byte == 4) && phi->group == 128 &&
-                              fpo->per_byte == phi->per_byte && fre->per_byte == phi->per_byte &&
-                              fpo->group == 128 && fre->group == 128 &&
-                              fpo->in_padded == phi->in_padded && fre->in_padded == phi->in_padded &&
-                              size_t(2 * nl + nl * nl) * phi->num_groups <= size_t(kMaxPhiPairs) &&
-                              size_t(2 * nl + nl * nl) * phi->num_groups <= size_t(kPhiPerThread * kT) &&
-                              nl * nl <= 64 && fpo->row_bytes % 16 == 0 && fre->row_bytes % 16 == 0 &&
-                              C == 1;
-        for (int li = 0; li < L; ++li) {
-            const Layer &l = m->layers[li];
-            const int site = site_of(c, li);
-            // previous layer's scatter up + this layer's mix down
-            if (li > 0 && !gates_in) ND_HIP(hipStreamWaitEvent(st, b->ev_gates[(li - 1) & 1], 0));
-            LayerIn in{b->lanes, b->y, b->gp, b->gr, li > 0, b->nxh, m->pre_nx, phi->packed,
-                       phi->norms, phi->lv, phi->row_bytes, int(phi->num_groups), li * nl,
-                       int(phi->bits == 5), m->b_pre + size_t(li) * nl, m->a_pre[li], li, nl, d,
-                       gates_in ? 1 : 0, fpo->packed, fre->packed, fpo->norms, fre->norms, fpo->lv, fre->lv,
-                       fpo->row_bytes, fre->row_bytes, li * nl, li * nl * nl, int(fpo->bits == 5),
-                       int(fre->bits == 5), b->graw,
-                       site >= 0 ? b->ek + size_t(site) * Rcap * d : nullptr,
-                       site >= 0 ? ev_conv + size_t(site) * Rcap * d : nullptr, l.norm_in, b->u, b->bx,
-                       b->hh, m->pre_h};
-            if (phi->per_byte == 2)
-                hipLaunchKernelGGL(k_layer_in<2>, dim3(B), dim3(kT), 0, st, in);
-            else
-                hipLaunchKernelGGL(k_layer_in<4>, dim3(B), dim3(kT), 0, st, in);
-            LCHK("k_layer_in");
-            if (!gates_in) {
-                // side stream: this layer's scatter-up gates from the prepared lanes
-                ND_HIP(hipEventRecord(b->ev_in[li & 1], st));
-                ND_HIP(hipStreamWaitEvent(side, b->ev_in[li & 1], 0));
-                {
-                    const nd_cq *ws[2] = {m->phi_post, m->phi_res};
-                    const size_t r0[2] = {size_t(li) * nl, size_t(li) * nl * nl};
-                    const size_t nr[2] = {size_t(nl), size_t(nl) * nl};
-                    float *ys[2] = {b->hpost, b->hres};
-                    CK(nd_cq_exact_set(ctx, side, 2, ws, b->nxh, size_t(B), r0, nr, ys, "v3 phi post/res"));
-                }
-                MhcGates mg{b->hpost, b->hres, m->b_post + size_t(li) * nl,
-                            m->b_res + size_t(li) * nl * nl, m->a_post[li], m->a_res[li], li, nl,
-                            b->gp, b->gr};
-                hipLaunchKernelGGL(k_mhc_gates, dim3(B), dim3(64), 0, side, mg);
-                LCHK("k_mhc_gates");
-                ND_HIP(hipEventRecord(b->ev_gates[li & 1], side));
-            }
-            // q, k, v and gate projections of the prepared h, one launch
+        return ND_OK;
+    }
+    if (phase < L) {
+        const int li = phase;
+        const Layer &l = m->layers[li];
+        const int site = site_of(c, li);
+        // previous layer's scatter up + this layer's mix down
+        if (li > 0 && !gates_in) ND_HIP(hipStreamWaitEvent(st, b->ev_gates[(li - 1) & 1], 0));
+        LayerIn in{b->lanes, b->y, b->gp, b->gr, li > 0, b->nxh, m->pre_nx, phi->packed,
+                   phi->norms, phi->lv, phi->row_bytes, int(phi->num_groups), li * nl,
+                   int(phi->bits == 5), m->b_pre + size_t(li) * nl, m->a_pre[li], li, nl, d,
+                   gates_in ? 1 : 0, fpo->packed, fre->packed, fpo->norms, fre->norms, fpo->lv, fre->lv,
+                   fpo->row_bytes, fre->row_bytes, li * nl, li * nl * nl, int(fpo->bits == 5),
+                   int(fre->bits == 5), b->graw,
+                   site >= 0 ? b->ek + size_t(site) * Rcap * d : nullptr,
+                   site >= 0 ? ev_conv + size_t(site) * Rcap * d : nullptr, l.norm_in, b->u, b->bx,
+                   b->hh, m->pre_h};
+        if (phi->per_byte == 2)
+            hipLaunchKernelGGL(k_layer_in<2>, dim3(B), dim3(kT), 0, st, in);
+        else
+            hipLaunchKernelGGL(k_layer_in<4>, dim3(B), dim3(kT), 0, st, in);
+        LCHK("k_layer_in");
+        if (!gates_in) {
+            // side stream: this layer's scatter-up gates from the prepared lanes
+            ND_HIP(hipEventRecord(b->ev_in[li & 1], st));
+            ND_HIP(hipStreamWaitEvent(side, b->ev_in[li & 1], 0));
             {
-                const nd_cq *ws[4] = {l.q, l.k, l.v, l.gate};
-                const size_t r0[4] = {0, 0, 0, 0};
-                const size_t nr[4] = {size_t(qd), size_t(kd), size_t(vd), size_t(od)};
-                float *ys[4] = {b->q, b->k, b->v, b->gate};
-                CK(nd_cq_exact_set(ctx, st, 4, ws, b->hh, size_t(B), r0, nr, ys, "v3 qkv/gate"));
+                const nd_cq *ws[2] = {m->phi_post, m->phi_res};
+                const size_t r0[2] = {size_t(li) * nl, size_t(li) * nl * nl};
+                const size_t nr[2] = {size_t(nl), size_t(nl) * nl};
+                float *ys[2] = {b->hpost, b->hres};
+                CK(nd_cq_exact_set(ctx, side, 2, ws, b->nxh, size_t(B), r0, nr, ys, "v3 phi post/res"));
             }
-            // this layer's scatter-up gates, when they ride in the layer's launches
-            MhcIn mi{};
-            if (gates_in) {
-                mi.on = 1;
-                mi.graw = b->graw;
-                mi.n = nl;
-                mi.layer = li;
-                mi.split = kGateSplit;
-                mi.b_post = m->b_post + size_t(li) * nl;
-                mi.b_res = m->b_res + size_t(li) * nl * nl;
-                mi.a_post = m->a_post[li];
-                mi.a_res = m->a_res[li];
-                mi.gp = b->gp;
-                mi.gr = b->gr;
-                mi.state = b->gstate;
-            }
-            const unsigned gy = gates_in ? 2u : 1u;
-            // conv, norm + RoPE, int8 KV append
-            {
-                const nd_kv_geom &g = b->geom[li];
-                QkvKv qk{b->q, b->k, b->v, b->qt[li], b->kt[li], b->vt[li], l.q_taps, l.k_taps,
-                         l.v_taps, l.q_norm, l.k_norm, m->rope_tab, pos_dev, qd, kd, vd,
-                         c.qkv_conv_taps, c.num_heads, c.num_kv_heads, c.qk_head_dim, c.v_head_dim,
-                         b->kv[li], b->kv_stride[li], nd_kv_v_offset(&g), nd_kv_ks_offset(&g),
-                         nd_kv_vs_offset(&g), g.cap, C, b->qn};
-                if (kf) qk.v_off = nd_kv_f32_v_offset(&g);
-                const dim3 qg(unsigned(B), gy);
-                if (C == 1) {
-                    if (kf)
-                        hipLaunchKernelGGL((k_qkv_kv<false, true>), qg, dim3(kT), 0, st, qk, mi);
-                    else
-                        hipLaunchKernelGGL((k_qkv_kv<false, false>), qg, dim3(kT), 0, st, qk, mi);
-                    LCHK("k_qkv_kv");
-                } else {
-                    // prefill passes run the gates on the side stream
-                    if (kf)
-                        hipLaunchKernelGGL((k_qkv_kv<true, true>), dim3(B), dim3(kT), 0, st, qk, mi);
-                    else
-                        hipLaunchKernelGGL((k_qkv_kv<true, false>), dim3(B), dim3(kT), 0, st, qk, mi);
-                    LCHK("k_qkv_kv");
-                    const int tt = c.qkv_conv_taps - 1;
-                    if (tt > 0) {
-                        hipLaunchKernelGGL(k_tails, dim3((qd + 255) / 256, S), dim3(256), 0, st, b->q,
-                                           b->qt[li], tt, C, qd);
-                        hipLaunchKernelGGL(k_tails, dim3((kd + 255) / 256, S), dim3(256), 0, st, b->k,
-                                           b->kt[li], tt, C, kd);
-                        hipLaunchKernelGGL(k_tails, dim3((vd + 255) / 256, S), dim3(256), 0, st, b->v,
-                                           b->vt[li], tt, C, vd);
-                        LCHK("k_tails");
-                    }
-                }
-            }
-            // attention over the int8 ring (query fake-quant fused); with
-            // 64-wide heads and 128-wide groups its epilogue also applies
-            // the sigmoid gate and the butterfly stages inside each head,
-            // and out_proj's load finishes prepare_input
-            if (gate_fused) {
-                CK(nd_attend_exact_rows(ctx, &b->geom[li], b->kv[li], b->kv_stride[li], size_t(B), C,
-                                        lo_dev + size_t(li) * B, hi_dev, C == 1 ? b->q : b->qn,
-                                        qk_scale, kf ? 0 : 1, b->attn, b->gate, kf));
-                const size_t r0 = 0, nr = size_t(d);
-                CK(nd_cq_exact_set(ctx, st, 1, &l.out, b->attn, size_t(B), &r0, &nr, &b->proj,
-                                   "v3 out projection", m->pre_attn.inv));
+            MhcGates mg{b->hpost, b->hres, m->b_post + size_t(li) * nl,
+                        m->b_res + size_t(li) * nl * nl, m->a_post[li], m->a_res[li], li, nl,
+                        b->gp, b->gr};
+            hipLaunchKernelGGL(k_mhc_gates, dim3(B), dim3(64), 0, side, mg);
+            LCHK("k_mhc_gates");
+            ND_HIP(hipEventRecord(b->ev_gates[li & 1], side));
+        }
+        // q, k, v and gate projections of the prepared h, one launch
+        {
+            const nd_cq *ws[4] = {l.q, l.k, l.v, l.gate};
+            const size_t r0[4] = {0, 0, 0, 0};
+            const size_t nr[4] = {size_t(qd), size_t(kd), size_t(vd), size_t(od)};
+            float *ys[4] = {b->q, b->k, b->v, b->gate};
+            CK(nd_cq_exact_set(ctx, st, 4, ws, b->hh, size_t(B), r0, nr, ys, "v3 qkv/gate"));
+        }
+        // this layer's scatter-up gates, when they ride in the layer's launches
+        MhcIn mi{};
+        if (gates_in) {
+            mi.on = 1;
+            mi.graw = b->graw;
+            mi.n = nl;
+            mi.layer = li;
+            mi.split = kGateSplit;
+            mi.b_post = m->b_post + size_t(li) * nl;
+            mi.b_res = m->b_res + size_t(li) * nl * nl;
+            mi.a_post = m->a_post[li];
+            mi.a_res = m->a_res[li];
+            mi.gp = b->gp;
+            mi.gr = b->gr;
+            mi.state = b->gstate;
+        }
+        const unsigned gy = gates_in ? 2u : 1u;
+        // conv, norm + RoPE, int8 KV append
+        {
+            const nd_kv_geom &g = b->geom[li];
+            QkvKv qk{b->q, b->k, b->v, b->qt[li], b->kt[li], b->vt[li], l.q_taps, l.k_taps,
+                     l.v_taps, l.q_norm, l.k_norm, m->rope_tab, pos_dev, qd, kd, vd,
+                     c.qkv_conv_taps, c.num_heads, c.num_kv_heads, c.qk_head_dim, c.v_head_dim,
+                     b->kv[li], b->kv_stride[li], nd_kv_v_offset(&g), nd_kv_ks_offset(&g),
+                     nd_kv_vs_offset(&g), g.cap, C, b->qn};
+            if (kf) qk.v_off = nd_kv_f32_v_offset(&g);
+            const dim3 qg(unsigned(B), gy);
+            if (C == 1) {
+                if (kf)
+                    hipLaunchKernelGGL((k_qkv_kv<false, true>), qg, dim3(kT), 0, st, qk, mi);
+                else
+                    hipLaunchKernelGGL((k_qkv_kv<false, false>), qg, dim3(kT), 0, st, qk, mi);
+                LCHK("k_qkv_kv");
             } else {
-                CK(nd_attend_exact_rows(ctx, &b->geom[li], b->kv[li], b->kv_stride[li], size_t(B), C,
-                                        lo_dev + size_t(li) * B, hi_dev, C == 1 ? b->q : b->qn,
-                                        qk_scale, kf ? 0 : 1, b->attn, nullptr, kf));
-                hipLaunchKernelGGL(k_gate_prep, dim3(B), dim3(kT), 0, st, b->attn, b->gate, b->ah, od,
-                                   m->pre_attn);
-                LCHK("k_gate_prep");
-                CK(project(ctx, l.out, b->ah, B, 0, d, b->proj));
+                // prefill passes run the gates on the side stream
+                if (kf)
+                    hipLaunchKernelGGL((k_qkv_kv<true, true>), dim3(B), dim3(kT), 0, st, qk, mi);
+                else
+                    hipLaunchKernelGGL((k_qkv_kv<true, false>), dim3(B), dim3(kT), 0, st, qk, mi);
+                LCHK("k_qkv_kv");
+                const int tt = c.qkv_conv_taps - 1;
+                if (tt > 0) {
+                    hipLaunchKernelGGL(k_tails, dim3((qd + 255) / 256, S), dim3(256), 0, st, b->q,
+                                       b->qt[li], tt, C, qd);
+                    hipLaunchKernelGGL(k_tails, dim3((kd + 255) / 256, S), dim3(256), 0, st, b->k,
+                                       b->kt[li], tt, C, kd);
+                    hipLaunchKernelGGL(k_tails, dim3((vd + 255) / 256, S), dim3(256), 0, st, b->v,
+                                       b->vt[li], tt, C, vd);
+                    LCHK("k_tails");
+                }
             }
-            HadaArgs ha{b->proj, l.post_norm, l.pre_hada, nd_sigmoidf(l.attn_gate), b->u, b->bx, b->y,
-                        l.d1, l.d2, l.b2, l.d3, l.d4, l.w1a, l.w1b, l.w2a, l.w2b, l.w3a, l.w3b,
-                        l.cond_v, l.cond_u, m->p1, m->p2, d, l.cond_rank};
-            hipLaunchKernelGGL(k_post_hada, dim3(unsigned(B), gy), dim3(1024), 0, st, ha, mi);
-            LCHK("k_post_hada");
         }
-        // ---- head ---------------------------------------------------------------
-        if (!gates_in) ND_HIP(hipStreamWaitEvent(st, b->ev_gates[(L - 1) & 1], 0));
-        hipLaunchKernelGGL(k_final, dim3(S), dim3(kT), 0, st, b->lanes, b->y, b->gp, b->gr,
-                           m->final_norm, b->xh, nl, d, m->pre_x, C);
-        LCHK("k_final");
-        CK(project(ctx, m->embedding, b->xh, S, 0, rows, b->logits));
-        if (argmax) {
-            hipLaunchKernelGGL(k_argmax, dim3(S), dim3(kT), 0, st, b->logits, int(rows), b->next);
-            LCHK("k_argmax");
+        // attention over the int8 ring (query fake-quant fused); with
+        // 64-wide heads and 128-wide groups its epilogue also applies
+        // the sigmoid gate and the butterfly stages inside each head,
+        // and out_proj's load finishes prepare_input
+        if (gate_fused) {
+            CK(nd_attend_exact_rows(ctx, &b->geom[li], b->kv[li], b->kv_stride[li], size_t(B), C,
+                                    lo_dev + size_t(li) * B, hi_dev, C == 1 ? b->q : b->qn,
+                                    qk_scale, kf ? 0 : 1, b->attn, b->gate, kf));
+            const size_t r0 = 0, nr = size_t(d);
+            CK(nd_cq_exact_set(ctx, st, 1, &l.out, b->attn, size_t(B), &r0, &nr, &b->proj,
+                               "v3 out projection", m->pre_attn.inv));
+        } else {
+            CK(nd_attend_exact_rows(ctx, &b->geom[li], b->kv[li], b->kv_stride[li], size_t(B), C,
+                                    lo_dev + size_t(li) * B, hi_dev, C == 1 ? b->q : b->qn,
+                                    qk_scale, kf ? 0 : 1, b->attn, nullptr, kf));
+            hipLaunchKernelGGL(k_gate_prep, dim3(B), dim3(kT), 0, st, b->attn, b->gate, b->ah, od,
+                               m->pre_attn);
+            LCHK("k_gate_prep");
+            CK(project(ctx, l.out, b->ah, B, 0, d, b->proj));
         }
+        HadaArgs ha{b->proj, l.post_norm, l.pre_hada, nd_sigmoidf(l.attn_gate), b->u, b->bx, b->y,
+                    l.d1, l.d2, l.b2, l.d3, l.d4, l.w1a, l.w1b, l.w2a, l.w2b, l.w3a, l.w3b,
+                    l.cond_v, l.cond_u, m->p1, m->p2, d, l.cond_rank};
+        hipLaunchKernelGGL(k_post_hada, dim3(unsigned(B), gy), dim3(1024), 0, st, ha, mi);
+        LCHK("k_post_hada");
+        return ND_OK;
+    }
+    // ---- head ---------------------------------------------------------------
+    if (!gates_in) ND_HIP(hipStreamWaitEvent(st, b->ev_gates[(L - 1) & 1], 0));
+    hipLaunchKernelGGL(k_final, dim3(S), dim3(kT), 0, st, b->lanes, b->y, b->gp, b->gr,
+                       m->final_norm, b->xh, nl, d, m->pre_x, C);
+    LCHK("k_final");
+    CK(project(ctx, m->embedding, b->xh, S, 0, rows, b->logits));
+    if (argmax) {
+        hipLaunchKernelGGL(k_argmax, dim3(S), dim3(kT), 0, st, b->logits, int(rows), b->next);
+        LCHK("k_argmax");
+    }
+    return ND_OK;
+}
+
+// A whole step of one batch: begin, every phase (eagerly, or replayed from
+// a captured graph), then the copies out and, with `next`, the wait.
+int step_impl(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *tokens, int C,
+              int32_t *next, float *logits)
+{
+    StepRun r{ctx, m, b, C};
+    if (int rc = r.begin(tokens)) return rc;
+    const int S = r.S, L = r.L;
+    const size_t rows = r.rows;
+    hipStream_t st = r.st;
+    auto enqueue = [&](bool argmax) -> int {
+        for (int ph = -1; ph <= L; ++ph)
+            if (int rc = r.enqueue(ph, argmax)) return rc;
         return ND_OK;
     };
     // One position per session, graphs on: replay the captured step on the
@@ -2406,12 +2465,14 @@ int step_impl(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *
         if (!b->graph_exec) {
             st = b->gstream;
             ctx->stream = b->gstream;
+            r.st = st;
             const hipError_t be = hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed);
             const int crc = be == hipSuccess ? enqueue(true) : ND_ERR_HIP;
             hipGraph_t g = nullptr;
             const hipError_t ce = be == hipSuccess ? hipStreamEndCapture(st, &g) : be;
             ctx->stream = user;
             st = user;
+            r.st = st;
             hipGraphExec_t ex = nullptr;
             const bool ok = crc == ND_OK && ce == hipSuccess && g &&
                             hipGraphInstantiate(&ex, g, nullptr, nullptr, 0) == hipSuccess;
@@ -2444,10 +2505,11 @@ int step_impl(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *
         std::memcpy(next, b->next_host, size_t(S) * 4);
     }
     for (int i = 0; i < S; ++i) b->s[i].pos += C;
-#undef CK
-#undef LCHK
     return ND_OK;
 }
+
+#undef CK
+#undef LCHK
 
 }  // namespace
 
