@@ -198,6 +198,8 @@ __device__ __forceinline__ float nd_fold_plain(const float *v, int n)
 template <int NT, int CMAX>
 __device__ __forceinline__ float nd_fold_nonneg(const float *v, int n, NdFoldLds<NT> &L)
 {
+    static_assert(NT % 64 == 0 && NT >= 64, "whole waves");
+    static_assert(CMAX >= 1 && CMAX <= 32, "the run map holds one bit per term in 32 bits");
     constexpr int NW = NT / 64;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int c = (n + NT - 1) / NT;

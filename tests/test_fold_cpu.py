@@ -1,10 +1,13 @@
 """CPU checks of the exact parallel fold (needle-rs_amd/csrc/nd_fold.h).
 
 The fold's arithmetic -- binade bounds, in-binade units, run sums -- is
-shared host/device code.  fold_fuzz.cpp models the device algorithm on the
-host with those functions and compares it bit for bit with the plain
-sequential loop over adversarial inputs (ties, subnormals, powers of two, a
-binade crossing every step, huge ranges).  The plain loop is the truth the
+shared host/device code.  fold_fuzz.cpp models the algorithm on the host
+with those functions, and emulates nd_fold_nonneg lane for lane (DPP scans,
+wave carries, the threads' item offsets), and compares both bit for bit with
+the plain sequential loop over adversarial inputs (ties, subnormals, powers
+of two, a binade crossing every step, huge ranges, a crossing at a wave's
+first or last chunk); the emulated items must match the sequential list in
+count and order.  The plain loop is the truth the
 reference's sums follow (kernels.rs:22-24, norm.rs:25,
 v3/attention.rs:361-365)."""
 import os
@@ -39,7 +42,8 @@ def test_parallel_fold_model_matches_the_loop(fuzz_bin, seed):
     assert lines[-1] == "OK"
     # every generator ran, none mismatched
     kinds = [l for l in lines if l.startswith("kind")]
-    assert len(kinds) == 11
+    assert len(kinds) == 12
+    assert "lead items" in lines[-2]
     assert all(" mismatches 0 " in l for l in kinds)
 
 
