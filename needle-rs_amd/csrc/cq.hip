@@ -290,6 +290,19 @@ __global__ __launch_bounds__(kThreads) void cq_gemv_stream_kernel(
     }
 }
 
+// Streaming shape shared by the batch-1 GEMVs below.  A launch's row tiles
+// are dealt to its workgroups round-robin (tile = blockIdx.x + it *
+// gridDim.x), so at any moment the workgroups read one contiguous front of
+// the weight.  Each workgroup keeps the codes and norms of its next D tiles
+// in registers, issuing a tile's refill right after the tile is consumed;
+// scheduling barriers hold that order, so each wait covers the oldest tile
+// only and the loads in flight slide instead of draining.  The first D
+// tiles are requested before the workgroup's lookup table is built.
+// Row results are staged in LDS and written out by whole tiles (coalesced,
+// nontemporal) every CAP tiles and at the end: a global store inside the
+// loop would put its write round trip under the next wait.  Rows past the
+// end reread the last row; the loop body has no branches.
+
 // Batch-1 GEMV on 2-bit (and ternary) rows of 16 * ND code dwords, ND <= 3
 // (in <= 768), by product lookup.  Each workgroup first builds, from the
 // prepared activation, T(p, e) = lvl(e & 3) * xh[2p] + lvl(e >> 2) * xh[2p+1]
@@ -305,34 +318,112 @@ __global__ __launch_bounds__(kThreads) void cq_gemv_stream_kernel(
 // offset riding in the instruction.  Every entry is a 32-dword block indexed
 // [row group & 1][j]: the two row groups of a half-wave read disjoint banks,
 // so a gather does not conflict whatever codes the lanes hold.  Two
-// 1024-thread workgroups share a CU; each streams a contiguous run of 64-row
-// tiles with the codes and norms of the next D tiles in flight (rows past the
-// end reread the last row and store nothing, so every load is unconditional).
+// 1024-thread workgroups share a CU, each streaming 64-row tiles as above.
 // The 16 partial sums of a row meet through DPP row rotations.
 constexpr int kNibThreads = 1024;
 constexpr int kNibRows = kNibThreads / kLanesPerRow;  // 64 rows per tile
+constexpr int kNibDepth = 4;                          // tiles in flight
+constexpr int kNibStage = 16;                         // staged tiles (4 KiB)
 
 __device__ inline float row16_sum(float v)
 {
-    // rotations within a 16-lane DPP row: 8, 4, 2, 1 (row_ror:n = 0x120 + n)
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x124, 0xf, 0xf, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x122, 0xf, 0xf, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x121, 0xf, 0xf, false));
+    // rotations within a 16-lane DPP row: 8, 4, 2, 1 (row_ror:n = 0x120 + n);
+    // every lane has a source, so bound_ctrl is moot and each step fuses
+    // into one v_add_f32_dpp
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xf, 0xf, true));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x124, 0xf, 0xf, true));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x122, 0xf, 0xf, true));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x121, 0xf, 0xf, true));
     return v;
 }
 
-template <int ND, int D>
+// ND code dwords from byte offset `off` of the buffer (one load).
+template <int ND>
+__device__ inline void load_dwords(__amdgpu_buffer_rsrc_t rc, int off, uint32_t *c)
+{
+    if constexpr (ND == 1) {
+        c[0] = __builtin_amdgcn_raw_buffer_load_b32(rc, off, 0, 2);
+    } else if constexpr (ND == 2) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(rc, off, 0, 2);
+        c[0] = v[0];
+        c[1] = v[1];
+    } else {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b96(rc, off, 0, 2);
+        c[0] = v[0];
+        c[1] = v[1];
+        c[2] = v[2];
+    }
+}
+
+// A workgroup barrier ordering LDS accesses only: unlike __syncthreads it
+// does not wait for the global loads in flight.
+__device__ inline void lds_barrier()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// The staged results of tiles it_end - count .. it_end - 1 (rpt rows a
+// tile, at stage[(it % cap) * rpt]) written to y, nontemporal; between two
+// barriers, so all NT threads of the workgroup call it.  (NT is a constant:
+// blockDim.x is a load from the dispatch packet, and its wait would drain
+// the loads in flight.)
+template <int NT>
+__device__ inline void flush_stage(const float *stage, int cap, int rpt, int it_end, int count,
+                                   int iters, int rows, float *y)
+{
+    lds_barrier();
+    for (int f = int(threadIdx.x); f < count * rpt; f += NT) {
+        const int it = it_end - count + f / rpt;
+        const int r = (int(blockIdx.x) + it * int(gridDim.x)) * rpt + f % rpt;
+        if (it < iters && r < rows) __builtin_nontemporal_store(stage[(it % cap) * rpt + f % rpt], y + r);
+    }
+    lds_barrier();
+}
+
+template <int ND>
 __global__ __launch_bounds__(kNibThreads, 2) void cq_gemv_nib_kernel(
     const uint8_t *__restrict__ packed, const float *__restrict__ norms,
     const float *__restrict__ lut, const float *__restrict__ xh, float *__restrict__ y,
-    int row_start, int rows, int row_bytes, int num_groups, int group, int tiles_per_block)
+    int row_start, int rows, int row_bytes, int num_groups, int group, int iters)
 {
     constexpr int NI = 8 * ND;  // nibble positions per lane
+    constexpr int D = kNibDepth;
     __shared__ float tab[16384];  // 64 KiB
+    __shared__ float stage[kNibStage * kNibRows];
     const int t = threadIdx.x;
     const int j = t & (kLanesPerRow - 1);
     const int rg = t / kLanesPerRow;  // row of the tile
+    // the lane's ND * 16 elements span groups g0 and g0 + 1 at most
+    const int g0 = (j * ND * 16) / group;
+    const int g1 = g0 + 1 < num_groups ? g0 + 1 : g0;
+    // the launch's rows through buffer resources: 32-bit offsets (the caller
+    // keeps rows * row_bytes and rows * num_groups * 4 below 2^31)
+    const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(packed + size_t(row_start) * row_bytes), (short)0, rows * row_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rn = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(norms + size_t(row_start) * num_groups), (short)0, rows * num_groups * 4, 0x00020000);
+    const int ntiles = (rows + kNibRows - 1) / kNibRows;
+    uint32_t cb[D][ND];
+    float nb[D][2];
+    auto load = [&](int it, int k) {
+        int tile = int(blockIdx.x) + it * int(gridDim.x);
+        tile = tile < ntiles ? tile : ntiles - 1;
+        int r = tile * kNibRows + rg;
+        r = r < rows ? r : rows - 1;
+        // rows < 2^24 here, so 24-bit multiplies give the offsets; codes are
+        // read once: nontemporal
+        load_dwords<ND>(rc, int(__umul24(uint32_t(r), uint32_t(row_bytes))) + j * (4 * ND), cb[k]);
+        const int no = int(__umul24(uint32_t(r), uint32_t(num_groups * 4)));
+        nb[k][0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rn, no + 4 * g0, 0, 0));
+        nb[k][1] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rn, no + 4 * g1, 0, 0));
+    };
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+        load(k, k);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     // lut[4c] is the level of code c (byte value c, first crumb), ternary
     // crumb map included
     for (int f = t; f < 16 * NI * kLanesPerRow; f += kNibThreads) {
@@ -344,69 +435,169 @@ __global__ __launch_bounds__(kNibThreads, 2) void cq_gemv_nib_kernel(
         tab[at / 4 + fj] = v;
         tab[at / 4 + 16 + fj] = v;
     }
-    // the lane's ND * 16 elements span groups g0 and g0 + 1 at most
-    const int g0 = (j * ND * 16) / group;
     bool second[ND];
 #pragma unroll
     for (int i = 0; i < ND; ++i) second[i] = ((j * ND + i) * 16) / group != g0;
-    const int g1 = g0 + 1 < num_groups ? g0 + 1 : g0;
     __syncthreads();
 
     const uint32_t lb = uint32_t(((rg & 1) * kLanesPerRow + j) * 4);
     const char *tb = reinterpret_cast<const char *>(tab);
-    // the launch's rows through buffer resources: 32-bit offsets (the caller
-    // keeps rows * row_bytes and rows * num_groups * 4 below 2^31)
+    for (int it0 = 0; it0 < iters; it0 += D) {
+#pragma unroll
+        for (int k = 0; k < D; ++k) {
+            const int it = it0 + k;
+            float total = 0.0f;
+#pragma unroll
+            for (int i = 0; i < ND; ++i) {
+                const uint32_t dw = cb[k][i];
+                const uint32_t cq[4] = {dw << 7, dw >> 1, dw >> 9, dw >> 17};
+                float dot = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int kk = 4 * i + q;
+                    const float lo = *reinterpret_cast<const float *>(tb + ((cq[q] & 0x780u) | lb) + (kk << 11));
+                    const float hi =
+                        *reinterpret_cast<const float *>(tb + ((cq[q] & 0x7800u) | lb) + (0x8000 | (kk << 7)));
+                    dot = q == 0 ? lo + hi : dot + lo + hi;
+                }
+                total += (second[i] ? nb[k][1] : nb[k][0]) * dot;
+            }
+            total = row16_sum(total);
+            stage[(it % kNibStage) * kNibRows + rg] = total;  // the row's 16 lanes agree
+            __builtin_amdgcn_sched_barrier(0);
+            load(it + D, k);
+            __builtin_amdgcn_sched_barrier(0);
+            if ((it + 1) % kNibStage == 0) flush_stage<kNibThreads>(stage, kNibStage, kNibRows, it + 1, kNibStage, iters, rows, y);
+        }
+    }
+    // the loop ran to a multiple of D; flush what the last full stage left
+    const int done = (iters + D - 1) / D * D;
+    if (done % kNibStage) flush_stage<kNibThreads>(stage, kNibStage, kNibRows, done, done % kNibStage, iters, rows, y);
+}
+
+// Batch-1 GEMV on 4-bit rows of 16 * ND code dwords, ND = 4..6 (in 512 to
+// 768), by byte lookup: a byte's two levels come from a 256-entry table of
+// float2 in LDS (REPL replicas, lane l reading replica l % REPL) and
+// multiply the lane's activations held in registers.  Lane j of a 16-lane
+// row group holds code bytes [16 j, 16 j + 16) (elements 32 j .. 32 j + 31,
+// one 128-bit load) and, for ND > 4, bytes [256 + 4 B j, 256 + 4 B (j + 1))
+// with B = ND - 4 (elements 512 + 8 B j ..): every load of a row group
+// covers a contiguous run of its row, and each part lies in one group when
+// the group is a multiple of 32.  512-thread workgroups (32-row tiles, one
+// 128-byte line of results each), two a CU, streaming as above.
+constexpr int kQ4Threads = 512;
+constexpr int kQ4Rows = kQ4Threads / kLanesPerRow;  // 32 rows per tile
+constexpr int kQ4Repl = 16;
+constexpr int kQ4Depth = 4;
+constexpr int kQ4Stage = 32;                        // staged tiles (4 KiB)
+
+template <int ND>
+__global__ __launch_bounds__(kQ4Threads) void cq_gemv_q4_kernel(
+    const uint8_t *__restrict__ packed, const float *__restrict__ norms,
+    const float *__restrict__ lut, const float *__restrict__ xh, float *__restrict__ y,
+    int row_start, int rows, int row_bytes, int num_groups, int group, int iters)
+{
+    constexpr int B = ND - 4;  // dwords of the second part
+    constexpr int D = kQ4Depth;
+    __shared__ float2 rep[256 * kQ4Repl];  // 32 KiB
+    __shared__ float stage[kQ4Stage * kQ4Rows];
+    const int t = threadIdx.x, lane = t & 63, j = t & (kLanesPerRow - 1), rg = t / kLanesPerRow;
+    // the lane's activations: part A elements 32 j + 8 i + e (i < 4), part B
+    // 512 + 8 B j + 8 (i - 4) + e
+    float xr[ND][8];
+#pragma unroll
+    for (int i = 0; i < ND; ++i) {
+        const int d = i < 4 ? 4 * j + i : 64 + B * j + (i - 4);
+        const float4 *xp = reinterpret_cast<const float4 *>(xh + d * 8);
+        const float4 a = xp[0], b = xp[1];
+        xr[i][0] = a.x;
+        xr[i][1] = a.y;
+        xr[i][2] = a.z;
+        xr[i][3] = a.w;
+        xr[i][4] = b.x;
+        xr[i][5] = b.y;
+        xr[i][6] = b.z;
+        xr[i][7] = b.w;
+    }
+    // the activations are loop invariants: an empty asm reading them puts
+    // the wait for their loads here, so the loop's waits do not count them
+    // as pending on every pass
+#pragma unroll
+    for (int i = 0; i < ND; ++i)
+#pragma unroll
+        for (int q = 0; q < 8; ++q) asm volatile("" ::"v"(xr[i][q]) : "memory");
+    const int ga = (32 * j) / group, gb = B > 0 ? (512 + 8 * B * j) / group : ga;
     const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t *>(packed + size_t(row_start) * row_bytes), (short)0, rows * row_bytes, 0x00020000);
     const __amdgpu_buffer_rsrc_t rn = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float *>(norms + size_t(row_start) * num_groups), (short)0, rows * num_groups * 4, 0x00020000);
-    const int ntiles = (rows + kNibRows - 1) / kNibRows;
-    const int tile0 = blockIdx.x * tiles_per_block;
-    const int tile1 = tile0 + tiles_per_block < ntiles ? tile0 + tiles_per_block : ntiles;
+    const int ntiles = (rows + kQ4Rows - 1) / kQ4Rows;
     uint32_t cb[D][ND];
-    float nb[D][2];
-    auto load = [&](int tile, uint32_t (&c)[ND], float (&nr)[2]) {
-        int r = tile * kNibRows + rg;
+    float na[D], nb[D];
+    auto load = [&](int it, int k) {
+        int tile = int(blockIdx.x) + it * int(gridDim.x);
+        tile = tile < ntiles ? tile : ntiles - 1;
+        int r = tile * kQ4Rows + rg;
         r = r < rows ? r : rows - 1;
-        // rows < 2^24 here, so 24-bit multiplies give the offsets; codes are
-        // read once: nontemporal (aux bit 1)
-        const int co = int(__umul24(uint32_t(r), uint32_t(row_bytes))) + j * (4 * ND);
-#pragma unroll
-        for (int i = 0; i < ND; ++i) c[i] = __builtin_amdgcn_raw_buffer_load_b32(rc, co + 4 * i, 0, 2);
+        const int ro = int(__umul24(uint32_t(r), uint32_t(row_bytes)));
+        const auto a = __builtin_amdgcn_raw_buffer_load_b128(rc, ro + 16 * j, 0, 2);
+        cb[k][0] = a[0];
+        cb[k][1] = a[1];
+        cb[k][2] = a[2];
+        cb[k][3] = a[3];
+        if constexpr (B == 1) {
+            cb[k][4] = __builtin_amdgcn_raw_buffer_load_b32(rc, ro + 256 + 4 * j, 0, 2);
+        } else if constexpr (B == 2) {
+            const auto b = __builtin_amdgcn_raw_buffer_load_b64(rc, ro + 256 + 8 * j, 0, 2);
+            cb[k][4] = b[0];
+            cb[k][5] = b[1];
+        }
         const int no = int(__umul24(uint32_t(r), uint32_t(num_groups * 4)));
-        nr[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rn, no + 4 * g0, 0, 0));
-        nr[1] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rn, no + 4 * g1, 0, 0));
+        na[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rn, no + 4 * ga, 0, 0));
+        nb[k] = B > 0 ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rn, no + 4 * gb, 0, 0))
+                      : 0.0f;
     };
 #pragma unroll
-    for (int k = 0; k < D; ++k) load(tile0 + k, cb[k], nb[k]);
-    for (int tile = tile0; tile < tile1; tile += D) {
+    for (int k = 0; k < D; ++k) {
+        load(k, k);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    for (int f = t; f < 256 * kQ4Repl; f += kQ4Threads)
+        rep[f] = *reinterpret_cast<const float2 *>(lut + (f / kQ4Repl) * 2);
+    __syncthreads();
+
+    const float2 *lutl = rep + (lane & (kQ4Repl - 1));
+    for (int it0 = 0; it0 < iters; it0 += D) {
 #pragma unroll
         for (int k = 0; k < D; ++k) {
-            const int tt = tile + k;
-            if (tt < tile1) {
-                float total = 0.0f;
+            const int it = it0 + k;
+            float ta = 0.0f, tb = 0.0f;
 #pragma unroll
-                for (int i = 0; i < ND; ++i) {
-                    const uint32_t dw = cb[k][i];
-                    const uint32_t cq[4] = {dw << 7, dw >> 1, dw >> 9, dw >> 17};
-                    float dot = 0.0f;
+            for (int i = 0; i < ND; ++i) {
+                const uint32_t dw = cb[k][i];
+                float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const int kk = 4 * i + q;
-                        const float lo = *reinterpret_cast<const float *>(tb + ((cq[q] & 0x780u) | lb) + (kk << 11));
-                        const float hi =
-                            *reinterpret_cast<const float *>(tb + ((cq[q] & 0x7800u) | lb) + (0x8000 | (kk << 7)));
-                        dot = q == 0 ? lo + hi : dot + lo + hi;
-                    }
-                    total += (second[i] ? nb[k][1] : nb[k][0]) * dot;
+                for (int b = 0; b < 4; ++b) {
+                    const float2 v = lutl[((dw >> (8 * b)) & 0xffu) * kQ4Repl];
+                    a0 += v.x * xr[i][2 * b];
+                    a1 += v.y * xr[i][2 * b + 1];
                 }
-                total = row16_sum(total);
-                const int r = tt * kNibRows + rg;
-                if (j == 0 && r < rows) y[r] = total;
+                if (i < 4)
+                    ta += a0 + a1;
+                else
+                    tb += a0 + a1;
             }
-            load(tt + D, cb[k], nb[k]);
+            float total = na[k] * ta + nb[k] * tb;
+            total = row16_sum(total);
+            stage[(it % kQ4Stage) * kQ4Rows + rg] = total;  // the row's 16 lanes agree
+            __builtin_amdgcn_sched_barrier(0);
+            load(it + D, k);
+            __builtin_amdgcn_sched_barrier(0);
+            if ((it + 1) % kQ4Stage == 0) flush_stage<kQ4Threads>(stage, kQ4Stage, kQ4Rows, it + 1, kQ4Stage, iters, rows, y);
         }
     }
+    const int done = (iters + D - 1) / D * D;
+    if (done % kQ4Stage) flush_stage<kQ4Threads>(stage, kQ4Stage, kQ4Rows, done, done % kQ4Stage, iters, rows, y);
 }
 
 // Reads code k of a row with the bit reader of cq.rs:914-925 (any width).
@@ -880,19 +1071,22 @@ int nd_cq_matvec_rows_prepared(nd_ctx *ctx, const nd_cq *w, const float *xh, siz
     // dwords at 2 bits, 96 at 4 bits); other rows take the per-dword kernel
     const bool stream = w->per_byte != 0 && w->row_bytes % 64 == 0 && row_dwords / 16 >= 1 &&
                         row_dwords / 16 <= 6 && size_t(E) * (row_dwords / 16) <= w->group;
-    if (stream && w->per_byte == 4 && row_dwords <= 16 * 3 && rows < (size_t(1) << 24) &&
-        rows * w->row_bytes < (size_t(1) << 31) && rows * w->num_groups * 4 < (size_t(1) << 31)) {
+    // buffer offsets of the streaming kernels are 32-bit, their row products
+    // 24-bit
+    const bool offsets32 = rows < (size_t(1) << 24) && rows * w->row_bytes < (size_t(1) << 31) &&
+                           rows * w->num_groups * 4 < (size_t(1) << 31);
+    const size_t slots = 2 * size_t(ctx->num_cus > 0 ? ctx->num_cus : 256);
+    const int args_rb = int(w->row_bytes), ng = int(w->num_groups), gr = int(w->group);
+    if (stream && w->per_byte == 4 && row_dwords <= 16 * 3 && offsets32) {
         // 2-bit / ternary, in <= 768: product lookup, two 1024-thread
-        // workgroups per CU
+        // workgroups per CU, the tiles dealt round-robin
         const size_t tiles = (rows + kNibRows - 1) / kNibRows;
-        const size_t slots = 2 * size_t(ctx->num_cus > 0 ? ctx->num_cus : 256);
-        const int tpb = int(tiles > slots ? (tiles + slots - 1) / slots : 1);
-        dim3 grid(unsigned((tiles + tpb - 1) / tpb));
-        const int args_rb = int(w->row_bytes), ng = int(w->num_groups), gr = int(w->group);
-#define ND_CQN(NDV)                                                                              \
-    hipLaunchKernelGGL((cq_gemv_nib_kernel<NDV, 8>), grid, dim3(kNibThreads), 0, ctx->stream,     \
-                       w->packed, w->norms, w->lut, xh, y, int(row_start), int(rows), args_rb, ng, \
-                       gr, tpb)
+        const size_t blocks = tiles < slots ? tiles : slots;
+        const int iters = int((tiles + blocks - 1) / blocks);
+#define ND_CQN(NDV)                                                                             \
+    hipLaunchKernelGGL((cq_gemv_nib_kernel<NDV>), dim3(unsigned(blocks)), dim3(kNibThreads), 0,  \
+                       ctx->stream, w->packed, w->norms, w->lut, xh, y, int(row_start), int(rows), \
+                       args_rb, ng, gr, iters)
         switch (row_dwords / 16) {
         case 1: ND_CQN(1); break;
         case 2: ND_CQN(2); break;
@@ -901,12 +1095,29 @@ int nd_cq_matvec_rows_prepared(nd_ctx *ctx, const nd_cq *w, const float *xh, siz
 #undef ND_CQN
         return nd::check_launch("cq_gemv_nib");
     }
+    if (stream && w->per_byte == 2 && row_dwords / 16 >= 4 && w->group % 32 == 0 && offsets32) {
+        // 4-bit, in 512 to 768: byte lookup, two 512-thread workgroups per
+        // CU, the tiles dealt round-robin
+        const size_t tiles = (rows + kQ4Rows - 1) / kQ4Rows;
+        const size_t blocks = tiles < slots ? tiles : slots;
+        const int iters = int((tiles + blocks - 1) / blocks);
+#define ND_CQ4(NDV)                                                                             \
+    hipLaunchKernelGGL((cq_gemv_q4_kernel<NDV>), dim3(unsigned(blocks)), dim3(kQ4Threads), 0,    \
+                       ctx->stream, w->packed, w->norms, w->lut, xh, y, int(row_start), int(rows), \
+                       args_rb, ng, gr, iters)
+        switch (row_dwords / 16) {
+        case 4: ND_CQ4(4); break;
+        case 5: ND_CQ4(5); break;
+        default: ND_CQ4(6); break;
+        }
+#undef ND_CQ4
+        return nd::check_launch("cq_gemv_q4");
+    }
     if (stream) {
         const size_t tiles = (rows + kRowsPerPass - 1) / kRowsPerPass;
-        const size_t slots = 4 * size_t(ctx->num_cus > 0 ? ctx->num_cus : 256);
-        const int tpb = int(tiles > slots ? (tiles + slots - 1) / slots : 1);
+        const size_t slots4 = 2 * slots;
+        const int tpb = int(tiles > slots4 ? (tiles + slots4 - 1) / slots4 : 1);
         dim3 grid(unsigned((tiles + tpb - 1) / tpb));
-        const int args_rb = int(w->row_bytes), ng = int(w->num_groups), gr = int(w->group);
 #define ND_CQS(P, NDV, REPL)                                                                   \
     hipLaunchKernelGGL((cq_gemv_stream_kernel<P, NDV, REPL, 4>), grid, dim3(kThreads), 0,       \
                        ctx->stream, w->packed, w->norms, w->lut, xh, y, int(row_start), int(rows), \

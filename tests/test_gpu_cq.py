@@ -128,3 +128,31 @@ def test_matvec_tall_multi_tile(ctx, bits):
     assert _close(y, o.matvec(x))
     band = host(g.matvec_rows_prepared(xh, 17, 39000))
     assert _close(band, y[17:17 + 39000])
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_matvec_streams_past_the_stage(ctx, bits):
+    """600,001 rows of in 768: each workgroup of the streaming GEMVs owns more
+    tiles than it stages results for (16 tiles of 64 rows at 2 bits, 32 of 32
+    at 4 bits, over 2 workgroups a CU), so results are written out mid-loop
+    as well as at the end.  Against the oracle, and bit for bit against two
+    half-height launches (fewer tiles a workgroup, no mid-loop write): a
+    row's arithmetic does not depend on how tiles are dealt."""
+    rng = np.random.default_rng(600001 + bits)
+    out, inn = 600001, 768
+    packed = rng.integers(0, 256, size=out * inn * bits // 8, dtype=np.uint8)
+    norms = (np.abs(rng.normal(0.0, 0.02, size=out * (inn // 128))) * np.sqrt(128.0))
+    blob = np.concatenate([packed, norms.astype(np.float16).view(np.uint8)])
+    del packed
+    g = nd.CqWeight(ctx, blob, out, inn, 128, bits, REAL_CB)
+    o = O.CqWeight(blob, out, inn, 128, bits, REAL_CB)
+    del blob
+    x = rng.normal(size=768).astype(np.float32)
+    xh = g.prepare_input(dev(x))[0]
+    y = host(g.matvec_prepared(xh))
+    assert _close(y, o.matvec(x))
+    half = out // 2
+    lo = host(g.matvec_rows_prepared(xh, 0, half))
+    hi = host(g.matvec_rows_prepared(xh, half, out - half))
+    assert np.array_equal(np.concatenate([lo, hi]).view(np.uint32), y.view(np.uint32))
+    g.close()
