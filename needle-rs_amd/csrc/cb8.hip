@@ -70,7 +70,7 @@ __global__ __launch_bounds__(kThreads, 4) void cb8_gemv_kernel(
 {
     constexpr int K = 256 * M;
     constexpr int kPasses = 8;  // 16 rows per wave, 2 per pass
-    constexpr int kFirst = kPasses / 2;
+    constexpr int kFirst = kPasses;
     __shared__ float4 rep4[256 * 32 / 4];  // 32 KB
 
     const size_t prob = blockIdx.y;
@@ -232,11 +232,21 @@ __global__ __launch_bounds__(kThreads) void cb8_gemv_generic_kernel(
 typedef __attribute__((__vector_size__(8 * sizeof(short)))) short bf16x8_t;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float floatx4_t;
 
+// fp32 to bf16, round to nearest even: gfx950's v_cvt_pk_bf16_f32 (two
+// values an instruction).  It equals the integer form (u + 0x7fff + lsb) >> 16
+// on every non-NaN input, checked over all 2^32 patterns on the device; NaNs
+// stay NaN.
+typedef __bf16 bf16x2_hw_t __attribute__((ext_vector_type(2)));
+
+__device__ inline uint32_t f32x2_to_bf16x2_rne(float lo, float hi)
+{
+    const bf16x2_hw_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
 __device__ inline unsigned short f32_to_bf16_rne(float f)
 {
-    uint32_t u = __float_as_uint(f);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return static_cast<unsigned short>(u >> 16);
+    return static_cast<unsigned short>(f32x2_to_bf16x2_rne(f, 0.0f));
 }
 
 constexpr int kGM = 64, kGN = 64, kGK = 128;
@@ -249,10 +259,8 @@ constexpr int kXRuns = 4;
 
 __device__ inline uint4 pack_bf16x8(float4 a, float4 b)
 {
-    return make_uint4(f32_to_bf16_rne(a.x) | (uint32_t(f32_to_bf16_rne(a.y)) << 16),
-                      f32_to_bf16_rne(a.z) | (uint32_t(f32_to_bf16_rne(a.w)) << 16),
-                      f32_to_bf16_rne(b.x) | (uint32_t(f32_to_bf16_rne(b.y)) << 16),
-                      f32_to_bf16_rne(b.z) | (uint32_t(f32_to_bf16_rne(b.w)) << 16));
+    return make_uint4(f32x2_to_bf16x2_rne(a.x, a.y), f32x2_to_bf16x2_rne(a.z, a.w),
+                      f32x2_to_bf16x2_rne(b.x, b.y), f32x2_to_bf16x2_rne(b.z, b.w));
 }
 
 __global__ __launch_bounds__(256) void x_to_bf16_kernel(const float *__restrict__ X, size_t xs,
