@@ -164,3 +164,37 @@ def test_gemm_batched_equals_single(ctx, R, M, N, K):
         assert np.array_equal(got[i], one)
         want = O.cb8_gemm(X[i], W[i], CB[i])
         assert np.max(np.abs(got[i] - want)) <= 2e-2 * np.max(np.abs(want))
+
+
+def _rne_bf16(a):
+    """fp32 -> bf16 (as fp32), round to nearest even, by the integer form."""
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16 << 16
+    return u.astype(np.uint32).view(np.float32)
+
+
+@pytest.mark.parametrize("count,m,out,inn", [(1, 64, 128, 128), (1, 128, 128, 64), (256, 256, 256, 64)])
+def test_gemm_bf16_rounding_is_round_to_nearest_even(ctx, count, m, out, inn):
+    """The GEMMs round X and the codebook to bf16 by round-to-nearest-even.
+    X in [1, 2) with its low 16 bits drawn from the tie and near-tie
+    patterns, codebook entries +-1 and +-1/2 (exact in bf16), K <= 128: every
+    product and partial sum is exact in fp32, so the output is the exact sum
+    of rne(x) * cb[code] whatever the accumulation order, and a rounding
+    other than RNE (ties away, truncation) changes it.  The shapes take the
+    M <= 64, 128x128 and 256x256 kernels."""
+    rng = np.random.default_rng(7 + m)
+    hi = rng.integers(0x3F80, 0x4000, size=(count, m, inn), dtype=np.uint32)
+    lo = rng.choice(np.array([0x8000, 0x7FFF, 0x8001, 0x0000, 0xFFFF], np.uint32), size=(count, m, inn))
+    X = ((hi << 16) | lo).view(np.float32)
+    W = rng.integers(0, 256, size=(count, out, inn), dtype=np.uint8)
+    CB = rng.choice(np.array([1.0, -1.0, 0.5, -0.5], np.float32), size=(count, out // 64, 256))
+    want = np.empty((count, m, out), np.float32)
+    for i in range(count):
+        wv = CB[i][np.arange(out)[:, None] // 64, W[i]].astype(np.float64)  # [out][in]
+        want[i] = (_rne_bf16(X[i]).astype(np.float64) @ wv.T).astype(np.float32)
+    # the ties decide: truncation or ties-away would differ somewhere
+    assert not np.array_equal(_rne_bf16(X), (X.view(np.uint32) >> 16 << 16).view(np.float32))
+    Y = torch.empty(count, m, out, device="cuda")
+    nd.cb8_gemm_batched(ctx, dev(X), dev(W), dev(CB), Y)
+    got = host(Y)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
