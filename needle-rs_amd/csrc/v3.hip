@@ -305,9 +305,13 @@ __global__ __launch_bounds__(256) void k_engram_fetch(EngramFetch a)
 // rows, the gated lane sum, the Engram gate and ZCRMSNorm, prepared for the
 // q/k/v/gate projections.  One workgroup per session.
 constexpr int kMaxLanesD = 4096;  // mhc_lanes * d_model
-constexpr int kFoldC = 12;        // terms a thread of the parallel rms fold (4 lanes x 768)
+constexpr int kFoldC256 = 12;     // terms a thread of the parallel rms fold at 256 threads (4 lanes x 768)
 constexpr int kMaxPhiPairs = 768; // (phi rows of a layer) * (phi input groups)
-constexpr int kPhiPerThread = 3;  // phi (row, group) pairs a thread holds codes for
+// k_layer_in's workgroup: one per session, so at most a few dozen run at
+// once; 8 waves give its parallel phases (the lane update, the phi dots,
+// the prepares) two waves per SIMD and half the work per thread, the
+// sequential chains being unchanged (16 waves spilled registers)
+constexpr int kLayerInThreads = 512;
 constexpr int kPadGroup = 132;    // a 128-group's stride in LDS, padded
 
 struct LayerIn {
@@ -339,14 +343,18 @@ struct LayerIn {
     Prep ph;
 };
 
-template <int PP>
-__global__ __launch_bounds__(kT) void k_layer_in(LayerIn a)
+template <int PP, int NTH>
+__global__ __launch_bounds__(NTH) void k_layer_in(LayerIn a)
 {
-    constexpr int kCh = 1024 / kT;  // model-dim channels per thread
+    constexpr int kCh = 1024 / NTH;  // model-dim channels per thread
+    // phi (row, group) pairs a thread holds codes for; terms a thread of the
+    // parallel rms fold
+    constexpr int kPhiPerThread = (kMaxPhiPairs + NTH - 1) / NTH;
+    constexpr int kFoldC = NTH >= 512 ? kMaxLanesD / NTH : kFoldC256;
     __shared__ __align__(16) float ln[kMaxLanesD], nb[kMaxLanesD];
     __shared__ __align__(16) float us[1024], bxs[1024], pa[1024], pb[1024], pc[1024];
     __shared__ float gs[kMaxPhiPairs], pn[kMaxPhiPairs], lvl[48], hp[16], gpp[16], grr[256], tot[4];
-    __shared__ NdFoldLds<kT> fl;
+    __shared__ NdFoldLds<NTH> fl;
     const size_t b = blockIdx.x;
     const int tid = threadIdx.x, n = a.n, d = a.d, nd = n * d;
     // phi rows: phi_pre's n, then (gates) phi_post's n and phi_res's n * n
@@ -359,7 +367,7 @@ __global__ __launch_bounds__(kT) void k_layer_in(LayerIn a)
     float old[kCh][kUpLanes], yv[kCh];
 #pragma unroll
     for (int k = 0; k < kCh; ++k) {
-        const int c = tid + k * kT;
+        const int c = tid + k * NTH;
         const bool on = up_regs && c < d;
         yv[k] = on ? a.y[b * d + c] : 0.0f;
 #pragma unroll
@@ -373,7 +381,7 @@ __global__ __launch_bounds__(kT) void k_layer_in(LayerIn a)
             // mhc.rs:140-151 from the preloaded values
 #pragma unroll
             for (int k = 0; k < kCh; ++k) {
-                const int c = tid + k * kT;
+                const int c = tid + k * NTH;
                 if (c >= d) continue;
 #pragma unroll
                 for (int i = 0; i < kUpLanes; ++i) {
@@ -391,11 +399,11 @@ __global__ __launch_bounds__(kT) void k_layer_in(LayerIn a)
             scatter_up(lg, ln, gpp, grr, a.y + b * d, n, d);
         }
     } else {
-        for (int e = tid; e < nd; e += kT) ln[e] = lg[e];
+        for (int e = tid; e < nd; e += NTH) ln[e] = lg[e];
     }
     __syncthreads();
     // rms_unit (kernels.rs:33-41): products, then one chain
-    for (int e = tid; e < nd; e += kT) nb[e] = ln[e] * ln[e];
+    for (int e = tid; e < nd; e += NTH) nb[e] = ln[e] * ln[e];
     __syncthreads();
     // operands needed after the chain, issued before lane 0 of wave 0 starts
     // folding: this thread's phi_pre group codes and norm, its channels'
@@ -422,7 +430,7 @@ __global__ __launch_bounds__(kT) void k_layer_in(LayerIn a)
     int wsel[kPhiPerThread];
 #pragma unroll
     for (int k = 0; k < kPhiPerThread; ++k) {
-        const int t = tid + k * kT;
+        const int t = tid + k * NTH;
         const bool has = t < pairs;
         const int r = has ? t / G : 0, g = has ? t - (t / G) * G : 0;
         const float *nr;
@@ -433,7 +441,7 @@ __global__ __launch_bounds__(kT) void k_layer_in(LayerIn a)
     float nin[kCh], ekv[kCh], evv[kCh];
 #pragma unroll
     for (int k = 0; k < kCh; ++k) {
-        const int c = tid + k * kT;
+        const int c = tid + k * NTH;
         nin[k] = c < d ? a.norm_in[c] : 0.0f;
         ekv[k] = ek && c < d ? ek[c] : 0.0f;
         evv[k] = ek && c < d ? a.ev[b * d + c] : 0.0f;
@@ -448,15 +456,15 @@ __global__ __launch_bounds__(kT) void k_layer_in(LayerIn a)
     }
     // the rms sum of squares: the workgroup folds it in parallel with the
     // chain's bits (nd_fold.h) when it fits kFoldC terms a thread
-    if (nd >= kNdFoldMinN && nd <= kT * kFoldC) {
-        const float f = nd_fold_nonneg<kT, kFoldC>(nb, nd, fl);
+    if (nd >= kNdFoldMinN && nd <= NTH * kFoldC) {
+        const float f = nd_fold_nonneg<NTH, kFoldC>(nb, nd, fl);
         if (tid == 0) tot[0] = f;
     } else if (tid == 0) {
         tot[0] = chain_sum(nb, nd);
     }
 #pragma unroll
     for (int k = 0; k < kPhiPerThread; ++k)
-        if (tid + k * kT < pairs) pn[tid + k * kT] = pnv[k];
+        if (tid + k * NTH < pairs) pn[tid + k * NTH] = pnv[k];
     if (tid < 48) lvl[tid] = lvv;
     __syncthreads();
     {
@@ -469,18 +477,18 @@ __global__ __launch_bounds__(kT) void k_layer_in(LayerIn a)
         float *xo = a.nxh + b * a.pnx.in_padded;
         // three groups a wave at a time, their shuffles overlapped
         constexpr int NG = 3;
-        for (int g0 = wave; g0 < G; g0 += NG * (kT / 64)) {
+        for (int g0 = wave; g0 < G; g0 += NG * (NTH / 64)) {
             float x0[NG], x1[NG];
 #pragma unroll
             for (int q = 0; q < NG; ++q) {
-                const int e0 = (g0 + q * (kT / 64)) * 128 + lane, e1 = e0 + 64;
+                const int e0 = (g0 + q * (NTH / 64)) * 128 + lane, e1 = e0 + 64;
                 x0[q] = e0 < nd ? ln[e0] * inv : 0.0f;
                 x1[q] = e1 < nd ? ln[e1] * inv : 0.0f;
             }
             fwht128_wave_n<NG>(x0, x1, a.pnx.inv);
 #pragma unroll
             for (int q = 0; q < NG; ++q) {
-                const int g = g0 + q * (kT / 64);
+                const int g = g0 + q * (NTH / 64);
                 if (g >= G) break;
                 xo[g * 128 + lane] = x0[q];
                 xo[g * 128 + 64 + lane] = x1[q];
@@ -493,7 +501,7 @@ __global__ __launch_bounds__(kT) void k_layer_in(LayerIn a)
     // this layer's phi rows (matvec_rows_prepared, reference order)
 #pragma unroll
     for (int k = 0; k < kPhiPerThread; ++k) {
-        const int t = tid + k * kT;
+        const int t = tid + k * NTH;
         if (t < pairs) gs[t] = cq_group_dot128<PP>(codes[k], lvl + 16 * wsel[k], nb + (t % G) * kPadGroup);
     }
     __syncthreads();
@@ -511,7 +519,7 @@ __global__ __launch_bounds__(kT) void k_layer_in(LayerIn a)
     // gated lane sum, Engram gate (engram.rs:111-132), ZCRMSNorm (norm.rs:23-30)
 #pragma unroll
     for (int k = 0; k < kCh; ++k) {
-        const int c = tid + k * kT;
+        const int c = tid + k * NTH;
         if (c >= d) continue;
         float acc = 0.0f;
         for (int l = 0; l < n; ++l) acc += hp[l] * ln[l * d + c];
@@ -533,14 +541,14 @@ __global__ __launch_bounds__(kT) void k_layer_in(LayerIn a)
         const float alpha = sigmoidf_(tot[3] * ux * uk / sqrtf(float(d)));
 #pragma unroll
         for (int k = 0; k < kCh; ++k) {
-            const int c = tid + k * kT;
+            const int c = tid + k * NTH;
             if (c >= d) continue;
             const float v = us[c] + alpha * evv[k];
             bxs[c] = v;
             pa[c] = v * v;
         }
     } else {
-        for (int c = tid; c < d; c += kT) {
+        for (int c = tid; c < d; c += NTH) {
             bxs[c] = us[c];
             pa[c] = us[c] * us[c];
         }
@@ -551,13 +559,13 @@ __global__ __launch_bounds__(kT) void k_layer_in(LayerIn a)
     const float inv = 1.0f / sqrtf(tot[0] / float(d) + 1e-6f);
 #pragma unroll
     for (int k = 0; k < kCh; ++k) {
-        const int c = tid + k * kT;
+        const int c = tid + k * NTH;
         if (c < d) {
             a.bx[b * d + c] = bxs[c];
             pa[c] = (1.0f + nin[k]) * bxs[c] * inv;
         }
     }
-    for (int c = d + tid; c < a.ph.in_padded; c += kT) pa[c] = 0.0f;
+    for (int c = d + tid; c < a.ph.in_padded; c += NTH) pa[c] = 0.0f;
     __syncthreads();
     prepare_lds(pa, a.hh + b * a.ph.in_padded, a.ph.in_padded, a.ph.group, a.ph.inv, false);
 }
@@ -2172,7 +2180,8 @@ int StepRun::begin(const int32_t *tokens)
                   fpo->group == 128 && fre->group == 128 &&
                   fpo->in_padded == phi->in_padded && fre->in_padded == phi->in_padded &&
                   size_t(2 * nl + nl * nl) * phi->num_groups <= size_t(kMaxPhiPairs) &&
-                  size_t(2 * nl + nl * nl) * phi->num_groups <= size_t(kPhiPerThread * kT) &&
+                  size_t(2 * nl + nl * nl) * phi->num_groups <=
+                      size_t((kMaxPhiPairs + kLayerInThreads - 1) / kLayerInThreads * kLayerInThreads) &&
                   nl * nl <= 64 && fpo->row_bytes % 16 == 0 && fre->row_bytes % 16 == 0 &&
                   C == 1;
     ev_conv = C == 1 ? b->ev : b->evc;
@@ -2308,9 +2317,9 @@ int StepRun::enqueue(int phase, bool argmax)
                    site >= 0 ? ev_conv + size_t(site) * Rcap * d : nullptr, l.norm_in, b->u, b->bx,
                    b->hh, m->pre_h};
         if (phi->per_byte == 2)
-            hipLaunchKernelGGL(k_layer_in<2>, dim3(B), dim3(kT), 0, st, in);
+            hipLaunchKernelGGL((k_layer_in<2, kLayerInThreads>), dim3(B), dim3(kLayerInThreads), 0, st, in);
         else
-            hipLaunchKernelGGL(k_layer_in<4>, dim3(B), dim3(kT), 0, st, in);
+            hipLaunchKernelGGL((k_layer_in<4, kLayerInThreads>), dim3(B), dim3(kLayerInThreads), 0, st, in);
         LCHK("k_layer_in");
         if (!gates_in) {
             // side stream: this layer's scatter-up gates from the prepared lanes

@@ -541,11 +541,12 @@ int main(int argc, char **argv)
     const int cases = argc > 1 ? std::atoi(argv[1]) : 2000;
     if (argc > 2) g_state = std::strtoull(argv[2], nullptr, 0);
     static const int sizes[] = {1, 2, 3, 7, 64, 65, 255, 256, 257, 768, 1000, 1024, 2048, 3072, 4095};
-    static const int threads[] = {256, 1024, 256, 64, 128};
-    // (threads, terms a thread): the device's instantiations (256 x 12 for
-    // the rms norms, 256 x 16 for the softmax sums and row folds), a
-    // 16-wave form, the single-wave form and a two-wave form
-    static const int cmax_of[] = {16, 4, 12, 32, 16};
+    static const int threads[] = {256, 512, 256, 1024, 64, 128};
+    // (threads, terms a thread): the device's instantiations (256 x 16 for
+    // the softmax sums and row folds, 512 x 8 for the layer input's rms
+    // norm, 256 x 12 for the other rms norms), a 16-wave form, the
+    // single-wave form and a two-wave form
+    static const int cmax_of[] = {16, 8, 12, 4, 32, 16};
     constexpr int kForms = sizeof(threads) / sizeof(threads[0]);
     int failures = 0;
     long long emulated = 0, cross_wave = 0;
