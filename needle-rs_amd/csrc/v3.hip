@@ -865,14 +865,17 @@ __global__ void k_tails(const float *__restrict__ rows, float *__restrict__ tail
 }
 
 constexpr int kMaxQkDims = 2048;  // (num_heads + num_kv_heads) * qk_head_dim
+// k_qkv_kv's workgroup, one per row: its conv, rope and quantise phases are
+// element-wise over ~800 channels
+constexpr int kQkvThreads = 512;
 constexpr int kMaxVDims = 1024;   // num_kv_heads * v_head_dim
 
 // KF: the session's cache is f32 (write_kv with KvPrecision::F32,
 // cache.rs:359-362): k and v are stored as they are.
 // With mhc.on (single positions), a second workgroup per row runs phase 0
 // of the layer's scatter-up gates in the same launch.
-template <bool CHUNK, bool KF>
-__global__ __launch_bounds__(kT) void k_qkv_kv(QkvKv a, MhcIn mhc)
+template <bool CHUNK, bool KF, int NTH>
+__global__ __launch_bounds__(NTH) void k_qkv_kv(QkvKv a, MhcIn mhc)
 {
     __shared__ __align__(16) float qk[kMaxQkDims], sq[kMaxQkDims], vl[kMaxVDims];
     __shared__ float rms[64];
@@ -885,7 +888,7 @@ __global__ __launch_bounds__(kT) void k_qkv_kv(QkvKv a, MhcIn mhc)
     const int r = CHUNK ? int(b % a.C) : 0;
     const int p = a.pos[b], T = a.taps, hd = a.hd, half = hd / 2;
     const int nq = a.qd + a.kd, heads = a.H + a.KVH;
-    for (int c = threadIdx.x; c < nq + a.vd; c += kT) {
+    for (int c = threadIdx.x; c < nq + a.vd; c += NTH) {
         if (c < a.qd) {
             float v = a.q[b * a.qd + c];
             if (T > 0) {
@@ -922,7 +925,7 @@ __global__ __launch_bounds__(kT) void k_qkv_kv(QkvKv a, MhcIn mhc)
         rms[threadIdx.x] = sqrtf(chain_sum(sq + threadIdx.x * hd, hd) / float(hd) + 1e-6f);
     __syncthreads();
     const float *cs = a.rope + size_t(p) * 2 * half, *sn = cs + half;
-    for (int e = threadIdx.x; e < heads * half; e += kT) {
+    for (int e = threadIdx.x; e < heads * half; e += NTH) {
         const int hh = e / half, i = e - hh * half;
         const float *sc = hh < a.H ? a.q_norm : a.k_norm;
         const float *x = qk + hh * hd;
@@ -946,7 +949,7 @@ __global__ __launch_bounds__(kT) void k_qkv_kv(QkvKv a, MhcIn mhc)
     uint8_t *blk = a.kv + sess * a.kv_stride;
     const int slot = p % a.cap;
     if constexpr (KF) {
-        for (int vec = wave; vec < 2 * a.KVH; vec += kT / 64) {
+        for (int vec = wave; vec < 2 * a.KVH; vec += NTH / 64) {
             const bool isv = vec >= a.KVH;
             const int h = isv ? vec - a.KVH : vec;
             const int dim = isv ? a.VD : hd;
@@ -956,7 +959,7 @@ __global__ __launch_bounds__(kT) void k_qkv_kv(QkvKv a, MhcIn mhc)
         }
         return;
     }
-    for (int vec = wave; vec < 2 * a.KVH; vec += kT / 64) {
+    for (int vec = wave; vec < 2 * a.KVH; vec += NTH / 64) {
         const bool isv = vec >= a.KVH;
         const int h = isv ? vec - a.KVH : vec;
         const int dim = isv ? a.VD : hd;
@@ -2376,16 +2379,16 @@ int StepRun::enqueue(int phase, bool argmax)
             const dim3 qg(unsigned(B), gy);
             if (C == 1) {
                 if (kf)
-                    hipLaunchKernelGGL((k_qkv_kv<false, true>), qg, dim3(kT), 0, st, qk, mi);
+                    hipLaunchKernelGGL((k_qkv_kv<false, true, kQkvThreads>), qg, dim3(kQkvThreads), 0, st, qk, mi);
                 else
-                    hipLaunchKernelGGL((k_qkv_kv<false, false>), qg, dim3(kT), 0, st, qk, mi);
+                    hipLaunchKernelGGL((k_qkv_kv<false, false, kQkvThreads>), qg, dim3(kQkvThreads), 0, st, qk, mi);
                 LCHK("k_qkv_kv");
             } else {
                 // prefill passes run the gates on the side stream
                 if (kf)
-                    hipLaunchKernelGGL((k_qkv_kv<true, true>), dim3(B), dim3(kT), 0, st, qk, mi);
+                    hipLaunchKernelGGL((k_qkv_kv<true, true, kQkvThreads>), dim3(B), dim3(kQkvThreads), 0, st, qk, mi);
                 else
-                    hipLaunchKernelGGL((k_qkv_kv<true, false>), dim3(B), dim3(kT), 0, st, qk, mi);
+                    hipLaunchKernelGGL((k_qkv_kv<true, false, kQkvThreads>), dim3(B), dim3(kQkvThreads), 0, st, qk, mi);
                 LCHK("k_qkv_kv");
                 const int tt = c.qkv_conv_taps - 1;
                 if (tt > 0) {
