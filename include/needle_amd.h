@@ -124,7 +124,11 @@ int nd_cq_prepare_input(nd_ctx *ctx, const nd_cq *w, const float *x,
                         size_t batch, float *xh);
 
 /* y[r] = W[row_start + r] . xh, r < rows.  Replaces
- * CqWeight::matvec_rows_prepared (cq.rs:301-307 -> 721-757, 838-873). */
+ * CqWeight::matvec_rows_prepared (cq.rs:301-307 -> 721-757, 838-873).
+ * Within the reference's tolerance (1e-4 * max(|want|, 1)); 2-bit and
+ * ternary weights in groups of 128 with at least 655,360 rows (the
+ * environment variable NEEDLE_AMD_CQ_FP4_MIN_ROWS moves the bound) run on
+ * the fp4 matrix cores, the rest on lookup-table kernels. */
 int nd_cq_matvec_rows_prepared(nd_ctx *ctx, const nd_cq *w, const float *xh,
                                size_t row_start, size_t rows, float *y);
 

@@ -24,6 +24,7 @@
 #include "nd_cq_internal.h"
 
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <vector>
@@ -477,8 +478,11 @@ __global__ __launch_bounds__(kNibThreads, 2) void cq_gemv_nib_kernel(
 
 // Batch-1 GEMV on 4-bit rows of 16 * ND code dwords, ND = 4..6 (in 512 to
 // 768), by byte lookup: a byte's two levels come from a 256-entry table of
-// float2 in LDS (REPL replicas, lane l reading replica l % REPL) and
-// multiply the lane's activations held in registers.  Lane j of a 16-lane
+// float2 in LDS (REPL = 32 replicas, lane l reading replica l % 32) and
+// multiply the lane's activations held in registers.  An entry's replicas
+// fill 256 bytes, so a lookup address is the code byte in bits 8-15 over
+// the lane's replica offset in bits 3-7: one v_perm_b32 of the code dword
+// and that offset, no shift and mask.  Lane j of a 16-lane
 // row group holds code bytes [16 j, 16 j + 16) (elements 32 j .. 32 j + 31,
 // one 128-bit load) and, for ND > 4, bytes [256 + 4 B j, 256 + 4 B (j + 1))
 // with B = ND - 4 (elements 512 + 8 B j ..): every load of a row group
@@ -487,7 +491,8 @@ __global__ __launch_bounds__(kNibThreads, 2) void cq_gemv_nib_kernel(
 // 128-byte line of results each), two a CU, streaming as above.
 constexpr int kQ4Threads = 512;
 constexpr int kQ4Rows = kQ4Threads / kLanesPerRow;  // 32 rows per tile
-constexpr int kQ4Repl = 16;
+constexpr int kQ4Repl = 32;                        // 256 B an entry
+static_assert(kQ4Repl * 8 == 256, "a lookup address puts the code byte at bit 8");
 constexpr int kQ4Depth = 4;
 constexpr int kQ4Stage = 32;                        // staged tiles (4 KiB)
 
@@ -499,7 +504,7 @@ __global__ __launch_bounds__(kQ4Threads) void cq_gemv_q4_kernel(
 {
     constexpr int B = ND - 4;  // dwords of the second part
     constexpr int D = kQ4Depth;
-    __shared__ float2 rep[256 * kQ4Repl];  // 32 KiB
+    __shared__ float2 rep[256 * kQ4Repl];  // 64 KiB
     __shared__ float stage[kQ4Stage * kQ4Rows];
     const int t = threadIdx.x, lane = t & 63, j = t & (kLanesPerRow - 1), rg = t / kLanesPerRow;
     // the lane's activations: part A elements 32 j + 8 i + e (i < 4), part B
@@ -566,7 +571,9 @@ __global__ __launch_bounds__(kQ4Threads) void cq_gemv_q4_kernel(
         rep[f] = *reinterpret_cast<const float2 *>(lut + (f / kQ4Repl) * 2);
     __syncthreads();
 
-    const float2 *lutl = rep + (lane & (kQ4Repl - 1));
+    // byte 0 of a lookup address: the lane's replica (8 bytes each)
+    const uint32_t lb = uint32_t(lane & (kQ4Repl - 1)) * uint32_t(sizeof(float2));
+    const char *repb = reinterpret_cast<const char *>(rep);
     for (int it0 = 0; it0 < iters; it0 += D) {
 #pragma unroll
         for (int k = 0; k < D; ++k) {
@@ -578,7 +585,10 @@ __global__ __launch_bounds__(kQ4Threads) void cq_gemv_q4_kernel(
                 float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
                 for (int b = 0; b < 4; ++b) {
-                    const float2 v = lutl[((dw >> (8 * b)) & 0xffu) * kQ4Repl];
+                    // bytes of (dw, lb): selector 4 + b is byte b of dw, 0 is
+                    // byte 0 of lb, 0x0c a zero byte
+                    const uint32_t at = __builtin_amdgcn_perm(dw, lb, 0x0c0c0000u | ((4u + b) << 8));
+                    const float2 v = *reinterpret_cast<const float2 *>(repb + at);
                     a0 += v.x * xr[i][2 * b];
                     a1 += v.y * xr[i][2 * b + 1];
                 }
@@ -598,6 +608,339 @@ __global__ __launch_bounds__(kQ4Threads) void cq_gemv_q4_kernel(
     }
     const int done = (iters + D - 1) / D * D;
     if (done % kQ4Stage) flush_stage<kQ4Threads>(stage, kQ4Stage, kQ4Rows, done, done % kQ4Stage, iters, rows, y);
+}
+
+// Batch-1 GEMV on 2-bit (and ternary) rows of NG groups of 128 (in <= 768)
+// on the matrix cores: v_mfma_scale_f32_16x16x128_f8f6f4 with both
+// operands fp4 (e2m1: a sign, two exponent bits, one mantissa bit), for the
+// tolerance arithmetic of the row dot.  The lookup kernels above spend ~18
+// VALU instructions a row per CU; this one ~7, so it stays bound by HBM
+// where the others are held back by the clock.
+//
+// Codes as fp4 planes.  A 2-bit code c = 2 b1 + b0 placed at bits 0-1, 1-2
+// or 2-3 of a zero nibble reads, as e2m1, P1(c) = {0, 0.5, 1, 1.5},
+// P2(c) = {0, 1, 2, 4} or P3(c) = {0, 2, -0, -2}.  With the constant these
+// span every function of c, so lvl(c) = L0 + beta P1(c) + gamma P2(c) +
+// delta P3(c) for any four levels.  `dw & 0x33333333` leaves the even codes
+// of a dword at nibble bits 0-1 and `dw & 0xcccccccc` the odd ones at bits
+// 2-3; one shift each gives the other planes, so 16 codes become three
+// planes of 16 nibbles in six VALU operations.
+//
+// The activation as fp4 pieces.  Over each 32-element block, coef_p * x is
+// split into kMf2Pieces pieces, each with its own power-of-two (E8M0)
+// scale: piece i is the residual the earlier pieces left, rounded to e2m1
+// at scale 2^(s0 - drop(i)), s0 mapping the block's largest magnitude into
+// [-6, 6]; from the third piece on each takes three more bits, and ten
+// leave under 2^-28 of that magnitude.  Each workgroup builds them as MFMA
+// A fragments in LDS while its first tiles load (the hardware's scaled
+// f32 -> fp4 conversion rounds to nearest even and its inverse is exact):
+// row i of A is piece i, the 128 K of one MFMA the 128 elements of one
+// group, in the plane order below.
+//
+// Per 16 rows, one MFMA per (group, plane): D[i][c] = sum_k A[i][k] B[k][c]
+// with column c of B the plane of weight row c; a group's three planes
+// accumulate into one D, whose 16 piece rows add up to
+// sum_k (lvl(c_k) - L0) x_k.  Lane c + 16 q holds weight row c: as B its
+// slice q of each group (codes 32 q .. 32 q + 31, two dwords), and D rows
+// 4 q .. 4 q + 3, which it sums and scales by the group's norm; slice 0
+// adds L0 X_g (X_g the group's activation sum), and two lane exchanges
+// finish the row.  In nibble order B's dword 0 holds codes 32 q + 2 n
+// (n = 0..7), dword 1 codes 32 q + 2 n + 1, dwords 2 and 3 the same from
+// code 32 q + 16 on; the A fragments follow that order.  Products of fp4
+// values are exact; the matrix core adds them in fp32.
+//
+// Four waves a workgroup, 16 rows each (64-row tiles dealt round-robin),
+// two workgroups a CU, kMf2Depth tiles of loads in flight, results staged
+// in LDS and written out as in the lookup kernels.  A wave loads its 16
+// rows as one contiguous run and regroups them into MFMA slices through
+// LDS: loading the slices directly (32 bytes of 16 rows per load) ran at
+// 60% of the contiguous rate.  An activation holding
+// a non-finite value (which fp4 cannot carry) takes a plain per-lane loop
+// over the same rows instead.
+constexpr int kMf2Pieces = 10;
+constexpr int kMf2Threads = 256;
+constexpr int kMf2Rows = 64;    // rows per tile
+constexpr int kMf2Depth = 3;    // tiles in flight
+constexpr int kMf2Stage = 16;   // staged tiles (4 KiB)
+constexpr int kMf2MaxGroups = 6;
+// Below this many rows the lookup kernel is as fast or faster (the rows
+// sit in the MALL; measured crossover ~700k rows of in 768).  The
+// environment variable NEEDLE_AMD_CQ_FP4_MIN_ROWS overrides it.
+constexpr size_t kMf2MinRows = 655360;
+
+typedef int nd_v8i __attribute__((ext_vector_type(8)));
+typedef float nd_v4f __attribute__((ext_vector_type(4)));
+
+// Exponent of piece i's scale below the block's first: 0, 2, 4, then 3 more
+// a piece.  With the block's largest |v| at most 6 * 2^s0, piece 0 leaves at
+// most 2^s0, piece 1 at most 2^(s1 - 1), and from there a residual of at
+// most 2 * 2^si leaves at most 2^(si - 2): three bits a piece.
+__host__ __device__ constexpr int mf2_piece_drop(int i)
+{
+    return i == 0 ? 0 : (i == 1 ? 2 : 4 + 3 * (i - 2));
+}
+
+// The plane coefficients of four crumb levels L0..L3: lvl(c) - L0 =
+// beta P1(c) + gamma P2(c) + delta P3(c) at c = 1, 2, 3.
+struct Mf2Coef {
+    float beta, gamma, delta, l0;
+};
+
+inline Mf2Coef mf2_coef(const float *lv)
+{
+    const double L0 = lv[0], d1 = double(lv[1]) - L0, d2 = double(lv[2]) - L0, d3 = double(lv[3]) - L0;
+    const double gam = d1 + d3 - 2.0 * d2, bet = d2 - 2.0 * gam, del = (d1 - 0.5 * bet - gam) * 0.5;
+    return {float(bet), float(gam), float(del), lv[0]};
+}
+
+// Maximum over a 16-lane DPP row (every lane receives it).
+__device__ inline float row16_max(float v)
+{
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xf, 0xf, true)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x124, 0xf, 0xf, true)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x122, 0xf, 0xf, true)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x121, 0xf, 0xf, true)));
+    return v;
+}
+
+// N consecutive floats from byte offset `off` of the buffer, in loads of up
+// to three dwords.  (The elements go through __uint_as_float by value:
+// hipcc compiles __builtin_bit_cast of a vector element as a read of
+// element 0.)
+template <int N>
+__device__ inline void load_floats(__amdgpu_buffer_rsrc_t rc, int off, float *v)
+{
+    if constexpr (N >= 3) {
+        const auto a = __builtin_amdgcn_raw_buffer_load_b96(rc, off, 0, 0);
+        v[0] = __uint_as_float(a[0]);
+        v[1] = __uint_as_float(a[1]);
+        v[2] = __uint_as_float(a[2]);
+        if constexpr (N > 3) load_floats<N - 3>(rc, off + 12, v + 3);
+    } else if constexpr (N == 2) {
+        const auto a = __builtin_amdgcn_raw_buffer_load_b64(rc, off, 0, 0);
+        v[0] = __uint_as_float(a[0]);
+        v[1] = __uint_as_float(a[1]);
+    } else if constexpr (N == 1) {
+        v[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rc, off, 0, 0));
+    }
+}
+
+template <int NG>
+__global__ __launch_bounds__(kMf2Threads, 2) void cq_gemv_mf2_kernel(
+    const uint8_t *__restrict__ packed, const float *__restrict__ norms, const float *__restrict__ lut,
+    const float *__restrict__ xh, float *__restrict__ y, Mf2Coef cf, int row_start, int rows,
+    int iters)
+{
+    constexpr int D = kMf2Depth;
+    constexpr int RB = 32 * NG;  // row bytes
+    constexpr int NF = 3 * NG;   // A fragments: (group, plane)
+    constexpr int NT = 4 * NF;   // piece tasks: (fragment, 32-element block)
+    constexpr int TPT = (NT + 15) / 16;  // tasks per 16-lane group
+    __shared__ float stage[kMf2Stage * kMf2Rows];
+    __shared__ uint2 xch[4 * 16 * (RB + 8) / 8];  // per wave: 16 rows, padded
+    __shared__ uint4 fr[NF][64];                  // A fragments, lane-major
+    __shared__ int s0s[NF][4];                    // each block's first scale exponent
+    __shared__ float xpart[NG][4];                // each block's activation sum
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6, c = lane & 15, q = lane >> 4;
+    // 32-bit buffer offsets (the caller keeps rows * RB below 2^31)
+    const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(packed + size_t(row_start) * RB), (short)0, rows * RB, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rn = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(norms + size_t(row_start) * NG), (short)0, rows * NG * 4, 0x00020000);
+    const int ntiles = (rows + kMf2Rows - 1) / kMf2Rows;
+    auto row_of = [&](int it) {
+        int tile = int(blockIdx.x) + it * int(gridDim.x);
+        tile = tile < ntiles ? tile : ntiles - 1;
+        const int r = tile * kMf2Rows + 16 * w + c;
+        return r < rows ? r : rows - 1;
+    };
+    uint32_t cw[D][NG][2];
+    float nw[D][NG];
+    auto load = [&](int it, int k) {
+        int tile = int(blockIdx.x) + it * int(gridDim.x);
+        tile = tile < ntiles ? tile : ntiles - 1;
+        // the wave's 16 rows as one contiguous run, 512 bytes a load (rows
+        // past the end read as zeros and are not stored); codes are read
+        // once: nontemporal
+        const int base = (tile * kMf2Rows + 16 * w) * RB + 8 * lane;
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(rc, base + 512 * g, 0, 2);
+            cw[k][g][0] = v[0];
+            cw[k][g][1] = v[1];
+        }
+        load_floats<NG>(rn, int(__umul24(uint32_t(row_of(it)), uint32_t(NG * 4))), nw[k]);
+    };
+
+    // The pieces.  Lane l of a 16-lane group, task (fragment f = 3 g + p,
+    // block b): elements e = 32 b + 16 (d >> 1) + 4 u + (d & 1) and e + 2,
+    // d = l >> 2, u = l & 3 -- nibbles 2 u and 2 u + 1 of dword d of every
+    // lane 16 b + i of the fragment.  The activations are loaded before the
+    // first tiles, so their wait does not wait for the tiles.
+    const int gl = t & 15, gt = t >> 4;
+    const int ed = gl >> 2, eu = gl & 3;
+    const int eo = 16 * (ed >> 1) + 4 * eu + (ed & 1);
+    float xa[TPT], xb[TPT];
+#pragma unroll
+    for (int j = 0; j < TPT; ++j) {
+        const int task = gt + 16 * j;
+        const int tk = task < NT ? task : NT - 1;
+        const int e = 128 * ((tk >> 2) / 3) + 32 * (tk & 3) + eo;
+        xa[j] = xh[e];
+        xb[j] = xh[e + 2];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+        load(k, k);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    bool nonfinite = false;
+    uint8_t *frb = reinterpret_cast<uint8_t *>(fr);
+#pragma unroll
+    for (int j = 0; j < TPT; ++j) {
+        const int task = gt + 16 * j;
+        if (task < NT) {  // uniform over the 16-lane group
+            const int f = task >> 2, b = task & 3, g = f / 3, p = f % 3;
+            const float coef = p == 0 ? cf.beta : (p == 1 ? cf.gamma : cf.delta);
+            nonfinite = nonfinite || !isfinite(xa[j]) || !isfinite(xb[j]);
+            float ra = coef * xa[j], rb = coef * xb[j];
+            // the block's scale: the smallest s0 with max |v| <= 6 * 2^s0
+            const float bm = row16_max(fmaxf(fabsf(ra), fabsf(rb)));
+            int s0 = 0;
+            if (bm > 0.0f && isfinite(bm)) {
+                const float fm = frexpf(bm / 6.0f, &s0);
+                if (fm == 0.5f) --s0;
+            }
+            uint8_t *dst = frb + (f * 64 + 16 * b) * 16 + 4 * ed + eu;
+#pragma unroll
+            for (int i = 0; i < kMf2Pieces; ++i) {
+                int si = s0 - mf2_piece_drop(i);
+                si = si < -126 ? -126 : si;
+                const float sc = ldexpf(1.0f, si);
+                // RNE(ra / sc) low nibble, RNE(rb / sc) high; back: value * sc
+                const uint32_t pk = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(0u, ra, rb, sc, 0);
+                const auto back = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(pk, sc, 0);
+                ra -= back[0];
+                rb -= back[1];
+                dst[i * 16] = uint8_t(pk);
+            }
+            if (gl == 0) s0s[f][b] = s0;
+            if (p == 0) {
+                float xs = xa[j] + xb[j];
+                xs = row16_sum(xs);
+                if (gl == 0) xpart[g][b] = xs;
+            }
+        }
+    }
+    // fragment rows past the pieces are zero
+    for (int z = t; z < NF * 4 * (16 - kMf2Pieces); z += kMf2Threads) {
+        const int f = z / (4 * (16 - kMf2Pieces)), rem = z % (4 * (16 - kMf2Pieces));
+        fr[f][16 * (rem / (16 - kMf2Pieces)) + kMf2Pieces + rem % (16 - kMf2Pieces)] = make_uint4(0, 0, 0, 0);
+    }
+    const int bad = __syncthreads_or(nonfinite);
+    if (bad) {
+        // a non-finite activation: lane c + 16 q sums its slices in order
+        for (int it = 0; it < iters; ++it) {
+            const int r = row_of(it);
+            float s = 0.0f;
+            for (int g = 0; g < NG; ++g) {
+                const uint2 cd = *reinterpret_cast<const uint2 *>(packed + size_t(row_start + r) * RB + 32 * g + 8 * q);
+                float part = 0.0f;
+                for (int j = 0; j < 32; ++j) {
+                    const uint32_t code = ((j < 16 ? cd.x : cd.y) >> (2 * (j & 15))) & 3u;
+                    part += lut[4 * code] * xh[128 * g + 32 * q + j];
+                }
+                s += norms[size_t(row_start + r) * NG + g] * part;
+            }
+            s += __shfl_xor(s, 16);
+            s += __shfl_xor(s, 32);
+            if (q == 0) stage[(it % kMf2Stage) * kMf2Rows + 16 * w + c] = s;
+            if ((it + 1) % kMf2Stage == 0)
+                flush_stage<kMf2Threads>(stage, kMf2Stage, kMf2Rows, it + 1, kMf2Stage, iters, rows, y);
+        }
+        if (iters % kMf2Stage)
+            flush_stage<kMf2Threads>(stage, kMf2Stage, kMf2Rows, iters, iters % kMf2Stage, iters, rows, y);
+        return;
+    }
+    // The loaded dwords reach their MFMA lanes through LDS: lane L's pair g
+    // (byte 512 g + 8 L of the 16 rows) is written at its row and column in
+    // the wave's own buffer, rows RS = RB + 8 bytes apart, and lane c + 16 q
+    // reads back row c, bytes 32 g + 8 q.  (RS / 8 is odd, so the 16 rows
+    // of one such read fall in distinct bank pairs.)  A wave reads only what
+    // it wrote, in order: no barrier.
+    constexpr int RS = RB + 8;
+    uint8_t *xb8 = reinterpret_cast<uint8_t *>(xch) + w * 16 * RS;
+    int wo[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        const int o = 512 * g + 8 * lane;
+        wo[g] = (o / RB) * RS + o % RB;
+    }
+    const int ro = c * RS + 8 * q;
+    // this lane's A fragments: piece c of block q
+    nd_v8i af[NF];
+    int sc[NF];
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+        const uint4 v = fr[f][lane];
+        af[f] = nd_v8i{int(v.x), int(v.y), int(v.z), int(v.w), 0, 0, 0, 0};
+        int si = s0s[f][q] - mf2_piece_drop(c < kMf2Pieces ? c : 0);
+        sc[f] = (si < -126 ? -126 : si) + 127;
+    }
+    float axq[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g)
+        axq[g] = q == 0 ? cf.l0 * (((xpart[g][0] + xpart[g][1]) + xpart[g][2]) + xpart[g][3]) : 0.0f;
+    // loop invariants: wait for them here, not on every pass of the loop
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+        asm volatile("" ::"v"(af[f][0]), "v"(af[f][1]), "v"(af[f][2]), "v"(af[f][3]), "v"(sc[f]) : "memory");
+    }
+#pragma unroll
+    for (int g = 0; g < NG; ++g) asm volatile("" ::"v"(axq[g]) : "memory");
+
+    for (int it0 = 0; it0 < iters; it0 += D) {
+#pragma unroll
+        for (int k = 0; k < D; ++k) {
+            const int it = it0 + k;
+#pragma unroll
+            for (int g = 0; g < NG; ++g)
+                *reinterpret_cast<uint2 *>(xb8 + wo[g]) = make_uint2(cw[k][g][0], cw[k][g][1]);
+            nd_v4f acc[NG];
+#pragma unroll
+            for (int g = 0; g < NG; ++g) {
+                const uint2 dd = *reinterpret_cast<const uint2 *>(xb8 + ro + 32 * g);
+                const uint32_t d0 = dd.x, d1 = dd.y;
+                const uint32_t e0 = d0 & 0x33333333u, o0 = d0 & 0xccccccccu;
+                const uint32_t e1 = d1 & 0x33333333u, o1 = d1 & 0xccccccccu;
+                const nd_v8i b1 = {int(e0), int(o0 >> 2), int(e1), int(o1 >> 2), 0, 0, 0, 0};
+                const nd_v8i b2 = {int(e0 << 1), int(o0 >> 1), int(e1 << 1), int(o1 >> 1), 0, 0, 0, 0};
+                const nd_v8i b3 = {int(e0 << 2), int(o0), int(e1 << 2), int(o1), 0, 0, 0, 0};
+                nd_v4f a = {0.0f, 0.0f, 0.0f, 0.0f};
+                // cbsz = blgp = 4: both operands fp4; B's scale 2^0
+                a = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[3 * g], b1, a, 4, 4, 0, sc[3 * g], 0, 127);
+                a = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[3 * g + 1], b2, a, 4, 4, 0, sc[3 * g + 1], 0, 127);
+                a = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[3 * g + 2], b3, a, 4, 4, 0, sc[3 * g + 2], 0, 127);
+                acc[g] = a;
+            }
+            float s = 0.0f;
+#pragma unroll
+            for (int g = 0; g < NG; ++g)
+                s += nw[k][g] * (((acc[g][0] + acc[g][1]) + (acc[g][2] + acc[g][3])) + axq[g]);
+            s += __shfl_xor(s, 16);
+            s += __shfl_xor(s, 32);
+            if (q == 0) stage[(it % kMf2Stage) * kMf2Rows + 16 * w + c] = s;
+            __builtin_amdgcn_sched_barrier(0);
+            load(it + D, k);
+            __builtin_amdgcn_sched_barrier(0);
+            if ((it + 1) % kMf2Stage == 0)
+                flush_stage<kMf2Threads>(stage, kMf2Stage, kMf2Rows, it + 1, kMf2Stage, iters, rows, y);
+        }
+    }
+    const int done = (iters + D - 1) / D * D;
+    if (done % kMf2Stage)
+        flush_stage<kMf2Threads>(stage, kMf2Stage, kMf2Rows, done, done % kMf2Stage, iters, rows, y);
 }
 
 // Reads code k of a row with the bit reader of cq.rs:914-925 (any width).
@@ -1054,6 +1397,17 @@ int nd_cq_prepare_input(nd_ctx *ctx, const nd_cq *w, const float *x, size_t batc
     return nd::check_launch("cq_prepare");
 }
 
+namespace {
+size_t mf2_min_rows()
+{
+    const char *v = std::getenv("NEEDLE_AMD_CQ_FP4_MIN_ROWS");
+    if (!v || !*v) return kMf2MinRows;
+    char *end = nullptr;
+    const unsigned long long n = std::strtoull(v, &end, 10);
+    return (end && *end == '\0') ? size_t(n) : kMf2MinRows;
+}
+}  // namespace
+
 int nd_cq_matvec_rows_prepared(nd_ctx *ctx, const nd_cq *w, const float *xh, size_t row_start,
                                size_t rows, float *y)
 {
@@ -1077,6 +1431,30 @@ int nd_cq_matvec_rows_prepared(nd_ctx *ctx, const nd_cq *w, const float *xh, siz
                            rows * w->num_groups * 4 < (size_t(1) << 31);
     const size_t slots = 2 * size_t(ctx->num_cus > 0 ? ctx->num_cus : 256);
     const int args_rb = int(w->row_bytes), ng = int(w->num_groups), gr = int(w->group);
+    if (w->per_byte == 4 && w->group == 128 && w->num_groups <= size_t(kMf2MaxGroups) &&
+        w->row_bytes == 32 * w->num_groups && rows >= mf2_min_rows() && offsets32) {
+        // 2-bit / ternary, groups of 128, in <= 768, tall: fp4 matrix cores
+        float lv[4];
+        for (uint32_t c = 0; c < 4; ++c) lv[c] = w->levels[w->bits == kTernary ? ternary_index(c) : int(c)];
+        const Mf2Coef cf = mf2_coef(lv);
+        const size_t tiles = (rows + kMf2Rows - 1) / kMf2Rows;
+        const size_t blocks = tiles < slots ? tiles : slots;
+        const int iters = int((tiles + blocks - 1) / blocks);
+#define ND_MF2(NGV)                                                                              \
+    hipLaunchKernelGGL((cq_gemv_mf2_kernel<NGV>), dim3(unsigned(blocks)), dim3(kMf2Threads), 0,   \
+                       ctx->stream, w->packed, w->norms, w->lut, xh, y, cf, int(row_start),       \
+                       int(rows), iters)
+        switch (w->num_groups) {
+        case 1: ND_MF2(1); break;
+        case 2: ND_MF2(2); break;
+        case 3: ND_MF2(3); break;
+        case 4: ND_MF2(4); break;
+        case 5: ND_MF2(5); break;
+        default: ND_MF2(6); break;
+        }
+#undef ND_MF2
+        return nd::check_launch("cq_gemv_mf2");
+    }
     if (stream && w->per_byte == 4 && row_dwords <= 16 * 3 && offsets32) {
         // 2-bit / ternary, in <= 768: product lookup, two 1024-thread
         // workgroups per CU, the tiles dealt round-robin

@@ -156,3 +156,101 @@ def test_matvec_streams_past_the_stage(ctx, bits):
     hi = host(g.matvec_rows_prepared(xh, half, out - half))
     assert np.array_equal(np.concatenate([lo, hi]).view(np.uint32), y.view(np.uint32))
     g.close()
+
+
+# A 2-bit slot that is neither monotone nor symmetric: the fp4 kernel's
+# plane coefficients are solved from the four levels, whatever they are.
+SKEW_CB = REAL_CB.copy()
+SKEW_CB[:4] = np.array([0.31, -0.02, 0.27, -0.4], np.float32)
+
+
+def _tall_blob(rng, out, inn):
+    packed = rng.integers(0, 256, size=out * inn // 4, dtype=np.uint8)
+    norms = np.abs(rng.normal(0.0, 0.02, size=out * (inn // 128))) * np.sqrt(128.0)
+    return np.concatenate([packed, norms.astype(np.float16).view(np.uint8)])
+
+
+@pytest.fixture
+def fp4_from_16k(monkeypatch):
+    """The fp4 matrix-core GEMV from 16,384 rows (by default from 655,360)."""
+    monkeypatch.setenv("NEEDLE_AMD_CQ_FP4_MIN_ROWS", "16384")
+
+
+@pytest.mark.parametrize("bits", [2, TERNARY])
+@pytest.mark.parametrize("inn", [128, 256, 384, 512, 640, 768])
+def test_matvec_fp4_cores(ctx, fp4_from_16k, bits, inn):
+    """20,011 rows of 2-bit or ternary codes, groups of 128, on the fp4
+    matrix-core kernel: every group count 1..6, a ragged last tile, a band
+    from an odd row, two codebooks, activations of one scale and of
+    magnitudes spread over 2^-8 .. 2^3 inside a block, against the oracle at
+    the reference's tolerance."""
+    rng = np.random.default_rng(inn * 10 + bits)
+    out = 20011
+    blob = _tall_blob(rng, out, inn)
+    xs = [rng.normal(size=inn).astype(np.float32),
+          (rng.normal(size=inn) * np.exp2(rng.uniform(-8, 3, size=inn))).astype(np.float32)]
+    for cb in (REAL_CB, SKEW_CB):
+        g = nd.CqWeight(ctx, blob, out, inn, 128, bits, cb)
+        o = O.CqWeight(blob, out, inn, 128, bits, cb)
+        for x in xs:
+            xh = g.prepare_input(dev(x))[0]
+            xo = o.prepare_input(x)
+            y = host(g.matvec_prepared(xh))
+            assert _close(y, o.matvec_rows_prepared(xo, 0, out))
+            band = host(g.matvec_rows_prepared(xh, 7, 17000))
+            assert _close(band, o.matvec_rows_prepared(xo, 7, 17000))
+        g.close()
+
+
+@pytest.mark.parametrize("bits", [2, TERNARY])
+def test_matvec_fp4_cores_non_finite(ctx, fp4_from_16k, bits):
+    """fp4 carries no infinity or NaN: a prepared activation holding one
+    takes the kernel's plain path, and each row's result is +-inf or NaN
+    exactly where the oracle's is."""
+    rng = np.random.default_rng(77 + bits)
+    out, inn = 20011, 768
+    blob = _tall_blob(rng, out, inn)
+    g = nd.CqWeight(ctx, blob, out, inn, 128, bits, REAL_CB)
+    o = O.CqWeight(blob, out, inn, 128, bits, REAL_CB)
+    base = rng.normal(size=inn).astype(np.float32)
+    for put in ({300: np.inf}, {5: -np.inf}, {5: np.inf, 700: -np.inf}, {129: np.nan}):
+        x = base.copy()
+        for k, v in put.items():
+            x[k] = v
+        y = host(g.matvec_rows_prepared(dev(x), 0, out))
+        want = o.matvec_rows_prepared(x, 0, out)
+        assert np.array_equal(np.isnan(y), np.isnan(want)), put
+        inf = np.isinf(want)
+        assert np.array_equal(y[inf], want[inf]), put
+        fin = np.isfinite(want)
+        assert _close(y[fin], want[fin]), put
+    # and a finite activation afterwards takes the matrix cores again
+    y = host(g.matvec_prepared(dev(base)))
+    assert _close(y, o.matvec_rows_prepared(base, 0, out))
+    g.close()
+
+
+def test_matvec_fp4_cores_default_bound(ctx):
+    """700,001 rows of in 768 take the fp4 kernel with no override: against
+    the oracle, and bit for bit against two halves of 350,000-odd rows run
+    on the same kernel (a row's arithmetic does not depend on its tile or
+    lane)."""
+    rng = np.random.default_rng(700001)
+    out, inn = 700001, 768
+    blob = _tall_blob(rng, out, inn)
+    g = nd.CqWeight(ctx, blob, out, inn, 128, 2, REAL_CB)
+    o = O.CqWeight(blob, out, inn, 128, 2, REAL_CB)
+    del blob
+    x = rng.normal(size=inn).astype(np.float32)
+    xh = g.prepare_input(dev(x))[0]
+    y = host(g.matvec_prepared(xh))
+    assert _close(y, o.matvec(x))
+    half = out // 2
+    os.environ["NEEDLE_AMD_CQ_FP4_MIN_ROWS"] = "16384"
+    try:
+        lo = host(g.matvec_rows_prepared(xh, 0, half))
+        hi = host(g.matvec_rows_prepared(xh, half, out - half))
+    finally:
+        del os.environ["NEEDLE_AMD_CQ_FP4_MIN_ROWS"]
+    assert np.array_equal(np.concatenate([lo, hi]).view(np.uint32), y.view(np.uint32))
+    g.close()
