@@ -654,9 +654,9 @@ __global__ __launch_bounds__(kQ4Threads) void cq_gemv_q4_kernel(
 // in LDS and written out as in the lookup kernels.  A wave loads its 16
 // rows as one contiguous run and regroups them into MFMA slices through
 // LDS: loading the slices directly (32 bytes of 16 rows per load) ran at
-// 60% of the contiguous rate.  An activation holding
-// a non-finite value (which fp4 cannot carry) takes a plain per-lane loop
-// over the same rows instead.
+// 60% of the contiguous rate.  An activation holding a non-finite value
+// (which fp4 cannot carry), or one whose coef * x or L0 * X_g leaves the
+// fp32 range, takes a plain per-lane loop over the same rows instead.
 constexpr int kMf2Pieces = 10;
 constexpr int kMf2Threads = 256;
 constexpr int kMf2Rows = 64;    // rows per tile
@@ -803,8 +803,9 @@ __global__ __launch_bounds__(kMf2Threads, 2) void cq_gemv_mf2_kernel(
         if (task < NT) {  // uniform over the 16-lane group
             const int f = task >> 2, b = task & 3, g = f / 3, p = f % 3;
             const float coef = p == 0 ? cf.beta : (p == 1 ? cf.gamma : cf.delta);
-            nonfinite = nonfinite || !isfinite(xa[j]) || !isfinite(xb[j]);
             float ra = coef * xa[j], rb = coef * xb[j];
+            // a non-finite activation, or coef * x past the fp32 range
+            nonfinite = nonfinite || !isfinite(ra) || !isfinite(rb);
             // the block's scale: the smallest s0 with max |v| <= 6 * 2^s0
             const float bm = row16_max(fmaxf(fabsf(ra), fabsf(rb)));
             int s0 = 0;
@@ -830,6 +831,7 @@ __global__ __launch_bounds__(kMf2Threads, 2) void cq_gemv_mf2_kernel(
                 float xs = xa[j] + xb[j];
                 xs = row16_sum(xs);
                 if (gl == 0) xpart[g][b] = xs;
+                nonfinite = nonfinite || !isfinite(xa[j]) || !isfinite(xb[j]);
             }
         }
     }
@@ -839,7 +841,13 @@ __global__ __launch_bounds__(kMf2Threads, 2) void cq_gemv_mf2_kernel(
         fr[f][16 * (rem / (16 - kMf2Pieces)) + kMf2Pieces + rem % (16 - kMf2Pieces)] = make_uint4(0, 0, 0, 0);
     }
     const int bad = __syncthreads_or(nonfinite);
-    if (bad) {
+    // after the barrier every thread reads the same group sums, so this
+    // test is uniform too
+    bool axbad = false;
+#pragma unroll
+    for (int g = 0; g < NG; ++g)
+        axbad = axbad || !isfinite(cf.l0 * (((xpart[g][0] + xpart[g][1]) + xpart[g][2]) + xpart[g][3]));
+    if (bad || axbad) {
         // a non-finite activation: lane c + 16 q sums its slices in order
         for (int it = 0; it < iters; ++it) {
             const int r = row_of(it);

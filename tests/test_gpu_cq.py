@@ -204,9 +204,10 @@ def test_matvec_fp4_cores(ctx, fp4_from_16k, bits, inn):
 
 @pytest.mark.parametrize("bits", [2, TERNARY])
 def test_matvec_fp4_cores_non_finite(ctx, fp4_from_16k, bits):
-    """fp4 carries no infinity or NaN: a prepared activation holding one
-    takes the kernel's plain path, and each row's result is +-inf or NaN
-    exactly where the oracle's is."""
+    """fp4 carries no infinity or NaN: a prepared activation holding one, or
+    one whose products with the plane coefficients overflow fp32, takes the
+    kernel's plain path, and each row's result is +-inf or NaN exactly where
+    the oracle's is."""
     rng = np.random.default_rng(77 + bits)
     out, inn = 20011, 768
     blob = _tall_blob(rng, out, inn)
@@ -224,6 +225,19 @@ def test_matvec_fp4_cores_non_finite(ctx, fp4_from_16k, bits):
         assert np.array_equal(y[inf], want[inf]), put
         fin = np.isfinite(want)
         assert _close(y[fin], want[fin]), put
+    # levels 0, 10, 0, 0: the plane coefficients are -20, 10, 5, so an
+    # activation of 2e37 is finite while -20 * 2e37 is not; the reference's
+    # terms (10 * 2e37 at most) stay finite, and so must the result
+    big_cb = REAL_CB.copy()
+    big_cb[:4] = np.array([0.0, 10.0, 0.0, 0.0], np.float32)
+    gb = nd.CqWeight(ctx, blob, out, inn, 128, 2, big_cb)
+    ob = O.CqWeight(blob, out, inn, 128, 2, big_cb)
+    x = base.copy()
+    x[200] = np.float32(2e37)
+    y = host(gb.matvec_rows_prepared(dev(x), 0, out))
+    want = ob.matvec_rows_prepared(x, 0, out)
+    assert np.all(np.isfinite(want)) and _close(y, want)
+    gb.close()
     # and a finite activation afterwards takes the matrix cores again
     y = host(g.matvec_prepared(dev(base)))
     assert _close(y, o.matvec_rows_prepared(base, 0, out))
