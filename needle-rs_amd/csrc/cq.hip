@@ -623,8 +623,8 @@ __global__ __launch_bounds__(kQ4Threads) void cq_gemv_q4_kernel(
 // span every function of c, so lvl(c) = L0 + beta P1(c) + gamma P2(c) +
 // delta P3(c) for any four levels.  `dw & 0x33333333` leaves the even codes
 // of a dword at nibble bits 0-1 and `dw & 0xcccccccc` the odd ones at bits
-// 2-3; one shift each gives the other planes, so 16 codes become three
-// planes of 16 nibbles in six VALU operations.
+// 2-3; two shifts of each give the other two planes, so 16 codes become
+// three planes of 16 nibbles in six VALU operations.
 //
 // The activation as fp4 pieces.  Over each 32-element block, coef_p * x is
 // split into kMf2Pieces pieces, each with its own power-of-two (E8M0)
