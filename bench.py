@@ -301,10 +301,12 @@ def gemm_runs(torch, nd, ctx, gen, steps):
     """Format B prefill GEMM, Y [512 x N] = X [512 x 768] . decode(W [N x 768]),
     bf16 MFMA with fp32 accumulate, for the two projection widths; R
     distinct problems per launch (one launch per step) so the step is long
-    enough to time on the device."""
+    enough to time on the device.  Both widths launch 768 tiles of 256 x 256
+    (three per CU): at N 768 with 64 problems (384 tiles, a wave and a half)
+    the second half-wave left half the CUs idle."""
     out = {}
     M, K = 512, 768
-    for N, R in ((3072, 32), (768, 64)):
+    for N, R in ((3072, 32), (768, 128)):
         X = torch.randn(R, M, K, device="cuda", generator=gen)
         W = torch.randint(0, 256, (R, N, K), dtype=torch.uint8, device="cuda", generator=gen)
         CB = torch.randn(R, N // 64, 256, device="cuda", generator=gen) * 0.02
