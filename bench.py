@@ -181,7 +181,12 @@ def cpu_baseline(sec=2.5):
     same workloads the GPU lines run.  Threads split the work as the
     reference's rayon pool would (row bands past cq.rs's size rules; one
     session per thread for independent sessions, as a server runs one
-    V3Cache per session)."""
+    V3Cache per session).  The Cactus-Quants kernels are the reference's
+    const-generic LUT loops (P = 2 and 4 instantiated separately, eight
+    lanes as vector multiplies then adds); Format B, which has no reference
+    function, runs the same eight-lane dot with one level per byte, and its
+    GEMM decodes each weight row once for all activation rows, as
+    matmul_rows_prepared does."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
@@ -201,10 +206,7 @@ def cpu_baseline(sec=2.5):
     def gemv(par):
         i = it[0] % copies
         it[0] += 1
-        if par:
-            O.cb8_gemv_omp(W[i], CB[i], X[i], y)
-        else:
-            O.lib().or_cb8_gemv(W[i], CB[i], X[i], y, GEMV_OUT, GEMV_IN)
+        O.cb8_gemv_lanes(W[i], CB[i], X[i], T if par else 1, y)
     gemv(True)
     n1, e1 = _time_for(lambda: gemv(False), sec, copies // 8)
     nT, eT = _time_for(lambda: gemv(True), 2 * sec, copies)
@@ -221,8 +223,8 @@ def cpu_baseline(sec=2.5):
         cb = rng.normal(0, 0.02, size=(N // 64, 256)).astype(np.float32)
         yy = np.zeros((512, N), np.float32)
         flops = 2.0 * 512 * 768 * N
-        a, ea = _time_for(lambda: O.cb8_gemm_omp(x, w, cb, 1, yy), sec / 2)
-        b, eb = _time_for(lambda: O.cb8_gemm_omp(x, w, cb, T, yy), sec / 2)
+        a, ea = _time_for(lambda: O.cb8_gemm_lanes(x, w, cb, 1, yy), sec / 2)
+        b, eb = _time_for(lambda: O.cb8_gemm_lanes(x, w, cb, T, yy), sec / 2)
         gemm[f"m512_n{N}_k768_GFLOPs"] = {"1_thread": round(a * flops / ea / 1e9, 2),
                                           "all_threads": round(b * flops / eb / 1e9, 2)}
     out["config2_gemm"] = gemm
@@ -289,7 +291,8 @@ def cpu_baseline(sec=2.5):
     del caches
     return {"value": round(gT, 3), "unit": "GB/s", "cores": T, "kind": "port",
             "sample": f"config 1: {nT} GEMVs of 3072x768 u8 over 64 distinct weight copies in "
-                      f"{eT:.1f} s (oracle or_cb8_gemv_omp, {T} OpenMP threads)",
+                      f"{eT:.1f} s (oracle or_cb8_gemv_lanes: the reference's eight-lane LUT "
+                      f"dot with one level per byte, row bands on {T} OpenMP threads)",
             "value_1_thread": round(g1, 3), "nproc": os.cpu_count(), "cpu_model": _cpu_model(),
             "configs": out}
 

@@ -797,29 +797,59 @@ void or_cq_prepare_input(const or_cq *w, const float *x, float *xh)
         or_fwht_normalized(xh + g * w->group, w->group);
 }
 
-/* cq.rs:838-873: eight-lane packed dot of one group, lanes summed 0..7. */
-static float dot_group(size_t P, const float *lut, const uint8_t *gbytes,
-                       size_t nbytes, const float *gx)
+/* The eight accumulator lanes as one vector: `lanes += v * xs` is eight
+ * independent IEEE multiplies and then eight adds (no contraction), lane k's
+ * arithmetic exactly that of `lanes[k] += vals[k] * xs[k]`. */
+typedef float or_lanes8 __attribute__((vector_size(ACC_LANES * sizeof(float))));
+typedef float or_lanes4 __attribute__((vector_size(4 * sizeof(float))));
+
+/* cq.rs:838-873: eight-lane packed dot of one group, lanes summed 0..7.
+ * Always inlined and called with a literal P (4 or 2), as the reference's
+ * `dot_group::<P>` is a const generic, so the loops unroll and the lane
+ * update runs as vector multiplies and then vector adds (no FMA): lane k's
+ * arithmetic is exactly `lanes[k] += vals[k] * xs[k]`.  For P = 4 the eight
+ * lanes are two 4-wide halves (one byte's LUT entry each); for P = 2 the
+ * four entries of 2 are copied into one 8-wide vector. */
+static inline __attribute__((always_inline)) float
+dot_group(const size_t P, const float *lut, const uint8_t *gbytes, size_t nbytes,
+          const float *gx)
 {
-    size_t per_iter = ACC_LANES / P;
-    float lanes[ACC_LANES] = {0};
+    const size_t per_iter = ACC_LANES / P;
+    or_lanes4 lo = {0}, hi = {0};
+    or_lanes8 lanes = {0};
     size_t full = nbytes - nbytes % per_iter;
     size_t bi = 0;
     while (bi < full) {
-        float vals[ACC_LANES];
-        for (size_t t = 0; t < per_iter; t++) {
-            size_t base = (size_t)gbytes[bi + t] * P;
-            for (size_t k = 0; k < P; k++)
-                vals[t * P + k] = lut[base + k];
+        const float *xp = gx + bi * P;
+        if (P == 4) {
+            or_lanes4 a, b, xa, xb;
+            memcpy(&a, lut + (size_t)gbytes[bi] * 4, sizeof a);
+            memcpy(&b, lut + (size_t)gbytes[bi + 1] * 4, sizeof b);
+            memcpy(&xa, xp, sizeof xa);
+            memcpy(&xb, xp + 4, sizeof xb);
+            lo += a * xa;
+            hi += b * xb;
+        } else {
+            float vals[ACC_LANES];
+            for (size_t t = 0; t < per_iter; t++)
+                memcpy(vals + t * P, lut + (size_t)gbytes[bi + t] * P, P * sizeof(float));
+            or_lanes8 v, xs;
+            memcpy(&v, vals, sizeof v);
+            memcpy(&xs, xp, sizeof xs);
+            lanes += v * xs;
         }
-        const float *xs = gx + bi * P;
-        for (size_t k = 0; k < ACC_LANES; k++)
-            lanes[k] += vals[k] * xs[k];
         bi += per_iter;
     }
     float acc = 0.0f;
-    for (size_t k = 0; k < ACC_LANES; k++)
-        acc += lanes[k];
+    if (P == 4) {
+        for (size_t k = 0; k < 4; k++)
+            acc += lo[k];
+        for (size_t k = 0; k < 4; k++)
+            acc += hi[k];
+    } else {
+        for (size_t k = 0; k < ACC_LANES; k++)
+            acc += lanes[k];
+    }
     for (size_t b = bi; b < nbytes; b++) {
         size_t base = (size_t)gbytes[b] * P;
         for (size_t k = 0; k < P; k++)
@@ -854,37 +884,72 @@ int or_get_threads(void) { return or_threads; }
 
 static size_t div_ceil(size_t a, size_t b) { return (a + b - 1) / b; }
 
-/* cq.rs:721-735 (LUT widths) and cq.rs:738-757 (3-bit generic). */
-static void matvec_rows_serial(const or_cq *w, const float *xh,
-                               size_t row_start, size_t rows, float *y)
+/* cq.rs:721-735: `matvec_lut_impl::<P>`, instantiated below for P = 4 and
+ * P = 2 (matvec_lut::<4|2>, cq.rs:693-709). */
+static inline __attribute__((always_inline)) void
+matvec_rows_lut(const size_t P, const or_cq *w, const float *xh, size_t row_start,
+                size_t rows, float *y)
 {
+    const size_t bpg = w->group / P;
+    const float *lut = w->lut;
     for (size_t yi = 0; yi < rows; yi++) {
         size_t o = row_start + yi;
         const uint8_t *row = w->packed + o * w->row_bytes;
         const float *rn = w->norms + o * w->num_groups;
         float total = 0.0f;
-        if (w->per_byte) {
-            size_t P = w->per_byte;
-            size_t bpg = w->group / P;
-            for (size_t g = 0; g < w->num_groups; g++)
-                total += rn[g] * dot_group(P, w->lut, row + g * bpg, bpg,
-                                           xh + g * w->group);
-        } else {
-            size_t bits = w->bits;
-            uint32_t mask = (1u << bits) - 1;
-            for (size_t g = 0; g < w->num_groups; g++) {
-                const float *gx = xh + g * w->group;
-                float acc = 0.0f;
-                for (size_t k = 0; k < w->group; k++) {
-                    size_t bit = (g * w->group + k) * bits;
-                    uint32_t idx = or_read_bits(row, bit, bits, mask);
-                    acc += w->levels[idx] * gx[k];
-                }
-                total += rn[g] * acc;
+        for (size_t g = 0; g < w->num_groups; g++)
+            total += rn[g] * dot_group(P, lut, row + g * bpg, bpg, xh + g * w->group);
+        y[yi] = total;
+    }
+}
+
+static void matvec_rows_lut4(const or_cq *w, const float *xh, size_t row_start,
+                             size_t rows, float *y)
+{
+    matvec_rows_lut(4, w, xh, row_start, rows, y);
+}
+
+static void matvec_rows_lut2(const or_cq *w, const float *xh, size_t row_start,
+                             size_t rows, float *y)
+{
+    matvec_rows_lut(2, w, xh, row_start, rows, y);
+}
+
+/* cq.rs:738-757: bit-at-a-time path for 3-bit rows. */
+static void matvec_rows_generic(const or_cq *w, const float *xh, size_t row_start,
+                                size_t rows, float *y)
+{
+    size_t bits = w->bits;
+    uint32_t mask = (1u << bits) - 1;
+    for (size_t yi = 0; yi < rows; yi++) {
+        size_t o = row_start + yi;
+        const uint8_t *row = w->packed + o * w->row_bytes;
+        const float *rn = w->norms + o * w->num_groups;
+        float total = 0.0f;
+        for (size_t g = 0; g < w->num_groups; g++) {
+            const float *gx = xh + g * w->group;
+            float acc = 0.0f;
+            for (size_t k = 0; k < w->group; k++) {
+                size_t bit = (g * w->group + k) * bits;
+                uint32_t idx = or_read_bits(row, bit, bits, mask);
+                acc += w->levels[idx] * gx[k];
             }
+            total += rn[g] * acc;
         }
         y[yi] = total;
     }
+}
+
+/* cq.rs:713-735 dispatch on the packing (per_byte 4, 2, or 0 for 3-bit). */
+static void matvec_rows_serial(const or_cq *w, const float *xh,
+                               size_t row_start, size_t rows, float *y)
+{
+    if (w->per_byte == 4)
+        matvec_rows_lut4(w, xh, row_start, rows, y);
+    else if (w->per_byte == 2)
+        matvec_rows_lut2(w, xh, row_start, rows, y);
+    else
+        matvec_rows_generic(w, xh, row_start, rows, y);
 }
 
 /* cq.rs:301-323: rows split into bands of max(ceil(rows/threads), 64) when
@@ -947,17 +1012,27 @@ void or_cq_matvec_prepared_reference(const or_cq *w, const float *xh, float *y)
     }
 }
 
-/* cq.rs:791-809: levels * norm for one group, before the rotation. */
+/* cq.rs:791-809: levels * norm for one group, before the rotation.  The
+ * byte-LUT widths go through decode_group_lut with a literal P, so the
+ * per-byte loop unrolls; the products are the same either way. */
+static inline __attribute__((always_inline)) void
+decode_group_lut(const size_t P, const float *lut, const uint8_t *gb, size_t bpg,
+                 float norm, float *buf)
+{
+    for (size_t bi = 0; bi < bpg; bi++)
+        for (size_t k = 0; k < P; k++)
+            buf[bi * P + k] = lut[(size_t)gb[bi] * P + k] * norm;
+}
+
 static void decode_group(const or_cq *w, const uint8_t *row, size_t g,
                          float norm, float *buf)
 {
-    if (w->per_byte) {
-        size_t p = w->per_byte;
-        size_t bpg = w->group / p;
-        const uint8_t *gb = row + g * bpg;
-        for (size_t bi = 0; bi < bpg; bi++)
-            for (size_t k = 0; k < p; k++)
-                buf[bi * p + k] = w->lut[(size_t)gb[bi] * p + k] * norm;
+    if (w->per_byte == 4) {
+        size_t bpg = w->group / 4;
+        decode_group_lut(4, w->lut, row + g * bpg, bpg, norm, buf);
+    } else if (w->per_byte == 2) {
+        size_t bpg = w->group / 2;
+        decode_group_lut(2, w->lut, row + g * bpg, bpg, norm, buf);
     } else {
         size_t bits = w->bits;
         uint32_t mask = (1u << bits) - 1;
@@ -972,10 +1047,13 @@ static void decode_group(const or_cq *w, const uint8_t *row, size_t g,
 static float group_dot_lanes(const float *u, const float *x, size_t n)
 {
     size_t chunks = n / ACC_LANES;
-    float lanes[ACC_LANES] = {0};
-    for (size_t c = 0; c < chunks; c++)
-        for (size_t k = 0; k < ACC_LANES; k++)
-            lanes[k] += u[c * ACC_LANES + k] * x[c * ACC_LANES + k];
+    or_lanes8 lanes = {0};
+    for (size_t c = 0; c < chunks; c++) {
+        or_lanes8 uu, xx;
+        memcpy(&uu, u + c * ACC_LANES, sizeof uu);
+        memcpy(&xx, x + c * ACC_LANES, sizeof xx);
+        lanes += uu * xx;
+    }
     float s = 0.0f;
     for (size_t k = 0; k < ACC_LANES; k++)
         s += lanes[k];
@@ -1153,6 +1231,66 @@ void or_cb8_gemm(const float *x, const uint8_t *w, const float *cb, float *y,
 {
     for (size_t i = 0; i < m; i++)
         or_cb8_gemv(w, cb, x + i * in, y + i * out, out, in);
+}
+
+/* Format B through the reference's LUT-kernel shape, for the CPU baseline
+ * (the format has no reference function; these are what its CPU path would
+ * be).  GEMV: dot_group with one level per byte (cq.rs:838-873, P = 1):
+ * eight accumulator lanes, element k into lane k % 8, lanes summed 0..7,
+ * rows in bands over `threads` (cq.rs:314-323).  GEMM: matmul_rows_prepared's
+ * order (cq.rs:632-679): each weight row decoded once through its codebook,
+ * then dotted with every activation row by group_dot_lanes (cq.rs:879-895).
+ * Both sum in a different order from or_cb8_gemv, so they agree with it to
+ * float rounding, not bit for bit. */
+static void cb8_row_lanes(const float *c, const uint8_t *row, const float *x, size_t in,
+                          float *y)
+{
+    or_lanes8 lanes = {0};
+    size_t full = in - in % ACC_LANES, k = 0;
+    for (; k < full; k += ACC_LANES) {
+        float vals[ACC_LANES];
+        for (size_t t = 0; t < ACC_LANES; t++)
+            vals[t] = c[row[k + t]];
+        or_lanes8 v, xs;
+        memcpy(&v, vals, sizeof v);
+        memcpy(&xs, x + k, sizeof xs);
+        lanes += v * xs;
+    }
+    float acc = 0.0f;
+    for (size_t t = 0; t < ACC_LANES; t++)
+        acc += lanes[t];
+    for (; k < in; k++)
+        acc += c[row[k]] * x[k];
+    *y = acc;
+}
+
+void or_cb8_gemv_lanes(const uint8_t *w, const float *cb, const float *x, float *y,
+                       size_t out, size_t in, int threads)
+{
+    long n = (long)out;
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+    for (long o = 0; o < n; o++)
+        cb8_row_lanes(cb + ((size_t)o / 64) * 256, w + (size_t)o * in, x, in, y + o);
+}
+
+void or_cb8_gemm_lanes(const float *x, const uint8_t *w, const float *cb, float *y,
+                       size_t m, size_t out, size_t in, int threads)
+{
+    long n = (long)out;
+#pragma omp parallel num_threads(threads > 0 ? threads : 1)
+    {
+        float *u = malloc((in ? in : 1) * sizeof(float));
+#pragma omp for schedule(static)
+        for (long o = 0; o < n; o++) {
+            const float *c = cb + ((size_t)o / 64) * 256;
+            const uint8_t *row = w + (size_t)o * in;
+            for (size_t k = 0; k < in; k++)
+                u[k] = c[row[k]];
+            for (size_t i = 0; i < m; i++)
+                y[i * out + (size_t)o] = group_dot_lanes(u, x + i * in, in);
+        }
+        free(u);
+    }
 }
 
 /* ======================================================================== */

@@ -143,6 +143,13 @@ void or_cb8_gemv_omp(const uint8_t *w, const float *cb, const float *x,
                      float *y, size_t out, size_t in);
 void or_cb8_gemm_omp(const float *x, const uint8_t *w, const float *cb, float *y,
                      size_t m, size_t out, size_t in, int threads);
+/* The CPU baseline's Format B kernels, in the reference's LUT-kernel order
+ * (eight lanes; the GEMM decodes each row once): within float rounding of
+ * the closed form above, rows in bands over `threads`. */
+void or_cb8_gemv_lanes(const uint8_t *w, const float *cb, const float *x, float *y,
+                       size_t out, size_t in, int threads);
+void or_cb8_gemm_lanes(const float *x, const uint8_t *w, const float *cb, float *y,
+                       size_t m, size_t out, size_t in, int threads);
 
 /* ---- v3/cache.rs ------------------------------------------------------ */
 void or_fake_quant_vec(float *x, size_t n, uint32_t bits);

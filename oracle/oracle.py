@@ -91,6 +91,8 @@ def lib():
         L.or_cb8_gemv_f64.argtypes = [_u8p, _f32p, _f32p, _f64p, _sz, _sz]
         L.or_cb8_gemm.argtypes = [_f32p, _u8p, _f32p, _f32p, _sz, _sz, _sz]
         L.or_cb8_gemm_omp.argtypes = [_f32p, _u8p, _f32p, _f32p, _sz, _sz, _sz, C.c_int]
+        L.or_cb8_gemv_lanes.argtypes = [_u8p, _f32p, _f32p, _f32p, _sz, _sz, C.c_int]
+        L.or_cb8_gemm_lanes.argtypes = [_f32p, _u8p, _f32p, _f32p, _sz, _sz, _sz, C.c_int]
         L.or_attend_step_i8_sessions.argtypes = [_sz, _f32p, _i8p, _f32p, _i8p, _f32p, _sz, _sz,
                                                  _sz, C.POINTER(_AttnDims), _f32p, C.c_int]
         L.or_fake_quant_vec.argtypes = [_f32p, _sz, C.c_uint32]
@@ -333,6 +335,28 @@ def cb8_gemm_omp(x, w, cb, threads, y=None):
     if y is None:
         y = np.zeros((m, out), np.float32)
     lib().or_cb8_gemm_omp(x, w, _f32(cb), y, m, out, inn, int(threads))
+    return y
+
+
+def cb8_gemv_lanes(w, cb, x, threads=1, y=None):
+    """Format B GEMV in the reference's eight-lane order (the CPU baseline's kernel)."""
+    w = np.ascontiguousarray(w, np.uint8)
+    out, inn = w.shape
+    if y is None:
+        y = np.zeros(out, np.float32)
+    lib().or_cb8_gemv_lanes(w, _f32(cb), _f32(x), y, out, inn, int(threads))
+    return y
+
+
+def cb8_gemm_lanes(x, w, cb, threads=1, y=None):
+    """Format B GEMM in matmul_rows_prepared's order (the CPU baseline's kernel)."""
+    x = _f32(x)
+    w = np.ascontiguousarray(w, np.uint8)
+    m = x.shape[0]
+    out, inn = w.shape
+    if y is None:
+        y = np.zeros((m, out), np.float32)
+    lib().or_cb8_gemm_lanes(x, w, _f32(cb), y, m, out, inn, int(threads))
     return y
 
 

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from cq_cases import TERNARY, WIDTHS, build_case, fake_codebook, pack_lsb, sylvester
+from cq_cases import TERNARY, WIDTHS, build_case, fake_codebook, pack_lsb, random_case, sylvester
 
 
 # ---- math.rs ----------------------------------------------------------------
@@ -152,6 +152,31 @@ def test_row_band_equals_full(bits):
         assert np.array_equal(w.matvec_rows_prepared(xh, start, n), full[start:start + n])
 
 
+@pytest.mark.parametrize("bits", [2, 4, TERNARY])
+@pytest.mark.parametrize("shape", [(6, 768, 128), (5, 40, 8), (3, 200, 64)])
+def test_matvec_lane_order_bit_exact(bits, shape):
+    """matvec_lut_impl::<P> (cq.rs:721-735) with dot_group::<P> (cq.rs:838-873)
+    restated in numpy float32: each group's levels go element k -> lane k % 8,
+    a multiply then an add, the lanes summed 0..7, then `total += norm * acc`
+    over the groups in order.  The oracle must give exactly these bits."""
+    rng = np.random.default_rng(7 + bits)
+    c = random_case(rng, *shape, bits, fake_codebook(shape[2]))
+    w = _weight(c)
+    x = rng.normal(size=c.in_feat).astype(np.float32)
+    xh = w.prepare_input(x)
+    got = w.matvec_prepared(xh)
+    vals = c.levels[c.idx]  # [out, in_pad] decoded levels
+    want = np.zeros(c.out, np.float32)
+    for o in range(c.out):
+        total = np.float32(0)
+        for g in range(c.num_groups):
+            sl = slice(g * c.group, (g + 1) * c.group)
+            acc = _lanes_dot(vals[o, sl], xh[sl])
+            total = np.float32(total + np.float32(c.norms_f32[o, g] * acc))
+        want[o] = total
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
 @pytest.mark.parametrize("bits", WIDTHS)
 @pytest.mark.parametrize("shape", [(16, 128, 128), (5, 40, 8), (7, 200, 64), (9, 512, 128)])
 def test_matvec_matches_simple_reference(bits, shape):
@@ -266,3 +291,48 @@ def test_cb8_gemv_against_f64_brute_force():
     X = rng.normal(size=(5, inn)).astype(np.float32)
     Y = O.cb8_gemm(X, w, cb)
     assert np.max(np.abs(Y - X.astype(np.float64) @ dense.T)) < 2e-6
+
+
+def _lanes_dot(u, x):
+    """cq.rs:879-895 / :838-873's eight-lane order in numpy float32: element
+    k into lane k % 8 (a multiply, then an add), lanes summed 0..7, then the
+    tail added in order."""
+    u = u.astype(np.float32)
+    x = x.astype(np.float32)
+    n = u.size - u.size % 8
+    lanes = np.zeros(8, np.float32)
+    for c in range(0, n, 8):
+        lanes = lanes + u[c:c + 8] * x[c:c + 8]
+    s = np.float32(0)
+    for v in lanes:
+        s = np.float32(s + v)
+    for k in range(n, u.size):
+        s = np.float32(s + u[k] * x[k])
+    return s
+
+
+@pytest.mark.parametrize("inn", [768, 96, 100, 7])
+def test_cb8_lanes_kernels_follow_the_eight_lane_order(inn):
+    """The CPU baseline's Format B kernels: the eight-lane order exactly (a
+    numpy restatement, tail included when `in` is not a multiple of 8),
+    within float rounding of the f64 closed form, and the same bits on any
+    thread count."""
+    rng = np.random.default_rng(31 + inn)
+    out = 130
+    w = rng.integers(0, 256, size=(out, inn), dtype=np.uint8)
+    cb = rng.normal(0, 0.02, size=((out + 63) // 64, 256)).astype(np.float32)
+    x = rng.normal(size=inn).astype(np.float32)
+    dense = cb[np.arange(out)[:, None] // 64, w]
+    got = O.cb8_gemv_lanes(w, cb, x)
+    want = np.array([_lanes_dot(dense[o], x) for o in range(out)], np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    ref = dense.astype(np.float64) @ x.astype(np.float64)
+    assert np.max(np.abs(got - ref)) < 2e-6
+    assert np.array_equal(O.cb8_gemv_lanes(w, cb, x, 4).view(np.uint32), got.view(np.uint32))
+    X = rng.normal(size=(6, inn)).astype(np.float32)
+    Y = O.cb8_gemm_lanes(X, w, cb)
+    wantY = np.array([[_lanes_dot(dense[o], X[i]) for o in range(out)] for i in range(6)],
+                     np.float32)
+    assert np.array_equal(Y.view(np.uint32), wantY.view(np.uint32))
+    assert np.array_equal(O.cb8_gemm_lanes(X, w, cb, 3).view(np.uint32), Y.view(np.uint32))
+    assert np.max(np.abs(Y - X.astype(np.float64) @ dense.T.astype(np.float64))) < 2e-6
