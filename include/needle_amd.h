@@ -27,6 +27,8 @@ enum nd_status {
     ND_ERR_ARG = 1,      /* invalid argument (shape, NULL, range) */
     ND_ERR_HIP = 2,      /* a HIP runtime call failed */
     ND_ERR_NOMEM = 3,    /* device or host allocation failed */
+    ND_ERR_BUSY = 4,     /* the context or batch is inside a call on another
+                          * host thread (see "Threads" below) */
     /* CqWeight::from_blob errors, cq.rs:76-89 (CqError), same order */
     ND_ERR_CQ_UNSUPPORTED_BITS = 11,
     ND_ERR_CQ_BAD_GROUP = 12,
@@ -46,6 +48,24 @@ enum nd_status {
  * next nd_* call on this thread.  Replaces needle_last_error
  * (needle.h:487; lib.rs:27-39). */
 const char *nd_last_error(void);
+
+/* ---- threads ----------------------------------------------------------- */
+/*
+ * Which objects may be shared between host threads (the reference: V3Model
+ * is Send + Sync and shared by every session, a V3Cache is per session,
+ * needle-infer/src/v3_engine.rs:544-561; a C handle is used by one thread at
+ * a time, docs/c-ffi.md:383-393):
+ *   - nd_cq and nd_v3_model are read-only once created: any number of
+ *     threads may use one at once, each through its own context on the
+ *     model's device;
+ *   - nd_ctx (a stream and a workspace) and nd_v3_batch (sessions' caches
+ *     and step state, like V3Cache) are used by one thread at a time.  They
+ *     may move between threads between calls.  A call on a context or batch
+ *     that another thread is inside fails with ND_ERR_BUSY and changes
+ *     nothing; a batch is stepped through one context at a time;
+ *   - nd_last_error() is per thread.
+ * Creating and freeing an object is not concurrent with its use.
+ */
 
 /* ---- context: one device, one stream ------------------------------------ */
 typedef struct nd_ctx nd_ctx;

@@ -501,7 +501,7 @@ int nd_v3_cact_config(const void *bytes, size_t len, nd_v3_cfg *cfg, size_t *can
 
 int nd_v3_model_from_cact(nd_ctx *ctx, const void *bytes, size_t len, nd_v3_model **out)
 {
-    if (int rc = nd::enter(ctx)) return rc;
+    ND_ENTER(ctx);
     ND_REQUIRE(out, "null output pointer");
     *out = nullptr;
     Container c;
@@ -561,7 +561,7 @@ int nd_v3_cact_config_at_depth(const void *bytes, size_t len, size_t depth, nd_v
 int nd_v3_model_from_cact_at_depth(nd_ctx *ctx, const void *bytes, size_t len, size_t depth,
                                    nd_v3_model **out)
 {
-    if (int rc = nd::enter(ctx)) return rc;
+    ND_ENTER(ctx);
     ND_REQUIRE(out, "null output pointer");
     *out = nullptr;
     Container c;

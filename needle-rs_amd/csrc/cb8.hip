@@ -888,7 +888,7 @@ extern "C" {
 int nd_cb8_gemv(nd_ctx *ctx, const uint8_t *w, const float *cb, const float *x, float *y,
                 size_t out, size_t in)
 {
-    if (int rc = nd::enter(ctx)) return rc;
+    ND_ENTER(ctx);
     return launch_gemv(ctx, 1, w, 0, cb, 0, x, 0, y, 0, out, in);
 }
 
@@ -896,7 +896,7 @@ int nd_cb8_gemv_batched(nd_ctx *ctx, size_t count, const uint8_t *w, size_t w_st
                         const float *cb, size_t cb_stride, const float *x, size_t x_stride,
                         float *y, size_t y_stride, size_t out, size_t in)
 {
-    if (int rc = nd::enter(ctx)) return rc;
+    ND_ENTER(ctx);
     return launch_gemv(ctx, count, w, w_stride, cb, cb_stride, x, x_stride, y, y_stride, out, in);
 }
 
@@ -904,7 +904,7 @@ int nd_cb8_gemm_batched(nd_ctx *ctx, size_t count, const float *x, size_t x_stri
                         const uint8_t *w, size_t w_stride, const float *cb, size_t cb_stride,
                         float *y, size_t y_stride, size_t m, size_t out, size_t in)
 {
-    if (int rc = nd::enter(ctx)) return rc;
+    ND_ENTER(ctx);
     if (count == 0) return ND_OK;
     ND_REQUIRE(x && w && cb && y, "null buffer");
     ND_REQUIRE(m > 0 && out > 0 && in > 0, "empty shape");

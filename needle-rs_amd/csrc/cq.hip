@@ -655,8 +655,9 @@ __global__ __launch_bounds__(kQ4Threads) void cq_gemv_q4_kernel(
 // rows as one contiguous run and regroups them into MFMA slices through
 // LDS: loading the slices directly (32 bytes of 16 rows per load) ran at
 // 60% of the contiguous rate.  An activation holding a non-finite value
-// (which fp4 cannot carry), or one whose coef * x or L0 * X_g leaves the
-// fp32 range, takes a plain per-lane loop over the same rows instead.
+// (which fp4 cannot carry), one whose coef * x or L0 * X_g leaves the fp32
+// range, or one whose coef * x exceeds kMf2MaxBlock takes a plain per-lane
+// loop over the same rows instead.
 constexpr int kMf2Pieces = 10;
 constexpr int kMf2Threads = 256;
 constexpr int kMf2Rows = 64;    // rows per tile
@@ -665,11 +666,30 @@ constexpr int kMf2Stage = 16;   // staged tiles (4 KiB)
 constexpr int kMf2MaxGroups = 6;
 // Below this many rows the lookup kernel is as fast or faster (the rows
 // sit in the MALL; measured crossover ~700k rows of in 768).  The
-// environment variable NEEDLE_AMD_CQ_FP4_MIN_ROWS overrides it.
+// environment variable NEEDLE_AMD_CQ_FP4_MIN_ROWS, read once when a weight
+// is created, overrides it for that weight.
 constexpr size_t kMf2MinRows = 655360;
+// The largest |coef * x| a block may hold on the matrix cores.  Its first
+// piece's scale 2^s0 is below max / 3, and one group's three planes sum at
+// most 3 x 128 products of a piece (<= 6 * 2^s0) and a plane value (<= 4):
+// 9216 * 2^s0 < 2^13.2 * max / 3.  Below 2^116 that stays under 2^128, so no
+// partial sum of the MFMAs can overflow where the reference's products do not.
+constexpr float kMf2MaxBlock = 0x1p116f;
 
 typedef int nd_v8i __attribute__((ext_vector_type(8)));
 typedef float nd_v4f __attribute__((ext_vector_type(4)));
+
+// Orders LDS accesses between the lanes of one wave: a release and an
+// acquire fence at wavefront scope around a wave barrier.  A wave executes
+// its LDS instructions in order, so this emits no wait; it keeps the
+// compiler from moving LDS accesses across it and makes a lane's read of
+// another lane's store well-defined.
+__device__ inline void nd_wave_lds_sync()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
 // Exponent of piece i's scale below the block's first: 0, 2, 4, then 3 more
 // a piece.  With the block's largest |v| at most 6 * 2^s0, piece 0 leaves at
@@ -808,6 +828,8 @@ __global__ __launch_bounds__(kMf2Threads, 2) void cq_gemv_mf2_kernel(
             nonfinite = nonfinite || !isfinite(ra) || !isfinite(rb);
             // the block's scale: the smallest s0 with max |v| <= 6 * 2^s0
             const float bm = row16_max(fmaxf(fabsf(ra), fabsf(rb)));
+            // too close to the top of the range for the MFMA sums
+            nonfinite = nonfinite || bm > kMf2MaxBlock;
             int s0 = 0;
             if (bm > 0.0f && isfinite(bm)) {
                 const float fm = frexpf(bm / 6.0f, &s0);
@@ -915,10 +937,17 @@ __global__ __launch_bounds__(kMf2Threads, 2) void cq_gemv_mf2_kernel(
 #pragma unroll
             for (int g = 0; g < NG; ++g)
                 *reinterpret_cast<uint2 *>(xb8 + wo[g]) = make_uint2(cw[k][g][0], cw[k][g][1]);
+            // the lanes' stores are visible to the wave's reads below
+            nd_wave_lds_sync();
+            uint2 dds[NG];
+#pragma unroll
+            for (int g = 0; g < NG; ++g) dds[g] = *reinterpret_cast<const uint2 *>(xb8 + ro + 32 * g);
+            // and every read is done before the next pass overwrites the buffer
+            nd_wave_lds_sync();
             nd_v4f acc[NG];
 #pragma unroll
             for (int g = 0; g < NG; ++g) {
-                const uint2 dd = *reinterpret_cast<const uint2 *>(xb8 + ro + 32 * g);
+                const uint2 dd = dds[g];
                 const uint32_t d0 = dd.x, d1 = dd.y;
                 const uint32_t e0 = d0 & 0x33333333u, o0 = d0 & 0xccccccccu;
                 const uint32_t e1 = d1 & 0x33333333u, o1 = d1 & 0xccccccccu;
@@ -1275,7 +1304,7 @@ int nd_cq_from_blob(nd_ctx *ctx, const uint8_t *blob, size_t blob_len, size_t ou
                     size_t in_feat, size_t group, uint8_t bits, const float *codebook,
                     size_t codebook_len, nd_cq **out)
 {
-    if (int rc = nd::enter(ctx)) return rc;
+    ND_ENTER(ctx);
     ND_REQUIRE(out, "null output pointer");
     *out = nullptr;
     // Validation order follows CqWeight::from_blob (cq.rs:189-225).
@@ -1328,6 +1357,12 @@ int nd_cq_from_blob(nd_ctx *ctx, const uint8_t *blob, size_t blob_len, size_t ou
     std::memcpy(w->levels, levels, sizeof levels);
     w->inv_sqrt_group = 1.0f / std::sqrt(float(group));
     w->per_byte = eff == 2 ? 4 : (eff == 4 ? 2 : 0);
+    w->fp4_min_rows = kMf2MinRows;
+    if (const char *v = std::getenv("NEEDLE_AMD_CQ_FP4_MIN_ROWS")) {
+        char *end = nullptr;
+        const unsigned long long n = std::strtoull(v, &end, 10);
+        if (*v && end && *end == '\0') w->fp4_min_rows = size_t(n);
+    }
 
     std::vector<float> norms(out_feat * num_groups);
     for (size_t i = 0; i < norms.size(); ++i) {
@@ -1393,7 +1428,7 @@ int nd_cq_shape(const nd_cq *w, size_t *out_feat, size_t *in_feat, size_t *in_pa
 
 int nd_cq_prepare_input(nd_ctx *ctx, const nd_cq *w, const float *x, size_t batch, float *xh)
 {
-    if (int rc = nd::enter(ctx)) return rc;
+    ND_ENTER(ctx);
     if (int rc = check_cq(w)) return rc;
     if (batch == 0) return ND_OK;
     ND_REQUIRE(x && xh, "null buffer");
@@ -1405,21 +1440,11 @@ int nd_cq_prepare_input(nd_ctx *ctx, const nd_cq *w, const float *x, size_t batc
     return nd::check_launch("cq_prepare");
 }
 
-namespace {
-size_t mf2_min_rows()
-{
-    const char *v = std::getenv("NEEDLE_AMD_CQ_FP4_MIN_ROWS");
-    if (!v || !*v) return kMf2MinRows;
-    char *end = nullptr;
-    const unsigned long long n = std::strtoull(v, &end, 10);
-    return (end && *end == '\0') ? size_t(n) : kMf2MinRows;
-}
-}  // namespace
 
 int nd_cq_matvec_rows_prepared(nd_ctx *ctx, const nd_cq *w, const float *xh, size_t row_start,
                                size_t rows, float *y)
 {
-    if (int rc = nd::enter(ctx)) return rc;
+    ND_ENTER(ctx);
     if (int rc = check_cq(w)) return rc;
     ND_REQUIRE(row_start + rows <= w->out_feat, "rows %zu+%zu beyond %zu", row_start, rows, w->out_feat);
     if (rows == 0) return ND_OK;
@@ -1440,7 +1465,7 @@ int nd_cq_matvec_rows_prepared(nd_ctx *ctx, const nd_cq *w, const float *xh, siz
     const size_t slots = 2 * size_t(ctx->num_cus > 0 ? ctx->num_cus : 256);
     const int args_rb = int(w->row_bytes), ng = int(w->num_groups), gr = int(w->group);
     if (w->per_byte == 4 && w->group == 128 && w->num_groups <= size_t(kMf2MaxGroups) &&
-        w->row_bytes == 32 * w->num_groups && rows >= mf2_min_rows() && offsets32) {
+        w->row_bytes == 32 * w->num_groups && rows >= w->fp4_min_rows && offsets32) {
         // 2-bit / ternary, groups of 128, in <= 768, tall: fp4 matrix cores
         float lv[4];
         for (uint32_t c = 0; c < 4; ++c) lv[c] = w->levels[w->bits == kTernary ? ternary_index(c) : int(c)];
@@ -1570,7 +1595,7 @@ int nd_cq_matvec_rows_prepared(nd_ctx *ctx, const nd_cq *w, const float *xh, siz
 int nd_cq_matmul_rows_prepared(nd_ctx *ctx, const nd_cq *w, const float *xh, size_t batch,
                                size_t row_start, size_t rows, float *y)
 {
-    if (int rc = nd::enter(ctx)) return rc;
+    ND_ENTER(ctx);
     if (int rc = check_cq(w)) return rc;
     ND_REQUIRE(row_start + rows <= w->out_feat, "rows %zu+%zu beyond %zu", row_start, rows, w->out_feat);
     if (rows == 0 || batch == 0) return ND_OK;
@@ -1606,7 +1631,7 @@ int nd_cq_matmul_rows_prepared(nd_ctx *ctx, const nd_cq *w, const float *xh, siz
 
 int nd_cq_dequantize_rows(nd_ctx *ctx, const nd_cq *w, const int32_t *rows, size_t n, float *out)
 {
-    if (int rc = nd::enter(ctx)) return rc;
+    ND_ENTER(ctx);
     if (int rc = check_cq(w)) return rc;
     if (n == 0) return ND_OK;
     ND_REQUIRE(rows && out, "null buffer");

@@ -37,12 +37,27 @@ int hip_fail(hipError_t e, const char *what)
                 hipGetErrorString(e));
 }
 
-int enter(nd_ctx *ctx)
+int claim(Owner &o, const char *what)
 {
-    if (!ctx) return fail(ND_ERR_ARG, "null context");
+    return owner_claim(o) ? ND_OK : fail(ND_ERR_BUSY, "%s is in use by another thread", what);
+}
+
+Entry::Entry(nd_ctx *ctx)
+{
+    if (!ctx) {
+        rc = fail(ND_ERR_ARG, "null context");
+        return;
+    }
     clear_error();
-    ND_HIP(hipSetDevice(ctx->device));
-    return ND_OK;
+    if ((rc = claim(ctx->owner, "the context")) != ND_OK) return;
+    ctx_ = ctx;
+    const hipError_t e = hipSetDevice(ctx->device);
+    if (e != hipSuccess) rc = hip_fail(e, "hipSetDevice(ctx->device)");
+}
+
+Entry::~Entry()
+{
+    if (ctx_) release(ctx_->owner);
 }
 
 int workspace(nd_ctx *ctx, size_t bytes, void **out)
@@ -94,9 +109,12 @@ static int ctx_create(int device, bool own, void *stream, nd_ctx **out)
         return nd::hip_fail(e, "hipGetDeviceProperties");
     }
     c->num_cus = prop.multiProcessorCount;
-    if (int rc = nd::noalloc_setup(device)) {
-        delete c;
-        return rc;
+    // The no-allocation entry point's scratch address: optional, so a
+    // failure here leaves it unset (that entry point then reports it) and
+    // the context is created all the same.
+    if (nd::noalloc_setup(device) != ND_OK) {
+        (void)hipGetLastError();
+        nd::clear_error();
     }
     if (!own) {
         c->stream = static_cast<hipStream_t>(stream);
@@ -131,14 +149,14 @@ void nd_ctx_destroy(nd_ctx *ctx)
 
 int nd_ctx_synchronize(nd_ctx *ctx)
 {
-    if (int rc = nd::enter(ctx)) return rc;
+    ND_ENTER(ctx);
     ND_HIP(hipStreamSynchronize(ctx->stream));
     return ND_OK;
 }
 
 int nd_malloc(nd_ctx *ctx, size_t bytes, void **out)
 {
-    if (int rc = nd::enter(ctx)) return rc;
+    ND_ENTER(ctx);
     ND_REQUIRE(out, "null output pointer");
     *out = nullptr;
     ND_HIP(hipMalloc(out, bytes ? bytes : 1));
@@ -147,7 +165,7 @@ int nd_malloc(nd_ctx *ctx, size_t bytes, void **out)
 
 int nd_free(nd_ctx *ctx, void *ptr)
 {
-    if (int rc = nd::enter(ctx)) return rc;
+    ND_ENTER(ctx);
     if (!ptr) return ND_OK;
     ND_HIP(hipStreamSynchronize(ctx->stream));
     ND_HIP(hipFree(ptr));
@@ -156,7 +174,7 @@ int nd_free(nd_ctx *ctx, void *ptr)
 
 int nd_memcpy_htod(nd_ctx *ctx, void *dst, const void *src, size_t bytes)
 {
-    if (int rc = nd::enter(ctx)) return rc;
+    ND_ENTER(ctx);
     if (!bytes) return ND_OK;
     ND_REQUIRE(dst && src, "null pointer");
     ND_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
@@ -166,7 +184,7 @@ int nd_memcpy_htod(nd_ctx *ctx, void *dst, const void *src, size_t bytes)
 
 int nd_memcpy_dtoh(nd_ctx *ctx, void *dst, const void *src, size_t bytes)
 {
-    if (int rc = nd::enter(ctx)) return rc;
+    ND_ENTER(ctx);
     if (!bytes) return ND_OK;
     ND_REQUIRE(dst && src, "null pointer");
     ND_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));

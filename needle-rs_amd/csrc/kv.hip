@@ -22,7 +22,9 @@
 // GPU (every device the library runs on holds its copy until the process
 // ends).  Host code never passes `scratch` itself to a kernel: its name is a
 // host-side stand-in, and the device address comes from hipGetSymbolAddress
-// once per device (nd::noalloc_setup, called when a context is created).
+// once per device (nd::noalloc_setup, called when a context is created; if
+// it fails there, the context is still created and this entry point reports
+// the missing address).
 static constexpr size_t kNoAllocScratchFloats = size_t(1) << 20;  // 4 MiB
 static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
 
@@ -504,7 +506,7 @@ size_t nd_kv_f32_block_bytes(const nd_kv_geom *g)
 int nd_kv_write_f32(nd_ctx *ctx, const nd_kv_geom *g, void *kv, size_t kv_stride, size_t count,
                     const int32_t *pos, const float *k, const float *v)
 {
-    if (int rc = nd::enter(ctx)) return rc;
+    ND_ENTER(ctx);
     if (int rc = check_geom(g)) return rc;
     if (count == 0) return ND_OK;
     ND_REQUIRE(kv && pos && k && v, "null buffer");
@@ -519,7 +521,7 @@ int nd_kv_write_f32(nd_ctx *ctx, const nd_kv_geom *g, void *kv, size_t kv_stride
 
 int nd_fake_quant(nd_ctx *ctx, float *x, size_t rows, size_t dim)
 {
-    if (int rc = nd::enter(ctx)) return rc;
+    ND_ENTER(ctx);
     if (rows == 0) return ND_OK;
     ND_REQUIRE(x && dim > 0 && dim <= (1u << 20), "bad arguments");
     const size_t blocks = (rows + 3) / 4;
@@ -532,7 +534,7 @@ int nd_fake_quant(nd_ctx *ctx, float *x, size_t rows, size_t dim)
 int nd_quantize_rows(nd_ctx *ctx, const float *x, size_t rows, size_t head_dim, int8_t *ints,
                      float *scales)
 {
-    if (int rc = nd::enter(ctx)) return rc;
+    ND_ENTER(ctx);
     if (rows == 0) return ND_OK;
     ND_REQUIRE(x && ints && scales && head_dim > 0 && head_dim <= (1u << 20), "bad arguments");
     const size_t blocks = (rows + 3) / 4;
@@ -545,7 +547,7 @@ int nd_quantize_rows(nd_ctx *ctx, const float *x, size_t rows, size_t head_dim, 
 int nd_kv_write(nd_ctx *ctx, const nd_kv_geom *g, void *kv, size_t kv_stride, size_t count,
                 const int32_t *pos, const float *k, const float *v)
 {
-    if (int rc = nd::enter(ctx)) return rc;
+    ND_ENTER(ctx);
     if (int rc = check_geom(g)) return rc;
     if (count == 0) return ND_OK;
     ND_REQUIRE(kv && pos && k && v, "null buffer");
@@ -566,7 +568,7 @@ int attend_i8(nd_ctx *ctx, const nd_kv_geom *g, const void *kv, size_t kv_stride
               const int32_t *lo, const int32_t *hi, const float *q, float scale, int quant_query,
               float *out, float *fixed, size_t fixed_floats)
 {
-    if (int rc = nd::enter(ctx)) return rc;
+    ND_ENTER(ctx);
     if (int rc = check_geom(g)) return rc;
     if (count == 0) return ND_OK;
     ND_REQUIRE(kv && lo && hi && q && out, "null buffer");

@@ -17,6 +17,9 @@ struct nd_cq {
     float *norms = nullptr;       // device [out][num_groups]
     float *lut = nullptr;         // device [256][per_byte] (empty for 3-bit)
     float *lv = nullptr;          // device levels[16]
+    // Rows from which a 2-bit / ternary matvec takes the fp4 matrix-core
+    // kernel; set once when the weight is created.
+    size_t fp4_min_rows = 0;
 };
 
 // f16 -> f32, exact: subnormals, infinities and NaN included (math.rs:53-68).

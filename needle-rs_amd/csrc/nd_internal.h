@@ -10,6 +10,7 @@
 #include <string>
 
 #include "needle_amd.h"
+#include "nd_owner.h"
 
 struct nd_ctx {
     int device = 0;
@@ -17,9 +18,11 @@ struct nd_ctx {
     bool owns_stream = false;
     int num_cus = 0;
     // Growable device workspace for split-K partials.  Owned by the context,
-    // reused by every call on it; calls on one context are stream-ordered.
+    // reused by every call on it; calls on one context are stream-ordered,
+    // and only one host thread is inside a call on it at a time (`owner`).
     void *work = nullptr;
     size_t work_bytes = 0;
+    nd::Owner owner;
 };
 
 namespace nd {
@@ -31,8 +34,43 @@ void clear_error();
 // Maps a failed HIP call to ND_ERR_HIP with the call's text.
 int hip_fail(hipError_t e, const char *what);
 
-// Makes the context's device current; returns ND_OK or an error.
-int enter(nd_ctx *ctx);
+// owner_claim with an error: ND_ERR_BUSY if another thread is inside a call
+// on the object (`what` names it in the message); release() undoes one claim.
+int claim(Owner &o, const char *what);
+inline void release(Owner &o) { owner_release(o); }
+
+// The scope of one entry-point call on a context: claims the context for
+// the calling thread and makes its device current; `rc` is ND_OK or the
+// error.  The claim ends with the scope.
+class Entry {
+public:
+    explicit Entry(nd_ctx *ctx);
+    ~Entry();
+    Entry(const Entry &) = delete;
+    Entry &operator=(const Entry &) = delete;
+    int rc = ND_OK;
+
+private:
+    nd_ctx *ctx_ = nullptr;
+};
+
+// The same for an object other than a context (a batch).
+class Hold {
+public:
+    Hold(Owner &o, const char *what) : o_(o), rc(claim(o, what)) {}
+    ~Hold()
+    {
+        if (rc == ND_OK) release(o_);
+    }
+    Hold(const Hold &) = delete;
+    Hold &operator=(const Hold &) = delete;
+
+private:
+    Owner &o_;
+
+public:
+    int rc;
+};
 
 // Ensures the context workspace holds at least `bytes`.
 int workspace(nd_ctx *ctx, size_t bytes, void **out);
@@ -53,6 +91,11 @@ inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
         hipError_t e_ = (call);                             \
         if (e_ != hipSuccess) return nd::hip_fail(e_, #call); \
     } while (0)
+
+// First statement of an entry point that takes a context.
+#define ND_ENTER(ctx)              \
+    nd::Entry nd_entry_(ctx);      \
+    if (nd_entry_.rc) return nd_entry_.rc
 
 #define ND_REQUIRE(cond, ...)                                  \
     do {                                                       \

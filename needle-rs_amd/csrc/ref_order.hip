@@ -331,7 +331,7 @@ int nd_cq_exact_multi(nd_ctx *ctx, hipStream_t stream, int n, const nd_cq *const
                       const float *const *xhs, size_t batch, const size_t *row_start,
                       const size_t *rows, float *const *y, const char *what, float half_inv)
 {
-    if (int rc = nd::enter(ctx)) return rc;
+    ND_ENTER(ctx);
     ND_REQUIRE(n >= 1 && n <= kMaxSet && w && xhs && row_start && rows && y, "%s: bad arguments",
                what);
     if (batch == 0) return ND_OK;
@@ -1008,7 +1008,7 @@ extern "C" {
 
 int nd_fold_rows(nd_ctx *ctx, const float *x, size_t rows, size_t n, float *y)
 {
-    if (int rc = nd::enter(ctx)) return rc;
+    ND_ENTER(ctx);
     ND_REQUIRE(n >= 1 && n <= size_t(kFoldRowMax), "fold_rows: n %zu outside 1..%d", n, kFoldRowMax);
     if (rows == 0) return ND_OK;
     ND_REQUIRE(x && y, "fold_rows: null buffer");
@@ -1055,7 +1055,7 @@ int nd_attend_exact_rows(nd_ctx *ctx, const nd_kv_geom *g, const void *kv, size_
                          const float *q, float scale, int quant_query, float *out,
                          const float *gate, int kv_f32)
 {
-    if (int rc = nd::enter(ctx)) return rc;
+    ND_ENTER(ctx);
     ND_REQUIRE(rows_per_block >= 1, "rows_per_block %d", rows_per_block);
     ND_REQUIRE(!gate || g->v_head_dim == 64, "the gated epilogue needs v_head_dim 64, not %d",
                g->v_head_dim);

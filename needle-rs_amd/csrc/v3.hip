@@ -1449,6 +1449,8 @@ struct nd_v3_batch {
     size_t step_bytes = 0;
     int32_t *next_host = nullptr;
     std::vector<void *> mem;
+    // the host thread inside a call on this batch (one at a time)
+    nd::Owner owner;
     // With `graphs` (off unless asked for), one decode position per session
     // replays a captured graph of the step's kernels on `gstream`: captured on
     // the second such step (the first, eager, has sized everything the
@@ -1564,7 +1566,7 @@ extern "C" {
 int nd_v3_model_create(nd_ctx *ctx, const nd_v3_cfg *cfg, const float *codebook,
                        size_t codebook_len, const nd_v3_record *recs, size_t n, nd_v3_model **out)
 {
-    if (int rc = nd::enter(ctx)) return rc;
+    ND_ENTER(ctx);
     ND_REQUIRE(cfg && recs && out && codebook, "null argument");
     ND_REQUIRE(codebook_len == 28, "codebook must be 28 floats (got %zu)", codebook_len);
     *out = nullptr;
@@ -1831,7 +1833,7 @@ int nd_v3_batch_create_chunked(nd_ctx *ctx, const nd_v3_model *m, size_t session
 int nd_v3_batch_create_ex(nd_ctx *ctx, const nd_v3_model *m, size_t sessions, size_t max_len,
                           size_t hint, size_t max_chunk, int kv_int8, nd_v3_batch **out)
 {
-    if (int rc = nd::enter(ctx)) return rc;
+    ND_ENTER(ctx);
     ND_REQUIRE(m && out, "null argument");
     *out = nullptr;
     const nd_v3_cfg &c = m->cfg;
@@ -2008,6 +2010,8 @@ int nd_v3_batch_set_graphs(nd_v3_batch *b, int on)
 {
     nd::clear_error();
     ND_REQUIRE(b, "null batch");
+    nd::Hold hold(b->owner, "the batch");
+    if (hold.rc) return hold.rc;
     ND_HIP(hipSetDevice(b->device));
     if (!on && b->graph_exec) {
         ND_HIP(hipDeviceSynchronize());
@@ -2022,13 +2026,15 @@ int nd_v3_positions(const nd_v3_batch *b, int32_t *pos)
 {
     nd::clear_error();
     ND_REQUIRE(b && pos, "null argument");
+    nd::Hold hold(const_cast<nd_v3_batch *>(b)->owner, "the batch");
+    if (hold.rc) return hold.rc;
     for (int i = 0; i < b->B; ++i) pos[i] = b->s[i].pos;
     return ND_OK;
 }
 
 int nd_libm_map(nd_ctx *ctx, int fn, const float *x, size_t n, float *y)
 {
-    if (int rc = nd::enter(ctx)) return rc;
+    ND_ENTER(ctx);
     ND_REQUIRE(fn >= 0 && fn <= 2, "libm function %d (0 expf, 1 logf, 2 sigmoid)", fn);
     if (n == 0) return ND_OK;
     ND_REQUIRE(x && y, "null buffer");
@@ -2040,7 +2046,7 @@ int nd_libm_map(nd_ctx *ctx, int fn, const float *x, size_t n, float *y)
 
 int nd_argmax_rows(nd_ctx *ctx, const float *x, size_t count, size_t n, int32_t *out)
 {
-    if (int rc = nd::enter(ctx)) return rc;
+    ND_ENTER(ctx);
     if (count == 0) return ND_OK;
     ND_REQUIRE(x && out, "argmax_rows: null buffer");
     ND_REQUIRE(n >= 1 && n <= 0x7fffffffu, "argmax_rows: row length %zu outside 1..2^31-1", n);
@@ -2084,7 +2090,7 @@ struct StepRun {
 
 int StepRun::begin(const int32_t *tokens)
 {
-    if (int rc = nd::enter(ctx)) return rc;
+    ND_ENTER(ctx);
     ND_REQUIRE(m && b && tokens, "null argument");
     ND_REQUIRE(C >= 1 && C <= b->chunk, "%d positions per step; the batch takes at most %d", C,
                b->chunk);
@@ -2447,6 +2453,11 @@ int StepRun::enqueue(int phase, bool argmax)
 int step_impl(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *tokens, int C,
               int32_t *next, float *logits)
 {
+    // the context and the batch belong to this thread for the whole step
+    ND_ENTER(ctx);
+    ND_REQUIRE(b, "null batch");
+    nd::Hold hold(b->owner, "the batch");
+    if (hold.rc) return hold.rc;
     StepRun r{ctx, m, b, C};
     if (int rc = r.begin(tokens)) return rc;
     const int S = r.S, L = r.L;

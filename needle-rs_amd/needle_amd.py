@@ -23,7 +23,7 @@ HEADER = os.path.join(os.path.dirname(HERE), "include", "needle_amd.h")
 
 ND_OK = 0
 ND_ERR_ARG, ND_ERR_CACT, ND_ERR_V3_GEOMETRY, ND_ERR_V3_LAYOUT = 1, 20, 21, 22
-ERRORS = {1: "ND_ERR_ARG", 2: "ND_ERR_HIP", 3: "ND_ERR_NOMEM", 11: "UnsupportedBits",
+ERRORS = {1: "ND_ERR_ARG", 2: "ND_ERR_HIP", 3: "ND_ERR_NOMEM", 4: "ND_ERR_BUSY", 11: "UnsupportedBits",
           12: "BadGroup", 13: "BadCodebookLen", 14: "ShortBlob", 15: "EmptyShape",
           20: "CactError", 21: "V3GeometryError", 22: "V3LayoutError"}
 
@@ -720,13 +720,17 @@ class V3Batch:
     int8 KV caches (kv_int8=True, KvPrecision::Int8) or f32 ones
     (KvPrecision::F32, needle_v3_generate's default); with max_chunk > 1 a
     prompt is prefilled up to max_chunk positions per pass (the reference's
-    chunked prefill, bit-identical to stepping)."""
+    chunked prefill, bit-identical to stepping).  The batch is stepped
+    through `ctx` (the model's context by default): a model is shared by any
+    number of threads, each stepping its own batches through its own
+    context."""
 
-    def __init__(self, model, sessions, max_len, hint=None, max_chunk=1, kv_int8=True):
+    def __init__(self, model, sessions, max_len, hint=None, max_chunk=1, kv_int8=True, ctx=None):
         self.model, self.sessions, self.max_chunk = model, sessions, max_chunk
+        self.ctx = ctx if ctx is not None else model.ctx
         self.kv_int8 = bool(kv_int8)
         h = C.c_void_p()
-        _check(lib().nd_v3_batch_create_ex(model.ctx.h, model.h, sessions, max_len,
+        _check(lib().nd_v3_batch_create_ex(self.ctx.h, model.h, sessions, max_len,
                                            hint or max_len, max_chunk, int(self.kv_int8),
                                            C.byref(h)))
         self.h = h
@@ -759,7 +763,7 @@ class V3Batch:
         next tokens, and fills `logits` ([sessions][rows] device tensor) if given."""
         tok = np.ascontiguousarray(tokens, np.int32).reshape(self.sessions)
         nxt = np.zeros(self.sessions, np.int32) if want_next else None
-        _check(lib().nd_v3_step(self.model.ctx.h, self.model.h, self.h,
+        _check(lib().nd_v3_step(self.ctx.h, self.model.h, self.h,
                                 tok.ctypes.data_as(C.c_void_p),
                                 nxt.ctypes.data_as(C.c_void_p) if want_next else None,
                                 self._logits_arg(logits)))
@@ -770,7 +774,7 @@ class V3Batch:
         one pass (V3Model::prefill); returns the greedy token after the last."""
         tok = np.ascontiguousarray(tokens, np.int32).reshape(self.sessions, -1)
         nxt = np.zeros(self.sessions, np.int32) if want_next else None
-        _check(lib().nd_v3_prefill(self.model.ctx.h, self.model.h, self.h,
+        _check(lib().nd_v3_prefill(self.ctx.h, self.model.h, self.h,
                                    tok.ctypes.data_as(C.c_void_p), tok.shape[1],
                                    nxt.ctypes.data_as(C.c_void_p) if want_next else None,
                                    self._logits_arg(logits)))

@@ -554,16 +554,35 @@ void or_v3_norm_and_rope(float *buf, const float *scale, const float *cs, const 
     }
 }
 
-/* model.rs:378-394, with math.rs's libm powf / cos / sin (or_powf, or_cosf,
- * or_sinf: the msun algorithms libm 0.2.16 carries). */
+/* Which routines build the RoPE table.  OR_ROPE_LIBM (the default) is the
+ * reference's: libm 0.2.16's powf, cosf and sinf (model.rs:376-394), restated
+ * as or_powf / or_cosf / or_sinf.  The other two exist to measure how much the
+ * greedy tokens depend on those routines' last bits: OR_ROPE_POWF_CR takes
+ * the correctly rounded theta^e (from powl) wherever or_powf differs from it,
+ * and OR_ROPE_GLIBC the C library's powf, cosf and sinf. */
+static int rope_variant = OR_ROPE_LIBM;
+
+void or_v3_set_rope_variant(int variant) { rope_variant = variant; }
+
+static float rope_pow(float theta, float e)
+{
+    if (rope_variant == OR_ROPE_GLIBC)
+        return powf(theta, e);
+    if (rope_variant == OR_ROPE_POWF_CR)
+        return (float)powl((long double)theta, (long double)e);
+    return or_powf(theta, e);
+}
+
+/* model.rs:376-394 */
 void or_v3_rope_at(const or_v3_cfg *c, size_t pos, float *cs, float *sn)
 {
     size_t half = c->qk_head_dim / 2;
+    int glibc = rope_variant == OR_ROPE_GLIBC;
     for (size_t i = 0; i < half; i++) {
-        float freq = 1.0f / or_powf(c->rope_theta, (float)(2 * i) / (float)c->qk_head_dim);
+        float freq = 1.0f / rope_pow(c->rope_theta, (float)(2 * i) / (float)c->qk_head_dim);
         float angle = (float)pos * freq;
-        cs[i] = or_cosf(angle);
-        sn[i] = or_sinf(angle);
+        cs[i] = glibc ? cosf(angle) : or_cosf(angle);
+        sn[i] = glibc ? sinf(angle) : or_sinf(angle);
     }
 }
 

@@ -113,6 +113,13 @@ void or_engram_indices(const uint32_t *tokens, size_t seq, const size_t *orders,
                        uint32_t *out);
 int or_ngram_valid(size_t p, size_t table, const size_t *orders, size_t heads);
 void or_v3_rope_at(const or_v3_cfg *c, size_t pos, float *cs, float *sn);
+/* The routines behind the RoPE table (process-wide; tests only):
+ * OR_ROPE_LIBM, the reference's (the default); OR_ROPE_POWF_CR, theta^e
+ * correctly rounded; OR_ROPE_GLIBC, the C library's powf/cosf/sinf. */
+#define OR_ROPE_LIBM 0
+#define OR_ROPE_POWF_CR 1
+#define OR_ROPE_GLIBC 2
+void or_v3_set_rope_variant(int variant);
 void or_v3_apply_site(float *x, const float *k, const float *v, size_t d);
 void or_v3_conv_step(float *tail, const float *taps, float *raw, size_t dim, size_t n_taps,
                      size_t pos);

@@ -554,6 +554,8 @@ def _v3_lib():
         L.or_ngram_valid.argtypes = [_sz, _sz, np.ctypeslib.ndpointer(np.uintp), _sz]
         L.or_ngram_valid.restype = C.c_int
         L.or_v3_rope_at.argtypes = [C.POINTER(V3Cfg), _sz, _f32p, _f32p]
+        L.or_v3_set_rope_variant.argtypes = [C.c_int]
+        L.or_v3_set_rope_variant.restype = None
         L.or_v3_apply_site.argtypes = [_f32p, _f32p, _f32p, _sz]
         L.or_v3_conv_step.argtypes = [_f32p, _f32p, _f32p, _sz, _sz, _sz]
         L.or_v3_engram_conv_step.argtypes = [_f32p, _f32p, _f32p, _sz, _sz, _sz, _sz, _sz]
@@ -669,6 +671,16 @@ def engram_indices(tokens, orders, heads, slots, seed_heads=0):
 
 def ngram_valid(p, table, orders, heads):
     return bool(_v3_lib().or_ngram_valid(p, table, np.ascontiguousarray(orders, np.uintp), heads))
+
+
+ROPE_LIBM, ROPE_POWF_CR, ROPE_GLIBC = 0, 1, 2
+
+
+def set_rope_variant(variant):
+    """The routines behind the oracle's RoPE table: ROPE_LIBM (the
+    reference's libm 0.2.16 restated; the default), ROPE_POWF_CR (theta^e
+    correctly rounded) or ROPE_GLIBC (the C library's powf/cosf/sinf)."""
+    _v3_lib().or_v3_set_rope_variant(int(variant))
 
 
 def rope_at(geom, pos):

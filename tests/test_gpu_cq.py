@@ -237,6 +237,14 @@ def test_matvec_fp4_cores_non_finite(ctx, fp4_from_16k, bits):
     y = host(gb.matvec_rows_prepared(dev(x), 0, out))
     want = ob.matvec_rows_prepared(x, 0, out)
     assert np.all(np.isfinite(want)) and _close(y, want)
+    # 8e36: -20 * 8e36 is finite, but a piece of it times a plane value
+    # (up to 4), summed over a group, is not; the block is past the matrix
+    # cores' headroom and takes the plain path, and the rows stay finite
+    x = base.copy()
+    x[200] = np.float32(8e36)
+    y = host(gb.matvec_rows_prepared(dev(x), 0, out))
+    want = ob.matvec_rows_prepared(x, 0, out)
+    assert np.all(np.isfinite(want)) and _close(y, want)
     gb.close()
     # and a finite activation afterwards takes the matrix cores again
     y = host(g.matvec_prepared(dev(base)))
@@ -244,15 +252,19 @@ def test_matvec_fp4_cores_non_finite(ctx, fp4_from_16k, bits):
     g.close()
 
 
-def test_matvec_fp4_cores_default_bound(ctx):
+def test_matvec_fp4_cores_default_bound(ctx, monkeypatch):
     """700,001 rows of in 768 take the fp4 kernel with no override: against
     the oracle, and bit for bit against two halves of 350,000-odd rows run
-    on the same kernel (a row's arithmetic does not depend on its tile or
-    lane)."""
+    on the same kernel by a weight created with the bound lowered (a row's
+    arithmetic does not depend on its tile or lane).  The bound is read when
+    a weight is created."""
+    monkeypatch.delenv("NEEDLE_AMD_CQ_FP4_MIN_ROWS", raising=False)
     rng = np.random.default_rng(700001)
     out, inn = 700001, 768
     blob = _tall_blob(rng, out, inn)
     g = nd.CqWeight(ctx, blob, out, inn, 128, 2, REAL_CB)
+    monkeypatch.setenv("NEEDLE_AMD_CQ_FP4_MIN_ROWS", "16384")
+    g16 = nd.CqWeight(ctx, blob, out, inn, 128, 2, REAL_CB)
     o = O.CqWeight(blob, out, inn, 128, 2, REAL_CB)
     del blob
     x = rng.normal(size=inn).astype(np.float32)
@@ -260,11 +272,10 @@ def test_matvec_fp4_cores_default_bound(ctx):
     y = host(g.matvec_prepared(xh))
     assert _close(y, o.matvec(x))
     half = out // 2
-    os.environ["NEEDLE_AMD_CQ_FP4_MIN_ROWS"] = "16384"
-    try:
-        lo = host(g.matvec_rows_prepared(xh, 0, half))
-        hi = host(g.matvec_rows_prepared(xh, half, out - half))
-    finally:
-        del os.environ["NEEDLE_AMD_CQ_FP4_MIN_ROWS"]
+    lo = host(g16.matvec_rows_prepared(xh, 0, half))
+    hi = host(g16.matvec_rows_prepared(xh, half, out - half))
     assert np.array_equal(np.concatenate([lo, hi]).view(np.uint32), y.view(np.uint32))
+    # the default-bound weight keeps its bound whatever the variable says now
+    assert np.array_equal(host(g.matvec_prepared(xh)).view(np.uint32), y.view(np.uint32))
+    g16.close()
     g.close()
