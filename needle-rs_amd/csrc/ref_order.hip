@@ -949,30 +949,39 @@ __global__ __launch_bounds__(kAttn2Threads, 4) void attn_exact2_kernel(
         }
     } else {
         const float *col = prod + (tid < g.VD ? tid : 0) * TS;
+        // whole chunks inside the loop, each group's adds waiting for that
+        // group's reads only (the next group's are in flight); a ragged last
+        // chunk after it, once no producer writes its buffer any more
+        const int nfull = span / T;
         for (int k = 0; k < steps; ++k) {
             const int c = k - 1;
-            if (c >= 0 && c < nch && tid < g.VD) {
+            if (c >= 0 && c < nfull && tid < g.VD) {
                 __builtin_amdgcn_s_setprio(2);
-                // T / 16 groups of 16 products, read into two register sets
-                // in turn so that a group's reads are in flight while the one
-                // before it is added
                 const float *buf = col + (c & 1) * kProdBuf;
-                const int rem = span - c * T;
                 float4 a[4], b[4];
                 nd_lds_read16(a, buf);
 #pragma unroll
                 for (int gi = 0; gi < T / 16; ++gi) {
                     if (gi % 2 == 0) {
                         if (gi + 1 < T / 16) nd_lds_read16(b, buf + (gi + 1) * 16);
-                        acc = nd_add_first(acc, a, rem - gi * 16);
+                        acc = nd_add16(acc, a);
                     } else {
                         if (gi + 1 < T / 16) nd_lds_read16(a, buf + (gi + 1) * 16);
-                        acc = nd_add_first(acc, b, rem - gi * 16);
+                        acc = nd_add16(acc, b);
                     }
                 }
                 __builtin_amdgcn_s_setprio(0);
             }
             __syncthreads();
+        }
+        if (nfull < nch && tid < g.VD) {
+            const float *buf = col + (nfull & 1) * kProdBuf;
+            const int rem = span - nfull * T;
+            for (int gi = 0; gi * 16 < rem; ++gi) {
+                float4 a[4];
+                nd_lds_read16(a, buf + gi * 16);
+                acc = nd_add_first(acc, a, rem - gi * 16);
+            }
         }
     }
     if (tid < g.VD)
