@@ -496,12 +496,16 @@ def forward_runs(torch, nd, ctx, sessions, ctx_len, check=True):
     model = nd.V3Model(ctx, g, recs, S.CODEBOOK)
     out = {}
 
-    def run(B, prompt_len, steps, chunk, prompts=None):
+    def run(B, prompt_len, steps, chunk, prompts=None, device_loop=True):
+        """Prefill, then `steps` greedy steps; returns the prefill and decode
+        wall times and the tokens each step fed ([B][steps]).  device_loop:
+        the steps run as nd_v3_generate (each choice fed back on the
+        device); else as nd_v3_step calls that return each step's tokens to
+        the host, which feeds them back."""
         batch = nd.V3Batch(model, B, max_len=prompt_len + steps, max_chunk=chunk)
         if prompts is None:
             prompts = np.stack([S.prompt_tokens(prompt_len, 100 + i) for i in range(B)])
         prompts = np.ascontiguousarray(prompts, np.int32)
-        toks = []
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         nxt = None
@@ -511,35 +515,53 @@ def forward_runs(torch, nd, ctx, sessions, ctx_len, check=True):
         torch.cuda.synchronize()
         t_pre = time.perf_counter() - t0
         t0 = time.perf_counter()
-        for _ in range(steps):
-            toks.append(nxt)
-            nxt = batch.step(nxt)
+        if device_loop:
+            out = batch.greedy(nxt, steps)
+            toks = np.concatenate([nxt[:, None], out[:, :-1]], axis=1)
+        else:
+            toks = []
+            for _ in range(steps):
+                toks.append(nxt)
+                nxt = batch.step(nxt)
+            toks = np.stack(toks, axis=1)
         t_dec = time.perf_counter() - t0
         batch.close()
-        return t_pre, t_dec, np.stack(toks, axis=1)
+        return t_pre, t_dec, toks
 
     # warm, untimed: code objects, and about half a second of steps so the
     # clocks have left their idle state before the timed decode
     run(1, 16, 240, 16)
-    t_pre, t_dec, _ = run(1, 128, 256, 128)
+    run(1, 16, 240, 16, device_loop=False)
+    t_pre, t_dec, toks1 = run(1, 128, 256, 128)
+    _, t_dec_h, toks1_h = run(1, 128, 256, 128, device_loop=False)
     out["batch1_prompt128_greedy256"] = {
         "workload": "shipped Needle-3 geometry (20 layers, d 768, 12 q / 2 kv heads, vocab "
                     "8192), random init, Cactus-Quants weights, int8 KV; one session, "
-                    "128-token uniform prompt prefilled in one pass, then 256 greedy tokens",
+                    "128-token uniform prompt prefilled in one pass, then 256 greedy tokens "
+                    "(the greedy loop on the device, nd_v3_generate; host_stepped: one "
+                    "nd_v3_step call per token, its token back on the host)",
         "prefill_ms": round(t_pre * 1e3, 3),
         "prefill_ms_per_token": round(t_pre / 128 * 1e3, 4),
         "decode_ms_per_token": round(t_dec / 256 * 1e3, 3),
         "decode_tok_per_s": round(256 / t_dec, 1),
+        "decode_ms_per_token_host_stepped": round(t_dec_h / 256 * 1e3, 3),
+        "tokens_equal_host_stepped": bool(np.array_equal(toks1, toks1_h)),
     }
     steps = 128
     t_pre, t_dec, toks = run(sessions, ctx_len, steps, 32)
+    _, t_dec_h, toks_h = run(sessions, ctx_len, steps, 32, device_loop=False)
     key = f"sessions{sessions}_ctx{ctx_len}_greedy{steps}"
     out[key] = {
         "workload": f"{sessions} sessions of the same model in lockstep, each prefilled with "
                     f"{ctx_len} uniform prompt tokens (32 positions per pass), then {steps} greedy "
-                    "steps; projections batched over sessions, attention per session",
+                    "steps; projections batched over sessions, attention per session; the "
+                    "greedy loop on the device (nd_v3_generate), and host_stepped: one "
+                    "nd_v3_step call per step, the tokens back on the host",
         "decode_tok_per_s": round(sessions * steps / t_dec, 1),
         "decode_ms_per_step": round(t_dec / steps * 1e3, 3),
+        "decode_tok_per_s_host_stepped": round(sessions * steps / t_dec_h, 1),
+        "decode_ms_per_step_host_stepped": round(t_dec_h / steps * 1e3, 3),
+        "tokens_equal_host_stepped": bool(np.array_equal(toks, toks_h)),
         "prefill_tok_per_s": round(sessions * ctx_len / t_pre, 1),
     }
     if check:

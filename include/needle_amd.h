@@ -433,6 +433,22 @@ int nd_argmax_rows(nd_ctx *ctx, const float *x, size_t count, size_t n, int32_t 
 int nd_v3_prefill(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *tokens,
                   size_t count, int32_t *next, float *logits);
 
+/* The greedy loop of V3Engine::generate_with (needle-infer/src/
+ * v3_engine.rs:254-312, behind needle_v3_generate, needle-c/src/v3.rs:219-250)
+ * with temperature 0 and no stop tokens, for every session at once:
+ * `steps` single-position steps, the first feeding first[i] (host, [sessions];
+ * e.g. the `next` of the prompt's last prefill pass), each later one the
+ * greedy token of the step before.  tokens (host, [sessions][steps],
+ * session-major) receives each step's greedy token: first[i] followed by
+ * tokens[i][..] is the reference's out_tokens.  The choices stay on the
+ * device between steps (the Engram hash of the retained ids runs there
+ * too), so the device does not wait for the host between steps; the
+ * tokens, caches and positions afterwards equal `steps` nd_v3_step calls
+ * that feed back `next`, bit for bit.  Sessions do not stop early: a caller
+ * with stop tokens truncates each row at its first one. */
+int nd_v3_generate(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *first,
+                   size_t steps, int32_t *tokens);
+
 /* ---- the .cact v3 container (needle-infer/src/cact.rs, v3.rs) ----------- */
 
 /* Reads a Needle-3 container held in host memory (`bytes`, `len`): the

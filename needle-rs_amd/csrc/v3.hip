@@ -1262,7 +1262,7 @@ __device__ inline void argmax_take(float &best, int &bi, float v, int i)
 }
 
 __global__ __launch_bounds__(kT) void k_argmax(const float *__restrict__ logits, int rows,
-                                              int32_t *__restrict__ next)
+                                              int32_t *__restrict__ next, int32_t *__restrict__ also)
 {
     __shared__ float sv[kT / 64];
     __shared__ int si[kT / 64];
@@ -1316,7 +1316,54 @@ __global__ __launch_bounds__(kT) void k_argmax(const float *__restrict__ logits,
     if (threadIdx.x == 0) {
         for (int k = 1; k < kT / 64; ++k) argmax_take(best, bi, sv[k], si[k]);
         next[b] = bi;
+        if (also) also[b] = bi;
     }
+}
+
+// ---- a step's tokens from the device (nd_v3_generate): each session's
+// token is the previous step's greedy choice.  Per session: the clamped id
+// for the embedding row (model.rs:196-200), the token pushed into the
+// retained history (cache.rs:283-289; kept right-aligned, the newest at
+// mo - 1, so that at position pos the history holds min(pos + 1, mo) ids),
+// and the Engram table rows hashed from it (engram.rs:30-67), -1 where an
+// order reaches before position 0.
+constexpr int kMaxOrders = 8;
+struct StepTokens {
+    const int32_t *src;  // [S]
+    const int32_t *pos;  // [S]
+    int32_t *tok;        // [S]
+    int32_t *hist;       // [S][mo]
+    int32_t *rows;       // [S][n_orders * e_heads]
+    int S, mo, vocab, n_orders, e_heads, stride, e_slots;
+    int orders[kMaxOrders];
+};
+
+__global__ void k_step_tokens(StepTokens a)
+{
+    const int row = int(blockIdx.x * blockDim.x + threadIdx.x);
+    if (row >= a.S) return;
+    const uint32_t tok = uint32_t(a.src[row]);
+    int32_t *h = a.hist + size_t(row) * a.mo;
+    for (int j = 0; j + 1 < a.mo; ++j) h[j] = h[j + 1];
+    h[a.mo - 1] = int32_t(tok);
+    a.tok[row] = int32_t(tok < uint32_t(a.vocab) ? tok : uint32_t(a.vocab - 1));
+    const int pos = a.pos[row];
+    const int here = (pos + 1 < a.mo ? pos + 1 : a.mo) - 1;
+    const int nt = a.n_orders * a.e_heads;
+    for (int oi = 0; oi < a.n_orders; ++oi)
+        for (int hh = 0; hh < a.e_heads; ++hh) {
+            const int table = oi * a.e_heads + hh;
+            uint32_t acc = 0x9E3779B9u * uint32_t(oi * a.stride + hh + 1);
+            for (int j = 0; j < a.orders[oi]; ++j) {
+                const uint32_t t2 = j > here ? 0u : uint32_t(h[a.mo - 1 - j]);
+                acc = (acc ^ t2) * 0x01000193u;
+            }
+            acc ^= acc >> 15;
+            const uint32_t slot = acc % uint32_t(a.e_slots);
+            const bool valid = pos + 1 >= a.orders[oi];
+            a.rows[size_t(row) * nt + table] =
+                valid ? int32_t(uint32_t(table) * uint32_t(a.e_slots) + slot) : -1;
+        }
 }
 
 // ---------------------------------------------------------------------------
@@ -1430,6 +1477,12 @@ struct nd_v3_batch {
     float *qn = nullptr, *evc = nullptr;
     size_t fh_width = 0;  // floats per row of a site's prepared key input
     int32_t *next = nullptr;
+    // nd_v3_generate: each session's retained token ids on the device
+    // ([B][mo], right-aligned), and the steps' greedy tokens ([steps][B],
+    // grown on demand, owned here)
+    int32_t *hist_dev = nullptr;
+    int32_t *gen_out = nullptr;
+    size_t gen_cap = 0;
     // The scatter-up gates of a layer depend only on its input lanes: they
     // run on `side` while the layer's attention and MLP run on the caller's
     // stream; ev_in[l % 2] marks a layer's input ready, ev_gates[l % 2] its
@@ -1473,6 +1526,7 @@ struct nd_v3_batch {
         if (side) (void)hipStreamSynchronize(side);
         for (int i = 0; i < kStages; ++i)
             if (stage_pending[i]) (void)hipEventSynchronize(stage_done[i]);
+        if (gen_out) (void)hipFree(gen_out);
         for (void *p : mem) (void)hipFree(p);  // hipFree waits for the device's work
         for (int i = 0; i < kStages; ++i) {
             if (stage_host[i]) (void)hipHostFree(stage_host[i]);
@@ -1950,6 +2004,7 @@ int nd_v3_batch_create_ex(nd_ctx *ctx, const nd_v3_model *m, size_t sessions, si
     A(gstate, size_t(B) * 64);
     A(graw, size_t(B) * (nl + nl * nl));
     A(next, size_t(S));
+    A(hist_dev, size_t(S) * max_order(c));
     if (b->chunk > 1) {
         A(qn, size_t(B) * qd);
         A(evc, size_t(c.n_sites > 0 ? c.n_sites : 1) * B * d);
@@ -2051,7 +2106,8 @@ int nd_argmax_rows(nd_ctx *ctx, const float *x, size_t count, size_t n, int32_t 
     ND_REQUIRE(x && out, "argmax_rows: null buffer");
     ND_REQUIRE(n >= 1 && n <= 0x7fffffffu, "argmax_rows: row length %zu outside 1..2^31-1", n);
     ND_REQUIRE(count <= 0x7fffffffu, "argmax_rows: %zu rows", count);
-    hipLaunchKernelGGL(k_argmax, dim3(unsigned(count)), dim3(kT), 0, ctx->stream, x, int(n), out);
+    hipLaunchKernelGGL(k_argmax, dim3(unsigned(count)), dim3(kT), 0, ctx->stream, x, int(n), out,
+                       nullptr);
     return nd::check_launch("argmax_rows");
 }
 
@@ -2083,6 +2139,9 @@ struct StepRun {
     bool gate_fused = false, gates_in = false;
     const nd_cq *phi = nullptr, *fpo = nullptr, *fre = nullptr;
     float *ev_conv = nullptr;  // [sites][Rcap][d], after the conv
+    // tokens == nullptr: this step's tokens are b->next on the device (the
+    // previous step's choices); the greedy choices are also written here
+    int32_t *argmax_also = nullptr;
 
     int begin(const int32_t *tokens);
     int enqueue(int phase, bool argmax);
@@ -2091,9 +2150,11 @@ struct StepRun {
 int StepRun::begin(const int32_t *tokens)
 {
     ND_ENTER(ctx);
-    ND_REQUIRE(m && b && tokens, "null argument");
+    ND_REQUIRE(m && b, "null argument");
+    const bool dev_tokens = tokens == nullptr;
     ND_REQUIRE(C >= 1 && C <= b->chunk, "%d positions per step; the batch takes at most %d", C,
                b->chunk);
+    ND_REQUIRE(!dev_tokens || C == 1, "device tokens take one position per step");
     const nd_v3_cfg &c = m->cfg;
     S = b->B;
     B = S * C;
@@ -2122,17 +2183,18 @@ int StepRun::begin(const int32_t *tokens)
         const int i = row;  // buffer row: session row / C, position pos + row % C
         SessionHost &sh = b->s[row / C];
         const int pos = sh.pos + row % C;
+        h_pos[i] = pos;
+        h_hi[i] = pos;
+        const int stride = c.e_seed_heads == 0 ? c.e_heads : c.e_seed_heads;
+        if (!dev_tokens) {
         const uint32_t tok = uint32_t(tokens[row]);
         // cache.rs:283-289 push_token, keeping max(order) ids
         sh.hist.push_back(tok);
         if (int(sh.hist.size()) > mo) sh.hist.erase(sh.hist.begin());
         // model.rs:196-200 embedding row of the clamped token
         h_tok[i] = int32_t(tok < uint32_t(c.vocab_size) ? tok : uint32_t(c.vocab_size - 1));
-        h_pos[i] = pos;
-        h_hi[i] = pos;
         // engram.rs:30-67 hash of the retained history at its last position
         const int here = int(sh.hist.size()) - 1;
-        const int stride = c.e_seed_heads == 0 ? c.e_heads : c.e_seed_heads;
         for (int oi = 0; oi < c.n_orders; ++oi)
             for (int hh = 0; hh < c.e_heads; ++hh) {
                 const int table = oi * c.e_heads + hh;
@@ -2146,6 +2208,7 @@ int StepRun::begin(const int32_t *tokens)
                 const bool valid = pos + 1 >= c.orders[oi];
                 h_rows[size_t(i) * nt + table] = valid ? int32_t(uint32_t(table) * uint32_t(c.e_slots) + slot) : -1;
             }
+        }
         // cache.rs:291-331 ensure + span per layer
         for (int li = 0; li < L; ++li) {
             const int cap = b->cap[li];
@@ -2173,6 +2236,16 @@ int StepRun::begin(const int32_t *tokens)
     b->stage_pending[stage] = true;
     b->stage_next = (stage + 1) % nd_v3_batch::kStages;
     st = ctx->stream;
+    if (dev_tokens) {
+        // the tokens, history and Engram rows from the previous step's choices
+        ND_REQUIRE(c.n_orders <= kMaxOrders, "%d Engram orders", int(c.n_orders));
+        StepTokens a{b->next, pos_dev, tok_dev, b->hist_dev, rows_dev, S, mo, int(c.vocab_size),
+                     int(c.n_orders), int(c.e_heads),
+                     int(c.e_seed_heads == 0 ? c.e_heads : c.e_seed_heads), int(c.e_slots), {}};
+        for (int oi = 0; oi < c.n_orders; ++oi) a.orders[oi] = c.orders[oi];
+        hipLaunchKernelGGL(k_step_tokens, dim3(unsigned((S + 63) / 64)), dim3(64), 0, st, a);
+        if (int rc = nd::check_launch("k_step_tokens")) return rc;
+    }
     qk_scale = 1.0f / std::sqrt(float(c.qk_head_dim));
     kf = b->kv_f32 ? 1 : 0;
     gate_fused = c.v_head_dim == 64 && m->pre_attn.group == 128 &&
@@ -2442,7 +2515,8 @@ int StepRun::enqueue(int phase, bool argmax)
     LCHK("k_final");
     CK(project(ctx, m->embedding, b->xh, S, 0, rows, b->logits));
     if (argmax) {
-        hipLaunchKernelGGL(k_argmax, dim3(S), dim3(kT), 0, st, b->logits, int(rows), b->next);
+        hipLaunchKernelGGL(k_argmax, dim3(S), dim3(kT), 0, st, b->logits, int(rows), b->next,
+                           argmax_also);
         LCHK("k_argmax");
     }
     return ND_OK;
@@ -2550,6 +2624,68 @@ int nd_v3_prefill(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32
     nd::clear_error();
     ND_REQUIRE(count >= 1 && count <= 256, "count %zu out of 1..256", count);
     return step_impl(ctx, m, b, tokens, int(count), next, logits);
+}
+
+int nd_v3_generate(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *first,
+                   size_t steps, int32_t *tokens)
+{
+    ND_ENTER(ctx);
+    ND_REQUIRE(m && b && first && tokens, "null argument");
+    nd::Hold hold(b->owner, "the batch");
+    if (hold.rc) return hold.rc;
+    if (steps == 0) return ND_OK;
+    const int S = b->B;
+    ND_REQUIRE(b->chunk >= 1, "batch without steps");
+    for (int i = 0; i < S; ++i)
+        ND_REQUIRE(size_t(b->s[i].pos) + steps <= size_t(b->max_len), "session %d: %zu steps from "
+                   "position %d pass its %d positions", i, steps, b->s[i].pos, b->max_len);
+    const int mo = max_order(m->cfg);
+    const size_t n_out = steps * size_t(S);
+    if (n_out > b->gen_cap) {
+        ND_HIP(hipStreamSynchronize(ctx->stream));
+        if (b->gen_out) ND_HIP(hipFree(b->gen_out));
+        b->gen_out = nullptr;
+        b->gen_cap = 0;
+        ND_HIP(hipMalloc(&b->gen_out, n_out * sizeof(int32_t)));
+        b->gen_cap = n_out;
+    }
+    // the first tokens, and each session's retained ids, right-aligned
+    std::vector<int32_t> init(size_t(S) * (1 + mo), 0);
+    for (int i = 0; i < S; ++i) {
+        init[i] = first[i];
+        const std::vector<uint32_t> &hv = b->s[i].hist;
+        const int n = int(hv.size()) < mo ? int(hv.size()) : mo;
+        for (int j = 0; j < n; ++j)
+            init[S + size_t(i) * mo + (mo - n + j)] = int32_t(hv[hv.size() - n + j]);
+    }
+    ND_HIP(hipMemcpyAsync(b->next, init.data(), size_t(S) * 4, hipMemcpyHostToDevice, ctx->stream));
+    ND_HIP(hipMemcpyAsync(b->hist_dev, init.data() + S, size_t(S) * mo * 4, hipMemcpyHostToDevice,
+                          ctx->stream));
+    // steps enqueued back to back: the host runs ahead of the device up to
+    // the staging ring's depth, and no step waits for the host
+    int rc = ND_OK;
+    for (size_t k = 0; k < steps && rc == ND_OK; ++k) {
+        StepRun r{ctx, m, b, 1};
+        r.argmax_also = b->gen_out + k * S;
+        rc = r.begin(nullptr);
+        for (int ph = -1; ph <= r.L && rc == ND_OK; ++ph) rc = r.enqueue(ph, true);
+        if (rc == ND_OK)
+            for (int i = 0; i < S; ++i) b->s[i].pos += 1;
+    }
+    if (rc != ND_OK) return rc;
+    std::vector<int32_t> got(n_out);
+    ND_HIP(hipMemcpyAsync(got.data(), b->gen_out, n_out * 4, hipMemcpyDeviceToHost, ctx->stream));
+    ND_HIP(hipStreamSynchronize(ctx->stream));
+    for (int i = 0; i < S; ++i) {
+        // the host's copy of the retained ids: the tokens the steps fed
+        std::vector<uint32_t> &hv = b->s[i].hist;
+        for (size_t k = 0; k < steps; ++k) {
+            hv.push_back(uint32_t(k == 0 ? first[i] : got[(k - 1) * S + i]));
+            if (int(hv.size()) > mo) hv.erase(hv.begin());
+            tokens[size_t(i) * steps + k] = got[k * S + i];
+        }
+    }
+    return ND_OK;
 }
 
 

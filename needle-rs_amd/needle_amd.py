@@ -91,6 +91,7 @@ _SIGS = [
     ("nd_argmax_rows", C.c_int, [_vp, _vp, _sz, _sz, _vp]),
     ("nd_v3_batch_create_chunked", C.c_int, [_vp, _vp, _sz, _sz, _sz, _sz, C.POINTER(_vp)]),
     ("nd_v3_prefill", C.c_int, [_vp, _vp, _vp, _vp, _sz, _vp, _vp]),
+    ("nd_v3_generate", C.c_int, [_vp, _vp, _vp, _vp, _sz, _vp]),
     ("nd_v3_cact_config", C.c_int, [_vp, _sz, _vp, C.POINTER(_sz)]),
     ("nd_v3_model_from_cact", C.c_int, [_vp, _vp, _sz, C.POINTER(_vp)]),
     ("nd_v3_batch_set_graphs", C.c_int, [_vp, C.c_int]),
@@ -779,6 +780,17 @@ class V3Batch:
                                    nxt.ctypes.data_as(C.c_void_p) if want_next else None,
                                    self._logits_arg(logits)))
         return nxt
+
+    def greedy(self, first, steps):
+        """`steps` greedy steps from first[i] (V3Engine's loop, nd_v3_generate):
+        returns [sessions][steps], each step's choice; the device feeds each
+        step's choice to the next without a host round trip."""
+        tok = np.ascontiguousarray(first, np.int32).reshape(self.sessions)
+        out = np.zeros((self.sessions, steps), np.int32)
+        _check(lib().nd_v3_generate(self.ctx.h, self.model.h, self.h,
+                                    tok.ctypes.data_as(C.c_void_p), steps,
+                                    out.ctypes.data_as(C.c_void_p)))
+        return out
 
     def generate(self, prompts, steps):
         """Prefill each session's prompt, max_chunk positions per pass (or by
