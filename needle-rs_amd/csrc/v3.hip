@@ -48,11 +48,26 @@ __device__ inline float sigmoidf_(float x) { return nd_sigmoidf(x); }
 // loops and iterator sums, run by one thread over values already in LDS.
 // Products are formed in parallel beforehand; a product rounds the same
 // whether it is formed here or inside the fold.
+// A workgroup barrier that orders LDS only: it does not wait for the
+// global loads in flight (__syncthreads does), whose registers the compiler
+// waits for at their first use.
+__device__ inline void lds_barrier()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ inline float chain_sum(const float *p, int n)
 {
-    if ((reinterpret_cast<uintptr_t>(p) & 15) == 0) return nd_lds_fold(0.0f, p, n);
+    __builtin_amdgcn_s_setprio(2);
     float s = 0.0f;
-    for (int i = 0; i < n; ++i) s += p[i];
+    if ((reinterpret_cast<uintptr_t>(p) & 15) == 0) {
+        s = nd_lds_fold(0.0f, p, n);
+    } else {
+        for (int i = 0; i < n; ++i) s += p[i];
+    }
+    __builtin_amdgcn_s_setprio(0);
     return s;
 }
 
@@ -364,19 +379,24 @@ __global__ __launch_bounds__(NTH) void k_layer_in(LayerIn a)
     // the previous layer's lanes and block delta for this thread's channels
     constexpr int kUpLanes = 4;
     const bool up_regs = a.update && n <= kUpLanes;
-    float old[kCh][kUpLanes], yv[kCh];
+    // every lane loads (indices clamped, values past the ends unused), so
+    // no lane waits inside a branch of its own before the rest are issued
+    float old[kCh][kUpLanes], yv[kCh], gpv = 0.0f, grv = 0.0f;
+    if (a.update) {
+        gpv = a.gp[b * n + (tid < n ? tid : 0)];
+        grv = a.gr[b * n * n + (tid < n * n ? tid : 0)];
+    }
 #pragma unroll
     for (int k = 0; k < kCh; ++k) {
-        const int c = tid + k * NTH;
-        const bool on = up_regs && c < d;
-        yv[k] = on ? a.y[b * d + c] : 0.0f;
+        const int c = tid + k * NTH, cc = c < d ? c : 0;
+        yv[k] = up_regs ? a.y[b * d + cc] : 0.0f;
 #pragma unroll
-        for (int j = 0; j < kUpLanes; ++j) old[k][j] = on && j < n ? lg[size_t(j) * d + c] : 0.0f;
+        for (int j = 0; j < kUpLanes; ++j) old[k][j] = up_regs && j < n ? lg[size_t(j) * d + cc] : 0.0f;
     }
     if (a.update) {
-        if (tid < n) gpp[tid] = a.gp[b * n + tid];
-        if (tid < n * n) grr[tid] = a.gr[b * n * n + tid];
-        __syncthreads();
+        if (tid < n) gpp[tid] = gpv;
+        if (tid < n * n) grr[tid] = grv;
+        lds_barrier();
         if (up_regs) {
             // mhc.rs:140-151 from the preloaded values
 #pragma unroll
@@ -401,10 +421,10 @@ __global__ __launch_bounds__(NTH) void k_layer_in(LayerIn a)
     } else {
         for (int e = tid; e < nd; e += NTH) ln[e] = lg[e];
     }
-    __syncthreads();
+    lds_barrier();
     // rms_unit (kernels.rs:33-41): products, then one chain
     for (int e = tid; e < nd; e += NTH) nb[e] = ln[e] * ln[e];
-    __syncthreads();
+    lds_barrier();
     // operands needed after the chain, issued before lane 0 of wave 0 starts
     // folding: this thread's phi_pre group codes and norm, its channels'
     // norm_in / Engram key and value, the phi levels; values bound for LDS
@@ -441,12 +461,12 @@ __global__ __launch_bounds__(NTH) void k_layer_in(LayerIn a)
     float nin[kCh], ekv[kCh], evv[kCh];
 #pragma unroll
     for (int k = 0; k < kCh; ++k) {
-        const int c = tid + k * NTH;
-        nin[k] = c < d ? a.norm_in[c] : 0.0f;
-        ekv[k] = ek && c < d ? ek[c] : 0.0f;
-        evv[k] = ek && c < d ? a.ev[b * d + c] : 0.0f;
+        const int c = tid + k * NTH, cc = c < d ? c : 0;
+        nin[k] = a.norm_in[cc];
+        ekv[k] = ek ? ek[cc] : 0.0f;
+        evv[k] = ek ? a.ev[b * d + cc] : 0.0f;
     }
-    const float bpre = tid < n ? a.b_pre[tid] : 0.0f;
+    const float bpre = a.b_pre[tid < n ? tid : 0];
     float lvv = 0.0f;
     if (tid < 48) {
         const int k = tid & 15, w = tid >> 4;
@@ -466,7 +486,7 @@ __global__ __launch_bounds__(NTH) void k_layer_in(LayerIn a)
     for (int k = 0; k < kPhiPerThread; ++k)
         if (tid + k * NTH < pairs) pn[tid + k * NTH] = pnv[k];
     if (tid < 48) lvl[tid] = lvv;
-    __syncthreads();
+    lds_barrier();
     {
         // prepare_input of rms_unit(lanes): one wave per 128-group straight
         // from the lanes; the result goes to global nxh and, each group
@@ -497,14 +517,14 @@ __global__ __launch_bounds__(NTH) void k_layer_in(LayerIn a)
             }
         }
     }
-    __syncthreads();
+    lds_barrier();
     // this layer's phi rows (matvec_rows_prepared, reference order)
 #pragma unroll
     for (int k = 0; k < kPhiPerThread; ++k) {
         const int t = tid + k * NTH;
         if (t < pairs) gs[t] = cq_group_dot128<PP>(codes[k], lvl + 16 * wsel[k], nb + (t % G) * kPadGroup);
     }
-    __syncthreads();
+    lds_barrier();
     if (tid < prows) {
         float total = 0.0f;
         for (int g = 0; g < G; ++g) total += pn[tid * G + g] * gs[tid * G + g];
@@ -515,7 +535,7 @@ __global__ __launch_bounds__(NTH) void k_layer_in(LayerIn a)
             a.graw[b * (prows - n) + (tid - n)] = total;  // nx . phi_post, nx . phi_res
         }
     }
-    __syncthreads();
+    lds_barrier();
     // gated lane sum, Engram gate (engram.rs:111-132), ZCRMSNorm (norm.rs:23-30)
 #pragma unroll
     for (int k = 0; k < kCh; ++k) {
@@ -531,11 +551,11 @@ __global__ __launch_bounds__(NTH) void k_layer_in(LayerIn a)
             pc[c] = acc * ekv[k];
         }
     }
-    __syncthreads();
+    lds_barrier();
     if (ek) {
         // three sequential sums, side by side on lanes 0-2
         if (tid < 3) tot[1 + tid] = chain_sum(tid == 0 ? pa : (tid == 1 ? pb : pc), d);
-        __syncthreads();
+        lds_barrier();
         const float ux = 1.0f / sqrtf(tot[1] / float(d) + 1e-6f);
         const float uk = 1.0f / sqrtf(tot[2] / float(d) + 1e-6f);
         const float alpha = sigmoidf_(tot[3] * ux * uk / sqrtf(float(d)));
@@ -553,9 +573,9 @@ __global__ __launch_bounds__(NTH) void k_layer_in(LayerIn a)
             pa[c] = us[c] * us[c];
         }
     }
-    __syncthreads();
+    lds_barrier();
     if (tid == 0) tot[0] = chain_sum(pa, d);
-    __syncthreads();
+    lds_barrier();
     const float inv = 1.0f / sqrtf(tot[0] / float(d) + 1e-6f);
 #pragma unroll
     for (int k = 0; k < kCh; ++k) {
@@ -566,7 +586,7 @@ __global__ __launch_bounds__(NTH) void k_layer_in(LayerIn a)
         }
     }
     for (int c = d + tid; c < a.ph.in_padded; c += NTH) pa[c] = 0.0f;
-    __syncthreads();
+    lds_barrier();
     prepare_lds(pa, a.hh + b * a.ph.in_padded, a.ph.in_padded, a.ph.group, a.ph.inv, false);
 }
 
@@ -1082,18 +1102,23 @@ __global__ __launch_bounds__(1024) void k_post_hada(HadaArgs a, MhcIn mhc)
     const size_t b = blockIdx.x;
     const int tid = threadIdx.x, d = a.d, r = a.rank;
     // what the first chain and the step after it need, up front
+    // loads from a clamped channel (the values of threads past d are never
+    // used): a load under a condition becomes a branch whose first use waits
+    // for it at once
     const bool ch = tid < d;
-    const float pv = ch ? a.proj[b * d + tid] : 0.0f;
-    const float bxv = ch ? a.bx[b * d + tid] : 0.0f;
-    const float post_n = ch ? a.post_norm[tid] : 0.0f;
+    const int cc = ch ? tid : 0;
+    const float pv = a.proj[b * d + cc];
+    const float bxv = a.bx[b * d + cc];
+    const float post_n = a.post_norm[cc];
     // post-norm of the projection, gated residual, pre-MLP norm: two chains
     buf[tid] = pv * pv;
     if (tid == 0) zf = 0;
-    __syncthreads();
+    lds_barrier();
     if (tid == 0) tot[0] = chain_sum(buf, d);
-    // every other operand, issued while lane 0 of wave 0 folds
-    const float uv = ch ? a.u[b * d + tid] : 0.0f;
-    const float pre_n = ch ? a.pre_hada[tid] : 0.0f;
+    // every other operand, issued while lane 0 of wave 0 folds (its own
+    // after the chain; nothing waits for them before the Kronecker passes)
+    const float uv = a.u[b * d + cc];
+    const float pre_n = a.pre_hada[cc];
     const float d1 = a.d1[tid], d2 = a.d2[tid], b2 = a.b2[tid], d3 = a.d3[tid], d4 = a.d4[tid];
     const float w1a = a.w1a[tid], w1b = a.w1b[tid], w2a = a.w2a[tid], w2b = a.w2b[tid];
     const float w3a = a.w3a[tid], w3b = a.w3b[tid];
@@ -1102,14 +1127,12 @@ __global__ __launch_bounds__(1024) void k_post_hada(HadaArgs a, MhcIn mhc)
     float cv[kMaxCondRegs], cu[kMaxCondRegs];
 #pragma unroll
     for (int j = 0; j < kMaxCondRegs; ++j) {
-        cv[j] = regs && ch && j < r ? a.cond_v[tid * r + j] : 0.0f;
-        cu[j] = regs && j < r ? a.cond_u[j * 1024 + tid] : 0.0f;
+        const bool on = regs && j < r;
+        const float v = a.cond_v[on ? cc * r + j : 0], u = a.cond_u[on ? j * 1024 + tid : 0];
+        cv[j] = on ? v : 0.0f;
+        cu[j] = on ? u : 0.0f;
     }
-    {
-        const unsigned zb = unsigned(w1a == 0.0f) | unsigned(w2a == 0.0f) << 1 | unsigned(w3a == 0.0f) << 2;
-        if (zb) atomicOr(&zf, zb);
-    }
-    __syncthreads();
+    lds_barrier();
     if (ch) {
         const float inv = 1.0f / sqrtf(tot[0] / float(d) + 1e-6f);
         const float pn = (1.0f + post_n) * pv * inv;
@@ -1117,9 +1140,9 @@ __global__ __launch_bounds__(1024) void k_post_hada(HadaArgs a, MhcIn mhc)
         nbs[tid] = nb;
         z[tid] = nb * nb;
     }
-    __syncthreads();
+    lds_barrier();
     if (tid == 0) tot[1] = chain_sum(z, d);
-    __syncthreads();
+    lds_barrier();
     const float xv = ch ? (1.0f + pre_n) * nbs[tid] * (1.0f / sqrtf(tot[1] / float(d) + 1e-6f)) : 0.0f;
     // cond = 1 + softmax(x . cond_v) . cond_u.  Projection j is one chain
     // over the model dim, the r chains side by side on lanes 0..r-1 of wave
@@ -1129,12 +1152,12 @@ __global__ __launch_bounds__(1024) void k_post_hada(HadaArgs a, MhcIn mhc)
 #pragma unroll
             for (int j = 0; j < kMaxCondRegs; ++j)
                 if (j < r) prod[j * d + tid] = xv * cv[j];
-        __syncthreads();
+        lds_barrier();
         if (tid < r) proj[tid] = chain_sum(prod + tid * d, d);
     } else {
         // wide rank: products a chunk of rows at a time
         buf[tid] = xv;
-        __syncthreads();
+        lds_barrier();
         const int chn = kCondProd / r;
         float acc = 0.0f;
         for (int i0 = 0; i0 < d; i0 += chn) {
@@ -1143,14 +1166,14 @@ __global__ __launch_bounds__(1024) void k_post_hada(HadaArgs a, MhcIn mhc)
                 const int ii = e / r, j = e - ii * r;
                 prod[j * chn + ii] = buf[i0 + ii] * a.cond_v[(i0 + ii) * r + j];
             }
-            __syncthreads();
+            lds_barrier();
             if (tid < r)
                 for (int ii = 0; ii < ni; ++ii) acc += prod[tid * chn + ii];
-            __syncthreads();
+            lds_barrier();
         }
         if (tid < r) proj[tid] = acc;
     }
-    __syncthreads();
+    lds_barrier();
     if (tid < 64) {
         // softmax over the r projections: the max is order-free, each exp
         // on its own lane, the sum one chain in j order (every lane folds it)
@@ -1162,7 +1185,7 @@ __global__ __launch_bounds__(1024) void k_post_hada(HadaArgs a, MhcIn mhc)
         for (int j = 0; j < r; ++j) sum += __shfl(e, j, 64);
         if (tid < r) proj[tid] = e / sum;
     }
-    __syncthreads();
+    lds_barrier();
     {
         float c = 1.0f;
         if (regs) {
@@ -1175,25 +1198,29 @@ __global__ __launch_bounds__(1024) void k_post_hada(HadaArgs a, MhcIn mhc)
         }
         cond[tid] = c;
     }
+    {
+        const unsigned zb = unsigned(w1a == 0.0f) | unsigned(w2a == 0.0f) << 1 | unsigned(w3a == 0.0f) << 2;
+        if (zb) atomicOr(&zf, zb);
+    }
     z[kron_t(tid)] = xv * d1;
     fa[(tid >> 5) * kKS + (tid & 31)] = w1a;  // w1a is stored transposed
     fb[(tid >> 5) * kKS + (tid & 31)] = w1b;  // w1b is stored transposed
-    __syncthreads();
+    lds_barrier();
     kron32(z, fa, fb, t, buf, zf & 1u);
     z[kron_t(tid)] = buf[p1];
     fa[(tid >> 5) * kKS + (tid & 31)] = w2a;  // w2a is stored transposed
     fb[(tid >> 5) * kKS + (tid & 31)] = w2b;  // w2b is stored transposed
-    __syncthreads();
+    lds_barrier();
     {
         const float zz = d2 * cond[tid] * z[kron_t(tid)] + b2;
         z[kron_t(tid)] = zz * sigmoidf_(zz);
     }
-    __syncthreads();
+    lds_barrier();
     kron32(z, fa, fb, t, buf, zf & 2u);
     z[kron_t(tid)] = buf[p2] * d3;
     fa[(tid >> 5) * kKS + (tid & 31)] = w3a;  // w3a is stored transposed
     fb[(tid >> 5) * kKS + (tid & 31)] = w3b;  // w3b is stored transposed
-    __syncthreads();
+    lds_barrier();
     kron32(z, fa, fb, t, buf, zf & 4u);
     if (ch) {
         const float o = buf[tid] * d4;
