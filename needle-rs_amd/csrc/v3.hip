@@ -759,9 +759,9 @@ __device__ __forceinline__ float transpose4x4(float m)
 // values pass between the phases through `state`.  So the gates need no
 // stream of their own and lengthen no launch of the layer's chain.
 constexpr int kSinkhornIters = 20;   // SINKHORN_ITERS (kernels.rs)
-// iterations in phase 0: about 1.1 us each, so 6 fit k_qkv_kv's time and
-// the other 14 k_post_hada's
-constexpr int kGateSplit = 6;
+// iterations in phase 0: about 1.1 us each; 4 fit k_qkv_kv's time (3 to 5
+// measured alike at 64 sessions, 6 slower) and the other 16 k_post_hada's
+constexpr int kGateSplit = 4;
 struct MhcIn {
     int on;                     // this launch runs a gate phase
     const float *graw;          // [B][n + n*n] from k_layer_in
@@ -908,7 +908,86 @@ __global__ __launch_bounds__(NTH) void k_qkv_kv(QkvKv a, MhcIn mhc)
     const int r = CHUNK ? int(b % a.C) : 0;
     const int p = a.pos[b], T = a.taps, hd = a.hd, half = hd / 2;
     const int nq = a.qd + a.kd, heads = a.H + a.KVH;
-    for (int c = threadIdx.x; c < nq + a.vd; c += NTH) {
+    // One position a session with at most kTapRegs taps: every operand of
+    // the thread's channels (projection, taps, tail) is loaded before the
+    // first is used, then the conv runs from registers.  The loop below
+    // waits for each tap's load in turn.
+    constexpr int kChRegs = (kMaxQkDims + kMaxVDims + NTH - 1) / NTH, kTapRegs = 4;
+    const int nc = nq + a.vd;
+    // the RoPE operands of the thread's (head, pair) items, loaded up front
+    // too (heads * hd <= kMaxQkDims)
+    constexpr int kRopeRegs = (kMaxQkDims / 2 + NTH - 1) / NTH;
+    const int ne = heads * half;
+    const float *cs = a.rope + size_t(p) * 2 * half, *sn = cs + half;
+    float rn1[kRopeRegs], rn2[kRopeRegs], rc[kRopeRegs], rs[kRopeRegs];
+#pragma unroll
+    for (int k = 0; k < kRopeRegs; ++k) {
+        if (k * NTH >= ne) break;
+        const int e0 = threadIdx.x + k * NTH, e = e0 < ne ? e0 : 0;
+        const int hh = e / half, i = e - hh * half;
+        const float *sc = hh < a.H ? a.q_norm : a.k_norm;
+        rn1[k] = sc[i];
+        rn2[k] = sc[half + i];
+        rc[k] = cs[i];
+        rs[k] = sn[i];
+    }
+    if (!CHUNK && T <= kTapRegs) {
+        // this session's rows and tails (per-lane offsets below stay 32-bit)
+        const size_t tr = size_t(T > 1 ? T - 1 : 0);
+        const float *rq = a.q + b * a.qd, *rk = a.k + b * a.kd, *rv = a.v + b * a.vd;
+        float *tq = a.qt + b * tr * a.qd, *tk = a.kt + b * tr * a.kd, *tw = a.vt + b * tr * a.vd;
+        float raw[kChRegs], tp[kChRegs][kTapRegs], tv[kChRegs][kTapRegs];
+#pragma unroll
+        for (int k = 0; k < kChRegs; ++k) {
+            if (k * NTH >= nc) break;
+            const int c0 = threadIdx.x + k * NTH, c = c0 < nc ? c0 : 0;
+            const int seg = c < a.qd ? 0 : (c < nq ? 1 : 2);
+            const int dim = seg == 0 ? a.qd : (seg == 1 ? a.kd : a.vd);
+            const int cl = seg == 0 ? c : (seg == 1 ? c - a.qd : c - nq);
+            const float *src = seg == 0 ? rq : (seg == 1 ? rk : rv);
+            const float *taps = seg == 0 ? a.q_taps : (seg == 1 ? a.k_taps : a.v_taps);
+            const float *tail = seg == 0 ? tq : (seg == 1 ? tk : tw);
+            raw[k] = src[cl];
+#pragma unroll
+            for (int j = 0; j < kTapRegs; ++j) {
+                tp[k][j] = j < T ? taps[j * dim + cl] : 0.0f;
+                // the value j positions back: tail row T - 1 - j
+                tv[k][j] = j >= 1 && j < T ? tail[(T - 1 - j) * dim + cl] : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kChRegs; ++k) {
+            if (k * NTH >= nc) break;
+            const int c = threadIdx.x + k * NTH;
+            if (c >= nc) break;
+            const int seg = c < a.qd ? 0 : (c < nq ? 1 : 2);
+            const int dim = seg == 0 ? a.qd : (seg == 1 ? a.kd : a.vd);
+            const int cl = seg == 0 ? c : (seg == 1 ? c - a.qd : c - nq);
+            float v = raw[k];
+            if (T > 0) {
+                // conv_one's order: tap 0, then each tap back while j <= p
+                float acc = tp[k][0] * v;
+#pragma unroll
+                for (int j = 1; j < kTapRegs; ++j)
+                    if (j < T && j <= p) acc += tp[k][j] * tv[k][j];
+                float *tail = seg == 0 ? tq : (seg == 1 ? tk : tw);
+                // the tail shifts one position: row r takes row r + 1's value,
+                // the value j = T - 2 - r positions back
+#pragma unroll
+                for (int j = 1; j + 1 < kTapRegs; ++j)
+                    if (j + 2 <= T) tail[(T - 2 - j) * dim + cl] = tv[k][j];
+                if (T > 1) tail[(T - 2) * dim + cl] = v;
+                v = acc;
+            }
+            if (seg == 2) {
+                vl[cl] = v;
+            } else {
+                qk[c] = v;
+                sq[c] = v * v;
+            }
+        }
+    }
+    for (int c = threadIdx.x; c < nc && (CHUNK || T > kTapRegs); c += NTH) {
         if (c < a.qd) {
             float v = a.q[b * a.qd + c];
             if (T > 0) {
@@ -939,20 +1018,21 @@ __global__ __launch_bounds__(NTH) void k_qkv_kv(QkvKv a, MhcIn mhc)
             vl[c - nq] = v;
         }
     }
-    __syncthreads();
+    lds_barrier();
     // one sequential sum of squares per head, the heads side by side
     if (threadIdx.x < heads)
         rms[threadIdx.x] = sqrtf(chain_sum(sq + threadIdx.x * hd, hd) / float(hd) + 1e-6f);
-    __syncthreads();
-    const float *cs = a.rope + size_t(p) * 2 * half, *sn = cs + half;
-    for (int e = threadIdx.x; e < heads * half; e += NTH) {
+    lds_barrier();
+#pragma unroll
+    for (int k = 0; k < kRopeRegs; ++k) {
+        const int e = threadIdx.x + k * NTH;
+        if (e >= ne) break;
         const int hh = e / half, i = e - hh * half;
-        const float *sc = hh < a.H ? a.q_norm : a.k_norm;
         const float *x = qk + hh * hd;
         const float r = rms[hh];
-        const float x1 = (1.0f + sc[i]) * x[i] / r;
-        const float x2 = (1.0f + sc[half + i]) * x[half + i] / r;
-        const float c = cs[i], s = sn[i];
+        const float x1 = (1.0f + rn1[k]) * x[i] / r;
+        const float x2 = (1.0f + rn2[k]) * x[half + i] / r;
+        const float c = rc[k], s = rs[k];
         const float o1 = x1 * c - x2 * s, o2 = x2 * c + x1 * s;
         if (hh < a.H) {
             float *o = (CHUNK ? a.q_out : a.q) + b * a.qd + hh * hd;
@@ -963,7 +1043,7 @@ __global__ __launch_bounds__(NTH) void k_qkv_kv(QkvKv a, MhcIn mhc)
             sq[hh * hd + half + i] = o2;
         }
     }
-    __syncthreads();
+    lds_barrier();
     // quantise (cache.rs:80-104): one wave per kv head vector, K then V
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     uint8_t *blk = a.kv + sess * a.kv_stride;
