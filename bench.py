@@ -83,6 +83,16 @@ def parse():
                    help="no GPU: print per-kernel statistics of the last --tail-steps forward "
                         "steps of a rocprofv3 kernel-trace CSV (steps end at k_final)")
     p.add_argument("--tail-steps", type=int, default=128)
+    p.add_argument("--summarize-pmc", metavar="CSV", default=None,
+                   help="no GPU: print the mean of each counter per dispatch of a rocprofv3 "
+                        "--pmc counter-collection CSV, per kernel and grid size")
+    p.add_argument("--pmc-period", type=int, default=0,
+                   help="with --summarize-pmc: also split each (kernel, grid) group by the "
+                        "dispatch's index modulo this period (e.g. 20: the layer of a step)")
+    p.add_argument("--pmc-runs", type=int, default=0,
+                   help="with --summarize-pmc: also split each group into this many runs of "
+                        "consecutive dispatches (e.g. 2: the two shapes --only gemm times "
+                        "with one grid)")
     return p.parse_args()
 
 
@@ -114,6 +124,52 @@ def summarize_trace(path, nsteps):
             name = name[5:]
         print(f"| `{name}` | {len(v) / nsteps:.2f} | {sum(v) / len(v) / 1e3:.2f} | "
               f"{min(v) / 1e3:.2f} | {max(v) / 1e3:.2f} | {sum(v) / nsteps / 1e3:.1f} |")
+
+
+def summarize_pmc(path, period, runs):
+    """Mean counter values per dispatch of a rocprofv3 --pmc CSV, grouped by
+    kernel and grid size (a workload's launches of one shape), with the mean
+    dispatch duration under the profiler.  With `period`, each group is also
+    split by the dispatch's index within the group modulo `period`; with
+    `runs`, into that many runs of consecutive dispatches."""
+    import collections
+    import csv
+    disp = collections.OrderedDict()
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            k = int(r["Dispatch_Id"])
+            e = disp.get(k)
+            if e is None:
+                name = r["Kernel_Name"].replace("(anonymous namespace)::", "").split("(")[0]
+                name = name[5:] if name.startswith("void ") else name
+                e = disp[k] = {"name": name, "grid": int(r["Grid_Size"]), "c": {},
+                               "us": (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3}
+            e["c"][r["Counter_Name"]] = float(r["Counter_Value"])
+    groups = collections.OrderedDict()
+    for k in sorted(disp):
+        e = disp[k]
+        groups.setdefault((e["name"], e["grid"]), []).append(e)
+    names = sorted({c for e in disp.values() for c in e["c"]})
+    print("| kernel | grid | part | dispatches | us (profiled) | " + " | ".join(names) + " |")
+    print("|---|---|---|---|---|" + "---|" * len(names))
+
+    def row(key, part, es):
+        us = sum(e["us"] for e in es) / len(es)
+        vals = [sum(e["c"].get(c, 0.0) for e in es) / len(es) for c in names]
+        print(f"| `{key[0]}` | {key[1]} | {part} | {len(es)} | {us:.2f} | " +
+              " | ".join(f"{v:,.0f}" for v in vals) + " |")
+
+    for key, es in groups.items():
+        row(key, "all", es)
+        if period > 0 and len(es) >= period:
+            for j in range(period):
+                sub = es[j::period]
+                if sub:
+                    row(key, f"{j} mod {period}", sub)
+        if runs > 1 and len(es) >= runs:
+            n = len(es) // runs
+            for j in range(runs):
+                row(key, f"run {j + 1} of {runs}", es[j * n:(j + 1) * n])
 
 
 MIN_WARM_S = 0.5
@@ -610,6 +666,9 @@ def main():
     MIN_WARM_S = args.min_warm
     if args.summarize_trace:
         summarize_trace(args.summarize_trace, args.tail_steps)
+        return
+    if args.summarize_pmc:
+        summarize_pmc(args.summarize_pmc, args.pmc_period, args.pmc_runs)
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1",
