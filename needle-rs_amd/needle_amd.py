@@ -795,7 +795,7 @@ class V3Batch:
     def generate(self, prompts, steps):
         """Prefill each session's prompt, max_chunk positions per pass (or by
         stepping; the reference proves the two bit-identical), then `steps`
-        greedy tokens."""
+        greedy tokens: the prefill's choice, then the device loop's."""
         prompts = np.asarray(prompts, np.int32).reshape(self.sessions, -1)
         nxt = None
         n = prompts.shape[1]
@@ -807,8 +807,8 @@ class V3Batch:
             else:
                 nxt = self.prefill(prompts[:, t0:t1], want_next=last)
         out = np.zeros((self.sessions, steps), np.int32)
-        for s in range(steps):
-            out[:, s] = nxt
-            if s + 1 < steps:
-                nxt = self.step(nxt)
+        if steps > 0:
+            out[:, 0] = nxt
+        if steps > 1:
+            out[:, 1:] = self.greedy(nxt, steps - 1)
         return out
