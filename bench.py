@@ -620,6 +620,44 @@ def forward_runs(torch, nd, ctx, sessions, ctx_len, check=True):
         "tokens_equal_host_stepped": bool(np.array_equal(toks, toks_h)),
         "prefill_tok_per_s": round(sessions * ctx_len / t_pre, 1),
     }
+    # the same sessions as two batches of sessions / 2 on two streams, their
+    # greedy loops enqueued in turn from this thread (nd_v3_generate_many):
+    # one batch's one-workgroup-per-session kernels run beside the other's
+    # projections and attention; projections batched over sessions / 2
+    if sessions % 2 == 0:
+        half = sessions // 2
+        streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+        ctxs = [nd.Ctx(0, stream=st) for st in streams]
+        batches, firsts = [], []
+        for k in range(2):
+            b = nd.V3Batch(model, half, max_len=ctx_len + steps, max_chunk=32, ctx=ctxs[k])
+            pr = np.ascontiguousarray(np.stack([S.prompt_tokens(ctx_len, 100 + k * half + i)
+                                                for i in range(half)]), np.int32)
+            nxt = None
+            for t in range(0, ctx_len, 32):
+                t1 = min(ctx_len, t + 32)
+                nxt = b.prefill(pr[:, t:t1], want_next=(t1 == ctx_len))
+            batches.append(b)
+            firsts.append(nxt)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        outs = nd.V3Batch.greedy_many(batches, firsts, steps)
+        t_dec2 = time.perf_counter() - t0
+        toks2 = np.concatenate([np.concatenate([f[:, None], o[:, :-1]], axis=1)
+                                for f, o in zip(firsts, outs)], axis=0)
+        out[key]["two_streams"] = {
+            "workload": f"the same {sessions} sessions as two batches of {half} on two streams, "
+                        "their greedy loops enqueued in turn from one host thread "
+                        "(nd_v3_generate_many); projections batched over each batch's "
+                        f"{half} sessions",
+            "decode_tok_per_s": round(sessions * steps / t_dec2, 1),
+            "decode_ms_per_step": round(t_dec2 / steps * 1e3, 3),
+            "tokens_equal_one_batch": bool(np.array_equal(toks2, toks)),
+        }
+        for b in batches:
+            b.close()
+        for c in ctxs:
+            c.close()
     if check:
         out[key]["check"] = forward_check(model, g, recs, toks, ctx_len, steps, run)
     model.close()

@@ -449,6 +449,22 @@ int nd_v3_prefill(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32
 int nd_v3_generate(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *first,
                    size_t steps, int32_t *tokens);
 
+/* nd_v3_generate for n (1..8) batches of one model at once, from one host
+ * thread: batch i on context ctxs[i] (its own stream), from first[i], into
+ * tokens[i].  Step k of every batch is enqueued before step k + 1 of any,
+ * so the batches' launches interleave on their streams and run side by
+ * side on the device (a batch's per-session kernels use one workgroup a
+ * session; another batch's projections and attention fill the rest).
+ * Each batch ends exactly as nd_v3_generate would leave it, bit for bit.
+ * The contexts and the batches must be distinct; all are held for the
+ * call.  No reference counterpart: the reference serves concurrent
+ * sessions from its own threads (V3Engine per session, v3_engine.rs:544-561);
+ * this is the one-thread form of that, for a server that groups its
+ * sessions into a few batches. */
+int nd_v3_generate_many(nd_ctx *const *ctxs, const nd_v3_model *m, nd_v3_batch *const *bs,
+                        size_t n, const int32_t *const *first, size_t steps,
+                        int32_t *const *tokens);
+
 /* ---- the .cact v3 container (needle-infer/src/cact.rs, v3.rs) ----------- */
 
 /* Reads a Needle-3 container held in host memory (`bytes`, `len`): the

@@ -34,6 +34,7 @@
 
 #include <cmath>
 #include <cstring>
+#include <memory>
 #include <new>
 #include <string>
 #include <vector>
@@ -1590,6 +1591,7 @@ struct nd_v3_batch {
     int32_t *hist_dev = nullptr;
     int32_t *gen_out = nullptr;
     size_t gen_cap = 0;
+    std::vector<int32_t> gen_init;  // the loop's first tokens and ids, read by its uploads
     // The scatter-up gates of a layer depend only on its input lanes: they
     // run on `side` while the layer's attention and MLP run on the caller's
     // stream; ev_in[l % 2] marks a layer's input ready, ev_gates[l % 2] its
@@ -2733,14 +2735,16 @@ int nd_v3_prefill(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32
     return step_impl(ctx, m, b, tokens, int(count), next, logits);
 }
 
-int nd_v3_generate(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *first,
-                   size_t steps, int32_t *tokens)
+}  // extern "C"
+
+namespace {
+
+// nd_v3_generate in three parts, so that several batches' loops can be
+// enqueued step by step in turn (nd_v3_generate_many).  The caller holds
+// the context and the batch.
+int gen_begin(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *first, size_t steps)
 {
-    ND_ENTER(ctx);
-    ND_REQUIRE(m && b && first && tokens, "null argument");
-    nd::Hold hold(b->owner, "the batch");
-    if (hold.rc) return hold.rc;
-    if (steps == 0) return ND_OK;
+    ND_REQUIRE(m && b && first, "null argument");
     const int S = b->B;
     ND_REQUIRE(b->chunk >= 1, "batch without steps");
     for (int i = 0; i < S; ++i)
@@ -2756,8 +2760,10 @@ int nd_v3_generate(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int3
         ND_HIP(hipMalloc(&b->gen_out, n_out * sizeof(int32_t)));
         b->gen_cap = n_out;
     }
-    // the first tokens, and each session's retained ids, right-aligned
-    std::vector<int32_t> init(size_t(S) * (1 + mo), 0);
+    // the first tokens, and each session's retained ids, right-aligned; the
+    // host buffer lives in the batch until the loop's tokens come back
+    std::vector<int32_t> &init = b->gen_init;
+    init.assign(size_t(S) * (1 + mo), 0);
     for (int i = 0; i < S; ++i) {
         init[i] = first[i];
         const std::vector<uint32_t> &hv = b->s[i].hist;
@@ -2768,23 +2774,35 @@ int nd_v3_generate(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int3
     ND_HIP(hipMemcpyAsync(b->next, init.data(), size_t(S) * 4, hipMemcpyHostToDevice, ctx->stream));
     ND_HIP(hipMemcpyAsync(b->hist_dev, init.data() + S, size_t(S) * mo * 4, hipMemcpyHostToDevice,
                           ctx->stream));
-    // steps enqueued back to back: the host runs ahead of the device up to
-    // the staging ring's depth, and no step waits for the host
-    int rc = ND_OK;
-    for (size_t k = 0; k < steps && rc == ND_OK; ++k) {
-        StepRun r{ctx, m, b, 1};
-        r.argmax_also = b->gen_out + k * S;
-        rc = r.begin(nullptr);
-        for (int ph = -1; ph <= r.L && rc == ND_OK; ++ph) rc = r.enqueue(ph, true);
-        if (rc == ND_OK)
-            for (int i = 0; i < S; ++i) b->s[i].pos += 1;
-    }
-    if (rc != ND_OK) return rc;
+    return ND_OK;
+}
+
+// Step k of the loop: enqueued, nothing waited for (the host runs ahead of
+// the device up to the staging ring's depth).
+int gen_step(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, size_t k)
+{
+    const int S = b->B;
+    StepRun r{ctx, m, b, 1};
+    r.argmax_also = b->gen_out + k * S;
+    int rc = r.begin(nullptr);
+    for (int ph = -1; ph <= r.L && rc == ND_OK; ++ph) rc = r.enqueue(ph, true);
+    if (rc == ND_OK)
+        for (int i = 0; i < S; ++i) b->s[i].pos += 1;
+    return rc;
+}
+
+// The tokens back to the host, and the host's copy of the retained ids.
+int gen_end(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *first, size_t steps,
+            int32_t *tokens)
+{
+    const int S = b->B;
+    const int mo = max_order(m->cfg);
+    const size_t n_out = steps * size_t(S);
     std::vector<int32_t> got(n_out);
     ND_HIP(hipMemcpyAsync(got.data(), b->gen_out, n_out * 4, hipMemcpyDeviceToHost, ctx->stream));
     ND_HIP(hipStreamSynchronize(ctx->stream));
     for (int i = 0; i < S; ++i) {
-        // the host's copy of the retained ids: the tokens the steps fed
+        // the tokens the steps fed
         std::vector<uint32_t> &hv = b->s[i].hist;
         for (size_t k = 0; k < steps; ++k) {
             hv.push_back(uint32_t(k == 0 ? first[i] : got[(k - 1) * S + i]));
@@ -2792,6 +2810,60 @@ int nd_v3_generate(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int3
             tokens[size_t(i) * steps + k] = got[k * S + i];
         }
     }
+    return ND_OK;
+}
+
+constexpr size_t kMaxGenBatches = 8;
+
+}  // namespace
+
+extern "C" {
+
+int nd_v3_generate(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int32_t *first,
+                   size_t steps, int32_t *tokens)
+{
+    ND_ENTER(ctx);
+    ND_REQUIRE(m && b && first && tokens, "null argument");
+    nd::Hold hold(b->owner, "the batch");
+    if (hold.rc) return hold.rc;
+    if (steps == 0) return ND_OK;
+    if (int rc = gen_begin(ctx, m, b, first, steps)) return rc;
+    for (size_t k = 0; k < steps; ++k)
+        if (int rc = gen_step(ctx, m, b, k)) return rc;
+    return gen_end(ctx, m, b, first, steps, tokens);
+}
+
+int nd_v3_generate_many(nd_ctx *const *ctxs, const nd_v3_model *m, nd_v3_batch *const *bs,
+                        size_t n, const int32_t *const *first, size_t steps,
+                        int32_t *const *tokens)
+{
+    nd::clear_error();
+    ND_REQUIRE(ctxs && m && bs && first && tokens, "null argument");
+    ND_REQUIRE(n >= 1 && n <= kMaxGenBatches, "%zu batches (1..%zu)", n, kMaxGenBatches);
+    for (size_t i = 0; i < n; ++i) {
+        ND_REQUIRE(ctxs[i] && bs[i] && first[i] && tokens[i], "batch %zu: null argument", i);
+        for (size_t j = 0; j < i; ++j)
+            ND_REQUIRE(ctxs[j] != ctxs[i] && bs[j] != bs[i], "batch %zu repeats a context or a batch", i);
+    }
+    std::vector<std::unique_ptr<nd::Entry>> entries;
+    std::vector<std::unique_ptr<nd::Hold>> holds;
+    for (size_t i = 0; i < n; ++i) {
+        entries.emplace_back(new nd::Entry(ctxs[i]));
+        if (entries.back()->rc) return entries.back()->rc;
+        holds.emplace_back(new nd::Hold(bs[i]->owner, "the batch"));
+        if (holds.back()->rc) return holds.back()->rc;
+    }
+    if (steps == 0) return ND_OK;
+    for (size_t i = 0; i < n; ++i)
+        if (int rc = gen_begin(ctxs[i], m, bs[i], first[i], steps)) return rc;
+    // step k of every batch before step k + 1 of any: each batch's launches
+    // go to its own stream, so one batch's single-workgroup-per-session
+    // kernels run beside another's wide ones
+    for (size_t k = 0; k < steps; ++k)
+        for (size_t i = 0; i < n; ++i)
+            if (int rc = gen_step(ctxs[i], m, bs[i], k)) return rc;
+    for (size_t i = 0; i < n; ++i)
+        if (int rc = gen_end(ctxs[i], m, bs[i], first[i], steps, tokens[i])) return rc;
     return ND_OK;
 }
 

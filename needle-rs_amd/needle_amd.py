@@ -92,6 +92,7 @@ _SIGS = [
     ("nd_v3_batch_create_chunked", C.c_int, [_vp, _vp, _sz, _sz, _sz, _sz, C.POINTER(_vp)]),
     ("nd_v3_prefill", C.c_int, [_vp, _vp, _vp, _vp, _sz, _vp, _vp]),
     ("nd_v3_generate", C.c_int, [_vp, _vp, _vp, _vp, _sz, _vp]),
+    ("nd_v3_generate_many", C.c_int, [_vp, _vp, _vp, _sz, _vp, _sz, _vp]),
     ("nd_v3_cact_config", C.c_int, [_vp, _sz, _vp, C.POINTER(_sz)]),
     ("nd_v3_model_from_cact", C.c_int, [_vp, _vp, _sz, C.POINTER(_vp)]),
     ("nd_v3_batch_set_graphs", C.c_int, [_vp, C.c_int]),
@@ -791,6 +792,23 @@ class V3Batch:
                                     tok.ctypes.data_as(C.c_void_p), steps,
                                     out.ctypes.data_as(C.c_void_p)))
         return out
+
+    @staticmethod
+    def greedy_many(batches, firsts, steps):
+        """greedy() for several batches of one model at once (nd_v3_generate_many):
+        batch i on its own context's stream, the steps enqueued in turn from
+        this thread; returns one [sessions][steps] array per batch."""
+        n = len(batches)
+        model = batches[0].model
+        assert all(b.model is model for b in batches), "one model"
+        toks = [np.ascontiguousarray(f, np.int32).reshape(b.sessions) for b, f in zip(batches, firsts)]
+        outs = [np.zeros((b.sessions, steps), np.int32) for b in batches]
+        ctxs = (C.c_void_p * n)(*[b.ctx.h.value for b in batches])
+        bs = (C.c_void_p * n)(*[b.h.value for b in batches])
+        fs = (C.c_void_p * n)(*[t.ctypes.data for t in toks])
+        ts = (C.c_void_p * n)(*[o.ctypes.data for o in outs])
+        _check(lib().nd_v3_generate_many(ctxs, model.h, bs, n, fs, steps, ts))
+        return outs
 
     def generate(self, prompts, steps):
         """Prefill each session's prompt, max_chunk positions per pass (or by

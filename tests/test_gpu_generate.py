@@ -96,3 +96,61 @@ def test_generate_rejects_overflow(ctx):
     assert list(b.positions()) == [0]
     b.close()
     dm.close()
+
+
+def test_generate_many_equals_each(ctx):
+    """nd_v3_generate_many: two batches of one model on two contexts (their
+    own streams), stepped in turn from this thread, end exactly where
+    nd_v3_generate leaves each alone: tokens, positions and the next
+    step's logits, bit for bit."""
+    g, recs = S.build_records(S.small_geometry(4), seed=5)
+    dm = nd.V3Model(ctx, g, recs, S.CODEBOOK)
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    ctxs = [nd.Ctx(0, stream=s) for s in streams]
+    shapes = [(3, 37, 8), (2, 20, 16)]  # sessions, prompt, chunk
+    steps = 30
+    prompts = [np.stack([S.prompt_tokens(n, 70 + 10 * k + i) for i in range(s)])
+               for k, (s, n, _) in enumerate(shapes)]
+
+    def prefilled(k, on):
+        s, n, chunk = shapes[k]
+        b = nd.V3Batch(dm, s, max_len=n + steps + 8, max_chunk=chunk, ctx=on)
+        nxt = None
+        for t0 in range(0, n, chunk):
+            t1 = min(n, t0 + chunk)
+            nxt = (b.step(prompts[k][:, t0], want_next=(t1 == n)) if t1 - t0 == 1
+                   else b.prefill(prompts[k][:, t0:t1], want_next=(t1 == n)))
+        return b, nxt
+
+    alone = [prefilled(k, ctx) for k in range(2)]
+    want = [b.greedy(f, steps) for b, f in alone]
+    many = [prefilled(k, ctxs[k]) for k in range(2)]
+    torch.cuda.synchronize()
+    got = nd.V3Batch.greedy_many([b for b, _ in many], [f for _, f in many], steps)
+    for k in range(2):
+        assert np.array_equal(got[k], want[k]), k
+        assert np.array_equal(many[k][0].positions(), alone[k][0].positions())
+        s = shapes[k][0]
+        la = torch.empty(s, dm.rows, device="cuda")
+        lb = torch.empty(s, dm.rows, device="cuda")
+        alone[k][0].step(want[k][:, -1], logits=la, want_next=False)
+        many[k][0].step(got[k][:, -1], logits=lb, want_next=False)
+        torch.cuda.synchronize()
+        assert np.array_equal(_bits(la.cpu().numpy()), _bits(lb.cpu().numpy())), k
+    for b, _ in alone + many:
+        b.close()
+    for c in ctxs:
+        c.close()
+    dm.close()
+
+
+def test_generate_many_rejects_repeats(ctx):
+    g, recs = S.build_records(S.small_geometry(2), seed=9)
+    dm = nd.V3Model(ctx, g, recs, S.CODEBOOK)
+    b = nd.V3Batch(dm, 1, max_len=16)
+    with pytest.raises(nd.NeedleError):
+        nd.V3Batch.greedy_many([b, b], [np.array([1], np.int32)] * 2, 2)
+    assert list(b.positions()) == [0]
+    b.close()
+    dm.close()
