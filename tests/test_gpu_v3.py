@@ -183,3 +183,29 @@ def test_shipped_geometry_prompt128_greedy256(ctx):
     print(f"shipped geometry: min margin {margins.min():.4e}, median {np.median(margins):.4e}, "
           f"distinct {len(set(toks.tolist()))}, first difference at {first_diff}")
     assert np.array_equal(got, toks.astype(np.int32)), first_diff
+
+
+@pytest.mark.parametrize("taps", [0, 1, 2, 4, 5])
+def test_conv_taps_track_the_oracle(ctx, taps):
+    """The q/k/v causal conv at other tap counts than the shipped 3: a
+    decode step holds a thread's conv operands in registers up to 4 taps
+    and loops over them beyond; 0 taps has no conv.  Two sessions stepped
+    past the taps' reach, every logit bit for bit the oracle's."""
+    geo = S.small_geometry(2)
+    geo["qkv_conv_taps"] = taps
+    g, recs = S.build_records(geo, seed=21 + taps)
+    om = O.V3Model(g, recs, S.CODEBOOK)
+    dm = nd.V3Model(ctx, g, recs, S.CODEBOOK)
+    prompts = np.stack([S.prompt_tokens(12, 200 + 3 * taps + i) for i in range(2)])
+    batch = nd.V3Batch(dm, 2, max_len=16)
+    got = torch.empty(2, dm.rows, device="cuda")
+    outs = []
+    for t in range(prompts.shape[1]):
+        batch.step(prompts[:, t], logits=got, want_next=False)
+        outs.append(got.cpu().numpy().copy())
+    outs = np.stack(outs, axis=1)
+    for i in range(2):
+        want = _oracle_logits(om, prompts[i])
+        assert np.array_equal(_bits(outs[i]), _bits(want)), (taps, i, np.max(np.abs(outs[i] - want)))
+    batch.close()
+    dm.close()
