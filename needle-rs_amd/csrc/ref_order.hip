@@ -571,11 +571,15 @@ constexpr int kProdBuf = 64 * 52;  // products per buffer: VD x (T + 4) <= 64 x 
 constexpr int kPrefetch = 8;
 constexpr int kAttn2MaxCap = 8192;  // scores 32 KB + two product buffers 26 KB
 constexpr int kScoreBatch = 4;      // positions per thread whose K rows load together
-// Spans of 2048..4096 positions sum by the parallel fold.  Measured per
-// workgroup against the chain (12 q / 2 kv heads, qk 48, vd 64): span 4096
-// 53.6 -> 45.9 us, 2048 29.0 -> 26.8 us, but 1024 16.4 -> 17.3 us and 384
-// 10.2 -> 12.8 us, where the fold's barrier rounds cost more than the chain.
-constexpr int kAttnFoldMin = 2048;
+// Spans of 1024..4096 positions sum by the parallel fold, its unrolled loop
+// sized to the terms a thread holds (4, 9 or 16: the masked iterations past
+// a thread's terms cost as much as real ones).  Measured against the chain
+// (12 q / 2 kv heads, qk 48, vd 64, one launch): span 4096 53.6 -> 45.9 us
+// a workgroup; span 2048 at 64 sessions 37.5 -> 35.9 us, at one session
+// 24.6 -> 23.7; span 1024 at one session 15.3 -> 14.7, at 64 sessions no
+// change.  Shorter spans keep the chain (at 384, 10.2 against 12.8 us for
+// the fold at 16 a thread).
+constexpr int kAttnFoldMin = 1024;
 constexpr int kAttnFoldC = 16;
 static_assert(sizeof(NdFoldLds<kAttn2Threads>) <= 2 * kProdBuf * sizeof(float),
               "the fold's LDS lives in the product buffers");
@@ -891,8 +895,12 @@ __global__ __launch_bounds__(kAttn2Threads, 4) void attn_exact2_kernel(
     // parallel fold, its LDS in the product buffers (first written after the
     // barrier below); a shorter or longer one is the chain itself.
     if (span >= kAttnFoldMin && span <= NT * kAttnFoldC) {
-        const float s = nd_fold_nonneg<NT, kAttnFoldC>(sc, span,
-                                                        *reinterpret_cast<NdFoldLds<NT> *>(prod));
+        NdFoldLds<NT> &fl = *reinterpret_cast<NdFoldLds<NT> *>(prod);
+        const int cpt = (span + NT - 1) / NT;
+        float s;
+        if (cpt <= 4) s = nd_fold_nonneg<NT, 4>(sc, span, fl);
+        else if (cpt <= 9) s = nd_fold_nonneg<NT, 9>(sc, span, fl);
+        else s = nd_fold_nonneg<NT, kAttnFoldC>(sc, span, fl);
         if (tid == 0) total = s;
     } else if (tid == 0) {
         __builtin_amdgcn_s_setprio(2);

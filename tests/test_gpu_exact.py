@@ -125,10 +125,11 @@ def test_attend_exact_ring_window(ctx, lo, hi):
     assert _same_bits(out, _oracle(g, host(blk), q, lo, hi))
 
 
-@pytest.mark.parametrize("span", [2047, 2048, 2049, 3333, 4096, 4097])
+@pytest.mark.parametrize("span", [1023, 1024, 1025, 2047, 2048, 2049, 2304, 2305, 3333, 4096, 4097])
 def test_attend_exact_softmax_sum_paths(ctx, span):
-    """Spans of 2048..4096 positions take the parallel fold for the softmax
-    sum, the others the chain; both give the chain's bits."""
+    """Spans of 1024..4096 positions take the parallel fold for the softmax
+    sum (its loop sized for 4, 9 or 16 terms a thread), the others the
+    chain; all give the chain's bits."""
     H, KVH, QK, VD, cap = 12, 2, 48, 64, 4200
     rng = np.random.default_rng(span)
     g, blk, nb = _fill(ctx, rng, H, KVH, QK, VD, cap, cap, scale=2.0)
