@@ -81,7 +81,8 @@ def parse():
                    help="also run a plain 1 GiB device copy (PMC byte-counter scale)")
     p.add_argument("--summarize-trace", metavar="CSV", default=None,
                    help="no GPU: print per-kernel statistics of the last --tail-steps forward "
-                        "steps of a rocprofv3 kernel-trace CSV (steps end at k_final)")
+                        "steps of a rocprofv3 kernel-trace CSV (steps end at k_final); with "
+                        "--tail-steps 0, of every launch, per kernel and grid size")
     p.add_argument("--tail-steps", type=int, default=128)
     p.add_argument("--summarize-pmc", metavar="CSV", default=None,
                    help="no GPU: print the mean of each counter per dispatch of a rocprofv3 "
@@ -98,21 +99,37 @@ def parse():
 
 def summarize_trace(path, nsteps):
     """Per-kernel durations over the last `nsteps` forward steps of a
-    rocprofv3 --kernel-trace CSV.  Each step launches k_final once, so the
-    window starts after the (nsteps + 1)-th last k_final ends; kernels of the
-    side stream in that window are included."""
+    rocprofv3 --kernel-trace CSV (plain or gzipped).  Each step launches
+    k_final once, so the window starts after the (nsteps + 1)-th last k_final
+    ends; kernels of the side stream in that window are included.  With
+    nsteps 0, every launch of the trace, grouped by kernel and grid size."""
     import collections
     import csv
+    import gzip
     rows = []
-    with open(path) as f:
+    with (gzip.open(path, "rt") if path.endswith(".gz") else open(path)) as f:
         for r in csv.DictReader(f):
-            rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]))
+            grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+            rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"], grid))
     rows.sort()
+    if nsteps == 0:
+        agg = collections.defaultdict(list)
+        for a, b, n, grid in rows:
+            agg[(n, grid)].append(b - a)
+        print("| kernel | grid | launches | avg us | min us | max us |")
+        print("|---|---|---|---|---|---|")
+        for (n, grid), v in sorted(agg.items(), key=lambda kv: -sum(kv[1])):
+            name = n.replace("(anonymous namespace)::", "").split("(")[0]
+            if name.startswith("void "):
+                name = name[5:]
+            print(f"| `{name}` | {grid} | {len(v)} | {sum(v) / len(v) / 1e3:.2f} | "
+                  f"{min(v) / 1e3:.2f} | {max(v) / 1e3:.2f} |")
+        return
     finals = [i for i, r in enumerate(rows) if "::k_final(" in r[2]]
     t0 = rows[finals[-(nsteps + 1)]][1]
     sel = [r for r in rows if r[0] > t0]
     agg = collections.defaultdict(list)
-    for a, b, n in sel:
+    for a, b, n, _ in sel:
         agg[n].append(b - a)
     span = (max(r[1] for r in sel) - t0) / 1e3
     print(f"last {nsteps} steps: {span / nsteps:.1f} us per step (profiler on), {len(sel)} kernels")
@@ -515,7 +532,7 @@ def exact_attention_runs(torch, nd, ctx, gen):
     """One session's reference-order decode attention (nd_attend_step_i8_exact,
     the forward's attention) over spans of 384..4096 positions, at the
     forward's head geometry (12 q / 2 kv heads, qk 48, vd 64): microseconds
-    per call.  Spans of 2048 and more sum the softmax with the parallel fold."""
+    per call.  Spans of 1024 and more sum the softmax with the parallel fold."""
     H, KVH, QK, VD = 12, 2, 48, 64
     out = {}
     for span in (384, 1024, 2048, 4096):

@@ -157,7 +157,12 @@ struct AttnShape {
     static constexpr int KPP = kThreads / KL;                 // positions per K pass
     static constexpr int VL = VD / VW;
     static constexpr int VPP = kThreads / VL;                 // positions per V pass
-    static constexpr int CH = REP <= 2 ? 512 : 256;           // positions per chunk
+    // positions per chunk: 256 keeps the registers at 119 (four waves a
+    // SIMD) and two chunks of a 512-long span in flight; 512 took 157
+    // (three), and at 12 heads x 64 measured 5.37 / 5.96 / 5.96 TB/s at ctx
+    // 512 / 2048 / 8192 against 5.69 / 6.32 / 6.34 with 256 (192: 5.10 /
+    // 5.83 / 5.91; 384: 4.43 / 5.47 / 5.73)
+    static constexpr int CH = 256;
     static constexpr int KP = (CH + KPP - 1) / KPP;           // K passes per chunk
     static constexpr int VP = CH / VPP;                       // V passes per chunk
 };
@@ -583,10 +588,14 @@ int attend_i8(nd_ctx *ctx, const nd_kv_geom *g, const void *kv, size_t kv_stride
     // give every CU a few blocks; the split partials merge in a second pass.
     const size_t pairs = count * size_t(g->num_kv_heads);
     const size_t want = size_t(ctx->num_cus > 0 ? ctx->num_cus : 256) * 4;
-    const int chunk = rep <= 2 ? 512 : 256;
-    const size_t max_chunks = (size_t(g->cap) + chunk - 1) / chunk;
+    // a split covers at least 512 positions (256 with more than two query
+    // heads a kv head): with one query head, splits of one 256-position
+    // chunk measured slower at one session (ctx 512: 13.1 against 10.6 us,
+    // ctx 8192: 20.4 against 14.9), the merge costing more than they save
+    const size_t span_min = rep <= 2 ? 512 : 256;
+    const size_t max_splits = (size_t(g->cap) + span_min - 1) / span_min;
     size_t splits = pairs >= want ? 1 : (want + pairs - 1) / pairs;
-    if (splits > max_chunks) splits = max_chunks;
+    if (splits > max_splits) splits = max_splits;
     if (splits > 65535) splits = 65535;
     float *po = nullptr, *pml = nullptr;
     if (splits > 1) {
