@@ -33,6 +33,7 @@
 #include "nd_kv_internal.h"
 #include "nd_libm.h"
 #include "nd_ref_order.h"
+#include "nd_attn_exact.h"
 
 #include <cmath>
 
@@ -400,30 +401,11 @@ int nd_cq_exact_multi(nd_ctx *ctx, hipStream_t stream, int n, const nd_cq *const
 
 namespace {
 
+using namespace ndattn;
+
 // ---------------------------------------------------------------------------
 // attend_step over the int8 view, in the reference's order.
 // ---------------------------------------------------------------------------
-__device__ inline float i8_lane(uint32_t dw, int b) { return float(int32_t(dw << (24 - 8 * b)) >> 24); }
-
-// Output column `lane` (0..63, all 64 lanes of the wave) of one head, with
-// `gate` set: attn * sigmoid(gate) (v3/model.rs:309-312), then butterfly
-// stages h = 1..32 of the normalised FWHT prepare_input applies to the
-// out projection's 128-wide groups (hadamard.rs:24-42): with a 64-wide head
-// each half of a group is one head, and those stages pair columns within
-// it.  The last stage (h = 64, across the two heads) and the 1/sqrt(128)
-// scale are left to the projection's activation load.
-__device__ inline float gate_half_fwht(float v, const float *gate, int lane)
-{
-    if (!gate) return v;
-    v = v * nd_sigmoidf(gate[lane]);
-#pragma unroll
-    for (int h = 1; h < 64; h <<= 1) {
-        const float p = __shfl_xor(v, h, 64);
-        v = (lane & h) ? p - v : v + p;
-    }
-    return v;
-}
-
 __global__ __launch_bounds__(kThreads) void attn_exact_kernel(ndkv::Geom g,
                                                              const uint8_t *__restrict__ kv,
                                                              size_t stride, int rows_per_block,
@@ -556,242 +538,17 @@ __global__ __launch_bounds__(kThreads) void attn_exact_kernel(ndkv::Geom g,
             gate_half_fwht(acc, gate ? gate + (i * g.H + h) * size_t(g.VD) : nullptr, tid);
 }
 
-// The same arithmetic, with the value pass split between roles.  Of the 256
-// threads, CW consumer waves hold one output column per lane and run the
-// column chains; the other 4 - CW producer waves stream V a chunk of
-// positions ahead, form each product ((e * inv) * v_scale) * v into an LDS
-// double buffer, and keep kPrefetch chunks of V loads in flight.  A chain
-// then costs one add per position.  At most 128 VGPRs, so four workgroups fit
-// a CU and a 64-session layer (768 workgroups) is resident at once.
-// Blocks are numbered so that the heads sharing a kv head run on one XCD
-// (workgroups are dealt to the 8 XCDs round-robin), where they share that
-// XCD's L2 copy of the span.
-constexpr int kAttn2Threads = 256;
-constexpr int kProdBuf = 64 * 52;  // products per buffer: VD x (T + 4) <= 64 x 52, 128 x 20
-constexpr int kPrefetch = 8;
-constexpr int kAttn2MaxCap = 8192;  // scores 32 KB + two product buffers 26 KB
-constexpr int kScoreBatch = 4;      // positions per thread whose K rows load together
-// Spans of 1024..4096 positions sum by the parallel fold, its unrolled loop
-// sized to the terms a thread holds (4, 9 or 16: the masked iterations past
-// a thread's terms cost as much as real ones).  Measured against the chain
-// (12 q / 2 kv heads, qk 48, vd 64, one launch): span 4096 53.6 -> 45.9 us
-// a workgroup; span 2048 at 64 sessions 37.5 -> 35.9 us, at one session
-// 24.6 -> 23.7; span 1024 at one session 15.3 -> 14.7, at 64 sessions no
-// change.  Shorter spans keep the chain (at 384, 10.2 against 12.8 us for
-// the fold at 16 a thread).
-constexpr int kAttnFoldMin = 1024;
-constexpr int kAttnFoldC = 16;
-static_assert(sizeof(NdFoldLds<kAttn2Threads>) <= 2 * kProdBuf * sizeof(float),
-              "the fold's LDS lives in the product buffers");
-
-// One (q, key) score chain per position, QC = qk / 16 pieces of 16 codes
-// (0: any qk, read piece by piece).  With QC set, a thread loads the K rows
-// of kScoreBatch positions at once and runs their chains interleaved.
-template <int QC, int NT>
-__device__ __forceinline__ float attn_scores(const ndkv::Geom &g, const float *qs, const int8_t *kb,
-                                    const float *ks, int base, int span, float scale, float *sc)
-{
-    const int tid = threadIdx.x;
-    float mx = -INFINITY;
-    if constexpr (QC > 0) {
-        for (int t0 = tid; t0 < span; t0 += NT * kScoreBatch) {
-            uint4 kw[kScoreBatch][QC];
-            float ksv[kScoreBatch];
-#pragma unroll
-            for (int u = 0; u < kScoreBatch; ++u) {
-                const int t = t0 + u * NT;
-                int slot = base + (t < span ? t : 0);
-                if (slot >= g.cap) slot -= g.cap;
-                const uint4 *kr = reinterpret_cast<const uint4 *>(kb + size_t(slot) * (16 * QC));
-#pragma unroll
-                for (int c = 0; c < QC; ++c) kw[u][c] = kr[c];
-                ksv[u] = ks[slot];
-            }
-            float acc[kScoreBatch];
-#pragma unroll
-            for (int u = 0; u < kScoreBatch; ++u) acc[u] = 0.0f;
-#pragma unroll
-            for (int c = 0; c < QC; ++c) {
-#pragma unroll
-                for (int d = 0; d < 4; ++d) {
-#pragma unroll
-                    for (int b = 0; b < 4; ++b) {
-                        const float qv = qs[c * 16 + d * 4 + b];
-#pragma unroll
-                        for (int u = 0; u < kScoreBatch; ++u) {
-                            const uint32_t dw = d == 0 ? kw[u][c].x
-                                              : d == 1 ? kw[u][c].y
-                                              : d == 2 ? kw[u][c].z
-                                                       : kw[u][c].w;
-                            acc[u] += qv * i8_lane(dw, b);
-                        }
-                    }
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < kScoreBatch; ++u) {
-                const int t = t0 + u * NT;
-                if (t < span) {
-                    const float s = acc[u] * ksv[u] * scale;
-                    sc[t] = s;
-                    if (s > mx) mx = s;
-                }
-            }
-        }
-    } else {
-        for (int t = tid; t < span; t += NT) {
-            int slot = base + t;
-            if (slot >= g.cap) slot -= g.cap;
-            const uint4 *kr = reinterpret_cast<const uint4 *>(kb + size_t(slot) * g.QK);
-            float acc = 0.0f;
-            for (int c = 0; c < g.QK / 16; ++c) {
-                const uint4 w = kr[c];
-                const uint32_t dws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-                for (int d = 0; d < 4; ++d)
-#pragma unroll
-                    for (int b = 0; b < 4; ++b) acc += qs[c * 16 + d * 4 + b] * i8_lane(dws[d], b);
-            }
-            const float s = acc * ks[slot] * scale;
-            sc[t] = s;
-            if (s > mx) mx = s;
-        }
-    }
-    return mx;
-}
-
-// The same over the f32 view (F32View::dot, attention.rs:171-178): each
-// score is its own qk-long chain of q[e] * k[e], then times 1/sqrt(qk); no
-// key scale.  QC > 0: two positions' K rows load together and their chains
-// run interleaved.
-template <int QC, int NT>
-__device__ __forceinline__ float attn_scores_f32(const ndkv::Geom &g, const float *qs,
-                                                 const float *kb, int base, int span, float scale,
-                                                 float *sc)
-{
-    constexpr int kB = QC >= 4 ? 1 : 2;  // K rows in registers: at most 96 floats
-    const int tid = threadIdx.x;
-    float mx = -INFINITY;
-    if constexpr (QC > 0) {
-        for (int t0 = tid; t0 < span; t0 += NT * kB) {
-            float4 kw[kB][4 * QC];
-#pragma unroll
-            for (int u = 0; u < kB; ++u) {
-                const int t = t0 + u * NT;
-                int slot = base + (t < span ? t : 0);
-                if (slot >= g.cap) slot -= g.cap;
-                const float4 *kr = reinterpret_cast<const float4 *>(kb + size_t(slot) * (16 * QC));
-#pragma unroll
-                for (int c = 0; c < 4 * QC; ++c) kw[u][c] = kr[c];
-            }
-            float acc[kB];
-#pragma unroll
-            for (int u = 0; u < kB; ++u) acc[u] = 0.0f;
-#pragma unroll
-            for (int c = 0; c < 4 * QC; ++c) {
-#pragma unroll
-                for (int u = 0; u < kB; ++u) {
-                    acc[u] += qs[4 * c] * kw[u][c].x;
-                    acc[u] += qs[4 * c + 1] * kw[u][c].y;
-                    acc[u] += qs[4 * c + 2] * kw[u][c].z;
-                    acc[u] += qs[4 * c + 3] * kw[u][c].w;
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < kB; ++u) {
-                const int t = t0 + u * NT;
-                if (t < span) {
-                    const float s = acc[u] * scale;
-                    sc[t] = s;
-                    if (s > mx) mx = s;
-                }
-            }
-        }
-    } else {
-        for (int t = tid; t < span; t += NT) {
-            int slot = base + t;
-            if (slot >= g.cap) slot -= g.cap;
-            const float4 *kr = reinterpret_cast<const float4 *>(kb + size_t(slot) * g.QK);
-            float acc = 0.0f;
-            for (int c = 0; c < g.QK / 4; ++c) {
-                const float4 w = kr[c];
-                acc += qs[4 * c] * w.x;
-                acc += qs[4 * c + 1] * w.y;
-                acc += qs[4 * c + 2] * w.z;
-                acc += qs[4 * c + 3] * w.w;
-            }
-            const float s = acc * scale;
-            sc[t] = s;
-            if (s > mx) mx = s;
-        }
-    }
-    return mx;
-}
-
-// One value item of the producers: 16 columns of one position, int8 codes
-// and the position's scale, or f32 values.
-template <bool KF>
-struct AttnVItem {
-    uint4 v;
-    float s;
-};
-template <>
-struct AttnVItem<true> {
-    float4 v[4];
-};
-
-// acc += v[0]; acc += v[1]; ... acc += v[n-1] in index order, v 16-byte
-// aligned LDS with at least 32 readable floats past v[n-1].  Terms go in
-// groups of 32, read into two register sets in turn, so that a group's
-// reads are in flight while the group before it is added.
-__device__ inline float lds_chain(float acc, const float *v, int n)
-{
-    const int G = (n + 31) / 32;
-    if (G == 0) return acc;
-    float4 a[8], b[8];
-    auto rd = [&](float4 (&r)[8], int gi) {
-        const float4 *v4 = reinterpret_cast<const float4 *>(v + gi * 32);
-#pragma unroll
-        for (int u = 0; u < 8; ++u) r[u] = v4[u];
-    };
-    auto add32 = [&](float s, const float4 (&r)[8], int m) {
-        const float4 lo[4] = {r[0], r[1], r[2], r[3]};
-        const float4 hi[4] = {r[4], r[5], r[6], r[7]};
-        if (m >= 32) return nd_add16(nd_add16(s, lo), hi);
-        s = nd_add_first(s, lo, m);
-        return m > 16 ? nd_add_first(s, hi, m - 16) : s;
-    };
-    rd(a, 0);
-    int gi = 0;
-    for (; gi + 2 < G; gi += 2) {
-        rd(b, gi + 1);
-        acc = add32(acc, a, 32);
-        rd(a, gi + 2);
-        acc = add32(acc, b, 32);
-    }
-    if (gi + 1 < G) {
-        rd(b, gi + 1);
-        acc = add32(acc, a, 32);
-        acc = add32(acc, b, n - (gi + 1) * 32);
-    } else {
-        acc = add32(acc, a, n - gi * 32);
-    }
-    return acc;
-}
-
-// KF: the cache is the f32 view (F32View, attention.rs:166-189): f32 K/V
-// rows at the f32 block's offsets, no scales, weights e * inv.
+// One workgroup per (query row, query head): the query head into LDS
+// (fake-quantised on request, quant_rows, v3/model.rs:289-293), then the
+// shared pass.  Blocks are numbered as described above.
 template <int CW, int QC, bool KF>
 __global__ __launch_bounds__(kAttn2Threads, 4) void attn_exact2_kernel(
     ndkv::Geom g, const uint8_t *__restrict__ kv, size_t stride, const int32_t *__restrict__ lo,
     const int32_t *__restrict__ hi, const float *__restrict__ q, float scale, int quant_query,
     float *__restrict__ out, int groups, int rows_per_block, const float *__restrict__ gate)
 {
-    constexpr int NT = kAttn2Threads;
     extern __shared__ __align__(16) float sm[];
-    __shared__ float qs[ndkv::kMaxDim];
-    __shared__ float red[NT / 64];
-    __shared__ float total;
+    __shared__ AttnLds L;
     const int tid = threadIdx.x;
     const int R = g.H / g.KVH;
     const int xcd = int(blockIdx.x) & 7, slot8 = int(blockIdx.x) >> 3;
@@ -802,201 +559,25 @@ __global__ __launch_bounds__(kAttn2Threads, 4) void attn_exact2_kernel(
     const uint8_t *blk = kv + size_t(i / rows_per_block) * stride;
     const int p0 = lo[i];
     const int span = hi[i] - p0 + 1;
+    float *orow = out + (size_t(i) * g.H + h) * g.VD;
     if (p0 < 0 || span < 1 || span > g.cap) {
-        for (int j = tid; j < g.VD; j += NT) out[(size_t(i) * g.H + h) * g.VD + j] = NAN;
+        for (int j = tid; j < g.VD; j += kAttn2Threads) orow[j] = NAN;
         return;
     }
-    float *sc = sm;                                   // [span] scores, then exps
-    float *prod = sm + ((g.cap + 3) & ~3);            // [2][kProdBuf] products
     const float *qv = q + (size_t(i) * g.H + h) * g.QK;
     if (tid < 64) {
-        // quant_rows (v3/model.rs:289-293): fake-quantised query head
         if (quant_query) {
             float s, inv;
             ndkv::quant_scale_wave(qv, g.QK, s, inv);
-            for (int e = tid; e < g.QK; e += 64) qs[e] = ndkv::quant_code(qv[e], inv) * s;
+            for (int e = tid; e < g.QK; e += 64) L.qs[e] = ndkv::quant_code(qv[e], inv) * s;
         } else {
-            for (int e = tid; e < g.QK; e += 64) qs[e] = qv[e];
+            for (int e = tid; e < g.QK; e += 64) L.qs[e] = qv[e];
         }
     }
     __syncthreads();
-    const int base = p0 % g.cap;
-    float mx;
-    if constexpr (KF) {
-        const float *kb = reinterpret_cast<const float *>(blk) + size_t(kvh) * g.cap * g.QK;
-        mx = attn_scores_f32<QC, NT>(g, qs, kb, base, span, scale, sc);
-    } else {
-        const int8_t *kb = reinterpret_cast<const int8_t *>(blk) + size_t(kvh) * g.cap * g.QK;
-        const float *ks = reinterpret_cast<const float *>(blk + g.ks_off) + size_t(kvh) * g.cap;
-        mx = attn_scores<QC, NT>(g, qs, kb, ks, base, span, scale, sc);
-    }
-    mx = ndkv::wave_max(mx);
-    if ((tid & 63) == 0) red[tid >> 6] = mx;
-    __syncthreads();
-    mx = red[0];
-    for (int w = 1; w < NT / 64; ++w) mx = red[w] > mx ? red[w] : mx;
-    for (int t0 = tid; t0 < span; t0 += 4 * NT) {
-        // four independent exps per thread in flight
-        float e[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int t = t0 + u * NT;
-            e[u] = nd_expf(sc[t < span ? t : 0] - mx);
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-            if (t0 + u * NT < span) sc[t0 + u * NT] = e[u];
-    }
-    __syncthreads();
-
-    // Products sit column-major, [VD][T + 4] per buffer: a consumer lane reads
-    // four positions of its column per 16-byte read, and the 4-float pad puts
-    // the columns of one read in different banks.  Producer item (pc, tl) of a
-    // chunk is position tl, columns pc*16..+15; a wave's items are consecutive
-    // positions of one column piece.
-    constexpr int T = CW == 1 ? 48 : 16;  // positions per chunk: one item per producer
-    constexpr int TS = T + 4;
-    const int pieces = g.VD / 16;
-    const int nch = (span + T - 1) / T;
-    const bool producer = tid >= 64 * CW;
-    const int pt = tid - 64 * CW;
-    const int pc = pt / T, tl = pt - (pt / T) * T;
-    const bool has_item = producer && pc < pieces;
-    // chunks of V loads in flight: f32 items are four times the registers
-    constexpr int PF = KF ? 2 : kPrefetch;
-    AttnVItem<KF> vb[PF];
-    // Every load is issued unconditionally (a position past the span reads
-    // position 0 and is never used), so the compiler can count the loads in
-    // flight and wait for the oldest one only.
-    auto load = [&](int k, AttnVItem<KF> &it) {
-        int t = k * T + tl;
-        t = has_item && t < span ? t : 0;
-        int slot = base + t;
-        if (slot >= g.cap) slot -= g.cap;
-        if constexpr (KF) {
-            // V is the f32 block's last part: a thread without an item reads
-            // piece 0, so no read passes the row
-            const float4 *src = reinterpret_cast<const float4 *>(
-                reinterpret_cast<const float *>(blk + g.v_off) +
-                (size_t(kvh) * g.cap + slot) * g.VD + (has_item ? pc : 0) * 16);
-#pragma unroll
-            for (int u = 0; u < 4; ++u) it.v[u] = src[u];
-        } else {
-            const int8_t *vbase = reinterpret_cast<const int8_t *>(blk + g.v_off) + size_t(kvh) * g.cap * g.VD;
-            const float *vs = reinterpret_cast<const float *>(blk + g.vs_off) + size_t(kvh) * g.cap;
-            it.v = *reinterpret_cast<const uint4 *>(vbase + size_t(slot) * g.VD + pc * 16);
-            it.s = vs[slot];
-        }
-    };
-#pragma unroll
-    for (int j = 0; j < PF; ++j) load(j, vb[j]);
-    // The softmax sum, with the bits of one chain in position order.  The
-    // exps are >= +0, so a span long enough to pay for it takes the exact
-    // parallel fold, its LDS in the product buffers (first written after the
-    // barrier below); a shorter or longer one is the chain itself.
-    if (span >= kAttnFoldMin && span <= NT * kAttnFoldC) {
-        NdFoldLds<NT> &fl = *reinterpret_cast<NdFoldLds<NT> *>(prod);
-        const int cpt = (span + NT - 1) / NT;
-        float s;
-        if (cpt <= 4) s = nd_fold_nonneg<NT, 4>(sc, span, fl);
-        else if (cpt <= 9) s = nd_fold_nonneg<NT, 9>(sc, span, fl);
-        else s = nd_fold_nonneg<NT, kAttnFoldC>(sc, span, fl);
-        if (tid == 0) total = s;
-    } else if (tid == 0) {
-        __builtin_amdgcn_s_setprio(2);
-        const float s = lds_chain(0.0f, sc, span);
-        total = s;
-        __builtin_amdgcn_s_setprio(0);
-    }
-    __syncthreads();
-    const float inv = 1.0f / total;
-    float acc = 0.0f;
-    // Step k: producers fill chunk k, consumers add chunk k - 1.  Each role
-    // runs its own loop; the roles are whole waves and both pass the same
-    // number of barriers (a multiple of PF, the last few empty).
-    const int steps = (nch + 1 + PF - 1) / PF * PF;
-    if (producer) {
-        // this item's exp for the step after the current one, read ahead
-        float e_next = sc[tl < span ? tl : 0];
-        for (int k0 = 0; k0 < steps; k0 += PF) {
-#pragma unroll
-            for (int j = 0; j < PF; ++j) {
-                const int k = k0 + j;
-                const int t = k * T + tl;
-                const float e = e_next;
-                const int tn = t + T;
-                e_next = sc[tn < span ? tn : 0];
-                if (has_item && k < nch && t < span) {
-                    float p[16];
-                    if constexpr (KF) {
-                        // F32View::accum: w = e * inv, then w * v
-                        const float w = e * inv;
-#pragma unroll
-                        for (int u = 0; u < 4; ++u) {
-                            p[4 * u] = w * vb[j].v[u].x;
-                            p[4 * u + 1] = w * vb[j].v[u].y;
-                            p[4 * u + 2] = w * vb[j].v[u].z;
-                            p[4 * u + 3] = w * vb[j].v[u].w;
-                        }
-                    } else {
-                        // Int8View::accum: w = (e * inv) * v_scale, then w * code
-                        const float w = e * inv * vb[j].s;
-                        const uint32_t dws[4] = {vb[j].v.x, vb[j].v.y, vb[j].v.z, vb[j].v.w};
-#pragma unroll
-                        for (int d = 0; d < 4; ++d)
-#pragma unroll
-                            for (int b = 0; b < 4; ++b) p[d * 4 + b] = w * i8_lane(dws[d], b);
-                    }
-                    float *dst = prod + (k & 1) * kProdBuf + (pc * 16) * TS + tl;
-#pragma unroll
-                    for (int u = 0; u < 16; ++u) dst[u * TS] = p[u];
-                }
-                load(k + PF, vb[j]);
-                __syncthreads();
-            }
-        }
-    } else {
-        const float *col = prod + (tid < g.VD ? tid : 0) * TS;
-        // whole chunks inside the loop, each group's adds waiting for that
-        // group's reads only (the next group's are in flight); a ragged last
-        // chunk after it, once no producer writes its buffer any more
-        const int nfull = span / T;
-        for (int k = 0; k < steps; ++k) {
-            const int c = k - 1;
-            if (c >= 0 && c < nfull && tid < g.VD) {
-                __builtin_amdgcn_s_setprio(2);
-                const float *buf = col + (c & 1) * kProdBuf;
-                float4 a[4], b[4];
-                nd_lds_read16(a, buf);
-#pragma unroll
-                for (int gi = 0; gi < T / 16; ++gi) {
-                    if (gi % 2 == 0) {
-                        if (gi + 1 < T / 16) nd_lds_read16(b, buf + (gi + 1) * 16);
-                        acc = nd_add16(acc, a);
-                    } else {
-                        if (gi + 1 < T / 16) nd_lds_read16(a, buf + (gi + 1) * 16);
-                        acc = nd_add16(acc, b);
-                    }
-                }
-                __builtin_amdgcn_s_setprio(0);
-            }
-            __syncthreads();
-        }
-        if (nfull < nch && tid < g.VD) {
-            const float *buf = col + (nfull & 1) * kProdBuf;
-            const int rem = span - nfull * T;
-            for (int gi = 0; gi * 16 < rem; ++gi) {
-                float4 a[4];
-                nd_lds_read16(a, buf + gi * 16);
-                acc = nd_add_first(acc, a, rem - gi * 16);
-            }
-        }
-    }
-    if (tid < g.VD)
-        out[(size_t(i) * g.H + h) * g.VD + tid] =
-            gate_half_fwht(acc, gate ? gate + (size_t(i) * g.H + h) * g.VD : nullptr, tid);
+    attn_exact2_run<CW, QC, KF, false>(g, blk, kvh, p0, span, scale, sm, L, nullptr, orow,
+                                       gate ? gate + (size_t(i) * g.H + h) * g.VD : nullptr);
 }
-
 
 // ---------------------------------------------------------------------------
 // Row sums in the reference's order: ((0 + x[0]) + x[1]) + ... per row, one

@@ -31,6 +31,7 @@
 #include "nd_kv_internal.h"
 #include "nd_libm.h"
 #include "nd_ref_order.h"
+#include "nd_attn_exact.h"
 
 #include <cmath>
 #include <cstring>
@@ -1074,6 +1075,141 @@ __global__ __launch_bounds__(NTH) void k_qkv_kv(QkvKv a, MhcIn mhc)
     }
 }
 
+// ---- a decode step's attention launch with the q/k/v step folded in.
+// Workgroup (session i, kv head kvh, query head h) of the exact attention
+// first forms what k_qkv_kv would have left for it, with k_qkv_kv's
+// arithmetic: the causal conv of its query head and of its kv head's k and
+// v over the retained tails (cache.rs:401-438), ZCRMSNorm + RoPE on q and k
+// (attention.rs:108-150), k and v quantised (cache.rs:80-104) and q
+// fake-quantised (quant_rows, model.rs:289-293).  The kv head's first
+// workgroup writes k and v to the ring slot; every workgroup reads the
+// step's own row from LDS (the slot is not read back in the launch).  The
+// tails shift afterwards, in k_post_hada.  With mhc.on, B more workgroups
+// after the attention's run the scatter-up gates' phase 0.
+struct AttnStep {
+    QkvKv a;             // projections, taps, tails, norms, RoPE table, KV blocks
+    ndkv::Geom g;
+    const int32_t *lo, *hi;
+    float scale;
+    float *out;          // [B][H * 64] gated, half-transformed attention
+    const float *gate;   // [B][H * 64]
+    int groups;          // B * KVH
+    int attn_blocks;     // 8 * R * ceil(groups / 8)
+};
+
+template <int QC>
+__global__ __launch_bounds__(ndattn::kAttn2Threads, 4) void k_attn_step(AttnStep s, MhcIn mhc)
+{
+    using namespace ndattn;
+    extern __shared__ __align__(16) float sm[];
+    __shared__ AttnLds L;
+    __shared__ AttnNewRow nr;
+    __shared__ __align__(16) float xs[3][64], sqs[2][64];
+    __shared__ float rms[2];
+    if (int(blockIdx.x) >= s.attn_blocks) {
+        mhc_gates_phase0(mhc, blockIdx.x - s.attn_blocks);
+        return;
+    }
+    const QkvKv &a = s.a;
+    const ndkv::Geom &g = s.g;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int R = g.H / g.KVH;
+    const int xcd = int(blockIdx.x) & 7, slot8 = int(blockIdx.x) >> 3;
+    const int grp = (slot8 / R) * 8 + xcd;
+    if (grp >= s.groups) return;  // padding block: the whole block leaves
+    const int i = grp / g.KVH, kvh = grp - (grp / g.KVH) * g.KVH;
+    const int h = kvh * R + slot8 % R;
+    const int hd = a.hd, half = hd / 2, T = a.taps, p = a.pos[i];
+    // wave 0: the query head's channels, wave 1 the kv head's k, wave 2 its
+    // v; lane = channel (lanes past the head read channel 0, unused)
+    const int seg = wave < 3 ? wave : 0;
+    const int dim = seg == 0 ? a.qd : (seg == 1 ? a.kd : a.vd);
+    const int width = seg == 2 ? a.VD : hd;
+    const int c = (seg == 0 ? h * hd : (seg == 1 ? kvh * hd : kvh * a.VD)) + (lane < width ? lane : 0);
+    const float *src = seg == 0 ? a.q : (seg == 1 ? a.k : a.v);
+    const float *taps = seg == 0 ? a.q_taps : (seg == 1 ? a.k_taps : a.v_taps);
+    const float *tail = seg == 0 ? a.qt : (seg == 1 ? a.kt : a.vt);
+    const size_t tr = size_t(T > 1 ? T - 1 : 0);
+    // every operand before the first use
+    const float raw = src[size_t(i) * dim + c];
+    float tp[4], tv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        tp[j] = j < T ? taps[j * dim + c] : 0.0f;
+        tv[j] = j >= 1 && j < T ? tail[(size_t(i) * tr + (T - 1 - j)) * dim + c] : 0.0f;
+    }
+    const int li = lane < half ? lane : 0;
+    const float *nrm = seg == 0 ? a.q_norm : a.k_norm;
+    const float rn1 = nrm[li], rn2 = nrm[half + li];
+    const float *cs = a.rope + size_t(p) * 2 * half;
+    const float rc = cs[li], rsn = cs[half + li];
+    // conv_one's order: tap 0, then each tap back while j <= p
+    float v = raw;
+    if (T > 0) {
+        float acc = tp[0] * v;
+#pragma unroll
+        for (int j = 1; j < 4; ++j)
+            if (j < T && j <= p) acc += tp[j] * tv[j];
+        v = acc;
+    }
+    if (wave < 3 && lane < width) {
+        xs[seg][lane] = v;
+        if (seg < 2) sqs[seg][lane] = v * v;
+    }
+    lds_barrier();
+    // ZCRMSNorm: one sequential sum of squares per head, q and k side by side
+    if (lane == 0 && wave < 2) rms[wave] = sqrtf(chain_sum(sqs[wave], hd) / float(hd) + 1e-6f);
+    lds_barrier();
+    if (wave < 2 && lane < half) {
+        float *x = xs[wave];
+        const float r = rms[wave];
+        const float x1 = (1.0f + rn1) * x[lane] / r;
+        const float x2 = (1.0f + rn2) * x[half + lane] / r;
+        x[lane] = x1 * rc - x2 * rsn;
+        x[half + lane] = x2 * rc + x1 * rsn;
+    }
+    lds_barrier();
+    // quantise: the query (fake), k and v into LDS and, by the kv head's
+    // first workgroup, into the ring slot
+    uint8_t *blk = a.kv + size_t(i) * a.kv_stride;
+    const int slot = p % g.cap;
+    const bool writer = slot8 % R == 0;
+    if (wave < 3) {
+        const float *x = xs[seg];
+        float scl, inv;
+        ndkv::quant_scale_wave(x, width, scl, inv);
+        if (seg == 0) {
+            for (int e = lane; e < hd; e += 64) L.qs[e] = ndkv::quant_code(x[e], inv) * scl;
+        } else {
+            int8_t *mine = reinterpret_cast<int8_t *>(seg == 1 ? nr.k : nr.v);
+            int8_t *dst = reinterpret_cast<int8_t *>(blk + (seg == 2 ? g.v_off : 0)) +
+                          (size_t(kvh) * g.cap + slot) * width;
+            for (int e = lane; e < width; e += 64) {
+                const int8_t code = int8_t(ndkv::quant_code(x[e], inv));
+                mine[e] = code;
+                if (writer) dst[e] = code;
+            }
+            if (lane == 0) {
+                if (seg == 1) nr.ks = scl; else nr.vs = scl;
+                if (writer)
+                    *(reinterpret_cast<float *>(blk + (seg == 2 ? g.vs_off : g.ks_off)) +
+                      size_t(kvh) * g.cap + slot) = scl;
+            }
+        }
+    }
+    __syncthreads();
+    const int p0 = s.lo[i];
+    const int span = s.hi[i] - p0 + 1;
+    float *orow = s.out + (size_t(i) * g.H + h) * g.VD;
+    // the span must end at the step's own position
+    if (p0 < 0 || span < 1 || span > g.cap || s.hi[i] != p) {
+        for (int j = tid; j < g.VD; j += kAttn2Threads) orow[j] = NAN;
+        return;
+    }
+    attn_exact2_run<1, QC, false, true>(g, blk, kvh, p0, span, s.scale, sm, L, &nr, orow,
+                                        s.gate + (size_t(i) * g.H + h) * g.VD);
+}
+
 // attn *= sigmoid(gate) (model.rs:309-312), then prepare_input for out_proj.
 constexpr int kMaxGatePad = 2048;
 
@@ -1106,6 +1242,14 @@ struct HadaArgs {
     const float *cond_u;  // [rank][1024]
     const int32_t *p1, *p2perm;  // [1024]
     int d, rank;
+    // Decode steps whose attention launch ran the q/k/v conv (k_attn_step):
+    // the conv tails of q, k and v shift here, one channel of the q|k|v
+    // concatenation per thread (at most 1024 channels, taps <= 4); the raw
+    // projections are still in their buffers.  shift_taps <= 1: nothing to do.
+    int shift_taps = 0;
+    const float *sraw[3] = {};  // [B][dim] raw q, k, v
+    float *stail[3] = {};       // [B][taps - 1][dim]
+    int sdim[3] = {};
 };
 
 // out[k][l] = sum_j (sum_i z[i][l] a[i][k]) b[j][l], i and j ascending, each
@@ -1213,6 +1357,24 @@ __global__ __launch_bounds__(1024) void k_post_hada(HadaArgs a, MhcIn mhc)
         cv[j] = on ? v : 0.0f;
         cu[j] = on ? u : 0.0f;
     }
+    // the conv tails' shift: this thread's channel, its raw value and the
+    // tail rows that move up, loaded now and stored after the norms
+    const int nsh = a.shift_taps > 1 ? a.sdim[0] + a.sdim[1] + a.sdim[2] : 0;
+    float shv[3] = {0.0f, 0.0f, 0.0f};
+    float *shp = nullptr;
+    int shd = 1;
+    if (nsh > 0) {
+        const int c = tid < nsh ? tid : 0;
+        const int sg = c < a.sdim[0] ? 0 : (c < a.sdim[0] + a.sdim[1] ? 1 : 2);
+        const int cl = sg == 0 ? c : (sg == 1 ? c - a.sdim[0] : c - a.sdim[0] - a.sdim[1]);
+        shd = sg == 0 ? a.sdim[0] : (sg == 1 ? a.sdim[1] : a.sdim[2]);
+        const float *rw = sg == 0 ? a.sraw[0] : (sg == 1 ? a.sraw[1] : a.sraw[2]);
+        float *tl = sg == 0 ? a.stail[0] : (sg == 1 ? a.stail[1] : a.stail[2]);
+        shp = tl + b * size_t(a.shift_taps - 1) * shd + cl;
+        shv[0] = rw[b * shd + cl];
+#pragma unroll
+        for (int j = 1; j < 3; ++j) shv[j] = j + 1 < a.shift_taps ? shp[size_t(j) * shd] : 0.0f;
+    }
     lds_barrier();
     if (ch) {
         const float inv = 1.0f / sqrtf(tot[0] / float(d) + 1e-6f);
@@ -1223,6 +1385,13 @@ __global__ __launch_bounds__(1024) void k_post_hada(HadaArgs a, MhcIn mhc)
     }
     lds_barrier();
     if (tid == 0) tot[1] = chain_sum(z, d);
+    // tail row r takes row r + 1, the last row the raw value (conv_one)
+    if (nsh > 0 && tid < nsh) {
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+            if (r + 2 < a.shift_taps) shp[size_t(r) * shd] = shv[r + 1];
+        shp[size_t(a.shift_taps - 2) * shd] = shv[0];
+    }
     lds_barrier();
     const float xv = ch ? (1.0f + pre_n) * nbs[tid] * (1.0f / sqrtf(tot[1] / float(d) + 1e-6f)) : 0.0f;
     // cond = 1 + softmax(x . cond_v) . cond_u.  Projection j is one chain
@@ -2555,15 +2724,21 @@ int StepRun::enqueue(int phase, bool argmax)
             mi.state = b->gstate;
         }
         const unsigned gy = gates_in ? 2u : 1u;
+        const nd_kv_geom &g = b->geom[li];
+        QkvKv qk{b->q, b->k, b->v, b->qt[li], b->kt[li], b->vt[li], l.q_taps, l.k_taps,
+                 l.v_taps, l.q_norm, l.k_norm, m->rope_tab, pos_dev, qd, kd, vd,
+                 c.qkv_conv_taps, c.num_heads, c.num_kv_heads, c.qk_head_dim, c.v_head_dim,
+                 b->kv[li], b->kv_stride[li], nd_kv_v_offset(&g), nd_kv_ks_offset(&g),
+                 nd_kv_vs_offset(&g), g.cap, C, b->qn};
+        if (kf) qk.v_off = nd_kv_f32_v_offset(&g);
+        // a decode step over the int8 ring with the gated epilogue forms its
+        // q, k and v inside the attention launch (k_attn_step)
+        const bool step_attn = C == 1 && !kf && gate_fused && c.qk_head_dim % 16 == 0 &&
+                               c.qk_head_dim <= 64 && c.v_head_dim == 64 &&
+                               c.qkv_conv_taps <= 4 && g.cap <= ndattn::kAttn2MaxCap &&
+                               qd + kd + vd <= 1024 && B <= 65535;
         // conv, norm + RoPE, int8 KV append
-        {
-            const nd_kv_geom &g = b->geom[li];
-            QkvKv qk{b->q, b->k, b->v, b->qt[li], b->kt[li], b->vt[li], l.q_taps, l.k_taps,
-                     l.v_taps, l.q_norm, l.k_norm, m->rope_tab, pos_dev, qd, kd, vd,
-                     c.qkv_conv_taps, c.num_heads, c.num_kv_heads, c.qk_head_dim, c.v_head_dim,
-                     b->kv[li], b->kv_stride[li], nd_kv_v_offset(&g), nd_kv_ks_offset(&g),
-                     nd_kv_vs_offset(&g), g.cap, C, b->qn};
-            if (kf) qk.v_off = nd_kv_f32_v_offset(&g);
+        if (!step_attn) {
             const dim3 qg(unsigned(B), gy);
             if (C == 1) {
                 if (kf)
@@ -2594,7 +2769,25 @@ int StepRun::enqueue(int phase, bool argmax)
         // 64-wide heads and 128-wide groups its epilogue also applies
         // the sigmoid gate and the butterfly stages inside each head,
         // and out_proj's load finishes prepare_input
-        if (gate_fused) {
+        if (step_attn) {
+            const int R = c.num_heads / c.num_kv_heads;
+            const size_t groups = size_t(B) * c.num_kv_heads;
+            const size_t ablocks = 8 * size_t(R) * ((groups + 7) / 8);
+            const size_t lds = size_t((g.cap + 3) & ~3) * 4 + 2 * ndattn::kProdBuf * sizeof(float);
+            AttnStep as{qk, ndkv::make_geom(&g), lo_dev + size_t(li) * B, hi_dev, qk_scale,
+                        b->attn, b->gate, int(groups), int(ablocks)};
+            const dim3 ag(unsigned(ablocks + (gates_in ? size_t(B) : 0)));
+            switch (c.qk_head_dim / 16) {
+            case 1: hipLaunchKernelGGL((k_attn_step<1>), ag, dim3(ndattn::kAttn2Threads), lds, st, as, mi); break;
+            case 2: hipLaunchKernelGGL((k_attn_step<2>), ag, dim3(ndattn::kAttn2Threads), lds, st, as, mi); break;
+            case 3: hipLaunchKernelGGL((k_attn_step<3>), ag, dim3(ndattn::kAttn2Threads), lds, st, as, mi); break;
+            default: hipLaunchKernelGGL((k_attn_step<4>), ag, dim3(ndattn::kAttn2Threads), lds, st, as, mi); break;
+            }
+            LCHK("k_attn_step");
+            const size_t r0 = 0, nr = size_t(d);
+            CK(nd_cq_exact_set(ctx, st, 1, &l.out, b->attn, size_t(B), &r0, &nr, &b->proj,
+                               "v3 out projection", m->pre_attn.inv));
+        } else if (gate_fused) {
             CK(nd_attend_exact_rows(ctx, &b->geom[li], b->kv[li], b->kv_stride[li], size_t(B), C,
                                     lo_dev + size_t(li) * B, hi_dev, C == 1 ? b->q : b->qn,
                                     qk_scale, kf ? 0 : 1, b->attn, b->gate, kf));
@@ -2613,6 +2806,18 @@ int StepRun::enqueue(int phase, bool argmax)
         HadaArgs ha{b->proj, l.post_norm, l.pre_hada, nd_sigmoidf(l.attn_gate), b->u, b->bx, b->y,
                     l.d1, l.d2, l.b2, l.d3, l.d4, l.w1a, l.w1b, l.w2a, l.w2b, l.w3a, l.w3b,
                     l.cond_v, l.cond_u, m->p1, m->p2, d, l.cond_rank};
+        if (step_attn && c.qkv_conv_taps > 1) {
+            ha.shift_taps = c.qkv_conv_taps;
+            ha.sraw[0] = b->q;
+            ha.sraw[1] = b->k;
+            ha.sraw[2] = b->v;
+            ha.stail[0] = b->qt[li];
+            ha.stail[1] = b->kt[li];
+            ha.stail[2] = b->vt[li];
+            ha.sdim[0] = qd;
+            ha.sdim[1] = kd;
+            ha.sdim[2] = vd;
+        }
         hipLaunchKernelGGL(k_post_hada, dim3(unsigned(B), gy), dim3(1024), 0, st, ha, mi);
         LCHK("k_post_hada");
         return ND_OK;
