@@ -84,6 +84,9 @@ def parse():
                         "steps of a rocprofv3 kernel-trace CSV (steps end at k_final); with "
                         "--tail-steps 0, of every launch, per kernel and grid size")
     p.add_argument("--tail-steps", type=int, default=128)
+    p.add_argument("--skip-steps", type=int, default=0,
+                   help="with --summarize-trace: leave out the trace's last N forward steps "
+                        "(e.g. 256: the two-stream run of 2 x 128 steps that ends --only forward)")
     p.add_argument("--summarize-pmc", metavar="CSV", default=None,
                    help="no GPU: print the mean of each counter per dispatch of a rocprofv3 "
                         "--pmc counter-collection CSV, per kernel and grid size")
@@ -97,12 +100,14 @@ def parse():
     return p.parse_args()
 
 
-def summarize_trace(path, nsteps):
+def summarize_trace(path, nsteps, skip=0):
     """Per-kernel durations over the last `nsteps` forward steps of a
-    rocprofv3 --kernel-trace CSV (plain or gzipped).  Each step launches
-    k_final once, so the window starts after the (nsteps + 1)-th last k_final
-    ends; kernels of the side stream in that window are included.  With
-    nsteps 0, every launch of the trace, grouped by kernel and grid size."""
+    rocprofv3 --kernel-trace CSV (plain or gzipped), leaving out the last
+    `skip` steps.  Each step launches k_final once, so the window runs from
+    the end of the (nsteps + skip + 1)-th last k_final to the end of the
+    (skip + 1)-th last; kernels of the side stream in that window are
+    included.  With nsteps 0, every launch of the trace, grouped by kernel and
+    grid size."""
     import collections
     import csv
     import gzip
@@ -126,12 +131,13 @@ def summarize_trace(path, nsteps):
                   f"{min(v) / 1e3:.2f} | {max(v) / 1e3:.2f} |")
         return
     finals = [i for i, r in enumerate(rows) if "::k_final(" in r[2]]
-    t0 = rows[finals[-(nsteps + 1)]][1]
-    sel = [r for r in rows if r[0] > t0]
+    t0 = rows[finals[-(nsteps + skip + 1)]][1]
+    t1 = rows[finals[-(skip + 1)]][1]
+    sel = [r for r in rows if t0 < r[0] and r[1] <= t1]
     agg = collections.defaultdict(list)
     for a, b, n, _ in sel:
         agg[n].append(b - a)
-    span = (max(r[1] for r in sel) - t0) / 1e3
+    span = (t1 - t0) / 1e3
     print(f"last {nsteps} steps: {span / nsteps:.1f} us per step (profiler on), {len(sel)} kernels")
     print("| kernel | per step | avg us | min us | max us | us per step |")
     print("|---|---|---|---|---|---|")
@@ -720,7 +726,7 @@ def main():
     args = parse()
     MIN_WARM_S = args.min_warm
     if args.summarize_trace:
-        summarize_trace(args.summarize_trace, args.tail_steps)
+        summarize_trace(args.summarize_trace, args.tail_steps, args.skip_steps)
         return
     if args.summarize_pmc:
         summarize_pmc(args.summarize_pmc, args.pmc_period, args.pmc_runs)

@@ -60,6 +60,16 @@ __device__ inline void lds_barrier()
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Orders one wave's LDS writes before its own later LDS reads of other
+// lanes' values (a wave's LDS operations execute in order; this keeps the
+// compiler from moving them across).
+__device__ inline void wave_lds_sync()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+}
+
 __device__ inline float chain_sum(const float *p, int n)
 {
     __builtin_amdgcn_s_setprio(2);
@@ -762,8 +772,12 @@ __device__ __forceinline__ float transpose4x4(float m)
 // stream of their own and lengthen no launch of the layer's chain.
 constexpr int kSinkhornIters = 20;   // SINKHORN_ITERS (kernels.rs)
 // iterations in phase 0: about 1.1 us each; 4 fit k_qkv_kv's time (3 to 5
-// measured alike at 64 sessions, 6 slower) and the other 16 k_post_hada's
+// measured alike at 64 sessions, 6 slower) and the other 16 k_post_hada's.
+// In the attention launch (k_attn_step), 6: 64 sessions 1.931 / 1.909 /
+// 1.912 / 1.911 / 1.914 ms a step at 4 / 6 / 8 / 10 / 12, one session 1.245
+// / 1.225 / 1.226 / 1.246 / 1.296 ms a token
 constexpr int kGateSplit = 4;
+constexpr int kGateSplitAttn = 6;
 struct MhcIn {
     int on;                     // this launch runs a gate phase
     const float *graw;          // [B][n + n*n] from k_layer_in
@@ -1105,7 +1119,6 @@ __global__ __launch_bounds__(ndattn::kAttn2Threads, 4) void k_attn_step(AttnStep
     __shared__ AttnLds L;
     __shared__ AttnNewRow nr;
     __shared__ __align__(16) float xs[3][64], sqs[2][64];
-    __shared__ float rms[2];
     if (int(blockIdx.x) >= s.attn_blocks) {
         mhc_gates_phase0(mhc, blockIdx.x - s.attn_blocks);
         return;
@@ -1120,8 +1133,10 @@ __global__ __launch_bounds__(ndattn::kAttn2Threads, 4) void k_attn_step(AttnStep
     const int i = grp / g.KVH, kvh = grp - (grp / g.KVH) * g.KVH;
     const int h = kvh * R + slot8 % R;
     const int hd = a.hd, half = hd / 2, T = a.taps, p = a.pos[i];
+    const int p0 = s.lo[i], hi = s.hi[i];
     // wave 0: the query head's channels, wave 1 the kv head's k, wave 2 its
-    // v; lane = channel (lanes past the head read channel 0, unused)
+    // v; lane = channel (lanes past the head read channel 0, unused).  Each
+    // wave's part is its own: it syncs with itself only, then all meet once.
     const int seg = wave < 3 ? wave : 0;
     const int dim = seg == 0 ? a.qd : (seg == 1 ? a.kd : a.vd);
     const int width = seg == 2 ? a.VD : hd;
@@ -1143,39 +1158,40 @@ __global__ __launch_bounds__(ndattn::kAttn2Threads, 4) void k_attn_step(AttnStep
     const float rn1 = nrm[li], rn2 = nrm[half + li];
     const float *cs = a.rope + size_t(p) * 2 * half;
     const float rc = cs[li], rsn = cs[half + li];
-    // conv_one's order: tap 0, then each tap back while j <= p
-    float v = raw;
-    if (T > 0) {
-        float acc = tp[0] * v;
-#pragma unroll
-        for (int j = 1; j < 4; ++j)
-            if (j < T && j <= p) acc += tp[j] * tv[j];
-        v = acc;
-    }
-    if (wave < 3 && lane < width) {
-        xs[seg][lane] = v;
-        if (seg < 2) sqs[seg][lane] = v * v;
-    }
-    lds_barrier();
-    // ZCRMSNorm: one sequential sum of squares per head, q and k side by side
-    if (lane == 0 && wave < 2) rms[wave] = sqrtf(chain_sum(sqs[wave], hd) / float(hd) + 1e-6f);
-    lds_barrier();
-    if (wave < 2 && lane < half) {
-        float *x = xs[wave];
-        const float r = rms[wave];
-        const float x1 = (1.0f + rn1) * x[lane] / r;
-        const float x2 = (1.0f + rn2) * x[half + lane] / r;
-        x[lane] = x1 * rc - x2 * rsn;
-        x[half + lane] = x2 * rc + x1 * rsn;
-    }
-    lds_barrier();
-    // quantise: the query (fake), k and v into LDS and, by the kv head's
-    // first workgroup, into the ring slot
     uint8_t *blk = a.kv + size_t(i) * a.kv_stride;
-    const int slot = p % g.cap;
-    const bool writer = slot8 % R == 0;
     if (wave < 3) {
-        const float *x = xs[seg];
+        // conv_one's order: tap 0, then each tap back while j <= p
+        float v = raw;
+        if (T > 0) {
+            float acc = tp[0] * v;
+#pragma unroll
+            for (int j = 1; j < 4; ++j)
+                if (j < T && j <= p) acc += tp[j] * tv[j];
+            v = acc;
+        }
+        float *x = xs[seg];
+        if (lane < width) {
+            x[lane] = v;
+            if (seg < 2) sqs[seg][lane] = v * v;
+        }
+        wave_lds_sync();
+        if (seg < 2) {
+            // ZCRMSNorm: the head's sequential sum of squares, then RoPE
+            float r = 0.0f;
+            if (lane == 0) r = sqrtf(chain_sum(sqs[seg], hd) / float(hd) + 1e-6f);
+            r = __shfl(r, 0, 64);
+            if (lane < half) {
+                const float x1 = (1.0f + rn1) * x[lane] / r;
+                const float x2 = (1.0f + rn2) * x[half + lane] / r;
+                x[lane] = x1 * rc - x2 * rsn;
+                x[half + lane] = x2 * rc + x1 * rsn;
+            }
+            wave_lds_sync();
+        }
+        // quantise: the query (fake), k and v into LDS and, by the kv
+        // head's first workgroup, into the ring slot
+        const int slot = p % g.cap;
+        const bool writer = slot8 % R == 0;
         float scl, inv;
         ndkv::quant_scale_wave(x, width, scl, inv);
         if (seg == 0) {
@@ -1198,11 +1214,10 @@ __global__ __launch_bounds__(ndattn::kAttn2Threads, 4) void k_attn_step(AttnStep
         }
     }
     __syncthreads();
-    const int p0 = s.lo[i];
-    const int span = s.hi[i] - p0 + 1;
+    const int span = hi - p0 + 1;
     float *orow = s.out + (size_t(i) * g.H + h) * g.VD;
     // the span must end at the step's own position
-    if (p0 < 0 || span < 1 || span > g.cap || s.hi[i] != p) {
+    if (p0 < 0 || span < 1 || span > g.cap || hi != p) {
         for (int j = tid; j < g.VD; j += kAttn2Threads) orow[j] = NAN;
         return;
     }
@@ -2737,6 +2752,7 @@ int StepRun::enqueue(int phase, bool argmax)
                                c.qk_head_dim <= 64 && c.v_head_dim == 64 &&
                                c.qkv_conv_taps <= 4 && g.cap <= ndattn::kAttn2MaxCap &&
                                qd + kd + vd <= 1024 && B <= 65535;
+        if (step_attn) mi.split = kGateSplitAttn;
         // conv, norm + RoPE, int8 KV append
         if (!step_attn) {
             const dim3 qg(unsigned(B), gy);
