@@ -209,3 +209,30 @@ def test_conv_taps_track_the_oracle(ctx, taps):
         assert np.array_equal(_bits(outs[i]), _bits(want)), (taps, i, np.max(np.abs(outs[i] - want)))
     batch.close()
     dm.close()
+
+
+@pytest.mark.parametrize("qk", [16, 32, 64])
+def test_head_dims_track_the_oracle(ctx, qk):
+    """q/k head widths other than the shipped 48: a decode step forms each
+    query head and its kv head's k and v inside the attention launch, with
+    the head read in qk / 16 pieces of 16 codes (1, 2 and 4 here).  Two
+    sessions stepped past the sliding window, every logit bit for bit the
+    oracle's."""
+    geo = S.small_geometry(2)
+    geo["qk_head_dim"] = qk
+    g, recs = S.build_records(geo, seed=31 + qk)
+    om = O.V3Model(g, recs, S.CODEBOOK)
+    dm = nd.V3Model(ctx, g, recs, S.CODEBOOK)
+    prompts = np.stack([S.prompt_tokens(40, 300 + qk + i) for i in range(2)])
+    batch = nd.V3Batch(dm, 2, max_len=48)
+    got = torch.empty(2, dm.rows, device="cuda")
+    outs = []
+    for t in range(prompts.shape[1]):
+        batch.step(prompts[:, t], logits=got, want_next=False)
+        outs.append(got.cpu().numpy().copy())
+    outs = np.stack(outs, axis=1)
+    for i in range(2):
+        want = _oracle_logits(om, prompts[i])
+        assert np.array_equal(_bits(outs[i]), _bits(want)), (qk, i, np.max(np.abs(outs[i] - want)))
+    batch.close()
+    dm.close()
