@@ -236,3 +236,31 @@ def test_head_dims_track_the_oracle(ctx, qk):
         assert np.array_equal(_bits(outs[i]), _bits(want)), (qk, i, np.max(np.abs(outs[i] - want)))
     batch.close()
     dm.close()
+
+
+def test_greedy_ties_take_the_first_index(ctx):
+    """Greedy ties go to the first index.  With the tied embedding's upper
+    half a copy of its lower half every logit appears twice (rows computed
+    by different workgroups, bit-identical), so every step is a tie: the
+    tokens must be the oracle's first-maximum choices, all in the lower
+    half."""
+    g, recs = S.build_records(S.small_geometry(2), seed=41)
+    emb = next(r for r in recs if r["name"] == "embedding")
+    V, pad = emb["out"], -(-emb["inn"] // emb["group"]) * emb["group"]
+    row_bytes, G = pad * emb["bits"] // 8, pad // emb["group"]
+    blob = emb["data"].copy()
+    codes = blob[:V * row_bytes].reshape(V, row_bytes)
+    norms = blob[V * row_bytes:].view(np.uint16).reshape(V, G)
+    codes[V // 2:] = codes[:V // 2]
+    norms[V // 2:] = norms[:V // 2]
+    emb["data"] = blob
+    om = O.V3Model(g, recs, S.CODEBOOK)
+    dm = nd.V3Model(ctx, g, recs, S.CODEBOOK)
+    prompt = S.prompt_tokens(12, 9)
+    toks, _ = O.v3_generate(om, prompt, 24)
+    batch = nd.V3Batch(dm, 2, max_len=48)
+    got = batch.generate(np.stack([prompt, prompt]), 24)
+    assert np.array_equal(got[0], toks.astype(np.int32)) and np.array_equal(got[1], got[0])
+    assert int(got.max()) < V // 2
+    batch.close()
+    dm.close()
