@@ -36,6 +36,13 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "needle-rs_amd"))
 
+# The forward's four-stream run needs a hardware queue per stream besides
+# the default stream's.  HIP gives a process four by default, with which two
+# of the four streams share one and run one after the other (3.27 against
+# 1.82 ms a step); set before anything initialises HIP.
+if int(os.environ.get("GPU_MAX_HW_QUEUES", "4")) < 8:
+    os.environ["GPU_MAX_HW_QUEUES"] = "8"
+
 HBM_PEAK_GBS = 8000.0
 FP32_MFMA_TFLOPS = 157.3
 GEMV_OUT, GEMV_IN = 3072, 768
@@ -643,19 +650,21 @@ def forward_runs(torch, nd, ctx, sessions, ctx_len, check=True):
         "tokens_equal_host_stepped": bool(np.array_equal(toks, toks_h)),
         "prefill_tok_per_s": round(sessions * ctx_len / t_pre, 1),
     }
-    # the same sessions as two batches of sessions / 2 on two streams, their
+    # the same sessions as n batches of sessions / n on n streams, their
     # greedy loops enqueued in turn from this thread (nd_v3_generate_many):
-    # one batch's one-workgroup-per-session kernels run beside the other's
-    # projections and attention; projections batched over sessions / 2
-    if sessions % 2 == 0:
-        half = sessions // 2
-        streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    # one batch's one-workgroup-per-session kernels run beside another's
+    # projections and attention; projections batched over sessions / n
+    for n, name in ((2, "two_streams"), (4, "four_streams")):
+        if sessions % n:
+            continue
+        part = sessions // n
+        streams = [torch.cuda.Stream() for _ in range(n)]
         ctxs = [nd.Ctx(0, stream=st) for st in streams]
         batches, firsts = [], []
-        for k in range(2):
-            b = nd.V3Batch(model, half, max_len=ctx_len + steps, max_chunk=32, ctx=ctxs[k])
-            pr = np.ascontiguousarray(np.stack([S.prompt_tokens(ctx_len, 100 + k * half + i)
-                                                for i in range(half)]), np.int32)
+        for k in range(n):
+            b = nd.V3Batch(model, part, max_len=ctx_len + steps, max_chunk=32, ctx=ctxs[k])
+            pr = np.ascontiguousarray(np.stack([S.prompt_tokens(ctx_len, 100 + k * part + i)
+                                                for i in range(part)]), np.int32)
             nxt = None
             for t in range(0, ctx_len, 32):
                 t1 = min(ctx_len, t + 32)
@@ -668,11 +677,12 @@ def forward_runs(torch, nd, ctx, sessions, ctx_len, check=True):
         t_dec2 = time.perf_counter() - t0
         toks2 = np.concatenate([np.concatenate([f[:, None], o[:, :-1]], axis=1)
                                 for f, o in zip(firsts, outs)], axis=0)
-        out[key]["two_streams"] = {
-            "workload": f"the same {sessions} sessions as two batches of {half} on two streams, "
+        out[key][name] = {
+            "workload": f"the same {sessions} sessions as {n} batches of {part} on {n} streams, "
                         "their greedy loops enqueued in turn from one host thread "
                         "(nd_v3_generate_many); projections batched over each batch's "
-                        f"{half} sessions",
+                        f"{part} sessions; {os.environ.get('GPU_MAX_HW_QUEUES', '4')} "
+                        "hardware queues a process",
             "decode_tok_per_s": round(sessions * steps / t_dec2, 1),
             "decode_ms_per_step": round(t_dec2 / steps * 1e3, 3),
             "tokens_equal_one_batch": bool(np.array_equal(toks2, toks)),
