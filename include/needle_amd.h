@@ -460,7 +460,10 @@ int nd_v3_generate(nd_ctx *ctx, const nd_v3_model *m, nd_v3_batch *b, const int3
  * call.  No reference counterpart: the reference serves concurrent
  * sessions from its own threads (V3Engine per session, v3_engine.rs:544-561);
  * this is the one-thread form of that, for a server that groups its
- * sessions into a few batches. */
+ * sessions into a few batches.  The streams run side by side only on
+ * hardware queues of their own: HIP gives a process GPU_MAX_HW_QUEUES
+ * (default 4) of them, shared with every other stream, so n batches want
+ * that at n + 1 or more (set before HIP starts). */
 int nd_v3_generate_many(nd_ctx *const *ctxs, const nd_v3_model *m, nd_v3_batch *const *bs,
                         size_t n, const int32_t *const *first, size_t steps,
                         int32_t *const *tokens);
