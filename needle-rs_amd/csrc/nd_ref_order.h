@@ -95,6 +95,27 @@ __device__ inline float cq_group_dot128(const CqGroupCodes<P> &c, const float *l
     return acc;
 }
 
+// Lanes 2q and 2q + 1 (q < 4) of cq_group_dot128's eight, with its
+// arithmetic: a quarter of the dot, for spreading one group over 4 threads.
+template <int P>
+__device__ inline void cq_group_quarter128(const CqGroupCodes<P> &c, const float *lvl, const float *x,
+                                           int q, float &l0, float &l1)
+{
+    constexpr int W = CqGroupCodes<P>::W;
+    constexpr uint32_t MASK = (1u << W) - 1;
+    constexpr int PER_DW = CqGroupCodes<P>::PER_DW;
+    l0 = 0.0f;
+    l1 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const uint32_t dw = c.dw[(i * 8) / PER_DW];
+        const int sh = ((i * 8 * W) & 31) + 2 * q * W;
+        const float2 xv = *reinterpret_cast<const float2 *>(x + i * 8 + 2 * q);
+        l0 += lvl[(dw >> sh) & MASK] * xv.x;
+        l1 += lvl[(dw >> (sh + W)) & MASK] * xv.y;
+    }
+}
+
 // acc += a[0].x; acc += a[0].y; ... acc += a[3].w: 16 dependent adds in one
 // asm block, so the compiler can neither reorder the terms nor move LDS
 // reads across the block (left to itself it hoists the next group's reads

@@ -382,6 +382,7 @@ __global__ __launch_bounds__(NTH) void k_layer_in(LayerIn a)
     __shared__ __align__(16) float us[1024], bxs[1024], pa[1024], pb[1024], pc[1024];
     __shared__ float gs[kMaxPhiPairs], pn[kMaxPhiPairs], lvl[48], hp[16], gpp[16], grr[256], tot[4];
     __shared__ NdFoldLds<NTH> fl;
+    __shared__ float qlanes[NTH / 4 * 8];  // split phi pairs' lane chains
     const size_t b = blockIdx.x;
     const int tid = threadIdx.x, n = a.n, d = a.d, nd = n * d;
     // phi rows: phi_pre's n, then (gates) phi_post's n and phi_res's n * n
@@ -460,9 +461,14 @@ __global__ __launch_bounds__(NTH) void k_layer_in(LayerIn a)
     CqGroupCodes<PP> codes[kPhiPerThread];
     float pnv[kPhiPerThread];
     int wsel[kPhiPerThread];
+    // pairs past the first NTH (at most NTH / 4 of them): four threads a
+    // pair, each two of its eight lane chains, so that no thread holds two
+    // whole dots (the phase would last two dots for one wave)
+    const int extra = pairs - NTH;
+    const bool quarters = kPhiPerThread == 2 && extra > 0 && extra <= NTH / 4;
 #pragma unroll
     for (int k = 0; k < kPhiPerThread; ++k) {
-        const int t = tid + k * NTH;
+        const int t = k == 1 && quarters ? NTH + (tid >> 2) : tid + k * NTH;
         const bool has = t < pairs;
         const int r = has ? t / G : 0, g = has ? t - (t / G) * G : 0;
         const float *nr;
@@ -495,8 +501,13 @@ __global__ __launch_bounds__(NTH) void k_layer_in(LayerIn a)
         tot[0] = chain_sum(nb, nd);
     }
 #pragma unroll
-    for (int k = 0; k < kPhiPerThread; ++k)
-        if (tid + k * NTH < pairs) pn[tid + k * NTH] = pnv[k];
+    for (int k = 0; k < kPhiPerThread; ++k) {
+        if (k == 1 && quarters) {
+            if ((tid & 3) == 0 && NTH + (tid >> 2) < pairs) pn[NTH + (tid >> 2)] = pnv[k];
+        } else if (tid + k * NTH < pairs) {
+            pn[tid + k * NTH] = pnv[k];
+        }
+    }
     if (tid < 48) lvl[tid] = lvv;
     lds_barrier();
     {
@@ -533,10 +544,30 @@ __global__ __launch_bounds__(NTH) void k_layer_in(LayerIn a)
     // this layer's phi rows (matvec_rows_prepared, reference order)
 #pragma unroll
     for (int k = 0; k < kPhiPerThread; ++k) {
+        if (k == 1 && quarters) {
+            const int t = NTH + (tid >> 2), q = tid & 3;
+            if (t < pairs) {
+                float l0, l1;
+                cq_group_quarter128<PP>(codes[k], lvl + 16 * wsel[k], nb + (t % G) * kPadGroup, q, l0, l1);
+                qlanes[(t - NTH) * 8 + 2 * q] = l0;
+                qlanes[(t - NTH) * 8 + 2 * q + 1] = l1;
+            }
+            continue;
+        }
         const int t = tid + k * NTH;
         if (t < pairs) gs[t] = cq_group_dot128<PP>(codes[k], lvl + 16 * wsel[k], nb + (t % G) * kPadGroup);
     }
     lds_barrier();
+    if (quarters) {
+        // the split pairs' lanes summed 0..7, as cq_group_dot128 ends
+        if (tid < extra) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) acc += qlanes[tid * 8 + k];
+            gs[NTH + tid] = acc;
+        }
+        lds_barrier();
+    }
     if (tid < prows) {
         float total = 0.0f;
         for (int g = 0; g < G; ++g) total += pn[tid * G + g] * gs[tid * G + g];
