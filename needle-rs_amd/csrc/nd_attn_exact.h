@@ -12,6 +12,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 namespace ndattn {
 
 __device__ inline float i8_lane(uint32_t dw, int b) { return float(int32_t(dw << (24 - 8 * b)) >> 24); }
@@ -92,13 +94,15 @@ __device__ __forceinline__ float attn_scores(const ndkv::Geom &g, const float *q
     const int tid = threadIdx.x;
     float mx = -INFINITY;
     if constexpr (QC > 0) {
-        for (int t0 = tid; t0 < span; t0 += NT * kScoreBatch) {
-            uint4 kw[kScoreBatch][QC];
-            float ksv[kScoreBatch];
+        // U positions t0, t0 + NT, ... (all inside the span) with their K
+        // rows loaded together and their chains interleaved
+        auto batch = [&](auto uc, int t0) {
+            constexpr int U = decltype(uc)::value;
+            uint4 kw[U][QC];
+            float ksv[U];
 #pragma unroll
-            for (int u = 0; u < kScoreBatch; ++u) {
-                const int t = t0 + u * NT;
-                int slot = base + (t < span ? t : 0);
+            for (int u = 0; u < U; ++u) {
+                int slot = base + t0 + u * NT;
                 if (slot >= g.cap) slot -= g.cap;
                 const uint4 *kr = reinterpret_cast<const uint4 *>(kb + size_t(slot) * (16 * QC));
 #pragma unroll
@@ -106,11 +110,10 @@ __device__ __forceinline__ float attn_scores(const ndkv::Geom &g, const float *q
                 ksv[u] = ks[slot];
             }
             if constexpr (NEW) {
-                // the span's last position, in this thread's last batch: the
-                // launch's own row
-                if (t0 + (kScoreBatch - 1) * NT >= span - 1) {
+                // the span's last position: the launch's own row
+                if (t0 + (U - 1) * NT >= span - 1) {
 #pragma unroll
-                    for (int u = 0; u < kScoreBatch; ++u)
+                    for (int u = 0; u < U; ++u)
                         if (t0 + u * NT == span - 1) {
 #pragma unroll
                             for (int c = 0; c < QC; ++c) kw[u][c] = nr->k[c];
@@ -118,9 +121,9 @@ __device__ __forceinline__ float attn_scores(const ndkv::Geom &g, const float *q
                         }
                 }
             }
-            float acc[kScoreBatch];
+            float acc[U];
 #pragma unroll
-            for (int u = 0; u < kScoreBatch; ++u) acc[u] = 0.0f;
+            for (int u = 0; u < U; ++u) acc[u] = 0.0f;
 #pragma unroll
             for (int c = 0; c < QC; ++c) {
 #pragma unroll
@@ -129,7 +132,7 @@ __device__ __forceinline__ float attn_scores(const ndkv::Geom &g, const float *q
                     for (int b = 0; b < 4; ++b) {
                         const float qv = qs[c * 16 + d * 4 + b];
 #pragma unroll
-                        for (int u = 0; u < kScoreBatch; ++u) {
+                        for (int u = 0; u < U; ++u) {
                             const uint32_t dw = d == 0 ? kw[u][c].x
                                               : d == 1 ? kw[u][c].y
                                               : d == 2 ? kw[u][c].z
@@ -140,15 +143,24 @@ __device__ __forceinline__ float attn_scores(const ndkv::Geom &g, const float *q
                 }
             }
 #pragma unroll
-            for (int u = 0; u < kScoreBatch; ++u) {
-                const int t = t0 + u * NT;
-                if (t < span) {
-                    const float s = acc[u] * ksv[u] * scale;
-                    sc[t] = s;
-                    if (s > mx) mx = s;
-                }
+            for (int u = 0; u < U; ++u) {
+                const float s = acc[u] * ksv[u] * scale;
+                sc[t0 + u * NT] = s;
+                if (s > mx) mx = s;
             }
+        };
+        // whole batches, then this thread's last one to three positions in
+        // batches of 2 and 1: a thread with one position more than another
+        // does a fraction of a batch more, not a whole batch of mostly
+        // unused chains (spans past a multiple of 4 * NT)
+        int t0 = tid;
+        for (; t0 + (kScoreBatch - 1) * NT < span; t0 += NT * kScoreBatch)
+            batch(std::integral_constant<int, kScoreBatch>{}, t0);
+        if (t0 + NT < span) {
+            batch(std::integral_constant<int, 2>{}, t0);
+            t0 += 2 * NT;
         }
+        if (t0 < span) batch(std::integral_constant<int, 1>{}, t0);
     } else {
         for (int t = tid; t < span; t += NT) {
             int slot = base + t;
@@ -324,18 +336,17 @@ __device__ __forceinline__ void attn_exact2_run(const ndkv::Geom &g, const uint8
     __syncthreads();
     mx = L.red[0];
     for (int w = 1; w < NT / 64; ++w) mx = L.red[w] > mx ? L.red[w] : mx;
-    for (int t0 = tid; t0 < span; t0 += 4 * NT) {
+    int te = tid;
+    for (; te + 3 * NT < span; te += 4 * NT) {
         // four independent exps per thread in flight
         float e[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int t = t0 + u * NT;
-            e[u] = nd_expf(sc[t < span ? t : 0] - mx);
-        }
+        for (int u = 0; u < 4; ++u) e[u] = nd_expf(sc[te + u * NT] - mx);
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-            if (t0 + u * NT < span) sc[t0 + u * NT] = e[u];
+        for (int u = 0; u < 4; ++u) sc[te + u * NT] = e[u];
     }
+    // the thread's last one to three, one at a time
+    for (; te < span; te += NT) sc[te] = nd_expf(sc[te] - mx);
     __syncthreads();
 
     // Products sit column-major, [VD][T + 4] per buffer: a consumer lane reads
