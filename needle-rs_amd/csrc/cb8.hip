@@ -20,6 +20,7 @@
 // with fp32 accumulation: 64x64 tiles below M = 96, 128x128 tiles, and
 // 256x256 tiles with two waves per SIMD once a launch has a tile per CU.
 #include "nd_internal.h"
+#include "nd_lanes.h"
 
 #include <hip/hip_bf16.h>
 
@@ -38,10 +39,13 @@ constexpr int kRowsPerPass = kThreads / kLanesPerRow;  // 16
 // 16-byte vectors (bytes 512k + 16j) and, for odd M, one 8-byte vector
 // (bytes 512*(M/2) + 8j) -- every load instruction covers two rows x 256 or
 // 512 contiguous bytes -- and keeps the matching 8*M activations in
-// registers.  The 16 row passes of a wave are loaded in two halves: the
-// second half is issued as the first pass starts computing, so HBM traffic
-// overlaps the gathers.  Rows past `out` are clamped (a valid row is read
-// and its sum discarded) rather than predicated.
+// registers.  A wave's 16 rows (8 passes of two) are all loaded before the
+// first gather.  Each pass leaves one partial a lane; the 8 partials are
+// summed over their half waves together at the end with VALU lane moves
+// (a per-pass shuffle reduction costs five LDS round trips a row, which
+// measured 72-75 % of HBM against 85 % for the deferred sum).  Rows past
+// `out` are clamped (a valid row is read and its sum discarded) rather than
+// predicated.
 //
 // The codebook sits in LDS as 32 lane-private replicas, entry-major (entry
 // e, replica r at dword 32e + r): lane l's gathers all hit bank l % 32, so a
@@ -123,6 +127,7 @@ __global__ __launch_bounds__(kThreads, 4) void cb8_gemv_kernel(
     __syncthreads();
 
     const float *cbl = reinterpret_cast<const float *>(rep4) + (lane & 31);
+    float sp[kPasses];
 #pragma unroll
     for (int p = 0; p < kPasses; ++p) {
         if (p == 0) {
@@ -154,15 +159,13 @@ __global__ __launch_bounds__(kThreads, 4) void cb8_gemv_kernel(
                     acc[b] += cbl[e * 32] * xb[4 * d + b];
                 }
         }
-        float s = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-        s += __shfl_xor(s, 16, 32);
-        s += __shfl_xor(s, 8, 32);
-        s += __shfl_xor(s, 4, 32);
-        s += __shfl_xor(s, 2, 32);
-        s += __shfl_xor(s, 1, 32);
-        const int r = row0 + 2 * p;
-        if (j == 0 && r < out) y[r] = s;
+        sp[p] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
     }
+    // The eight rows' half-wave sums in one lane-exchange tree; lane j ends
+    // with the row of pass half_wave_slot<8>(j), and lanes 4k store.
+    const float s = ndl::half_wave_sum<kPasses>(sp, j);
+    const int r = row0 + 2 * ndl::half_wave_slot<kPasses>(j);
+    if ((j & 3) == 0 && r < out) y[r] = s;
 }
 
 // Any `in` (multiple of 16): activations staged in LDS instead of registers.

@@ -1,0 +1,99 @@
+// Cross-lane sums for gfx950 kernels that reduce many rows a wave at once.
+//
+// A per-row shuffle reduction (`__shfl_xor` five times) lowers to five
+// ds_bpermute round trips through the LDS pipe, each waited on before the
+// next add.  Kernels that finish a row every few hundred instructions spend
+// more time in those waits than in their gathers.  The helpers here keep the
+// partials of several rows in registers and reduce them together with VALU
+// lane moves: v_permlane16_swap for lanes 16 apart, DPP row_ror:8 for 8,
+// one ds_swizzle for 4 and DPP quad_perm for 2 and 1.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace ndl {
+
+// Lane l reads lane l ^ D of x, for D = 8, 4, 2 or 1 (within 32-lane halves).
+template <int D>
+__device__ inline float lane_xor(float x)
+{
+    static_assert(D == 8 || D == 4 || D == 2 || D == 1, "lane distance");
+    const int xi = __float_as_int(x);
+    if constexpr (D == 8)
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, xi, 0x128, 0xf, 0xf, false));  // row_ror:8
+    else if constexpr (D == 4)
+        return __int_as_float(__builtin_amdgcn_ds_swizzle(xi, 0x101f));  // and 0x1f, xor 4
+    else if constexpr (D == 2)
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, xi, 0x4e, 0xf, 0xf, false));  // quad_perm [2,3,0,1]
+    else
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, xi, 0xb1, 0xf, 0xf, false));  // quad_perm [1,0,3,2]
+}
+
+// One level of the tree at lane distance D over n open partials.  With
+// exchange, a lane keeps the upper half of its partials when bit D of its
+// index is set, the lower half otherwise, and adds its partner's copy of the
+// half it keeps; n halves.  Without exchange every partial adds its partner's.
+template <int D>
+__device__ inline void sum_level(float *v, int n, int j)
+{
+    const bool up = (j & D) != 0;
+    if (n > 1) {
+        const int h = n / 2;
+#pragma unroll
+        for (int q = 0; q < h; ++q) {
+            const float keep = up ? v[q + h] : v[q];
+            const float give = up ? v[q] : v[q + h];
+            v[q] = keep + lane_xor<D>(give);
+        }
+    } else {
+        v[0] += lane_xor<D>(v[0]);
+    }
+}
+
+// Sums P per-lane partials (P = 1, 2, 4 or 8) over each 32-lane half of a
+// wave.  Every total is the tree a shuffle reduction at lane distances 16, 8,
+// 4, 2, 1 forms, bit for bit (each level adds a lane's value and its
+// partner's).  The first log2(P) levels exchange halves, so lane j ends with
+// the total of partial half_wave_slot<P>(j) and v is overwritten.
+template <int P>
+__device__ inline int half_wave_slot(int j)
+{
+    static_assert(P == 1 || P == 2 || P == 4 || P == 8, "partials a lane");
+    int s = 0, w = P / 2;
+#pragma unroll
+    for (int bit = 16; bit >= 1 && w > 0; bit >>= 1, w >>= 1)
+        if (j & bit) s += w;
+    return s;
+}
+
+template <int P>
+__device__ inline float half_wave_sum(float (&v)[P], int j)
+{
+    static_assert(P == 1 || P == 2 || P == 4 || P == 8, "partials a lane");
+    // Distance 16: v_permlane16_swap exchanges odd 16-lane rows of its first
+    // operand with even rows of its second, so after swapping (lower half,
+    // upper half) an even-row lane holds its own and its partner's lower
+    // partial and an odd-row lane its partner's and its own upper one.
+    if constexpr (P > 1) {
+#pragma unroll
+        for (int q = 0; q < P / 2; ++q) {
+            const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[q]),
+                                                             __float_as_uint(v[q + P / 2]), false, false);
+            v[q] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+        }
+    } else {
+        const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[0]), __float_as_uint(v[0]), false, false);
+        v[0] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    }
+    int n = P > 1 ? P / 2 : 1;
+    sum_level<8>(v, n, j);
+    n = n > 1 ? n / 2 : 1;
+    sum_level<4>(v, n, j);
+    n = n > 1 ? n / 2 : 1;
+    sum_level<2>(v, n, j);
+    n = n > 1 ? n / 2 : 1;
+    sum_level<1>(v, n, j);
+    return v[0];
+}
+
+}  // namespace ndl
