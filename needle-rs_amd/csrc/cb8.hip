@@ -219,10 +219,10 @@ __global__ __launch_bounds__(kThreads) void cb8_gemv_generic_kernel(
             }
         }
         float s = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-        s += __shfl_xor(s, 8, kLanesPerRow);
-        s += __shfl_xor(s, 4, kLanesPerRow);
-        s += __shfl_xor(s, 2, kLanesPerRow);
-        s += __shfl_xor(s, 1, kLanesPerRow);
+        s += ndl::wave_xor<8>(s);
+        s += ndl::wave_xor<4>(s);
+        s += ndl::wave_xor<2>(s);
+        s += ndl::wave_xor<1>(s);
         if (j == 0 && r < out) y[r] = s;
     }
 }

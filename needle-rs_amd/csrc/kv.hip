@@ -374,7 +374,7 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(
     for (int r = 0; r < REP; ++r)
 #pragma unroll
         for (int e = 0; e < VW; ++e)
-            for (int off = S::VL; off < 64; off <<= 1) acc[r][e] += __shfl_xor(acc[r][e], off, 64);
+            acc[r][e] = ndl::wave_sum_from<S::VL>(acc[r][e]);
     if (lane < S::VL) {
 #pragma unroll
         for (int r = 0; r < REP; ++r)

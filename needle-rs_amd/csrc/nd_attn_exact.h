@@ -29,12 +29,7 @@ __device__ inline float gate_half_fwht(float v, const float *gate, int lane)
 {
     if (!gate) return v;
     v = v * nd_sigmoidf(gate[lane]);
-#pragma unroll
-    for (int h = 1; h < 64; h <<= 1) {
-        const float p = __shfl_xor(v, h, 64);
-        v = (lane & h) ? p - v : v + p;
-    }
-    return v;
+    return ndl::wave_fwht64(v);
 }
 
 // The same arithmetic, with the value pass split between roles.  Of the 256

@@ -3,23 +3,17 @@
 #pragma once
 
 #include "nd_internal.h"
+#include "nd_lanes.h"
 
 namespace ndkv {
 
 constexpr int kMaxRep = 8;
 constexpr int kMaxDim = 256;
 
-__device__ inline float wave_max(float v)
-{
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
-}
+// Lane pairs at distances 32 .. 1 through DPP and lane swaps (no LDS).
+__device__ inline float wave_max(float v) { return ndl::wave_max64(v); }
 
-__device__ inline float wave_sum(float v)
-{
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
+__device__ inline float wave_sum(float v) { return ndl::wave_sum64(v); }
 
 // absmax of a head vector read by one wave; returns (scale, inv) exactly as
 // quant_scale (cache.rs:80-91).

@@ -29,6 +29,96 @@ __device__ inline float lane_xor(float x)
         return __int_as_float(__builtin_amdgcn_update_dpp(0, xi, 0xb1, 0xf, 0xf, false));  // quad_perm [1,0,3,2]
 }
 
+// Lane l reads lane l ^ H of x across the whole wave, H = 1 .. 32 -- what
+// __shfl_xor(x, H, 64) returns, without its ds_bpermute round trip: DPP
+// quad_perm for 1 and 2, a row_shl:4 / row_shr:4 pair for 4, row_ror:8 for
+// 8, and for 16 and 32 one v_permlane16_swap / v_permlane32_swap of x with
+// itself (an even row, or the lower half, finds its partner's value in the
+// second result, the other lanes in the first).
+template <int H>
+__device__ inline float wave_xor(float x)
+{
+    static_assert(H == 32 || H == 16 || H == 8 || H == 4 || H == 2 || H == 1, "lane distance");
+    const int lane = threadIdx.x & 63;
+    if constexpr (H == 32 || H == 16) {
+        const uint32_t xi = __float_as_uint(x);
+        const auto sw = H == 32 ? __builtin_amdgcn_permlane32_swap(xi, xi, false, false)
+                                : __builtin_amdgcn_permlane16_swap(xi, xi, false, false);
+        return __uint_as_float((lane & H) ? sw[0] : sw[1]);
+    } else if constexpr (H == 4) {
+        const int xi = __float_as_int(x);
+        const int up = __builtin_amdgcn_update_dpp(0, xi, 0x104, 0xf, 0xf, false);  // row_shl:4, lane + 4
+        const int dn = __builtin_amdgcn_update_dpp(0, xi, 0x114, 0xf, 0xf, false);  // row_shr:4, lane - 4
+        return __int_as_float((lane & 4) ? dn : up);
+    } else {
+        return lane_xor<H>(x);
+    }
+}
+
+// The same for an int (argmax indices ride beside their values).
+template <int H>
+__device__ inline int wave_xor_int(int x)
+{
+    return __float_as_int(wave_xor<H>(__int_as_float(x)));
+}
+
+// Max and sum over the whole wave, pairing lanes at distances 32, 16, .., 1
+// (the tree of the usual shuffle loop, bit for bit); every lane gets the
+// result.
+__device__ inline float wave_max64(float v)
+{
+    v = fmaxf(v, wave_xor<32>(v));
+    v = fmaxf(v, wave_xor<16>(v));
+    v = fmaxf(v, wave_xor<8>(v));
+    v = fmaxf(v, wave_xor<4>(v));
+    v = fmaxf(v, wave_xor<2>(v));
+    return fmaxf(v, wave_xor<1>(v));
+}
+
+__device__ inline float wave_sum64(float v)
+{
+    v += wave_xor<32>(v);
+    v += wave_xor<16>(v);
+    v += wave_xor<8>(v);
+    v += wave_xor<4>(v);
+    v += wave_xor<2>(v);
+    return v + wave_xor<1>(v);
+}
+
+// v summed with its partners at lane distances D, 2 D, .., 32, in that
+// order (lanes sharing l mod D end with their group's total).
+template <int D>
+__device__ inline float wave_sum_from(float v)
+{
+    if constexpr (D < 64) {
+        v += wave_xor<D>(v);
+        return wave_sum_from<2 * D>(v);
+    } else {
+        return v;
+    }
+}
+
+// One Walsh-Hadamard butterfly stage across lanes H apart: the lane with
+// bit H clear forms a + b, the other a - b (its partner's value minus its
+// own), exactly the butterfly's two results.
+template <int H>
+__device__ inline float wave_butterfly(float v)
+{
+    const float p = wave_xor<H>(v);
+    return (threadIdx.x & H) ? p - v : v + p;
+}
+
+// Stages H = 1, 2, .., 32 in order.
+__device__ inline float wave_fwht64(float v)
+{
+    v = wave_butterfly<1>(v);
+    v = wave_butterfly<2>(v);
+    v = wave_butterfly<4>(v);
+    v = wave_butterfly<8>(v);
+    v = wave_butterfly<16>(v);
+    return wave_butterfly<32>(v);
+}
+
 // One level of the tree at lane distance D over n open partials.  With
 // exchange, a lane keeps the upper half of its partials when bit D of its
 // index is set, the lower half otherwise, and adds its partner's copy of the

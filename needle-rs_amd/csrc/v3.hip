@@ -111,14 +111,8 @@ __device__ inline void fwht_groups_lds(float *buf, int n, int group, float inv)
 // other a - b, exactly the butterfly's two results.  No block barrier.
 __device__ inline void fwht128_wave(float &x0, float &x1, float inv)
 {
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int h = 1; h < 64; h <<= 1) {
-        const float p0 = __shfl_xor(x0, h, 64), p1 = __shfl_xor(x1, h, 64);
-        const bool hi = (lane & h) != 0;
-        x0 = hi ? p0 - x0 : x0 + p0;
-        x1 = hi ? p1 - x1 : x1 + p1;
-    }
+    x0 = ndl::wave_fwht64(x0);
+    x1 = ndl::wave_fwht64(x1);
     const float a = x0, b = x1;
     x0 = (a + b) * inv;
     x1 = (a - b) * inv;
@@ -127,25 +121,25 @@ __device__ inline void fwht128_wave(float &x0, float &x1, float inv)
 // fwht128_wave over NG groups at once (one pair of registers per group),
 // each stage applied to every group before the next, so the shuffles of
 // different groups overlap; the same operations as fwht128_wave per group.
+template <int H, int NG>
+__device__ inline void fwht_stage_n(float (&x0)[NG], float (&x1)[NG])
+{
+#pragma unroll
+    for (int q = 0; q < NG; ++q) {
+        x0[q] = ndl::wave_butterfly<H>(x0[q]);
+        x1[q] = ndl::wave_butterfly<H>(x1[q]);
+    }
+}
+
 template <int NG>
 __device__ inline void fwht128_wave_n(float (&x0)[NG], float (&x1)[NG], float inv)
 {
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int h = 1; h < 64; h <<= 1) {
-        float p0[NG], p1[NG];
-#pragma unroll
-        for (int q = 0; q < NG; ++q) {
-            p0[q] = __shfl_xor(x0[q], h, 64);
-            p1[q] = __shfl_xor(x1[q], h, 64);
-        }
-        const bool hi = (lane & h) != 0;
-#pragma unroll
-        for (int q = 0; q < NG; ++q) {
-            x0[q] = hi ? p0[q] - x0[q] : x0[q] + p0[q];
-            x1[q] = hi ? p1[q] - x1[q] : x1[q] + p1[q];
-        }
-    }
+    fwht_stage_n<1>(x0, x1);
+    fwht_stage_n<2>(x0, x1);
+    fwht_stage_n<4>(x0, x1);
+    fwht_stage_n<8>(x0, x1);
+    fwht_stage_n<16>(x0, x1);
+    fwht_stage_n<32>(x0, x1);
 #pragma unroll
     for (int q = 0; q < NG; ++q) {
         const float a = x0[q], b = x1[q];
@@ -1210,7 +1204,7 @@ __global__ __launch_bounds__(ndattn::kAttn2Threads, 4) void k_attn_step(AttnStep
             // ZCRMSNorm: the head's sequential sum of squares, then RoPE
             float r = 0.0f;
             if (lane == 0) r = sqrtf(chain_sum(sqs[seg], hd) / float(hd) + 1e-6f);
-            r = __shfl(r, 0, 64);
+            r = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r), 0));
             if (lane < half) {
                 const float x1 = (1.0f + rn1) * x[lane] / r;
                 const float x2 = (1.0f + rn2) * x[half + lane] / r;
@@ -1475,10 +1469,10 @@ __global__ __launch_bounds__(1024) void k_post_hada(HadaArgs a, MhcIn mhc)
         // on its own lane, the sum one chain in j order (every lane folds it)
         const float pj = tid < r ? proj[tid] : -INFINITY;
         float mx = pj;
-        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+        mx = ndl::wave_max64(mx);
         const float e = tid < r ? nd_expf(pj - mx) : 0.0f;
         float sum = 0.0f;
-        for (int j = 0; j < r; ++j) sum += __shfl(e, j, 64);
+        for (int j = 0; j < r; ++j) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
         if (tid < r) proj[tid] = e / sum;
     }
     lds_barrier();
@@ -1624,12 +1618,12 @@ __global__ __launch_bounds__(kT) void k_argmax(const float *__restrict__ logits,
             }
         }
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const float ov = __shfl_xor(best, off, 64);
-        const int oi = __shfl_xor(bi, off, 64);
-        argmax_take(best, bi, ov, oi);
-    }
+    argmax_take(best, bi, ndl::wave_xor<32>(best), ndl::wave_xor_int<32>(bi));
+    argmax_take(best, bi, ndl::wave_xor<16>(best), ndl::wave_xor_int<16>(bi));
+    argmax_take(best, bi, ndl::wave_xor<8>(best), ndl::wave_xor_int<8>(bi));
+    argmax_take(best, bi, ndl::wave_xor<4>(best), ndl::wave_xor_int<4>(bi));
+    argmax_take(best, bi, ndl::wave_xor<2>(best), ndl::wave_xor_int<2>(bi));
+    argmax_take(best, bi, ndl::wave_xor<1>(best), ndl::wave_xor_int<1>(bi));
     const int w = threadIdx.x >> 6;
     if ((threadIdx.x & 63) == 0) {
         sv[w] = best;
