@@ -22,6 +22,7 @@
 //   cq_dequant   dequantize_row (cq.rs:763-779), bit-identical.
 #include "nd_internal.h"
 #include "nd_cq_internal.h"
+#include "nd_lanes.h"
 
 #include <cmath>
 #include <cstdlib>
@@ -176,10 +177,10 @@ __global__ __launch_bounds__(kThreads) void cq_gemv_kernel(
             for (int q = 1; q < P; ++q) dot += acc[q];
             if (r < rows && d < row_dwords) total += nr[gi[i]] * dot;
         }
-        total += __shfl_xor(total, 8, kLanesPerRow);
-        total += __shfl_xor(total, 4, kLanesPerRow);
-        total += __shfl_xor(total, 2, kLanesPerRow);
-        total += __shfl_xor(total, 1, kLanesPerRow);
+        total += ndl::wave_xor<8>(total);
+        total += ndl::wave_xor<4>(total);
+        total += ndl::wave_xor<2>(total);
+        total += ndl::wave_xor<1>(total);
         if (j == 0 && r < rows) y[r] = total;
     }
 }
@@ -279,10 +280,10 @@ __global__ __launch_bounds__(kThreads) void cq_gemv_stream_kernel(
                     for (int q = 1; q < P; ++q) dot += acc[q];
                     total += (second[i] ? nb[k][1] : nb[k][0]) * dot;
                 }
-                total += __shfl_xor(total, 8, kLanesPerRow);
-                total += __shfl_xor(total, 4, kLanesPerRow);
-                total += __shfl_xor(total, 2, kLanesPerRow);
-                total += __shfl_xor(total, 1, kLanesPerRow);
+                total += ndl::wave_xor<8>(total);
+                total += ndl::wave_xor<4>(total);
+                total += ndl::wave_xor<2>(total);
+                total += ndl::wave_xor<1>(total);
                 const int r = tt * kRowsPerPass + rg;
                 if (j == 0 && r < rows) y[r] = total;
             }
@@ -883,8 +884,8 @@ __global__ __launch_bounds__(kMf2Threads, 2) void cq_gemv_mf2_kernel(
                 }
                 s += norms[size_t(row_start + r) * NG + g] * part;
             }
-            s += __shfl_xor(s, 16);
-            s += __shfl_xor(s, 32);
+            s += ndl::wave_xor<16>(s);
+            s += ndl::wave_xor<32>(s);
             if (q == 0) stage[(it % kMf2Stage) * kMf2Rows + 16 * w + c] = s;
             if ((it + 1) % kMf2Stage == 0)
                 flush_stage<kMf2Threads>(stage, kMf2Stage, kMf2Rows, it + 1, kMf2Stage, iters, rows, y);
@@ -965,8 +966,8 @@ __global__ __launch_bounds__(kMf2Threads, 2) void cq_gemv_mf2_kernel(
 #pragma unroll
             for (int g = 0; g < NG; ++g)
                 s += nw[k][g] * (((acc[g][0] + acc[g][1]) + (acc[g][2] + acc[g][3])) + axq[g]);
-            s += __shfl_xor(s, 16);
-            s += __shfl_xor(s, 32);
+            s += ndl::wave_xor<16>(s);
+            s += ndl::wave_xor<32>(s);
             if (q == 0) stage[(it % kMf2Stage) * kMf2Rows + 16 * w + c] = s;
             __builtin_amdgcn_sched_barrier(0);
             load(it + D, k);
@@ -1021,7 +1022,7 @@ __global__ __launch_bounds__(256) void cq_gemv_generic_kernel(
         }
         total += nr[g] * acc;
     }
-    for (int off = 32; off > 0; off >>= 1) total += __shfl_xor(total, off, 64);
+    total = ndl::wave_sum64(total);
     if (lane == 0) y[r] = total;
     (void)in_padded;
 }
