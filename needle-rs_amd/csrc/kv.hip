@@ -164,6 +164,13 @@ struct AttnShape {
     // 5.83 / 5.91; 384: 4.43 / 5.47 / 5.73)
     static constexpr int CH = 256;
     static constexpr int KP = (CH + KPP - 1) / KPP;           // K passes per chunk
+    // One query head a kv head, KL a power of two (qk 16 .. 256) and one
+    // pass per lane of a position: the KL partial dots meet through DPP in
+    // registers, no LDS and no barrier.  qk 48 (three lanes a position)
+    // sums them in LDS, and so do grouped heads (their REP dots a pass held
+    // across the passes took 6-55 more VGPRs than the LDS sums)
+    static constexpr bool kLaneSums =
+        REP == 1 && (KL & (KL - 1)) == 0 && KL <= 16 && KP == KL && KPP * KL == kThreads;
     static constexpr int VP = CH / VPP;                       // V passes per chunk
 };
 
@@ -272,6 +279,47 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(
 
     for (int c = c_begin; c < c_end; ++c) {
         const int n = min(CH, span - c * CH);
+        float cmax[REP];
+#pragma unroll
+        for (int r = 0; r < REP; ++r) cmax[r] = -INFINITY;
+        if constexpr (S::kLaneSums) {
+            // ---- scores: lane partial dots summed across the position's KL
+            // lanes by DPP; lane ksub keeps pass ksub's position ----
+            const int own = ksub * S::KPP + kpos;
+            const float ks = ksb[(lo + c * CH + min(own, n - 1)) % g.cap];
+            float dot[REP];
+#pragma unroll
+            for (int r = 0; r < REP; ++r) dot[r] = 0.0f;
+#pragma unroll
+            for (int p = 0; p < S::KP; ++p) {
+                const uint32_t dw[4] = {kr[p].x, kr[p].y, kr[p].z, kr[p].w};
+                float kf[16];
+#pragma unroll
+                for (int d = 0; d < 4; ++d)
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) kf[4 * d + b] = i8_at(dw[d], b);
+#pragma unroll
+                for (int r = 0; r < REP; ++r) {
+                    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 16; e += 2) {
+                        a0 += qr[r][e] * kf[e];
+                        a1 += qr[r][e + 1] * kf[e + 1];
+                    }
+                    const float v = ndl::group_sum<S::KL>(a0 + a1);
+                    dot[r] = ksub == p ? v : dot[r];
+                }
+            }
+            if (c + 1 < c_end) load_k(c + 1);  // lands during softmax and values
+            if (own < n) {
+#pragma unroll
+                for (int r = 0; r < REP; ++r) {
+                    const float sc = (dot[r] * ks) * scale;
+                    wsh[r][own] = sc;
+                    cmax[r] = sc;
+                }
+            }
+        } else {
         // ---- scores: lane partial dots ----
 #pragma unroll
         for (int p = 0; p < S::KP; ++p) {
@@ -298,9 +346,6 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(
         if (c + 1 < c_end) load_k(c + 1);  // lands during softmax and values
         __syncthreads();
         // ---- per-position score, chunk max ----
-        float cmax[REP];
-#pragma unroll
-        for (int r = 0; r < REP; ++r) cmax[r] = -INFINITY;
         for (int pl = t; pl < n; pl += kThreads) {
             const int slot = (lo + c * CH + pl) % g.cap;
             const float ks = ksb[slot];
@@ -313,6 +358,7 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(
                 wsh[r][pl] = sc;
                 cmax[r] = fmaxf(cmax[r], sc);
             }
+        }
         }
 #pragma unroll
         for (int r = 0; r < REP; ++r) {

@@ -98,6 +98,20 @@ __device__ inline float wave_sum_from(float v)
     }
 }
 
+// Sum over aligned groups of N consecutive lanes (N = 1, 2, 4, 8, 16),
+// pairing lanes at distances 1, 2, .., N / 2; every lane of a group gets
+// the group's total.
+template <int N>
+__device__ inline float group_sum(float v)
+{
+    static_assert(N == 1 || N == 2 || N == 4 || N == 8 || N == 16, "group size");
+    if constexpr (N >= 2) v += wave_xor<1>(v);
+    if constexpr (N >= 4) v += wave_xor<2>(v);
+    if constexpr (N >= 8) v += wave_xor<4>(v);
+    if constexpr (N >= 16) v += wave_xor<8>(v);
+    return v;
+}
+
 // One Walsh-Hadamard butterfly stage across lanes H apart: the lane with
 // bit H clear forms a + b, the other a - b (its partner's value minus its
 // own), exactly the butterfly's two results.
