@@ -55,6 +55,14 @@ __device__ inline float wave_xor(float x)
     }
 }
 
+// Lane K of x's aligned group of four lanes (DPP quad_perm [K,K,K,K]).
+template <int K>
+__device__ inline float quad_lane(float x)
+{
+    static_assert(K >= 0 && K < 4, "quad lane");
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), K * 0x55, 0xf, 0xf, false));
+}
+
 // The same for an int (argmax indices ride beside their values).
 template <int H>
 __device__ inline int wave_xor_int(int x)

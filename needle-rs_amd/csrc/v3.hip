@@ -376,7 +376,6 @@ __global__ __launch_bounds__(NTH) void k_layer_in(LayerIn a)
     __shared__ __align__(16) float us[1024], bxs[1024], pa[1024], pb[1024], pc[1024];
     __shared__ float gs[kMaxPhiPairs], pn[kMaxPhiPairs], lvl[48], hp[16], gpp[16], grr[256], tot[4];
     __shared__ NdFoldLds<NTH> fl;
-    __shared__ float qlanes[NTH / 4 * 8];  // split phi pairs' lane chains
     const size_t b = blockIdx.x;
     const int tid = threadIdx.x, n = a.n, d = a.d, nd = n * d;
     // phi rows: phi_pre's n, then (gates) phi_post's n and phi_res's n * n
@@ -543,8 +542,18 @@ __global__ __launch_bounds__(NTH) void k_layer_in(LayerIn a)
             if (t < pairs) {
                 float l0, l1;
                 cq_group_quarter128<PP>(codes[k], lvl + 16 * wsel[k], nb + (t % G) * kPadGroup, q, l0, l1);
-                qlanes[(t - NTH) * 8 + 2 * q] = l0;
-                qlanes[(t - NTH) * 8 + 2 * q + 1] = l1;
+                // the pair's eight lane chains summed 0..7, as
+                // cq_group_dot128 ends, from the quad's registers
+                float acc = 0.0f;
+                acc += ndl::quad_lane<0>(l0);
+                acc += ndl::quad_lane<0>(l1);
+                acc += ndl::quad_lane<1>(l0);
+                acc += ndl::quad_lane<1>(l1);
+                acc += ndl::quad_lane<2>(l0);
+                acc += ndl::quad_lane<2>(l1);
+                acc += ndl::quad_lane<3>(l0);
+                acc += ndl::quad_lane<3>(l1);
+                if (q == 0) gs[t] = acc;
             }
             continue;
         }
@@ -552,16 +561,6 @@ __global__ __launch_bounds__(NTH) void k_layer_in(LayerIn a)
         if (t < pairs) gs[t] = cq_group_dot128<PP>(codes[k], lvl + 16 * wsel[k], nb + (t % G) * kPadGroup);
     }
     lds_barrier();
-    if (quarters) {
-        // the split pairs' lanes summed 0..7, as cq_group_dot128 ends
-        if (tid < extra) {
-            float acc = 0.0f;
-#pragma unroll
-            for (int k = 0; k < 8; ++k) acc += qlanes[tid * 8 + k];
-            gs[NTH + tid] = acc;
-        }
-        lds_barrier();
-    }
     if (tid < prows) {
         float total = 0.0f;
         for (int g = 0; g < G; ++g) total += pn[tid * G + g] * gs[tid * G + g];
