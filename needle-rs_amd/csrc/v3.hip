@@ -118,9 +118,7 @@ __device__ inline void fwht128_wave(float &x0, float &x1, float inv)
     x1 = (a - b) * inv;
 }
 
-// fwht128_wave over NG groups at once (one pair of registers per group),
-// each stage applied to every group before the next, so the shuffles of
-// different groups overlap; the same operations as fwht128_wave per group.
+// Butterfly stage H of fwht128_wave on NG groups' register pairs.
 template <int H, int NG>
 __device__ inline void fwht_stage_n(float (&x0)[NG], float (&x1)[NG])
 {
@@ -131,6 +129,9 @@ __device__ inline void fwht_stage_n(float (&x0)[NG], float (&x1)[NG])
     }
 }
 
+// fwht128_wave over NG groups at once (one pair of registers per group),
+// each stage applied to every group before the next, so the lane moves of
+// different groups overlap; the same operations as fwht128_wave per group.
 template <int NG>
 __device__ inline void fwht128_wave_n(float (&x0)[NG], float (&x1)[NG], float inv)
 {
@@ -511,7 +512,7 @@ __global__ __launch_bounds__(NTH) void k_layer_in(LayerIn a)
         const float inv = 1.0f / sqrtf(tot[0] / float(nd) + 1e-6f);
         const int wave = tid >> 6, lane = tid & 63;
         float *xo = a.nxh + b * a.pnx.in_padded;
-        // three groups a wave at a time, their shuffles overlapped
+        // three groups a wave at a time, their lane moves overlapped
         constexpr int NG = 3;
         for (int g0 = wave; g0 < G; g0 += NG * (NTH / 64)) {
             float x0[NG], x1[NG];
@@ -653,7 +654,8 @@ __device__ inline float lse_row(const float *x, int n)
 // of one wave: every row (then column) logsumexp is the reference's loop --
 // max, sequential sum of exps, max + log.  Each lane exponentiates its own
 // entry; the lanes of a row (column) then fold the row's exps in index
-// order from shuffles, all rows at once.
+// order from shuffles, all rows at once (any n; the decode step's split
+// gate phases use the DPP form below for n = 4).
 __device__ inline float sinkhorn_wave(float m, int n)
 {
     const int lane = threadIdx.x & 63;
