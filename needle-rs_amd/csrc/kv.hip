@@ -282,11 +282,16 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(
         float cmax[REP];
 #pragma unroll
         for (int r = 0; r < REP; ++r) cmax[r] = -INFINITY;
+        // the position this lane scores, its score and V scale (lane sums)
+        const int own = ksub * S::KPP + kpos;
+        float own_sc[REP], own_vs = 0.0f;
         if constexpr (S::kLaneSums) {
             // ---- scores: lane partial dots summed across the position's KL
-            // lanes by DPP; lane ksub keeps pass ksub's position ----
-            const int own = ksub * S::KPP + kpos;
-            const float ks = ksb[(lo + c * CH + min(own, n - 1)) % g.cap];
+            // lanes by DPP; lane ksub keeps pass ksub's position, and its
+            // K and V scales are requested before the dots ----
+            const int oslot = (lo + c * CH + min(own, n - 1)) % g.cap;
+            const float ks = ksb[oslot];
+            own_vs = vsb[oslot];
             float dot[REP];
 #pragma unroll
             for (int r = 0; r < REP; ++r) dot[r] = 0.0f;
@@ -311,13 +316,10 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(
                 }
             }
             if (c + 1 < c_end) load_k(c + 1);  // lands during softmax and values
-            if (own < n) {
 #pragma unroll
-                for (int r = 0; r < REP; ++r) {
-                    const float sc = (dot[r] * ks) * scale;
-                    wsh[r][own] = sc;
-                    cmax[r] = sc;
-                }
+            for (int r = 0; r < REP; ++r) {
+                own_sc[r] = (dot[r] * ks) * scale;
+                if (own < n) cmax[r] = own_sc[r];
             }
         } else {
         // ---- scores: lane partial dots ----
@@ -378,14 +380,25 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(
             l_loc[r] *= alpha[r];
         }
         // ---- weights e * v_scale; running sum ----
-        for (int pl = t; pl < n; pl += kThreads) {
-            const int slot = (lo + c * CH + pl) % g.cap;
-            const float vs = vsb[slot];
+        if constexpr (S::kLaneSums) {
+            if (own < n) {
 #pragma unroll
-            for (int r = 0; r < REP; ++r) {
-                const float e = expf(wsh[r][pl] - mnew[r]);
-                l_loc[r] = l_loc[r] + e;
-                wsh[r][pl] = e * vs;
+                for (int r = 0; r < REP; ++r) {
+                    const float e = expf(own_sc[r] - mnew[r]);
+                    l_loc[r] = l_loc[r] + e;
+                    wsh[r][own] = e * own_vs;
+                }
+            }
+        } else {
+            for (int pl = t; pl < n; pl += kThreads) {
+                const int slot = (lo + c * CH + pl) % g.cap;
+                const float vs = vsb[slot];
+#pragma unroll
+                for (int r = 0; r < REP; ++r) {
+                    const float e = expf(wsh[r][pl] - mnew[r]);
+                    l_loc[r] = l_loc[r] + e;
+                    wsh[r][pl] = e * vs;
+                }
             }
         }
         __syncthreads();
