@@ -7,6 +7,11 @@
 // partials of several rows in registers and reduce them together with VALU
 // lane moves: v_permlane16_swap for lanes 16 apart, DPP row_ror:8 for 8,
 // one ds_swizzle for 4 and DPP quad_perm for 2 and 1.
+//
+// Lanes are numbered threadIdx.x % 64: every caller launches one-dimensional
+// blocks whose width is a multiple of 64, with all lanes of the wave active
+// where it calls (DPP and the lane swaps read the partner's register
+// directly).
 #pragma once
 
 #include <hip/hip_runtime.h>
