@@ -175,11 +175,13 @@ def test_attend_step_causal(ctx, H, KVH, QK, VD, ctxlen):
     assert np.max(np.abs(out - want)) <= 1e-4
 
 
+@pytest.mark.parametrize("H,KVH,QK", [(12, 2, 48), (12, 12, 64)])
 @pytest.mark.parametrize("lo,hi", [(0, 0), (5, 5), (3, 16), (1000, 1023), (1000, 2023),
                                    (4000, 5023), (17, 1040)])
-def test_attend_step_ring_window(ctx, lo, hi):
-    """A 1024-slot local ring read across its wrap point."""
-    H, KVH, QK, VD, cap = 12, 2, 48, 64, 1024
+def test_attend_step_ring_window(ctx, H, KVH, QK, lo, hi):
+    """A 1024-slot local ring read across its wrap point: the v3 GQA geometry
+    (lane dots summed in LDS) and the MHA cache (lane dots summed by DPP)."""
+    VD, cap = 64, 1024
     rng = np.random.default_rng(lo * 31 + hi)
     g = nd.kv_geom(H, KVH, QK, VD, cap)
     blk, nb = nd.kv_alloc(g)
